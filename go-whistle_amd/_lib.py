@@ -1,0 +1,86 @@
+"""ctypes binding of libcqhip.so (include/cqhip.h).
+
+The library is the product: a missing or unloadable libcqhip.so raises
+here, loudly; nothing falls back to a CPU path.
+"""
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int8, c_int32, c_longlong, c_size_t, c_uint8, c_void_p
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libcqhip.so")
+
+CQ_OK, CQ_ERR_ARG, CQ_ERR_MISUSE, CQ_ERR_DEVICE, CQ_ERR_UNSUPPORTED = 0, 1, 2, 3, 4
+
+# Every symbol include/cqhip.h declares, with (restype, argtypes).
+SIGNATURES = {
+    "cq_last_error": (c_char_p, []),
+    "cq_version": (c_char_p, []),
+    "cq_device_info": (c_int, [c_char_p, c_size_t]),
+    "cq_new": (c_int, [c_int, c_int, c_int, c_int, c_int, POINTER(c_float), c_size_t, POINTER(c_uint8), c_size_t,
+                       POINTER(c_uint8), c_size_t, c_int, POINTER(c_void_p)]),
+    "cq_free": (None, [c_void_p]),
+    "cq_out": (c_int, [c_void_p]),
+    "cq_in": (c_int, [c_void_p]),
+    "cq_bits": (c_int, [c_void_p]),
+    "cq_prepare": (c_int, [c_void_p]),
+    "cq_bytes": (c_longlong, [c_void_p]),
+    "cq_device_bytes": (c_longlong, [c_void_p]),
+    "cq_rows": (c_int, [c_void_p, c_int, c_int, POINTER(c_void_p)]),
+    "cq_exact": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "cq_kernel_name": (c_char_p, [c_void_p]),
+    "cq_row": (c_int, [c_void_p, POINTER(c_float), c_size_t, c_int]),
+    "cq_gemm": (c_int, [c_void_p, POINTER(c_float), c_size_t, POINTER(c_float), c_size_t, c_int]),
+    "cq_gemms": (c_int, [c_int, POINTER(c_void_p), POINTER(POINTER(c_float)), POINTER(c_size_t), POINTER(c_float),
+                         c_size_t, c_int]),
+    "cq_gemm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "cq_gemms_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p]),
+    "cq_row_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
+    "cq_row_gather_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "kv_quantize_rows": (c_int, [POINTER(c_int8), POINTER(c_float), POINTER(c_float), c_int, c_int, c_int]),
+    "kv_quantize_rows_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "kv_attend_int8_dev": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p,
+                                   c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_longlong, c_longlong, c_void_p,
+                                   c_int, c_float, c_int, c_int, c_void_p]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library with its signatures set; raises if it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libcqhip.so is not built ({LIB_PATH}); run __graft_entry__.build()")
+        lb = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(lb, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = lb
+    return _lib
+
+
+class CQError(Exception):
+    """A construction error: what the Go API returns as an error value."""
+
+
+class CQPanic(Exception):
+    """Shape misuse: where the Go API panics."""
+
+
+class CQDeviceError(Exception):
+    """A HIP runtime failure or a geometry the library does not run."""
+
+
+def check(rc):
+    if rc == CQ_OK:
+        return
+    msg = lib().cq_last_error().decode()
+    if rc == CQ_ERR_ARG:
+        raise CQError(msg)
+    if rc == CQ_ERR_MISUSE:
+        raise CQPanic(msg)
+    raise CQDeviceError(f"{msg} (status {rc})")

@@ -1,0 +1,170 @@
+"""go-whistle's internal/cq Matrix API over libcqhip's C ABI.
+
+Mirrors the Go surface (internal/cq/matrix.go:25-189, kernel.go:76-158):
+New / NewGather, Out, In, Bits, Prepare, Bytes, Rows, Exact, Row, GEMV,
+GEMM and GEMMs, with the same argument meaning. Construction errors raise
+CQError (the Go error result), shape misuse raises CQPanic (the Go panic).
+Host arrays are numpy float32; the *_dev methods take torch tensors that
+live on the GPU and queue the work on torch's current stream.
+"""
+
+from dataclasses import dataclass
+import ctypes
+from ctypes import POINTER, c_float, c_size_t, c_uint8, c_void_p
+
+import numpy as np
+
+from ._lib import CQPanic, check, lib
+
+
+@dataclass
+class Packed:
+    """cact.Packed (internal/cact/packed.go:18-29): a CQ tensor as stored."""
+
+    Out: int
+    In: int
+    Group: int
+    Bits: int
+    Width: int
+    Codebook: np.ndarray  # float32, 2^Bits levels
+    Index: np.ndarray     # uint8, Out * RowBytes
+    Norms: np.ndarray     # uint8, 2 * Out * Groups little-endian FP16
+
+    def Groups(self):
+        return (self.In + self.Group - 1) // self.Group
+
+    def RowBytes(self):
+        return self.Groups() * self.Group * self.Width // 8
+
+
+def _fptr(a):
+    return a.ctypes.data_as(POINTER(c_float))
+
+
+def _f32(a):
+    a = np.asarray(a)
+    if a.dtype != np.float32 or not a.flags.c_contiguous:
+        raise CQPanic("cq: float32 contiguous arrays expected")
+    return a
+
+
+def _stream():
+    import torch
+
+    return c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Matrix:
+    """A CQ matrix or view (internal/cq/matrix.go:25-41), on the device."""
+
+    def __init__(self, handle):
+        self._h = c_void_p(handle)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().cq_free(h)
+            self._h = None
+
+    @property
+    def handle(self):
+        return self._h
+
+    # --- construction (matrix.go:46-96) ---
+    @staticmethod
+    def _new(p: Packed, gather: bool):
+        cb = np.ascontiguousarray(p.Codebook, dtype=np.float32)
+        idx = np.ascontiguousarray(p.Index, dtype=np.uint8)
+        nrm = np.ascontiguousarray(p.Norms, dtype=np.uint8)
+        out = c_void_p()
+        check(lib().cq_new(p.Out, p.In, p.Group, p.Bits, p.Width, _fptr(cb), cb.size,
+                           idx.ctypes.data_as(POINTER(c_uint8)), idx.size, nrm.ctypes.data_as(POINTER(c_uint8)),
+                           nrm.size, 1 if gather else 0, ctypes.byref(out)))
+        return Matrix(out.value)
+
+    def Out(self):
+        return lib().cq_out(self._h)
+
+    def In(self):
+        return lib().cq_in(self._h)
+
+    def Bits(self):
+        return lib().cq_bits(self._h)
+
+    def Prepare(self):
+        check(lib().cq_prepare(self._h))
+
+    def Bytes(self):
+        return lib().cq_bytes(self._h)
+
+    def DeviceBytes(self):
+        return lib().cq_device_bytes(self._h)
+
+    def Rows(self, lo, hi):
+        v = c_void_p()
+        check(lib().cq_rows(self._h, lo, hi, ctypes.byref(v)))
+        return Matrix(v.value)
+
+    def Exact(self):
+        v = c_void_p()
+        check(lib().cq_exact(self._h, ctypes.byref(v)))
+        return Matrix(v.value)
+
+    def Kernel(self):
+        return lib().cq_kernel_name(self._h).decode()
+
+    # --- host-slice products ---
+    def Row(self, dst, r):
+        dst = _f32(dst)
+        check(lib().cq_row(self._h, _fptr(dst), dst.size, r))
+
+    def GEMV(self, dst, x):
+        self.GEMM(dst, x, 1)
+
+    def GEMM(self, dst, x, rows):
+        dst, x = _f32(dst), _f32(x)
+        check(lib().cq_gemm(self._h, _fptr(dst), dst.size, _fptr(x), x.size, rows))
+
+    # --- device tensors (torch, on the GPU) ---
+    def gemm_dev(self, y, x, rows):
+        check(lib().cq_gemm_dev(self._h, c_void_p(y.data_ptr()), c_void_p(x.data_ptr()), rows, _stream()))
+
+    def row_dev(self, dst, r):
+        check(lib().cq_row_dev(self._h, c_void_p(dst.data_ptr()), r, _stream()))
+
+    def row_gather_dev(self, dst, rows_i32):
+        check(lib().cq_row_gather_dev(self._h, c_void_p(dst.data_ptr()), c_void_p(rows_i32.data_ptr()),
+                                      int(rows_i32.numel()), _stream()))
+
+
+def New(p: Packed) -> Matrix:
+    """cq.New (matrix.go:46-55)."""
+    return Matrix._new(p, False)
+
+
+def NewGather(p: Packed) -> Matrix:
+    """cq.NewGather (matrix.go:60-96)."""
+    return Matrix._new(p, True)
+
+
+def GEMMs(ms, dsts, x, rows):
+    """cq.GEMMs (kernel.go:134-158) on host arrays."""
+    if len(ms) != len(dsts):
+        raise CQPanic(f"cq: GEMMs of {len(ms)} matrices into {len(dsts)} outputs")
+    n = len(ms)
+    x = _f32(x)
+    dsts = [_f32(d) for d in dsts]
+    hs = (c_void_p * max(n, 1))(*[m.handle for m in ms])
+    ds = (POINTER(c_float) * max(n, 1))(*[_fptr(d) for d in dsts])
+    ls = (c_size_t * max(n, 1))(*[d.size for d in dsts])
+    check(lib().cq_gemms(n, hs, ds, ls, _fptr(x), x.size, rows))
+
+
+def gemms_dev(ms, ys, x, rows):
+    """cq.GEMMs on device tensors."""
+    n = len(ms)
+    if n != len(ys):
+        raise CQPanic(f"cq: GEMMs of {n} matrices into {len(ys)} outputs")
+    hs = (c_void_p * max(n, 1))(*[m.handle for m in ms])
+    ds = (c_void_p * max(n, 1))(*[c_void_p(y.data_ptr()) for y in ys])
+    check(lib().cq_gemms_dev(n, hs, ds, c_void_p(x.data_ptr()), rows, _stream()))

@@ -1,0 +1,574 @@
+// C-ABI of libcqhip (include/cqhip.h): the host side of go-whistle's
+// internal/cq Matrix API and the int8 KV entry points, over the gfx950
+// kernels of cq_kernels.hip and int8_kernels.hip.
+//
+// A cq_matrix is a view {storage, first row, rows, exact} of an immutable
+// device storage shared by every view (internal/cq/matrix.go:25-41, 131-157).
+// Validation, error texts and the Bytes accounting follow the reference
+// (matrix.go:46-145, kernel.go:100-158); shape misuse, which the Go API
+// answers with a panic, returns CQ_ERR_MISUSE with the panic's text.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/cqhip.h"
+#include "cq_internal.hpp"
+
+using namespace cqhip;
+
+namespace {
+
+thread_local std::string t_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(CQ_ERR_DEVICE, "cq: %s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                          \
+    do {                                             \
+        hipError_t e_ = (expr);                      \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+struct DeviceInfo {
+    int device = -1;
+    int cus = 256;
+    size_t max_lds = 64 * 1024;
+    std::string name;
+};
+
+DeviceInfo &device_info() {
+    static DeviceInfo info;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return;
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return;
+        info.device = dev;
+        info.cus = p.multiProcessorCount;
+        info.max_lds = std::max<size_t>(p.sharedMemPerBlock, 64 * 1024);
+        info.name = p.gcnArchName;
+    });
+    return info;
+}
+
+// Per-thread stream and device staging for the host-slice calls.
+struct Staging {
+    hipStream_t stream = nullptr;
+    void *buf = nullptr;
+    size_t cap = 0;
+    ~Staging() {
+        if (buf) (void)hipFree(buf);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+    hipError_t ensure(size_t bytes) {
+        if (!stream) {
+            hipError_t e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
+            if (e != hipSuccess) return e;
+        }
+        if (bytes <= cap) return hipSuccess;
+        if (buf) (void)hipFree(buf);
+        buf = nullptr;
+        cap = 0;
+        size_t want = std::max<size_t>(bytes, 1 << 20);
+        hipError_t e = hipMalloc(&buf, want);
+        if (e != hipSuccess) return e;
+        cap = want;
+        return hipSuccess;
+    }
+};
+thread_local Staging t_stage;
+
+size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace
+
+// ---- matrix storage and views -----------------------------------------------
+
+struct CqStore {
+    int out, in, group, groups, width, row_bytes, group_bytes, unit_bytes, units, nblk;
+    float cb[16];
+    int ncb;
+    float cb_max, lut_step, inv_sqrt;
+    uint8_t *d_idx = nullptr;
+    uint16_t *d_norm = nullptr;
+    size_t idx_bytes = 0, norm_bytes = 0;
+    std::atomic<bool> prepared{false};
+    ~CqStore() {
+        if (d_idx) (void)hipFree(d_idx);
+        if (d_norm) (void)hipFree(d_norm);
+    }
+};
+
+struct cq_matrix {
+    std::shared_ptr<CqStore> st;
+    int row0, out;
+    bool exact;
+};
+
+namespace {
+
+// best() (internal/cq/kernel.go:92-98): lut unless Exact or the groups are
+// wider than the lut kernel's 256 bytes.
+bool uses_lut(const cq_matrix *m) { return !m->exact && m->st->group_bytes <= kLutMaxGroupBytes; }
+
+float gomax(float a, float b) {
+    if (a != a || b != b) return NAN;
+    return a > b ? a : b;
+}
+
+// The shared-table test of lut.go:206-209.
+bool shares_tables(const CqStore &a, const CqStore &b) {
+    if (a.in != b.in || a.group != b.group || a.width != b.width || a.cb_max != b.cb_max) return false;
+    for (int c = 0; c < a.ncb; ++c)
+        if (a.cb[c] != b.cb[c]) return false;
+    return true;
+}
+
+struct LaunchPlan {
+    int tb, gc;
+    size_t lds;
+};
+
+LaunchPlan plan(const CqStore &s, int mode, long long nblk_total, int rows) {
+    const DeviceInfo &d = device_info();
+    LaunchPlan p;
+    // Up to four blocks per tile once there are enough tiles to fill the chip.
+    long long want = 2LL * d.cus;
+    long long work = nblk_total * std::max(rows, 1);
+    p.tb = static_cast<int>(std::min<long long>(4, std::max<long long>(1, work / want)));
+    const size_t budget = std::min<size_t>(d.max_lds, 96 * 1024);
+    p.gc = s.groups;
+    while (p.gc > 1 && product_lds_bytes(s.width, s.group_bytes, mode, p.gc, p.tb) > budget) p.gc--;
+    p.lds = product_lds_bytes(s.width, s.group_bytes, mode, p.gc, p.tb);
+    return p;
+}
+
+int check_geometry(const CqStore &s, int mode) {
+    if (mode == kModeLut && s.group_bytes > kLutMaxGroupBytes)
+        return fail(CQ_ERR_UNSUPPORTED, "cq: lut kernel with %d index bytes per group", s.group_bytes);
+    if (s.group_bytes > 512)
+        return fail(CQ_ERR_UNSUPPORTED, "cq: group %d of %d bits is wider than this library runs", s.group, s.width);
+    const size_t need = product_lds_bytes(s.width, s.group_bytes, mode, 1, 1);
+    if (need > device_info().max_lds)
+        return fail(CQ_ERR_UNSUPPORTED, "cq: group %d needs %zu bytes of LDS", s.group, need);
+    return CQ_OK;
+}
+
+void fill_common(ProdArgs &a, const CqStore &s, int rows) {
+    a.in = s.in;
+    a.groups = s.groups;
+    a.row_bytes = s.row_bytes;
+    a.rows = rows;
+    for (int c = 0; c < 16; ++c) a.cb[c] = c < s.ncb ? s.cb[c] : 0.0f;
+    a.cb_max = s.cb_max;
+    a.lut_step = s.lut_step;
+    a.inv_sqrt = s.inv_sqrt;
+    a.nib4_rows = rows - rows % 4;  // gemmScalar (kernel.go:170-183)
+}
+
+// Launches the product of up to kMaxMatrices views sharing their tables.
+int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+    const CqStore &s0 = *ms[0]->st;
+    const int mode = uses_lut(ms[0]) ? kModeLut : kModeExact;
+    int rc = check_geometry(s0, mode);
+    if (rc) return rc;
+    ProdArgs a;
+    std::memset(&a, 0, sizeof a);
+    fill_common(a, s0, rows);
+    a.x = x;
+    a.x_stride = s0.in;
+    long long nblk_total = 0;
+    for (int k = 0; k < n; ++k) {
+        const int row0 = ms[k]->row0, out = ms[k]->out;
+        nblk_total += (row0 + out + kBlockRows - 1) / kBlockRows - row0 / kBlockRows;
+    }
+    LaunchPlan p = plan(s0, mode, nblk_total, rows);
+    a.tb = p.tb;
+    a.gc = p.gc;
+    int tiles = 0;
+    a.nmats = 0;
+    for (int k = 0; k < n; ++k) {
+        const cq_matrix *m = ms[k];
+        if (m->out == 0) continue;
+        MatDesc &d = a.mats[a.nmats++];
+        d.idx = m->st->d_idx;
+        d.norm = m->st->d_norm;
+        d.y = dsts[k];
+        d.y_stride = m->out;
+        d.row0 = m->row0;
+        d.out = m->out;
+        d.blk0 = m->row0 / kBlockRows;
+        d.tile0 = tiles;
+        const int nb = (m->row0 + m->out + kBlockRows - 1) / kBlockRows - d.blk0;
+        tiles += (nb + p.tb - 1) / p.tb;
+    }
+    a.tiles = tiles;
+    if (a.nmats == 0 || rows == 0) return CQ_OK;
+    HIP_TRY(launch_product(a, s0.width, s0.group_bytes, mode, p.lds, stream), "product launch");
+    if (mode == kModeLut)
+        for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
+    return CQ_OK;
+}
+
+// cq.GEMMs on device pointers: one launch per run of up to kMaxMatrices
+// matrices that share their tables and kernel, else one launch per matrix
+// (each gives the same bits either way: kernel.go:127-133).
+int gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+    int k = 0;
+    while (k < n) {
+        int e = k + 1;
+        while (e < n && e - k < kMaxMatrices && uses_lut(ms[e]) == uses_lut(ms[k]) &&
+               shares_tables(*ms[k]->st, *ms[e]->st))
+            ++e;
+        int rc = run_product(ms + k, e - k, dsts + k, x, rows, stream);
+        if (rc) return rc;
+        k = e;
+    }
+    return CQ_OK;
+}
+
+int row_args(const cq_matrix *m, RowArgs &a) {
+    const CqStore &s = *m->st;
+    std::memset(&a, 0, sizeof a);
+    a.idx = s.d_idx;
+    a.norm = s.d_norm;
+    a.in = s.in;
+    a.group = s.group;
+    a.groups = s.groups;
+    a.row_bytes = s.row_bytes;
+    a.width = s.width;
+    a.units = s.units;
+    a.unit_bytes = s.unit_bytes;
+    for (int c = 0; c < 16; ++c) a.cb[c] = c < s.ncb ? s.cb[c] : 0.0f;
+    a.inv_sqrt = s.inv_sqrt;
+    if (static_cast<size_t>(s.group) * 4 > device_info().max_lds)
+        return fail(CQ_ERR_UNSUPPORTED, "cq: Row of group %d", s.group);
+    return CQ_OK;
+}
+
+}  // namespace
+
+// ---- C ABI -----------------------------------------------------------------
+
+extern "C" {
+
+const char *cq_last_error(void) { return t_err.c_str(); }
+
+const char *cq_version(void) { return "libcqhip 0.1 (gfx950)"; }
+
+int cq_device_info(char *buf, size_t len) {
+    const DeviceInfo &d = device_info();
+    if (d.device < 0) return fail(CQ_ERR_DEVICE, "cq: no HIP device");
+    if (buf && len)
+        snprintf(buf, len, "device %d %s, %d CUs, %zu bytes LDS per workgroup; kernels: lut, nibble4, nibble, row, "
+                 "int8 quantize, int8 attend", d.device, d.name.c_str(), d.cus, d.max_lds);
+    return CQ_OK;
+}
+
+int cq_new(int out, int in, int group, int bits, int width, const float *codebook, size_t codebook_len,
+           const uint8_t *index, size_t index_len, const uint8_t *norms_fp16, size_t norms_len, int gather,
+           cq_matrix **mp) {
+    if (!mp) return fail(CQ_ERR_MISUSE, "cq: nil result pointer");
+    *mp = nullptr;
+    // internal/cq/matrix.go:61-73, in the reference's order.
+    if ((bits != 2 && bits != 4) || width != bits)
+        return fail(CQ_ERR_ARG, "cq: %d-bit CQ (index width %d) not supported, only 2 and 4", bits, width);
+    if (group < 8 || (group & (group - 1)) != 0)
+        return fail(CQ_ERR_ARG, "cq: group %d is not a power of two >= 8", group);
+    if (out < 0 || in <= 0) return fail(CQ_ERR_ARG, "cq: bad shape [%d, %d]", out, in);
+    if (codebook_len != (static_cast<size_t>(1) << bits))
+        return fail(CQ_ERR_ARG, "cq: %zu codebook levels for %d bits", codebook_len, bits);
+    const int groups = (in + group - 1) / group;
+    const long long row_bytes = static_cast<long long>(groups) * group * width / 8;
+    if (index_len != static_cast<size_t>(out) * row_bytes || norms_len != 2 * static_cast<size_t>(out) * groups)
+        return fail(CQ_ERR_ARG, "cq: %zu index and %zu norm bytes for [%d, %d], want %lld and %lld", index_len,
+                    norms_len, out, in, static_cast<long long>(out) * row_bytes, 2LL * out * groups);
+    if (device_info().device < 0) return fail(CQ_ERR_DEVICE, "cq: no HIP device");
+
+    auto st = std::make_shared<CqStore>();
+    st->out = out;
+    st->in = in;
+    st->group = group;
+    st->groups = groups;
+    st->width = width;
+    st->row_bytes = static_cast<int>(row_bytes);
+    st->group_bytes = group * width / 8;
+    st->unit_bytes = std::min(16, st->group_bytes);
+    st->units = st->row_bytes / st->unit_bytes;
+    st->nblk = (out + kBlockRows - 1) / kBlockRows;
+    st->ncb = 1 << bits;
+    st->cb_max = 0;
+    for (int c = 0; c < st->ncb; ++c) {
+        st->cb[c] = codebook[c];
+        st->cb_max = gomax(st->cb_max, std::fabs(codebook[c]));
+    }
+    st->lut_step = static_cast<float>(1.0 / (kLutQ * std::sqrt(static_cast<double>(group))));  // lut.go:213-215
+    st->inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(group)));          // kernel.go:377
+
+    // Device layout (cq_internal.hpp): blocks of 64 rows, units side by side.
+    const size_t nrows = static_cast<size_t>(std::max(st->nblk, 1)) * kBlockRows;
+    st->idx_bytes = nrows * st->row_bytes;
+    st->norm_bytes = nrows * groups * sizeof(uint16_t);
+    std::vector<uint8_t> hidx(st->idx_bytes, 0);
+    std::vector<uint16_t> hnorm(nrows * groups, 0);
+    const int U = st->unit_bytes;
+    for (int r = 0; r < out; ++r) {
+        const size_t blk = r / kBlockRows, lane = r % kBlockRows;
+        const uint8_t *src = index + static_cast<size_t>(r) * row_bytes;
+        for (int u = 0; u < st->units; ++u)
+            std::memcpy(&hidx[((blk * st->units + u) * kBlockRows + lane) * U], src + static_cast<size_t>(u) * U, U);
+        for (int g = 0; g < groups; ++g) {
+            const uint8_t *nb = norms_fp16 + 2 * (static_cast<size_t>(r) * groups + g);
+            hnorm[(blk * groups + g) * kBlockRows + lane] = static_cast<uint16_t>(nb[0] | (nb[1] << 8));
+        }
+    }
+    HIP_TRY(hipMalloc(&st->d_idx, align256(st->idx_bytes)), "hipMalloc index");
+    HIP_TRY(hipMalloc(&st->d_norm, align256(st->norm_bytes)), "hipMalloc norms");
+    HIP_TRY(hipMemcpy(st->d_idx, hidx.data(), st->idx_bytes, hipMemcpyHostToDevice), "upload index");
+    HIP_TRY(hipMemcpy(st->d_norm, hnorm.data(), st->norm_bytes, hipMemcpyHostToDevice), "upload norms");
+
+    auto *m = new cq_matrix{st, 0, out, false};
+    if (!gather && uses_lut(m)) st->prepared.store(true);  // New = NewGather + Prepare (matrix.go:46-55)
+    *mp = m;
+    return CQ_OK;
+}
+
+void cq_free(cq_matrix *m) { delete m; }
+
+int cq_out(const cq_matrix *m) { return m ? m->out : 0; }
+int cq_in(const cq_matrix *m) { return m ? m->st->in : 0; }
+int cq_bits(const cq_matrix *m) { return m ? m->st->width : 0; }
+
+int cq_prepare(cq_matrix *m) {
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    if (uses_lut(m)) m->st->prepared.store(true);  // matrix.go:111-115
+    return CQ_OK;
+}
+
+long long cq_bytes(const cq_matrix *m) {
+    // matrix.go:121-129: packed index + float32 norms + codebook, and the
+    // lut copy of the view's 32-row blocks once built (lut.go:82-86).
+    if (!m) return 0;
+    const CqStore &s = *m->st;
+    long long n = static_cast<long long>(m->out) * s.row_bytes + 4LL * m->out * s.groups + 4LL * s.ncb;
+    if (uses_lut(m) && s.prepared.load()) {
+        const long long b0 = m->row0 / 32, b1 = (m->row0 + m->out + 31) / 32;
+        n += (b1 - b0) * 32 * (s.row_bytes + 4LL * s.groups);
+    }
+    return n;
+}
+
+long long cq_device_bytes(const cq_matrix *m) {
+    return m ? static_cast<long long>(m->st->idx_bytes + m->st->norm_bytes) : 0;
+}
+
+int cq_rows(const cq_matrix *m, int lo, int hi, cq_matrix **view) {
+    if (!m || !view) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    if (lo < 0 || hi < lo || hi > m->out) return fail(CQ_ERR_MISUSE, "cq: Rows(%d, %d) of %d rows", lo, hi, m->out);
+    *view = new cq_matrix{m->st, m->row0 + lo, hi - lo, m->exact};
+    return CQ_OK;
+}
+
+int cq_exact(const cq_matrix *m, cq_matrix **view) {
+    if (!m || !view) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    *view = new cq_matrix{m->st, m->row0, m->out, true};
+    return CQ_OK;
+}
+
+const char *cq_kernel_name(const cq_matrix *m) { return m && uses_lut(m) ? "lut" : "nibble4"; }
+
+int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream) {
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "cq: GEMM of %d rows", rows);
+    if (rows == 0 || m->out == 0) return CQ_OK;  // kernel.go:105-107
+    cq_matrix *mm = const_cast<cq_matrix *>(m);
+    return run_product(&mm, 1, &dst, x, rows, static_cast<hipStream_t>(stream));
+}
+
+int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream) {
+    if (n < 0 || (n > 0 && (!ms || !dsts))) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d matrices", n);
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d rows", rows);
+    for (int k = 0; k < n; ++k)
+        if (!ms[k] || ms[k]->st->in != ms[0]->st->in)
+            return fail(CQ_ERR_MISUSE, "cq: GEMMs over matrices of different input widths");
+    if (rows == 0 || n == 0) return CQ_OK;
+    return gemms_dev(n, ms, dsts, x, rows, static_cast<hipStream_t>(stream));
+}
+
+int cq_gemm(const cq_matrix *m, float *dst, size_t dst_len, const float *x, size_t x_len, int rows) {
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    const CqStore &s = *m->st;
+    // kernel.go:100-103
+    if (rows < 0 || x_len != static_cast<size_t>(rows) * s.in || dst_len != static_cast<size_t>(rows) * m->out)
+        return fail(CQ_ERR_MISUSE, "cq: GEMM(len %zu, len %zu, %d rows) on [%d, %d]", dst_len, x_len, rows, m->out,
+                    s.in);
+    if (rows == 0 || m->out == 0) return CQ_OK;
+    const size_t xb = align256(x_len * 4), yb = align256(dst_len * 4);
+    HIP_TRY(t_stage.ensure(xb + yb), "staging");
+    char *base = static_cast<char *>(t_stage.buf);
+    float *dx = reinterpret_cast<float *>(base), *dy = reinterpret_cast<float *>(base + xb);
+    HIP_TRY(hipMemcpyAsync(dx, x, x_len * 4, hipMemcpyHostToDevice, t_stage.stream), "copy x");
+    cq_matrix *mm = const_cast<cq_matrix *>(m);
+    int rc = run_product(&mm, 1, &dy, dx, rows, t_stage.stream);
+    if (rc) {
+        (void)hipStreamSynchronize(t_stage.stream);
+        return rc;
+    }
+    HIP_TRY(hipMemcpyAsync(dst, dy, dst_len * 4, hipMemcpyDeviceToHost, t_stage.stream), "copy y");
+    HIP_TRY(hipStreamSynchronize(t_stage.stream), "sync");
+    return CQ_OK;
+}
+
+int cq_gemms(int n, cq_matrix *const *ms, float *const *dsts, const size_t *dst_lens, const float *x, size_t x_len,
+             int rows) {
+    if (n < 0 || (n > 0 && (!ms || !dsts || !dst_lens))) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d matrices", n);
+    // kernel.go:135-144
+    for (int k = 0; k < n; ++k) {
+        const cq_matrix *m = ms[k];
+        if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+        if (rows < 0 || x_len != static_cast<size_t>(rows) * m->st->in ||
+            dst_lens[k] != static_cast<size_t>(rows) * m->out)
+            return fail(CQ_ERR_MISUSE, "cq: GEMMs(len %zu, len %zu, %d rows) on [%d, %d]", dst_lens[k], x_len, rows,
+                        m->out, m->st->in);
+    }
+    if (rows == 0 || n == 0) return CQ_OK;
+    size_t total = align256(x_len * 4);
+    std::vector<size_t> off(n);
+    for (int k = 0; k < n; ++k) {
+        off[k] = total;
+        total += align256(dst_lens[k] * 4);
+    }
+    HIP_TRY(t_stage.ensure(total), "staging");
+    char *base = static_cast<char *>(t_stage.buf);
+    float *dx = reinterpret_cast<float *>(base);
+    std::vector<float *> dy(n);
+    for (int k = 0; k < n; ++k) dy[k] = reinterpret_cast<float *>(base + off[k]);
+    HIP_TRY(hipMemcpyAsync(dx, x, x_len * 4, hipMemcpyHostToDevice, t_stage.stream), "copy x");
+    int rc = gemms_dev(n, ms, dy.data(), dx, rows, t_stage.stream);
+    if (rc) {
+        (void)hipStreamSynchronize(t_stage.stream);
+        return rc;
+    }
+    for (int k = 0; k < n; ++k)
+        if (dst_lens[k])
+            HIP_TRY(hipMemcpyAsync(dsts[k], dy[k], dst_lens[k] * 4, hipMemcpyDeviceToHost, t_stage.stream), "copy y");
+    HIP_TRY(hipStreamSynchronize(t_stage.stream), "sync");
+    return CQ_OK;
+}
+
+int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream) {
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    if (r < 0 || r >= m->out) return fail(CQ_ERR_MISUSE, "cq: Row(%d) of [%d, %d]", r, m->out, m->st->in);
+    RowArgs a;
+    int rc = row_args(m, a);
+    if (rc) return rc;
+    a.dst = dst;
+    a.r0 = m->row0 + r;
+    a.n = 1;
+    HIP_TRY(launch_rows(a, static_cast<hipStream_t>(stream)), "row launch");
+    return CQ_OK;
+}
+
+int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n, void *stream) {
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    if (n < 0) return fail(CQ_ERR_MISUSE, "cq: gather of %d rows", n);
+    if (m->row0 != 0) return fail(CQ_ERR_UNSUPPORTED, "cq: row gather on a Rows view");
+    RowArgs a;
+    int rc = row_args(m, a);
+    if (rc) return rc;
+    a.dst = dst;
+    a.rows = rows;
+    a.n = n;
+    HIP_TRY(launch_rows(a, static_cast<hipStream_t>(stream)), "row gather launch");
+    return CQ_OK;
+}
+
+int cq_row(const cq_matrix *m, float *dst, size_t dst_len, int r) {
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    // matrix.go:162-164
+    if (r < 0 || r >= m->out || dst_len != static_cast<size_t>(m->st->in))
+        return fail(CQ_ERR_MISUSE, "cq: Row(len %zu, %d) of [%d, %d]", dst_len, r, m->out, m->st->in);
+    HIP_TRY(t_stage.ensure(align256(dst_len * 4)), "staging");
+    float *dd = static_cast<float *>(t_stage.buf);
+    int rc = cq_row_dev(m, dd, r, t_stage.stream);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(dst, dd, dst_len * 4, hipMemcpyDeviceToHost, t_stage.stream), "copy row");
+    HIP_TRY(hipStreamSynchronize(t_stage.stream), "sync");
+    return CQ_OK;
+}
+
+// ---- int8 KV -----------------------------------------------------------------
+
+int kv_quantize_rows_dev(int8_t *q, float *s, const float *x, int rows, int cols, int width, void *stream) {
+    // NewInt8Rows / Append checks (int8.go:107-128)
+    if (width <= 0 || cols % width != 0)
+        return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "needle: %d rows", rows);
+    const long long chunks = static_cast<long long>(rows) * (cols / width);
+    HIP_TRY(launch_quantize_rows(q, s, x, chunks, width, static_cast<hipStream_t>(stream)), "quantize launch");
+    return CQ_OK;
+}
+
+int kv_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, int width) {
+    if (width <= 0 || cols % width != 0)
+        return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "needle: %d rows", rows);
+    const size_t n = static_cast<size_t>(rows) * cols, chunks = static_cast<size_t>(rows) * (cols / width);
+    if (n == 0) return CQ_OK;
+    const size_t xb = align256(n * 4), qb = align256(n), sb = align256(chunks * 4);
+    HIP_TRY(t_stage.ensure(xb + qb + sb), "staging");
+    char *base = static_cast<char *>(t_stage.buf);
+    float *dx = reinterpret_cast<float *>(base);
+    int8_t *dq = reinterpret_cast<int8_t *>(base + xb);
+    float *ds = reinterpret_cast<float *>(base + xb + qb);
+    HIP_TRY(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, t_stage.stream), "copy x");
+    int rc = kv_quantize_rows_dev(dq, ds, dx, rows, cols, width, t_stage.stream);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(q, dq, n, hipMemcpyDeviceToHost, t_stage.stream), "copy q");
+    HIP_TRY(hipMemcpyAsync(s, ds, chunks * 4, hipMemcpyDeviceToHost, t_stage.stream), "copy s");
+    HIP_TRY(hipStreamSynchronize(t_stage.stream), "sync");
+    return CQ_OK;
+}
+
+int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                       const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                       int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
+                       float scale, int quant_q, int batch, void *stream) {
+    if (qk <= 0 || vd <= 0 || k_cols % qk != 0)
+        return fail(CQ_ERR_MISUSE, "needle: int8 keys of %d in chunks of %d", k_cols, qk);
+    const int kv_heads = k_cols / qk;
+    if (heads <= 0 || heads % kv_heads != 0 || v_cols != kv_heads * vd)
+        return fail(CQ_ERR_MISUSE, "needle: %d heads over %d KV heads (values %d of %d)", heads, kv_heads, v_cols, vd);
+    if (qk > 256 || qk % 4 != 0 || k_cols % 4 != 0)
+        return fail(CQ_ERR_UNSUPPORTED, "needle: int8 attention with head width %d", qk);
+    if (t < 0 || batch < 0 || nk_max < 0) return fail(CQ_ERR_MISUSE, "needle: bad attention sizes");
+    const size_t lds = sizeof(float) * static_cast<size_t>(nk_max) + 64 * static_cast<size_t>(vd);
+    if (lds > device_info().max_lds) return fail(CQ_ERR_UNSUPPORTED, "needle: %d keys exceed LDS", nk_max);
+    AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
+                 kv_stride, s_stride, spans, nk_max, scale, quant_q, batch};
+    HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");
+    return CQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,92 @@
+// Internal interfaces between the C-ABI host code (cq_api.cpp) and the
+// gfx950 kernels (cq_kernels.hip, int8_kernels.hip).
+//
+// Device layout of a CQ matrix (built once at construction, never changed):
+//   rows are padded to blocks of 64 (one wavefront, one row per lane);
+//   index: per block, per unit of U = min(16, groupBytes) bytes, the 64 rows'
+//          units side by side: idx[((blk * units + u) * 64 + lane) * U + k]
+//          is index byte u*U + k of row blk*64 + lane, the packed LSB-first
+//          bytes of cact.Packed.Index unchanged (internal/cact/packed.go:24-27);
+//          a wavefront's load of one unit is 64*U contiguous bytes;
+//   norms: FP16 as stored, norm[(blk * groups + g) * 64 + lane].
+// Padding rows hold zero bytes and zero norms and are never written out.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cqhip {
+
+constexpr int kBlockRows = 64;   // rows per block: one per lane of a wavefront
+constexpr int kThreads = 256;    // threads per workgroup: four wavefronts
+constexpr int kLutQ = 8191;      // internal/cq/lut.go:33
+constexpr int kLutMaxGroupBytes = 256;  // internal/cq/lut.go:38
+constexpr int kMaxMatrices = 8;  // matrices per shared-table launch
+
+enum Mode { kModeLut = 0, kModeExact = 1 };
+
+// One matrix (or Rows view) of a product launch.
+struct MatDesc {
+    const uint8_t *idx;    // device layout above
+    const uint16_t *norm;  // device layout above
+    float *y;              // output rows of this matrix, y_stride floats apart
+    long long y_stride;
+    int row0, out;         // view: root rows [row0, row0 + out)
+    int blk0;              // row0 / 64
+    int tile0;             // first tile of this matrix in the launch's tile list
+};
+
+struct ProdArgs {
+    MatDesc mats[kMaxMatrices];
+    int nmats;
+    int tiles;             // total tiles over all matrices
+    const float *x;        // activations, x_stride floats apart
+    long long x_stride;
+    int in, groups, row_bytes;
+    int tb;                // 64-row blocks per tile
+    int gc;                // groups per LDS chunk
+    int rows;              // activations
+    int nib4_rows;         // Exact: activations [0, nib4_rows) use nibble4's order
+    float cb[16];
+    float cb_max, lut_step, inv_sqrt;
+};
+
+// Launches the product (one matrix or several sharing their tables).
+// bits, group_bytes select the template; mode is kModeLut or kModeExact.
+hipError_t launch_product(const ProdArgs &a, int bits, int group_bytes, int mode, size_t lds_bytes,
+                          hipStream_t stream);
+// LDS bytes per group of a chunk, and the fixed part, for choosing gc.
+size_t product_lds_bytes(int bits, int group_bytes, int mode, int gc, int tb);
+
+struct RowArgs {
+    const uint8_t *idx;
+    const uint16_t *norm;
+    float *dst;            // n rows of `in` floats
+    const int32_t *rows;   // device row list (root rows), or nullptr: rows r0 .. r0+n-1
+    int r0, n;
+    int in, group, groups, row_bytes, width, units, unit_bytes;
+    float cb[16];
+    float inv_sqrt;
+};
+hipError_t launch_rows(const RowArgs &a, hipStream_t stream);
+
+// int8 numerics
+hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
+                                hipStream_t stream);
+
+struct AttendArgs {
+    float *out; long long out_stride;
+    const float *q; long long q_stride;
+    int t, heads;
+    const int8_t *kq; const float *ks; int k_cols, qk;
+    const int8_t *vq; const float *vs; int v_cols, vd;
+    long long kv_stride, s_stride;
+    const int32_t *spans;
+    int nk_max;
+    float scale;
+    int quant_q;
+    int batch;
+};
+hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream);
+
+}  // namespace cqhip

@@ -1,0 +1,256 @@
+// gfx950 kernels for go-whistle's int8 KV numerics (internal/needle/int8.go).
+//
+// quantize_kernel: QuantizeRow (int8.go:36-55) per chunk of `width` values,
+//   one wavefront per chunk: s = max|x|/127 (1 for a zero chunk), codes
+//   RNE(x/s) clipped to [-128, 127]; the same bits as the reference (the
+//   max is exact in any order, the divide is IEEE, the rounding is RNE).
+//
+// attend_kernel: AttendInt8Spans (int8.go:208-272) for one (stream, query
+//   row, head) per workgroup:
+//   1. logits, one thread per key: the int8 query's exact int32 dot times
+//      (s_q * s_k) / scale (int8Logits, int8.go:278-285), or the float32
+//      query against the codes summed in order, * s_k / scale (dotsF32I8,
+//      int8.go:289-300);
+//   2. softmaxInPlace (load.go:128-138): the max, then expSubSum as amd64
+//      runs it (exp_amd64.go:13-25): on the multiple-of-8 prefix the AVX2
+//      kernel's Cephes exponent (exp_amd64.s:84-112; S. L. Moshier's
+//      published expf, with the kernel's fused steps) summed in eight lanes
+//      of stride 8 and reduced as the kernel does; the tail, or the whole row
+//      under 8 values, float32 of the float64 exponent summed in order;
+//      then every value divided by the sum;
+//   3. the weights times the value scales, and axpysI8 (int8kernel.go:
+//      360-368): per output, one key after the other, each product rounded
+//      before the add. One thread per output carries that chain; the value
+//      codes of 64 keys at a time are staged in LDS by the workgroup.
+#include "cq_internal.hpp"
+
+#include <climits>
+
+namespace cqhip {
+namespace {
+
+__global__ __launch_bounds__(256) void quantize_kernel(int8_t *q, float *s, const float *x, long long chunks,
+                                                       int width) {
+    const int lane = threadIdx.x & 63;
+    const long long c = static_cast<long long>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
+    if (c >= chunks) return;
+    const float *xc = x + c * width;
+    float m = 0.0f;
+    for (int i = lane; i < width; i += 64) m = fmaxf(m, fabsf(xc[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+    int8_t *qc = q + c * width;
+    for (int i = lane; i < width; i += 64) {
+        float r = rintf(xc[i] / sc);
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        qc[i] = static_cast<int8_t>(static_cast<int>(r));
+    }
+    if (lane == 0) s[c] = sc;
+}
+
+// One lane of the amd64 kernel's exponent (exp_amd64.s:84-112), constants
+// bit for bit (exp_amd64.s:7-51).
+__device__ __forceinline__ float exp_lane(float x) {
+    const float log2e = 0x1.715476p+0f, ln2hi = 0x1.63p-1f, ln2lo = -0x1.bd0106p-13f;
+    const float c6 = 0x1.a0d2cep-13f, c5 = 0x1.6e879cp-10f, c4 = 0x1.111210p-7f;
+    const float c3 = 0x1.555382p-5f, c2 = 0x1.555554p-3f, c1 = 0x1p-1f;
+    const float lo = -0x1.5d51ecp+6f;
+    const bool lt = x < lo;
+    const float xc = (x != x) ? x : (lo > x ? lo : x);
+    const float k = rintf(xc * log2e);
+    float r = fmaf(-k, ln2hi, xc);
+    r = fmaf(-k, ln2lo, r);
+    const float r2 = r * r;
+    float p = c6;
+    p = fmaf(p, r, c5);
+    p = fmaf(p, r, c4);
+    p = fmaf(p, r, c3);
+    p = fmaf(p, r, c2);
+    p = fmaf(p, r, c1);
+    float yv = fmaf(p, r2, r);
+    yv = yv + 1.0f;
+    const int ki = (k != k || k >= 2147483648.0f || k < -2147483648.0f) ? INT_MIN : static_cast<int>(k);
+    const float e = __uint_as_float(__float_as_uint(yv) + (static_cast<unsigned>(ki) << 23));
+    return lt ? 0.0f : e;
+}
+
+__device__ __forceinline__ float exp_generic(float d) { return static_cast<float>(exp(static_cast<double>(d))); }
+
+constexpr int kAttThreads = 256;
+constexpr int kVStage = 64;  // keys of value codes staged per round
+
+__device__ __forceinline__ float block_max(float v, float *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < kAttThreads / 64; ++w) r = fmaxf(r, red[w]);
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int h = blockIdx.x, i = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int kv_heads = a.k_cols / a.qk;
+    const int kv = h / (a.heads / kv_heads);
+    const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
+    const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
+    const int n = len0 + len1;
+    if (len0 < 0 || len1 < 0 || n > a.nk_max) return;  // malformed spans: nothing to attend
+
+    float *s = reinterpret_cast<float *>(smem);                 // n logits / weights
+    int8_t *vstage = reinterpret_cast<int8_t *>(s + a.nk_max);  // kVStage rows of vd codes
+    __shared__ float red[8];
+    __shared__ int8_t q8[256];
+    __shared__ float sq_sh, sum_sh;
+
+    const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
+    const int8_t *kq = a.kq + b * a.kv_stride;
+    const float *ks = a.ks + b * a.s_stride;
+    const int8_t *vq = a.vq + b * a.kv_stride;
+    const float *vs = a.vs + b * a.s_stride;
+
+    // QuantizeRow of the query head (int8.go:226-228).
+    if (a.quant_q) {
+        float m = 0.0f;
+        for (int c = tid; c < a.qk; c += kAttThreads) m = fmaxf(m, fabsf(qi[c]));
+        m = block_max(m, red);
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+        for (int c = tid; c < a.qk; c += kAttThreads) {
+            float r = rintf(qi[c] / sc);
+            r = fminf(fmaxf(r, -128.0f), 127.0f);
+            q8[c] = static_cast<int8_t>(static_cast<int>(r));
+        }
+        if (tid == 0) sq_sh = sc;
+        __syncthreads();
+    }
+    const float sq = a.quant_q ? sq_sh : 0.0f;
+
+    // 1. Logits.
+    for (int j = tid; j < n; j += kAttThreads) {
+        const int key = j < len0 ? lo0 + j : lo1 + (j - len0);
+        const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
+        const float sk = ks[static_cast<long long>(key) * kv_heads + kv];
+        float lg;
+        if (a.quant_q) {
+            int dot = 0;
+            for (int c = 0; c < a.qk; c += 4) {
+                const int w = *reinterpret_cast<const int *>(krow + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dot += static_cast<int>(q8[c + e]) * static_cast<int>(static_cast<int8_t>(w >> (8 * e)));
+            }
+            const float scl = sq * sk;
+            const float t1 = static_cast<float>(dot) * scl;
+            lg = t1 / a.scale;
+        } else {
+            float dot = 0.0f;
+            for (int c = 0; c < a.qk; c += 4) {
+                const int w = *reinterpret_cast<const int *>(krow + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float pr = qi[c + e] * static_cast<float>(static_cast<int8_t>(w >> (8 * e)));
+                    dot = dot + pr;
+                }
+            }
+            const float t1 = dot * sk;
+            lg = t1 / a.scale;
+        }
+        s[j] = lg;
+    }
+    __syncthreads();
+
+    // 2. softmaxInPlace with amd64's expSubSum.
+    float m = -INFINITY;
+    for (int j = tid; j < n; j += kAttThreads) m = fmaxf(m, s[j]);
+    m = block_max(m, red);
+    const int n8 = n & ~7;
+    const bool kernel_path = n8 > 0;
+    for (int j = tid; j < n; j += kAttThreads) {
+        const float d = s[j] - m;
+        s[j] = (kernel_path && j < n8) ? exp_lane(d) : exp_generic(d);
+    }
+    __syncthreads();
+    if (tid < 8 && kernel_path) {
+        float acc = 0.0f;
+        for (int j = tid; j < n8; j += 8) acc = acc + s[j];
+        red[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float sum;
+        if (kernel_path) {
+            const float x0 = red[0] + red[4], x1 = red[1] + red[5], x2 = red[2] + red[6], x3 = red[3] + red[7];
+            const float h0 = x0 + x1, h1 = x2 + x3;
+            sum = h0 + h1;
+            if (n8 != n) {
+                float tail = 0.0f;
+                for (int j = n8; j < n; ++j) tail = tail + s[j];
+                sum = sum + tail;
+            }
+        } else {
+            sum = 0.0f;
+            for (int j = 0; j < n; ++j) sum = sum + s[j];
+        }
+        sum_sh = sum;
+    }
+    __syncthreads();
+    const float sum = sum_sh;
+    for (int j = tid; j < n; j += kAttThreads) {
+        const int key = j < len0 ? lo0 + j : lo1 + (j - len0);
+        const float p = s[j] / sum;
+        s[j] = p * vs[static_cast<long long>(key) * kv_heads + kv];
+    }
+    __syncthreads();
+
+    // 3. axpysI8 per output, keys in order.
+    float acc = 0.0f;
+    for (int j0 = 0; j0 < n; j0 += kVStage) {
+        const int cnt = min(kVStage, n - j0);
+        for (int e = tid; e < cnt * a.vd; e += kAttThreads) {
+            const int jj = e / a.vd, d = e % a.vd;
+            const int j = j0 + jj;
+            const int key = j < len0 ? lo0 + j : lo1 + (j - len0);
+            vstage[e] = vq[static_cast<long long>(key) * a.v_cols + kv * a.vd + d];
+        }
+        __syncthreads();
+        if (tid < a.vd) {
+            for (int jj = 0; jj < cnt; ++jj) {
+                const float pr = s[j0 + jj] * static_cast<float>(vstage[jj * a.vd + tid]);
+                acc = acc + pr;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < a.vd) a.out[b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * a.vd + tid] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
+                                hipStream_t stream) {
+    if (chunks <= 0) return hipSuccess;
+    const long long blocks = (chunks + 3) / 4;
+    for (long long c0 = 0; c0 < blocks; c0 += 1 << 30) {
+        const long long nb = blocks - c0 < (1LL << 30) ? blocks - c0 : (1LL << 30);
+        const long long ch0 = c0 * 4;
+        hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, stream, q + ch0 * width,
+                           s + ch0, x + ch0 * width, chunks - ch0, width);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
+    if (a.t <= 0 || a.heads <= 0 || a.batch <= 0) return hipSuccess;
+    const size_t lds = sizeof(float) * static_cast<size_t>(a.nk_max) + static_cast<size_t>(kVStage) * a.vd;
+    hipLaunchKernelGGL(attend_kernel, dim3(a.heads, a.t, a.batch), dim3(kAttThreads), lds, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace cqhip

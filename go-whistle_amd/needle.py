@@ -1,0 +1,57 @@
+"""go-whistle's int8 KV numerics (internal/needle/int8.go) over libcqhip.
+
+QuantizeRows / Int8Rows.Append (int8.go:116-141) on host arrays or device
+tensors, and AttendInt8Spans (int8.go:208-272) on device tensors for one
+or many independent streams.
+"""
+
+import ctypes
+from ctypes import POINTER, c_float, c_int8, c_void_p
+
+import numpy as np
+
+from ._lib import CQPanic, check, lib
+
+
+def QuantizeRows(x, cols, width):
+    """Codes and scales of x, rows of cols values, per chunk of width (host)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if width <= 0 or cols % width != 0:
+        raise CQPanic(f"needle: int8 rows of {cols} in chunks of {width}")
+    if x.size % cols != 0:
+        raise CQPanic(f"needle: {x.size} values are not rows of {cols}")
+    rows = x.size // cols
+    q = np.zeros(x.size, dtype=np.int8)
+    s = np.zeros(rows * (cols // width), dtype=np.float32)
+    check(lib().kv_quantize_rows(q.ctypes.data_as(POINTER(c_int8)), s.ctypes.data_as(POINTER(c_float)),
+                                 x.ctypes.data_as(POINTER(c_float)), rows, cols, width))
+    return q, s
+
+
+def QuantizeRow(x):
+    """QuantizeRow (int8.go:36-55): codes and the scale of one chunk."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q, s = QuantizeRows(x, x.size, x.size) if x.size else (np.zeros(0, np.int8), np.ones(1, np.float32))
+    return q, float(s[0])
+
+
+def _stream():
+    import torch
+
+    return c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def quantize_rows_dev(q, s, x, rows, cols, width):
+    """Device form: q int8 [rows*cols], s float32 [rows*cols/width], x float32."""
+    check(lib().kv_quantize_rows_dev(c_void_p(q.data_ptr()), c_void_p(s.data_ptr()), c_void_p(x.data_ptr()),
+                                     rows, cols, width, _stream()))
+
+
+def attend_int8_dev(out, q, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, spans, nk_max, scale, quant_q,
+                    batch=1, out_stride=0, q_stride=0, kv_stride=0, s_stride=0):
+    """AttendInt8Spans on device tensors for `batch` streams (see cqhip.h)."""
+    check(lib().kv_attend_int8_dev(c_void_p(out.data_ptr()), out_stride, c_void_p(q.data_ptr()), q_stride, t, heads,
+                                   c_void_p(kq.data_ptr()), c_void_p(ks.data_ptr()), k_cols, qk,
+                                   c_void_p(vq.data_ptr()), c_void_p(vs.data_ptr()), v_cols, vd, kv_stride, s_stride,
+                                   c_void_p(spans.data_ptr()), nk_max, float(scale), 1 if quant_q else 0, batch,
+                                   _stream()))

@@ -1,0 +1,130 @@
+/*
+ * libcqhip: go-whistle's CQ quantized-matrix path and int8 KV numerics on
+ * AMD Instinct MI355X (gfx950), behind a plain C ABI.
+ *
+ * Each entry point replaces one method of the reference's Go API (cited as
+ * file:line in the go-whistle repository); a Go caller binds them through
+ * cgo (the stub a maintainer would add is in INTEGRATION.md). Host-slice
+ * entry points copy their operands to and from the device within the call,
+ * as cgo requires of Go memory; the _dev entry points take device pointers
+ * and a HIP stream for device-resident pipelines.
+ *
+ * Errors: every call returns CQ_OK or a status; cq_last_error() returns the
+ * failing call's message on the calling thread. Construction errors carry
+ * the reference's "cq: ..." text (the Go API returns them as error values);
+ * misuse that the Go API answers with a panic (lengths that do not match
+ * the shape, rows out of range) returns CQ_ERR_MISUSE.
+ *
+ * Threads: matrices are immutable after construction and safe for
+ * concurrent use from any thread (internal/cq/matrix.go:22-24). Host-slice
+ * calls run on a per-thread stream with per-thread staging buffers.
+ */
+#ifndef CQHIP_H
+#define CQHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    CQ_OK = 0,
+    CQ_ERR_ARG = 1,         /* construction rejected: the Go API's error result */
+    CQ_ERR_MISUSE = 2,      /* shape misuse: the Go API panics */
+    CQ_ERR_DEVICE = 3,      /* HIP runtime failure or no device */
+    CQ_ERR_UNSUPPORTED = 4, /* a geometry this library does not run */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *cq_last_error(void);
+
+/* Library version string and the device it runs on (cf. `whistle doctor`,
+ * cmd/whistle/doctor.go:349-370, which names the active kernels). */
+const char *cq_version(void);
+int cq_device_info(char *buf, size_t len);
+
+typedef struct cq_matrix cq_matrix;
+
+/* cq.New (internal/cq/matrix.go:46-55) when gather == 0, cq.NewGather
+ * (matrix.go:60-96) when gather != 0: validates the packed form of
+ * cact.Packed (internal/cact/packed.go:18-29) with the reference's checks and
+ * messages, widens nothing on the host, and uploads the index and FP16 norms
+ * to the device in the product layout. No host pointer is kept. */
+int cq_new(int out, int in, int group, int bits, int width, const float *codebook, size_t codebook_len,
+           const uint8_t *index, size_t index_len, const uint8_t *norms_fp16, size_t norms_len, int gather,
+           cq_matrix **m);
+
+/* Releases a matrix or a view; the storage goes with the last of them (the
+ * Go shim calls it from a runtime.AddCleanup, as *cq.Matrix has no Close). */
+void cq_free(cq_matrix *m);
+
+int cq_out(const cq_matrix *m);  /* Matrix.Out  (matrix.go:99) */
+int cq_in(const cq_matrix *m);   /* Matrix.In   (matrix.go:102) */
+int cq_bits(const cq_matrix *m); /* Matrix.Bits (matrix.go:105) */
+/* Matrix.Prepare (matrix.go:111-115). */
+int cq_prepare(cq_matrix *m);
+/* Matrix.Bytes (matrix.go:121-129): the reference's accounting. */
+long long cq_bytes(const cq_matrix *m);
+/* Device memory the matrix's storage holds (no reference counterpart). */
+long long cq_device_bytes(const cq_matrix *m);
+/* Matrix.Rows (matrix.go:133-145): a view of rows [lo, hi) sharing storage. */
+int cq_rows(const cq_matrix *m, int lo, int hi, cq_matrix **view);
+/* Matrix.Exact (matrix.go:152-157): a view whose products use the float
+ * nibble tables (kernel.go:239-374) instead of the lut kernel. */
+int cq_exact(const cq_matrix *m, cq_matrix **view);
+/* Name of the kernel the matrix's products run: "lut" or "nibble4"
+ * (kernel.go:30-43, 92-98). */
+const char *cq_kernel_name(const cq_matrix *m);
+
+/* Matrix.Row (matrix.go:161-181): row r dequantised as cact.CQ does, bit
+ * for bit; dst holds In floats (host). */
+int cq_row(const cq_matrix *m, float *dst, size_t dst_len, int r);
+/* Matrix.GEMM (kernel.go:85-87); GEMV (kernel.go:78-80) is rows = 1.
+ * x is [rows][In], dst [rows][Out], host row-major. */
+int cq_gemm(const cq_matrix *m, float *dst, size_t dst_len, const float *x, size_t x_len, int rows);
+/* cq.GEMMs (kernel.go:134-158): dsts[k] = ms[k].GEMM of the same x. */
+int cq_gemms(int n, cq_matrix *const *ms, float *const *dsts, const size_t *dst_lens, const float *x, size_t x_len,
+             int rows);
+
+/* Device-pointer forms of GEMM, GEMMs and Row: every pointer is device
+ * memory, work is queued on `stream` (a hipStream_t; NULL = the null
+ * stream) and the call returns without waiting. */
+int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream);
+int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream);
+int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream);
+/* Rows gathered by index: dst[i] = Row(rows[i]) for i < n, rows a device
+ * int32 array: the decoder's token-embedding lookup for several streams
+ * (internal/decoder/decoder.go:269-275) in one launch. */
+int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n, void *stream);
+
+/* ---- int8 KV numerics (internal/needle/int8.go) ------------------------- */
+
+/* QuantizeRows (int8.go:116-121, Append :125-141): x is rows of cols
+ * floats; each chunk of width values gets its codes and one scale as
+ * QuantizeRow (int8.go:36-55) gives them, bit for bit. Host and device
+ * forms. */
+int kv_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, int width);
+int kv_quantize_rows_dev(int8_t *q, float *s, const float *x, int rows, int cols, int width, void *stream);
+
+/* AttendInt8Spans (int8.go:208-272) on device memory for `batch`
+ * independent streams (beam hypotheses, internal/search/beam.go:508-521).
+ * Stream b reads q + b*q_stride (t rows of heads*qk floats), its keys and
+ * values at kq + b*kv_stride codes (nk rows of k_cols / v_cols) with scales
+ * at ks/vs + b*s_stride, its spans at spans + b*t*4 (per query row the
+ * two ascending disjoint key spans {lo0, hi0, lo1, hi1}), and writes t rows
+ * of heads*vd floats at out + b*out_stride. quant_q chooses the int8 query
+ * (int8Logits, int8.go:278-285) or the float32 query (dotsF32I8,
+ * int8.go:289-300). The softmax is softmaxInPlace (load.go:128-138) with
+ * the amd64 kernel's exponent (exp_amd64.s:68-124). */
+int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                       const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                       int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
+                       float scale, int quant_q, int batch, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,216 @@
+"""ctypes binding of the CPU oracle (liboracle.so, oracle.h).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.
+"""
+
+import ctypes
+import os
+from ctypes import POINTER, Structure, c_char_p, c_float, c_int, c_int8, c_int32, c_size_t, c_uint8, c_uint16, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+GATHER, NIBBLE, NIBBLE4, LUT = 0, 1, 2, 3
+
+
+class _Packed(Structure):
+    _fields_ = [("out", c_int), ("in_", c_int), ("group", c_int), ("bits", c_int), ("width", c_int),
+                ("codebook", POINTER(c_float)), ("index", POINTER(c_uint8)), ("norms", POINTER(c_uint8)),
+                ("index_len", c_size_t), ("norms_len", c_size_t), ("codebook_len", c_size_t)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle not built ({LIB_PATH}): make -C oracle")
+        lb = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_f16_to_f32": (c_float, [c_uint16]),
+            "orc_f16_to_f32_n": (None, [POINTER(c_float), POINTER(c_uint16), c_size_t]),
+            "orc_unpack_lsb": (None, [POINTER(c_uint8), POINTER(c_uint8), c_int, c_int]),
+            "orc_fwht": (None, [POINTER(c_float), c_int]),
+            "orc_cq_dequant": (c_int, [POINTER(c_float), POINTER(_Packed)]),
+            "orc_new": (c_void_p, [POINTER(_Packed), c_char_p, c_size_t]),
+            "orc_free": (None, [c_void_p]),
+            "orc_rows": (c_void_p, [c_void_p, c_int, c_int]),
+            "orc_out": (c_int, [c_void_p]),
+            "orc_in": (c_int, [c_void_p]),
+            "orc_gemm": (c_int, [c_void_p, c_int, POINTER(c_float), POINTER(c_float), c_int]),
+            "orc_gemms": (c_int, [POINTER(c_void_p), c_int, c_int, POINTER(POINTER(c_float)), POINTER(c_float), c_int]),
+            "orc_row": (c_int, [c_void_p, POINTER(c_float), c_int]),
+            "orc_lut_tables2": (c_float, [POINTER(c_uint8), POINTER(c_float), c_int, POINTER(c_float), c_float]),
+            "orc_lut_tables4": (c_float, [POINTER(c_uint8), POINTER(c_float), c_int, POINTER(c_float), c_float]),
+            "orc_lut_lookup": (None, [POINTER(c_float), POINTER(c_uint8), POINTER(c_uint8), POINTER(c_float),
+                                      POINTER(c_float), c_int, c_int, c_int]),
+            "orc_lut_step": (c_float, [c_int]),
+            "orc_quantize_row": (c_float, [POINTER(c_int8), POINTER(c_float), c_int]),
+            "orc_quantize_rows": (None, [POINTER(c_int8), POINTER(c_float), POINTER(c_float), c_int, c_int, c_int]),
+            "orc_dots_i8": (None, [POINTER(c_int32), c_int, POINTER(c_int8), c_int, POINTER(c_int8), c_int]),
+            "orc_axpys_i8": (None, [POINTER(c_float), c_int, POINTER(c_float), c_int, POINTER(c_int8), c_int]),
+            "orc_dots_f32_i8": (None, [POINTER(c_float), c_int, POINTER(c_float), c_int, POINTER(c_int8), c_int]),
+            "orc_exp_sub_sum": (c_float, [POINTER(c_float), c_int, c_float, c_int]),
+            "orc_softmax": (None, [POINTER(c_float), c_int, c_int]),
+            "orc_attend_int8_spans": (c_int, [POINTER(c_float), POINTER(c_float), c_int, c_int, POINTER(c_int8),
+                                              POINTER(c_float), c_int, c_int, POINTER(c_int8), POINTER(c_float), c_int,
+                                              c_int, c_int, POINTER(c_int32), c_float, c_int, c_int, POINTER(c_float)]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(lb, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = lb
+    return _lib
+
+
+def fp(a):
+    return a.ctypes.data_as(POINTER(c_float))
+
+
+def u8p(a):
+    return a.ctypes.data_as(POINTER(c_uint8))
+
+
+def i8p(a):
+    return a.ctypes.data_as(POINTER(c_int8))
+
+
+def i32p(a):
+    return a.ctypes.data_as(POINTER(c_int32))
+
+
+def _packed(p):
+    cb = np.ascontiguousarray(p.Codebook, dtype=np.float32)
+    idx = np.ascontiguousarray(p.Index, dtype=np.uint8)
+    nrm = np.ascontiguousarray(p.Norms, dtype=np.uint8)
+    s = _Packed(p.Out, p.In, p.Group, p.Bits, p.Width, fp(cb), u8p(idx), u8p(nrm), idx.size, nrm.size, cb.size)
+    return s, (cb, idx, nrm)
+
+
+class OracleError(Exception):
+    pass
+
+
+class OMatrix:
+    """The oracle's cq.Matrix (New) and Rows views."""
+
+    def __init__(self, h, keep):
+        self.h = c_void_p(h)
+        self._keep = keep
+
+    @staticmethod
+    def new(p):
+        s, keep = _packed(p)
+        err = ctypes.create_string_buffer(256)
+        h = lib().orc_new(ctypes.byref(s), err, 256)
+        if not h:
+            raise OracleError(err.value.decode())
+        return OMatrix(h, keep)
+
+    def __del__(self):
+        if getattr(self, "h", None) is not None and self.h.value:
+            lib().orc_free(self.h)
+            self.h = None
+
+    def rows(self, lo, hi):
+        h = lib().orc_rows(self.h, lo, hi)
+        if not h:
+            raise OracleError(f"cq: Rows({lo}, {hi})")
+        return OMatrix(h, self)
+
+    def out(self):
+        return lib().orc_out(self.h)
+
+    def inp(self):
+        return lib().orc_in(self.h)
+
+    def gemm(self, x, rows, kernel=LUT):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(rows * self.out(), dtype=np.float32)
+        rc = lib().orc_gemm(self.h, kernel, fp(y), fp(x), rows)
+        if rc:
+            raise OracleError(f"orc_gemm: {rc}")
+        return y
+
+    def row(self, r):
+        y = np.zeros(self.inp(), dtype=np.float32)
+        if lib().orc_row(self.h, fp(y), r):
+            raise OracleError(f"Row({r})")
+        return y
+
+
+def gemms(ms, x, rows, kernel=LUT):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ys = [np.zeros(rows * m.out(), dtype=np.float32) for m in ms]
+    hs = (c_void_p * len(ms))(*[m.h for m in ms])
+    ds = (POINTER(c_float) * len(ms))(*[fp(y) for y in ys])
+    rc = lib().orc_gemms(hs, len(ms), kernel, ds, fp(x), rows)
+    if rc:
+        raise OracleError(f"orc_gemms: {rc}")
+    return ys
+
+
+def dequant(p):
+    s, keep = _packed(p)
+    w = np.zeros(p.Out * p.In, dtype=np.float32)
+    if lib().orc_cq_dequant(fp(w), ctypes.byref(s)):
+        raise OracleError("dequant")
+    return w.reshape(p.Out, p.In)
+
+
+def fwht(x):
+    x = np.array(x, dtype=np.float32)
+    lib().orc_fwht(fp(x), x.size)
+    return x
+
+
+def quantize_row(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.zeros(x.size, dtype=np.int8)
+    s = lib().orc_quantize_row(i8p(q), fp(x), x.size)
+    return q, np.float32(s)
+
+
+def quantize_rows(x, cols, width):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows = x.size // cols
+    q = np.zeros(x.size, dtype=np.int8)
+    s = np.zeros(rows * (cols // width), dtype=np.float32)
+    lib().orc_quantize_rows(i8p(q), fp(s), fp(x), rows, cols, width)
+    return q, s
+
+
+def exp_sub_sum(s, m, variant):
+    s = np.array(s, dtype=np.float32)
+    total = lib().orc_exp_sub_sum(fp(s), s.size, np.float32(m), variant)
+    return s, np.float32(total)
+
+
+def softmax(s, variant):
+    s = np.array(s, dtype=np.float32)
+    lib().orc_softmax(fp(s), s.size, variant)
+    return s
+
+
+def attend_int8_spans(q, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, nk, spans, scale, quant_q, variant=1,
+                      want_probs=False):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kq = np.ascontiguousarray(kq, dtype=np.int8)
+    vq = np.ascontiguousarray(vq, dtype=np.int8)
+    ks = np.ascontiguousarray(ks, dtype=np.float32)
+    vs = np.ascontiguousarray(vs, dtype=np.float32)
+    spans = np.ascontiguousarray(spans, dtype=np.int32)
+    out = np.zeros(t * heads * vd, dtype=np.float32)
+    probs = np.zeros(t * heads * nk, dtype=np.float32) if want_probs else None
+    rc = lib().orc_attend_int8_spans(fp(out), fp(q), t, heads, i8p(kq), fp(ks), k_cols, qk, i8p(vq), fp(vs), v_cols,
+                                     vd, nk, i32p(spans), np.float32(scale), 1 if quant_q else 0, variant,
+                                     fp(probs) if probs is not None else None)
+    if rc:
+        raise OracleError(f"attend: {rc}")
+    return (out, probs) if want_probs else out

@@ -1,0 +1,109 @@
+/*
+ * CPU oracle for go-whistle's CQ quantized-matrix path and its int8 KV
+ * numerics: a plain-C restatement of the reference's Go arithmetic, used as
+ * the checker for the HIP library.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load liboracle.so. The product library
+ * (libcqhip.so) neither links nor calls it.
+ *
+ * Every function names the reference file:line it follows. Build flags
+ * (Makefile): -O2 -ffp-contract=off -fno-fast-math, so that every float32
+ * multiply and add rounds on its own as in Go on amd64 (which never fuses).
+ *
+ * Pinning (what checks each function independently of this file) is listed
+ * in the header comment of each source file; tests/test_oracle_*.py hold
+ * the checks.
+ */
+#ifndef CQ_ORACLE_H
+#define CQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- internal/cact: the packed CQ form ---------------------------------- */
+
+/* cact.Packed (internal/cact/packed.go:18-29): Out rows of RowBytes index
+ * bytes (LSB-first bitstream of the group-padded row), Out*Groups FP16 norms
+ * (little-endian, [out][groups]) and the 2^bits codebook. */
+typedef struct {
+    int out, in, group, bits, width; /* width: bits per stored index (Packed.Width) */
+    const float *codebook;  /* 1 << bits levels */
+    const uint8_t *index;   /* out * row_bytes */
+    const uint8_t *norms;   /* 2 * out * groups */
+    size_t index_len, norms_len, codebook_len;
+} orc_packed;
+
+float orc_f16_to_f32(uint16_t h);                      /* half.go:8-40 */
+void orc_f16_to_f32_n(float *dst, const uint16_t *h, size_t n);
+void orc_unpack_lsb(uint8_t *idx, const uint8_t *packed, int n, int width); /* cq.go:124-137 */
+void orc_fwht(float *x, int n);                        /* cq/kernel.go:384-393 */
+/* cact.CQ: the dequantised [out][in] matrix (internal/cact/cq.go:67-118). */
+int orc_cq_dequant(float *w, const orc_packed *p);
+
+/* ---- internal/cq: Matrix ------------------------------------------------ */
+
+typedef struct orc_matrix orc_matrix;
+
+/* cq.New / cq.NewGather (internal/cq/matrix.go:46-96). Returns NULL and
+ * writes a "cq: ..." message to err (if non-NULL, errlen bytes) on bad
+ * input. The matrix copies everything it needs. */
+orc_matrix *orc_new(const orc_packed *p, char *err, size_t errlen);
+void orc_free(orc_matrix *m);
+/* Matrix.Rows (matrix.go:131-145): a view sharing storage; NULL on a bad
+ * range. Views must be freed with orc_free and before their root. */
+orc_matrix *orc_rows(const orc_matrix *m, int lo, int hi);
+int orc_out(const orc_matrix *m);
+int orc_in(const orc_matrix *m);
+
+enum { ORC_GATHER = 0, ORC_NIBBLE = 1, ORC_NIBBLE4 = 2, ORC_LUT = 3 };
+
+/* Matrix.gemm with the named kernel (kernel.go:100-125): dst [rows][out],
+ * x [rows][in]. Returns -1 on a shape mismatch (the reference panics). */
+int orc_gemm(const orc_matrix *m, int kernel, float *dst, const float *x, int rows);
+/* cq.GEMMs (kernel.go:134-158): all matrices must share the lut tables for
+ * the shared path; otherwise each runs its own GEMM. kernel is ORC_LUT for
+ * Matrix.GEMM's default on amd64 with AVX2, ORC_NIBBLE4 for Exact views. */
+int orc_gemms(orc_matrix *const *ms, int n, int kernel, float *const *dsts, const float *x, int rows);
+/* Matrix.Row (matrix.go:159-181). */
+int orc_row(const orc_matrix *m, float *dst, int r);
+
+/* The lut kernel's routines (internal/cq/lut.go), for direct tests. */
+float orc_lut_tables2(uint8_t *tab, const float *x, int n, const float *cb, float cb_max); /* lut.go:239-258 */
+float orc_lut_tables4(uint8_t *tab, const float *x, int n, const float *cb, float cb_max); /* lut.go:263-282 */
+void orc_lut_lookup(float *y, const uint8_t *idx, const uint8_t *tab, const float *norm, const float *steps,
+                    int blocks, int groups, int gb);                                       /* lut.go:289-313 */
+float orc_lut_step(int group);                                                             /* lut.go:213-215 */
+
+/* ---- internal/needle: int8 numerics ------------------------------------- */
+
+float orc_quantize_row(int8_t *q, const float *x, int n);                /* int8.go:36-55 */
+void orc_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, int width); /* int8.go:116-141 */
+void orc_dots_i8(int32_t *dst, int n, const int8_t *q, int width, const int8_t *k, int stride);   /* int8kernel.go:346-357 */
+void orc_axpys_i8(float *out, int width, const float *w, int n, const int8_t *v, int stride);     /* int8kernel.go:360-368 */
+void orc_dots_f32_i8(float *dst, int n, const float *q, int width, const int8_t *k, int stride); /* int8.go:289-300 */
+
+/* expSubSum: variant 0 = expSubSumGeneric (exp.go:21-31), float64 exp per
+ * value; variant 1 = the amd64 AVX2+FMA kernel's arithmetic on the
+ * multiple-of-8 prefix plus the generic tail (exp_amd64.go:13-25,
+ * exp_amd64.s:68-124). */
+float orc_exp_sub_sum(float *s, int n, float m, int variant);
+void orc_softmax(float *s, int n, int variant);                           /* load.go:125-138 */
+
+/* AttendInt8Spans (int8.go:208-272). q: t rows of heads*qk floats; k codes
+ * [nk][k_cols], k scales [nk][k_cols/qk]; v likewise with vd. spans: per
+ * query row i, two ascending disjoint spans {lo0, hi0, lo1, hi1}. out: t rows
+ * of heads*vd. probs (optional): [(i*heads+h)*nk + j]. */
+int orc_attend_int8_spans(float *out, const float *q, int t, int heads, const int8_t *kq, const float *ks,
+                          int k_cols, int qk, const int8_t *vq, const float *vs, int v_cols, int vd, int nk,
+                          const int32_t *spans, float scale, int quant_q, int exp_variant, float *probs);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
