@@ -1,0 +1,197 @@
+"""Benchmark: go-whistle's CQ LUT GEMV at batch 1 on one MI355X.
+
+Workload (the reference's GEMV sweep): 2- and 4-bit CQ matrices of
+512x512, 2048x512, 512x2048 and 16384x512 (group 128, 4 or 16 codebook
+levels ~N(0, 0.05), uniform random indices, FP16 norms), x ~N(0, 1), one
+activation each. A step multiplies every matrix of `copies` distinct device
+copies of the sweep once (the copies together exceed twice the 256 MiB
+MALL, so the weights stream from HBM), as one captured HIP graph of
+batch-1 GEMV launches through the C ABI. Inputs are resident in HBM before
+the timed region.
+
+value = weight bytes (packed index + FP16 norms) of all GEMVs of a step /
+step time, in GB/s. The roofline object is the 16384x512 4-bit lut GEMV
+kernel alone (HIP events around each launch on its stream). The
+cpu_baseline is the C restatement of the reference's lut kernel
+(oracle/), one thread, on a bounded sample of the same sweep.
+"""
+
+import argparse
+import importlib.util
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+SHAPES = [(512, 512), (2048, 512), (512, 2048), (16384, 512)]
+BITS = (4, 2)
+GROUP = 128
+
+
+def _package():
+    if "go_whistle_amd" in sys.modules:
+        return sys.modules["go_whistle_amd"]
+    pkg_dir = os.path.join(ROOT, "go-whistle_amd")
+    spec = importlib.util.spec_from_file_location("go_whistle_amd", os.path.join(pkg_dir, "__init__.py"),
+                                                  submodule_search_locations=[pkg_dir])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["go_whistle_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def weight_bytes(out, inp, bits):
+    groups = (inp + GROUP - 1) // GROUP
+    return out * groups * GROUP * bits // 8 + 2 * out * groups
+
+
+def algorithmic_bytes(out, inp, bits):
+    return weight_bytes(out, inp, bits) + 4 * inp + 4 * out + 4 * (1 << bits)
+
+
+def cpu_baseline(gw, packs, seconds):
+    """The oracle's lut GEMV (single thread) over the sweep, bounded in time."""
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from oracle import binding as orc
+
+    g = gw.synth.rng(99)
+    mats = [(orc.OMatrix.new(p), gw.synth.activations(g, 1, p.In), weight_bytes(p.Out, p.In, p.Bits))
+            for p in packs]
+    done, t0 = 0, time.perf_counter()
+    passes = 0
+    while True:
+        for m, x, wb in mats:
+            m.gemm(x, 1, orc.LUT)
+            done += wb
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{passes} passes over the 8-matrix sweep (one copy each), oracle lut GEMV, 1 thread, "
+                      f"{el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--copies", type=int, default=0, help="device copies of the sweep (0: > 2x MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    gw = _package()
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+
+    g = gw.synth.rng(20261201)
+    packs = [gw.synth.random_packed(g, o, i, GROUP, b, sigma=0.05) for b in BITS for (o, i) in SHAPES]
+    sweep_bytes = sum(weight_bytes(p.Out, p.In, p.Bits) for p in packs)
+    copies = args.copies or max(1, math.ceil(2 * 256 * 2 ** 20 / sweep_bytes))
+    mats = [[gw.cq.New(p) for p in packs] for _ in range(copies)]
+    xs = {i: torch.from_numpy(gw.synth.activations(g, 1, i)).to(dev) for i in {p.In for p in packs}}
+    ys = [[torch.zeros(p.Out, dtype=torch.float32, device=dev) for p in packs] for _ in range(copies)]
+
+    def step():
+        for c in range(copies):
+            for k, p in enumerate(packs):
+                mats[c][k].gemm_dev(ys[c][k], xs[p.In], 1)
+
+    step()  # kernel attributes are set outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    value = sweep_bytes * copies / (ms / 1e3) / 1e9
+
+    # Per-shape GB/s (graph of that matrix's copies) and the dominant kernel.
+    detail = {}
+    for k, p in enumerate(packs):
+        gk = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gk):
+            for c in range(copies):
+                mats[c][k].gemm_dev(ys[c][k], xs[p.In], 1)
+        gk.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(2, args.steps // 4)
+        e0.record()
+        for _ in range(reps):
+            gk.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+        wb = weight_bytes(p.Out, p.In, p.Bits)
+        detail[f"{p.Out}x{p.In}_cq{p.Bits}"] = {"us_per_gemv": round(us, 3), "weight_GBps": round(wb / us / 1e3, 1)}
+
+    # Roofline: the 16384x512 4-bit lut GEMV, events around each launch.
+    kdom = packs.index(next(p for p in packs if p.Out == 16384 and p.Bits == 4))
+    pd = packs[kdom]
+    n = min(copies, 64)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for c in range(n):
+        mats[c][kdom].gemm_dev(ys[c][kdom], xs[pd.In], 1)
+    torch.cuda.synchronize()
+    for c in range(n):
+        evs[c][0].record()
+        mats[c][kdom].gemm_dev(ys[c][kdom], xs[pd.In], 1)
+        evs[c][1].record()
+    torch.cuda.synchronize()
+    dur_s = sum(a.elapsed_time(b) for a, b in evs) / n / 1e3
+    alg = algorithmic_bytes(pd.Out, pd.In, pd.Bits)
+    achieved = alg / dur_s / 1e9
+
+    line = {
+        "metric": "CQ LUT GEMV HBM GB/s (% of peak) + decode tokens/sec, batch 1 and 256",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": "batch-1 CQ LUT GEMV sweep, 2/4-bit x {512x512, 2048x512, 512x2048, 16384x512}, "
+                               "group 128",
+                   "copies": copies, "gemvs_per_step": copies * len(packs),
+                   "weight_bytes_per_step": sweep_bytes * copies, "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "product_kernel<4,64,lut> 16384x512 CQ4 GEMV",
+                     "launch_us": round(dur_s * 1e6, 3), "algorithmic_bytes": alg},
+        "detail": detail,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(gw, packs, args.cpu_seconds)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -204,6 +204,8 @@ int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x,
         nblk_total += (row0 + out + kBlockRows - 1) / kBlockRows - row0 / kBlockRows;
     }
     LaunchPlan p = plan(s0, mode, nblk_total, rows);
+    if (p.lds > device_info().max_lds)
+        return fail(CQ_ERR_UNSUPPORTED, "cq: a product of group %d needs %zu bytes of LDS", s0.group, p.lds);
     a.tb = p.tb;
     a.gc = p.gc;
     int tiles = 0;
@@ -262,6 +264,7 @@ int row_args(const cq_matrix *m, RowArgs &a) {
     a.unit_bytes = s.unit_bytes;
     for (int c = 0; c < 16; ++c) a.cb[c] = c < s.ncb ? s.cb[c] : 0.0f;
     a.inv_sqrt = s.inv_sqrt;
+    a.nrows = s.out;
     if (static_cast<size_t>(s.group) * 4 > device_info().max_lds)
         return fail(CQ_ERR_UNSUPPORTED, "cq: Row of group %d", s.group);
     return CQ_OK;
@@ -565,6 +568,8 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
     if (t < 0 || batch < 0 || nk_max < 0) return fail(CQ_ERR_MISUSE, "needle: bad attention sizes");
     const size_t lds = sizeof(float) * static_cast<size_t>(nk_max) + 64 * static_cast<size_t>(vd);
     if (lds > device_info().max_lds) return fail(CQ_ERR_UNSUPPORTED, "needle: %d keys exceed LDS", nk_max);
+    if (out_stride == 0) out_stride = static_cast<long long>(t) * heads * vd;  // dense streams
+    if (q_stride == 0) q_stride = static_cast<long long>(t) * heads * qk;
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
                  kv_stride, s_stride, spans, nk_max, scale, quant_q, batch};
     HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");

@@ -64,6 +64,7 @@ struct RowArgs {
     float *dst;            // n rows of `in` floats
     const int32_t *rows;   // device row list (root rows), or nullptr: rows r0 .. r0+n-1
     int r0, n;
+    int nrows;             // root rows: listed rows outside [0, nrows) give zeros
     int in, group, groups, row_bytes, width, units, unit_bytes;
     float cb[16];
     float inv_sqrt;
@@ -82,7 +83,7 @@ struct AttendArgs {
     const int8_t *vq; const float *vs; int v_cols, vd;
     long long kv_stride, s_stride;
     const int32_t *spans;
-    int nk_max;
+    int nk_max;            // key rows each stream's arrays hold; spans must lie in [0, nk_max)
     float scale;
     int quant_q;
     int batch;

@@ -392,6 +392,14 @@ __global__ __launch_bounds__(kThreads) void rows_kernel(RowArgs a) {
     float *buf = reinterpret_cast<float *>(smem);
     const int g = blockIdx.x, i = blockIdx.y;
     const int r = a.rows ? a.rows[i] : a.r0 + i;
+    float *dst = a.dst + static_cast<size_t>(i) * a.in;
+    if (r < 0 || r >= a.nrows) {  // a listed row outside the matrix: zeros, no read
+        for (int k = threadIdx.x; k < a.group; k += blockDim.x) {
+            const int col = g * a.group + k;
+            if (col < a.in) dst[col] = 0.0f;
+        }
+        return;
+    }
     const int blk = r / kBlockRows, lane = r % kBlockRows;
     const float s = half_bits_to_float(a.norm[(static_cast<size_t>(blk) * a.groups + g) * 64 + lane]) * a.inv_sqrt;
     const int G = a.group, mask = (1 << a.width) - 1;
@@ -414,7 +422,6 @@ __global__ __launch_bounds__(kThreads) void rows_kernel(RowArgs a) {
         }
         __syncthreads();
     }
-    float *dst = a.dst + static_cast<size_t>(i) * a.in;
     for (int k = threadIdx.x; k < G; k += blockDim.x) {
         const int col = g * G + k;
         if (col < a.in) dst[col] = buf[k];

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
     const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
     const int n = len0 + len1;
-    if (len0 < 0 || len1 < 0 || n > a.nk_max) return;  // malformed spans: nothing to attend
+    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
 
     float *s = reinterpret_cast<float *>(smem);                 // n logits / weights
     int8_t *vstage = reinterpret_cast<int8_t *>(s + a.nk_max);  // kVStage rows of vd codes

@@ -114,7 +114,10 @@ int kv_quantize_rows_dev(int8_t *q, float *s, const float *x, int rows, int cols
  * values at kq + b*kv_stride codes (nk rows of k_cols / v_cols) with scales
  * at ks/vs + b*s_stride, its spans at spans + b*t*4 (per query row the
  * two ascending disjoint key spans {lo0, hi0, lo1, hi1}), and writes t rows
- * of heads*vd floats at out + b*out_stride. quant_q chooses the int8 query
+ * of heads*vd floats at out + b*out_stride (out_stride and q_stride 0 mean
+ * dense streams; kv_stride and s_stride 0 share one cache). nk_max is the
+ * number of key rows each stream's arrays hold: spans outside [0, nk_max)
+ * leave that output untouched. quant_q chooses the int8 query
  * (int8Logits, int8.go:278-285) or the float32 query (dotsF32I8,
  * int8.go:289-300). The softmax is softmaxInPlace (load.go:128-138) with
  * the amd64 kernel's exponent (exp_amd64.s:68-124). */

@@ -1,0 +1,136 @@
+"""GPU parity of the int8 KV numerics with the CPU oracle, through the C
+ABI: QuantizeRows codes and scales bit for bit, and AttendInt8Spans bit for
+bit with amd64's softmax exponent, for decode self-attention over a causal
+KV cache (1..448 keys), cross-attention over 1500 frames, GQA, windows with
+a sink, and many streams at once."""
+
+import math
+
+import numpy as np
+import pytest
+
+import go_whistle_amd as gw
+from go_whistle_amd import needle, synth
+from oracle import binding as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def same_bits(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("width", [48, 64, 17, 2048])
+def test_quantize_rows_bit_exact(width):
+    g = synth.rng(width)
+    cols = width * 4
+    rows = 37
+    x = (g.standard_normal(rows * cols) * g.choice([1e-6, 1, 1e4], size=rows * cols)).astype(np.float32)
+    x[: cols // 2] = 0  # zero chunks: scale 1
+    x[cols * 3 + 5] = 127.0
+    q, s = needle.QuantizeRows(x, cols, width)
+    wq, ws = orc.quantize_rows(x, cols, width)
+    assert np.array_equal(q, wq)
+    assert same_bits(s, ws)
+
+
+def test_quantize_hand_vectors():
+    q, s = needle.QuantizeRow(np.array([127, 2.5, -2.5, 3.5, -0.5, 1.4999], np.float32))
+    assert s == 1 and list(q) == [127, 2, -2, 4, 0, 1]
+    q, s = needle.QuantizeRow(np.array([-6.35, 0.05, 3], np.float32))
+    assert list(q) == [-127, 1, 60]
+
+
+def _cache(g, n, kv_heads, qk, vd):
+    kq, ks = orc.quantize_rows(g.standard_normal(n * kv_heads * qk).astype(np.float32), kv_heads * qk, qk)
+    vq, vs = orc.quantize_rows(g.standard_normal(n * kv_heads * vd).astype(np.float32), kv_heads * vd, vd)
+    return kq, ks, vq, vs
+
+
+def _attend_gpu(q, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, spans, nk_max, scale, quant_q, batch=1,
+                q_stride=0, kv_stride=0, s_stride=0, out_stride=0):
+    import torch
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out = torch.zeros(max(1, batch * (out_stride or t * heads * vd)), dtype=torch.float32, device="cuda")
+    needle.attend_int8_dev(out, dev(q), t, heads, dev(kq), dev(ks), k_cols, qk, dev(vq), dev(vs), v_cols, vd,
+                           dev(spans.astype(np.int32)), nk_max, scale, quant_q, batch=batch, out_stride=out_stride,
+                           q_stride=q_stride, kv_stride=kv_stride, s_stride=s_stride)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("quant_q", [True, False])
+@pytest.mark.parametrize("n", [1, 5, 8, 9, 37, 64, 447, 448])
+def test_self_attention_decode_bit_exact(quant_q, n):
+    heads, qk, vd = 8, 64, 64
+    g = synth.rng(n + 7 * quant_q)
+    kq, ks, vq, vs = _cache(g, n, heads, qk, vd)
+    q = g.standard_normal(heads * qk).astype(np.float32)
+    spans = np.array([[0, 0, 0, n]], np.int32)
+    scale = np.float32(math.sqrt(qk))
+    got = _attend_gpu(q, 1, heads, kq, ks, heads * qk, qk, vq, vs, heads * vd, vd, spans, n, scale, quant_q)
+    want = orc.attend_int8_spans(q, 1, heads, kq, ks, heads * qk, qk, vq, vs, heads * vd, vd, n, spans, scale,
+                                 quant_q, 1)
+    assert same_bits(got[:want.size], want)
+
+
+@pytest.mark.parametrize("quant_q", [True, False])
+def test_cross_attention_1500_and_block_rows(quant_q):
+    heads, qk, vd, n, t = 8, 64, 64, 1500, 3
+    g = synth.rng(1500)
+    kq, ks, vq, vs = _cache(g, n, heads, qk, vd)
+    q = g.standard_normal(t * heads * qk).astype(np.float32)
+    spans = np.array([[0, 0, 0, n]] * t, np.int32)
+    got = _attend_gpu(q, t, heads, kq, ks, heads * qk, qk, vq, vs, heads * vd, vd, spans, n, 8.0, quant_q)
+    want = orc.attend_int8_spans(q, t, heads, kq, ks, heads * qk, qk, vq, vs, heads * vd, vd, n, spans, 8.0,
+                                 quant_q, 1)
+    assert same_bits(got[:want.size], want)
+
+
+def test_gqa_causal_and_windows():
+    # Whistle's self-attention geometry: 8 query heads of 48 over 2 KV heads
+    # (int8_test.go:212-284), causal rows, and a window with a sink.
+    heads, kv_heads, qk, vd, n, t = 8, 2, 48, 64, 37, 3
+    g = synth.rng(9)
+    kq, ks, vq, vs = _cache(g, n, kv_heads, qk, vd)
+    q = g.standard_normal(t * heads * qk).astype(np.float32)
+    scale = np.float32(math.sqrt(qk))
+    for spans in (np.array([[0, 0, 0, n - t + i + 1] for i in range(t)], np.int32),
+                  np.array([[0, 2, 10 + i, 30 + i] for i in range(t)], np.int32)):
+        for quant_q in (True, False):
+            got = _attend_gpu(q, t, heads, kq, ks, kv_heads * qk, qk, vq, vs, kv_heads * vd, vd, spans, n, scale,
+                              quant_q)
+            want = orc.attend_int8_spans(q, t, heads, kq, ks, kv_heads * qk, qk, vq, vs, kv_heads * vd, vd, n, spans,
+                                         scale, quant_q, 1)
+            assert same_bits(got[:want.size], want)
+
+
+def test_many_streams():
+    # 16 independent streams (beam hypotheses), each its own cache length.
+    heads, qk, vd, nk, batch = 8, 64, 64, 300, 16
+    g = synth.rng(256)
+    kqs, kss, vqs, vss, qs, spans = [], [], [], [], [], []
+    for b in range(batch):
+        kq, ks, vq, vs = _cache(g, nk, heads, qk, vd)
+        kqs.append(kq); kss.append(ks); vqs.append(vq); vss.append(vs)
+        qs.append(g.standard_normal(heads * qk).astype(np.float32))
+        spans.append([0, 0, 0, 1 + (b * 37) % nk])
+    spans = np.array(spans, np.int32)
+    got = _attend_gpu(np.concatenate(qs), 1, heads, np.concatenate(kqs), np.concatenate(kss), heads * qk, qk,
+                      np.concatenate(vqs), np.concatenate(vss), heads * vd, vd, spans, nk, 8.0, True, batch=batch,
+                      q_stride=heads * qk, kv_stride=nk * heads * qk, s_stride=nk * heads, out_stride=heads * vd)
+    for b in range(batch):
+        want = orc.attend_int8_spans(qs[b], 1, heads, kqs[b], kss[b], heads * qk, qk, vqs[b], vss[b], heads * vd, vd,
+                                     nk, spans[b:b + 1], 8.0, True, 1)
+        assert same_bits(got[b * heads * vd:(b + 1) * heads * vd], want), b
+
+
+def test_attend_misuse():
+    import torch
+
+    z = torch.zeros(64, dtype=torch.float32, device="cuda")
+    with pytest.raises(gw.CQPanic):
+        needle.attend_int8_dev(z, z, 1, 8, z, z, 100, 64, z, z, 512, 64, z, 1, 8.0, True)

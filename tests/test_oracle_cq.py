@@ -334,3 +334,83 @@ def test_lut_tables_byte_planes():
             scale = 8191 / float(mm) if mm > 0 else 0
             assert np.all(np.abs(v - exact * scale) <= 0.5 + 1e-3 * np.abs(exact * scale) + 1e-6)
             assert np.abs(v).max() <= 8191
+
+
+def _f32_of_exact(q):
+    """float32 nearest (ties to even) to an exact rational."""
+    q = Fraction(q)
+    f = np.float32(float(q))  # may double-round: step to the true nearest
+    best = f
+    for cand in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        d, db = abs(Fraction(float(cand)) - q), abs(Fraction(float(best)) - q)
+        if d < db or (d == db and (cand.view(np.uint32) & 1) == 0 and cand != best):
+            best = cand
+    return np.float32(best)
+
+
+def test_lut_accumulate_is_unfused():
+    # Two groups of 8 (4 bits), x̂_g = (8 s_g, 0, ...) so S_g = v(cbMax) =
+    # 8191. y = (0 + S0*c0) + S1*c1 with each product rounded (Go on amd64
+    # never fuses): find a group-1 scale where a fused multiply-add would
+    # round differently, and require the unfused result.
+    cb = np.linspace(-1, 1, 16).astype(np.float32)
+    top = 15
+    lut_step = np.float32(1 / (8191 * np.sqrt(8.0)))
+    norms = np.array([0x3C00, 0x3C00], dtype="<u2").view(np.uint8)
+    index = np.array([top, 0, 0, 0, top, 0, 0, 0], np.uint8)
+    g = synth.rng(99)
+    for _ in range(2000):
+        s1 = np.float32(g.uniform(0.3, 0.9))
+        prods, coefs = [], []
+        for s in (np.float32(1), s1):
+            mm = np.float32(np.float32(1) * np.float32(np.float32(8) * s))
+            inv = np.float32(np.float32(8191) / mm)
+            v = _rne(np.float32(cb[top] * np.float32(np.float32(8) * s * inv)))
+            coef = np.float32(np.float32(1) * np.float32(mm * lut_step))
+            coefs.append((v, coef))
+            prods.append(np.float32(np.float32(v) * coef))
+        y0 = np.float32(np.float32(0) + prods[0])
+        unfused = np.float32(y0 + prods[1])
+        fused = _f32_of_exact(Fraction(float(y0)) + Fraction(coefs[1][0]) * Fraction(float(coefs[1][1])))
+        if fused != unfused:
+            break
+    else:
+        raise AssertionError("no discriminating case")
+    x = np.concatenate([np.full(8, 1, np.float32), np.full(8, s1, np.float32)])
+    m = orc.OMatrix.new(_packed(1, 16, 8, 4, cb, index, norms))
+    got = m.gemm(x, 1, orc.LUT)
+    assert got.view(np.uint32)[0] == unfused.view(np.uint32)
+
+
+def test_lut2_table_entry_is_unfused():
+    # A 2-bit entry is RNE(float32(cb[lo]*a) + float32(cb[hi]*b)) (lut.go:253);
+    # find a pair where fusing either product would move the rounded entry.
+    g = synth.rng(7)
+    cb = np.sort(g.standard_normal(4).astype(np.float32))
+    cb_max = np.float32(np.abs(cb).max())
+    for _ in range(20000):
+        x = g.standard_normal(8).astype(np.float32)
+        xh = orc.fwht(x)
+        mx = np.float32(0)
+        for q in range(0, 8, 2):
+            mx = max(mx, np.float32(abs(xh[q]) + abs(xh[q + 1])))
+        mm = np.float32(cb_max * mx)
+        inv = np.float32(np.float32(8191) / mm)
+        a, b = np.float32(xh[0] * inv), np.float32(xh[1] * inv)
+        hit = None
+        for c in range(16):
+            lo, hi = np.float32(cb[c & 3] * a), np.float32(cb[c >> 2] * b)
+            unfused = np.float32(lo + hi)
+            f1 = _f32_of_exact(Fraction(float(cb[c & 3])) * Fraction(float(a)) + Fraction(float(hi)))
+            f2 = _f32_of_exact(Fraction(float(lo)) + Fraction(float(cb[c >> 2])) * Fraction(float(b)))
+            if _rne(unfused) != _rne(f1) or _rne(unfused) != _rne(f2):
+                hit = (c, _rne(unfused))
+                break
+        if hit:
+            break
+    else:
+        raise AssertionError("no discriminating case")
+    tab = np.zeros(32 * 4, np.uint8)
+    orc.lib().orc_lut_tables2(orc.u8p(tab), orc.fp(xh), 8, orc.fp(cb), cb_max)
+    c, v = hit
+    assert 128 * (int(tab[16 + c]) - 64) + int(tab[c]) == v
