@@ -5,15 +5,17 @@ Workload (the reference's GEMV sweep): 2- and 4-bit CQ matrices of
 levels ~N(0, 0.05), uniform random indices, FP16 norms), x ~N(0, 1), one
 activation each. A step multiplies every matrix of `copies` distinct device
 copies of the sweep once (the copies together exceed twice the 256 MiB
-MALL, so the weights stream from HBM), as one captured HIP graph of
-batch-1 GEMV launches through the C ABI. Inputs are resident in HBM before
-the timed region.
+MALL, so the weights stream from HBM). The GEMVs run through a batch
+plan of the C ABI (cq_batch_*): one lut-kernel launch per index width, 2
+launches per step, each GEMV bit for bit cq_gemm_dev's result. Inputs are
+resident in HBM before the timed region.
 
 value = weight bytes (packed index + FP16 norms) of all GEMVs of a step /
-step time, in GB/s. The roofline object is the 16384x512 4-bit lut GEMV
-kernel alone (HIP events around each launch on its stream). The
-cpu_baseline is the C restatement of the reference's lut kernel
-(oracle/), one thread, on a bounded sample of the same sweep.
+step time, in GB/s. The roofline object is the step's dominant launch, the
+4-bit one (HIP events around it on its stream). detail holds per-shape
+rates and the rate of one launch per GEMV (a captured graph of 8 * copies
+launches). The cpu_baseline is the C restatement of the reference's lut
+kernel (oracle/), one thread, on a bounded sample of the same sweep.
 """
 
 import argparse
@@ -104,65 +106,57 @@ def main():
     xs = {i: torch.from_numpy(gw.synth.activations(g, 1, i)).to(dev) for i in {p.In for p in packs}}
     ys = [[torch.zeros(p.Out, dtype=torch.float32, device=dev) for p in packs] for _ in range(copies)]
 
+    def timed(fn, reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps  # ms
+
+    by_bits = {b: [(c, k) for c in range(copies) for k, p in enumerate(packs) if p.Bits == b] for b in BITS}
+    plans = {b: gw.cq.Batch([mats[c][k] for c, k in jobs], [ys[c][k] for c, k in jobs],
+                            [xs[packs[k].In] for c, k in jobs]) for b, jobs in by_bits.items()}
+
     def step():
+        for b in BITS:
+            plans[b].run()
+
+    for _ in range(args.warmup):
+        step()
+    ms = timed(step, args.steps)
+    value = sweep_bytes * copies / (ms / 1e3) / 1e9
+
+    # One launch per GEMV: a captured graph of the whole sweep.
+    def per_launch():
         for c in range(copies):
             for k, p in enumerate(packs):
                 mats[c][k].gemm_dev(ys[c][k], xs[p.In], 1)
 
-    step()  # kernel attributes are set outside the capture
+    per_launch()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        step()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    for _ in range(args.steps):
-        graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / args.steps
-    value = sweep_bytes * copies / (ms / 1e3) / 1e9
+        per_launch()
+    graph.replay()
+    ms_launch = timed(graph.replay, max(2, args.steps // 4))
 
-    # Per-shape GB/s (graph of that matrix's copies) and the dominant kernel.
-    detail = {}
+    detail = {"one_launch_per_gemv": {"ms_per_step": round(ms_launch, 4),
+                                      "weight_GBps": round(sweep_bytes * copies / ms_launch / 1e6, 1)}}
     for k, p in enumerate(packs):
-        gk = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gk):
-            for c in range(copies):
-                mats[c][k].gemm_dev(ys[c][k], xs[p.In], 1)
-        gk.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = max(2, args.steps // 4)
-        e0.record()
-        for _ in range(reps):
-            gk.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+        plan = gw.cq.Batch([mats[c][k] for c in range(copies)], [ys[c][k] for c in range(copies)],
+                           [xs[p.In]] * copies)
+        plan.run()
+        msk = timed(plan.run, max(2, args.steps // 2))
         wb = weight_bytes(p.Out, p.In, p.Bits)
-        detail[f"{p.Out}x{p.In}_cq{p.Bits}"] = {"us_per_gemv": round(us, 3), "weight_GBps": round(wb / us / 1e3, 1)}
+        detail[f"{p.Out}x{p.In}_cq{p.Bits}"] = {"us_per_gemv": round(msk * 1e3 / copies, 3),
+                                                 "weight_GBps": round(wb * copies / msk / 1e6, 1)}
 
-    # Roofline: the 16384x512 4-bit lut GEMV, events around each launch.
-    kdom = packs.index(next(p for p in packs if p.Out == 16384 and p.Bits == 4))
-    pd = packs[kdom]
-    n = min(copies, 64)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for c in range(n):
-        mats[c][kdom].gemm_dev(ys[c][kdom], xs[pd.In], 1)
-    torch.cuda.synchronize()
-    for c in range(n):
-        evs[c][0].record()
-        mats[c][kdom].gemm_dev(ys[c][kdom], xs[pd.In], 1)
-        evs[c][1].record()
-    torch.cuda.synchronize()
-    dur_s = sum(a.elapsed_time(b) for a, b in evs) / n / 1e3
-    alg = algorithmic_bytes(pd.Out, pd.In, pd.Bits)
+    # Roofline: the 4-bit launch of the step, timed on its own.
+    dur_s = timed(plans[4].run, max(3, args.steps)) / 1e3
+    alg = sum(algorithmic_bytes(packs[k].Out, packs[k].In, 4) for c, k in by_bits[4])
     achieved = alg / dur_s / 1e9
 
     line = {
@@ -184,7 +178,7 @@ def main():
                    "weight_bytes_per_step": sweep_bytes * copies, "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "product_kernel<4,64,lut> 16384x512 CQ4 GEMV",
+                     "kernel": "lut_kernel<4,64,dev>: the step's 4-bit batch launch",
                      "launch_us": round(dur_s * 1e6, 3), "algorithmic_bytes": alg},
         "detail": detail,
     }

@@ -38,6 +38,11 @@ SIGNATURES = {
     "cq_gemms_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p]),
     "cq_row_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "cq_row_gather_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "cq_batch_new": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p), POINTER(c_int),
+                             POINTER(c_void_p)]),
+    "cq_batch_run": (c_int, [c_void_p, c_void_p]),
+    "cq_batch_launches": (c_int, [c_void_p]),
+    "cq_batch_free": (None, [c_void_p]),
     "kv_quantize_rows": (c_int, [POINTER(c_int8), POINTER(c_float), POINTER(c_float), c_int, c_int, c_int]),
     "kv_quantize_rows_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "kv_attend_int8_dev": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p,

@@ -168,3 +168,35 @@ def gemms_dev(ms, ys, x, rows):
     hs = (c_void_p * max(n, 1))(*[m.handle for m in ms])
     ds = (c_void_p * max(n, 1))(*[c_void_p(y.data_ptr()) for y in ys])
     check(lib().cq_gemms_dev(n, hs, ds, c_void_p(x.data_ptr()), rows, _stream()))
+
+
+class Batch:
+    """A plan of independent products on device tensors (cq_batch_*): job k
+    is ms[k].GEMM of rows[k] activations xs[k] into ys[k]. run() queues one
+    lut-kernel launch per kernel geometry on torch's current stream."""
+
+    def __init__(self, ms, ys, xs, rows=None):
+        n = len(ms)
+        if not (len(ys) == len(xs) == n):
+            raise CQPanic(f"cq: batch of {n} matrices, {len(ys)} outputs, {len(xs)} inputs")
+        rows = [1] * n if rows is None else list(rows)
+        self._keep = (list(ms), list(ys), list(xs))
+        hs = (c_void_p * max(n, 1))(*[m.handle for m in ms])
+        yp = (c_void_p * max(n, 1))(*[c_void_p(y.data_ptr()) for y in ys])
+        xp = (c_void_p * max(n, 1))(*[c_void_p(x.data_ptr()) for x in xs])
+        rp = (ctypes.c_int * max(n, 1))(*rows)
+        h = c_void_p()
+        check(lib().cq_batch_new(n, hs, yp, xp, rp, ctypes.byref(h)))
+        self._h = h
+
+    def run(self):
+        check(lib().cq_batch_run(self._h, _stream()))
+
+    def launches(self):
+        return lib().cq_batch_launches(self._h)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().cq_batch_free(h)
+            self._h = None

@@ -187,10 +187,86 @@ void fill_common(ProdArgs &a, const CqStore &s, int rows) {
     a.nib4_rows = rows - rows % 4;  // gemmScalar (kernel.go:170-183)
 }
 
+void fill_job(JobDesc &j, const cq_matrix *m, const float *x, float *y, int rows) {
+    const CqStore &s = *m->st;
+    std::memset(&j, 0, sizeof j);
+    j.idx = s.d_idx;
+    j.norm = s.d_norm;
+    j.x = x;
+    j.y = y;
+    j.x_stride = s.in;
+    j.y_stride = m->out;
+    j.row0 = m->row0;
+    j.out = m->out;
+    j.blk0 = m->row0 / kBlockRows;
+    j.nblk = (m->row0 + m->out + kBlockRows - 1) / kBlockRows - j.blk0;
+    j.in = s.in;
+    j.groups = s.groups;
+    j.units = s.units;
+    j.rows = rows;
+    for (int c = 0; c < 16; ++c) j.cb[c] = c < s.ncb ? s.cb[c] : 0.0f;
+    j.cb_max = s.cb_max;
+    j.lut_step = s.lut_step;
+}
+
+constexpr int kLutTile = 4;  // blocks per tile of the lut kernel
+
+int lut_waves(int groups_max) { return std::min(8, std::max(4, groups_max)); }
+
+// The lut kernel runs a geometry whose tables for every group fit in LDS.
+bool lut_fits(const CqStore &s) {
+    return lut_geometry_supported(s.width, s.group_bytes) &&
+           lut_lds_bytes(s.width, s.group_bytes, s.groups, kLutTile) <= std::min<size_t>(device_info().max_lds, 128 * 1024);
+}
+
+int blocks_per_workgroup(long long blocks) {
+    const long long want = 4LL * device_info().cus;
+    return static_cast<int>(std::min<long long>(16, std::max<long long>(1, blocks / want)));
+}
+
+// One launch of the lut kernel for up to kKernargJobs views of one geometry
+// and the same activations.
+int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+    const CqStore &s0 = *ms[0]->st;
+    LutLaunch a;
+    std::memset(&a, 0, sizeof a);
+    long long blocks = 0;
+    int groups_max = 0;
+    for (int k = 0; k < n; ++k) {
+        if (ms[k]->out == 0) continue;
+        JobDesc &j = a.jobs[a.njobs++];
+        fill_job(j, ms[k], x, dsts[k], rows);
+        blocks += static_cast<long long>(j.nblk) * rows;
+        groups_max = std::max(groups_max, j.groups);
+    }
+    if (a.njobs == 0 || rows == 0) return CQ_OK;
+    a.bpw = blocks_per_workgroup(blocks);
+    int wg = 0;
+    for (int k = 0; k < a.njobs; ++k) {
+        a.wg0[k] = wg;
+        wg += (a.jobs[k].nblk + a.bpw - 1) / a.bpw;
+    }
+    a.tb = kLutTile;
+    a.groups_max = groups_max;
+    const size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, groups_max, a.tb);
+    for (int r0 = 0; r0 < rows; r0 += 65535) {
+        LutLaunch b = a;
+        const int nr = std::min(65535, rows - r0);
+        for (int k = 0; k < b.njobs; ++k) {
+            b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
+            b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
+        }
+        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, lut_waves(groups_max), wg, nr, lds, stream), "lut launch");
+    }
+    for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
+    return CQ_OK;
+}
+
 // Launches the product of up to kMaxMatrices views sharing their tables.
 int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
     const CqStore &s0 = *ms[0]->st;
     const int mode = uses_lut(ms[0]) ? kModeLut : kModeExact;
+    if (mode == kModeLut && lut_fits(s0) && n <= kKernargJobs) return run_lut(ms, n, dsts, x, rows, stream);
     int rc = check_geometry(s0, mode);
     if (rc) return rc;
     ProdArgs a;
@@ -520,6 +596,108 @@ int cq_row(const cq_matrix *m, float *dst, size_t dst_len, int r) {
     HIP_TRY(hipStreamSynchronize(t_stage.stream), "sync");
     return CQ_OK;
 }
+
+// ---- batch plans: many independent products in few launches -----------------
+
+}  // extern "C"
+
+struct cq_batch {
+    struct Launch {
+        int bits, gb, waves, grid;
+        size_t lds;
+        LutLaunch args;
+    };
+    std::vector<Launch> launches;
+    std::vector<void *> dev_mem;
+    std::vector<std::shared_ptr<CqStore>> keep;  // storage stays alive with the plan
+    ~cq_batch() {
+        for (void *p : dev_mem) (void)hipFree(p);
+    }
+};
+
+extern "C" {
+
+int cq_batch_new(int n, cq_matrix *const *ms, float *const *ys, const float *const *xs, const int *rows,
+                 cq_batch **plan) {
+    if (!plan || n < 0 || (n > 0 && (!ms || !ys || !xs || !rows))) return fail(CQ_ERR_MISUSE, "cq: batch of %d", n);
+    *plan = nullptr;
+    auto b = std::make_unique<cq_batch>();
+    // Jobs by kernel geometry (bits, group bytes): one launch each.
+    std::vector<std::pair<std::pair<int, int>, std::vector<int>>> classes;
+    for (int k = 0; k < n; ++k) {
+        const cq_matrix *m = ms[k];
+        if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix in batch");
+        if (rows[k] < 0) return fail(CQ_ERR_MISUSE, "cq: batch job %d of %d rows", k, rows[k]);
+        if (!uses_lut(m) || !lut_fits(*m->st))
+            return fail(CQ_ERR_UNSUPPORTED, "cq: batch job %d needs the %s kernel; batches run the lut kernel", k,
+                        cq_kernel_name(m));
+        if (m->out == 0 || rows[k] == 0) continue;
+        const std::pair<int, int> key{m->st->width, m->st->group_bytes};
+        auto it = std::find_if(classes.begin(), classes.end(), [&](auto &c) { return c.first == key; });
+        if (it == classes.end()) {
+            classes.push_back({key, {}});
+            it = classes.end() - 1;
+        }
+        it->second.push_back(k);
+        b->keep.push_back(m->st);
+    }
+    for (auto &cls : classes) {
+        std::vector<JobDesc> jobs;
+        std::vector<WorkUnit> units;
+        long long blocks = 0;
+        int groups_max = 0;
+        for (int k : cls.second) blocks += static_cast<long long>((ms[k]->row0 + ms[k]->out + 63) / 64 - ms[k]->row0 / 64) * rows[k];
+        const int bpw = blocks_per_workgroup(blocks);
+        for (int k : cls.second) {
+            JobDesc j;
+            fill_job(j, ms[k], xs[k], ys[k], rows[k]);
+            groups_max = std::max(groups_max, j.groups);
+            const int ji = static_cast<int>(jobs.size());
+            jobs.push_back(j);
+            for (int act = 0; act < rows[k]; ++act)
+                for (int blk = 0; blk < j.nblk; blk += bpw) units.push_back({ji, blk, std::min(bpw, j.nblk - blk), act});
+        }
+        void *dj = nullptr, *du = nullptr;
+        HIP_TRY(hipMalloc(&dj, align256(jobs.size() * sizeof(JobDesc))), "hipMalloc batch jobs");
+        b->dev_mem.push_back(dj);
+        HIP_TRY(hipMalloc(&du, align256(units.size() * sizeof(WorkUnit))), "hipMalloc batch units");
+        b->dev_mem.push_back(du);
+        HIP_TRY(hipMemcpy(dj, jobs.data(), jobs.size() * sizeof(JobDesc), hipMemcpyHostToDevice), "upload jobs");
+        HIP_TRY(hipMemcpy(du, units.data(), units.size() * sizeof(WorkUnit), hipMemcpyHostToDevice), "upload units");
+        cq_batch::Launch L;
+        std::memset(&L.args, 0, sizeof L.args);
+        L.bits = cls.first.first;
+        L.gb = cls.first.second;
+        L.waves = lut_waves(groups_max);
+        L.args.djobs = static_cast<const JobDesc *>(dj);
+        L.args.dunits = static_cast<const WorkUnit *>(du);
+        L.args.tb = kLutTile;
+        L.args.groups_max = groups_max;
+        L.lds = lut_lds_bytes(L.bits, L.gb, groups_max, kLutTile);
+        L.grid = static_cast<int>(units.size());
+        b->launches.push_back(L);
+    }
+    for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
+    *plan = b.release();
+    return CQ_OK;
+}
+
+int cq_batch_run(const cq_batch *plan, void *stream) {
+    if (!plan) return fail(CQ_ERR_MISUSE, "cq: nil batch");
+    for (const auto &L : plan->launches)
+        for (int g0 = 0; g0 < L.grid; g0 += 1 << 30) {
+            LutLaunch a = L.args;
+            a.dunits += g0;
+            HIP_TRY(launch_lut(a, L.bits, L.gb, L.waves, std::min(L.grid - g0, 1 << 30), 1, L.lds,
+                               static_cast<hipStream_t>(stream)),
+                    "batch launch");
+        }
+    return CQ_OK;
+}
+
+int cq_batch_launches(const cq_batch *plan) { return plan ? static_cast<int>(plan->launches.size()) : 0; }
+
+void cq_batch_free(cq_batch *plan) { delete plan; }
 
 // ---- int8 KV -----------------------------------------------------------------
 

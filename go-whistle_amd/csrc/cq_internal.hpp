@@ -58,6 +58,48 @@ hipError_t launch_product(const ProdArgs &a, int bits, int group_bytes, int mode
 // LDS bytes per group of a chunk, and the fixed part, for choosing gc.
 size_t product_lds_bytes(int bits, int group_bytes, int mode, int gc, int tb);
 
+// ---- the lut kernel (lut_kernels.hip) ----
+
+// One product job: a matrix view, its activations and its output.
+struct JobDesc {
+    const uint8_t *idx;
+    const uint16_t *norm;
+    const float *x;        // activations, x_stride floats apart
+    float *y;              // outputs, y_stride floats apart
+    long long x_stride, y_stride;
+    int row0, out;         // view: root rows [row0, row0 + out)
+    int blk0, nblk;        // first 64-row block of the view and the blocks covering it
+    int in, groups, units; // geometry; units = row bytes / unit bytes
+    int rows;              // activations
+    float cb[16];
+    float cb_max, lut_step;
+};
+
+// A workgroup's share of a job: blocks [blk, blk + nb) (counted from the
+// job's blk0) for activations [act, act + nact).
+struct WorkUnit {
+    int job, blk, nb, act;
+};
+
+constexpr int kKernargJobs = 8;
+
+struct LutLaunch {
+    JobDesc jobs[kKernargJobs];  // kernel-argument jobs (when dunits is null)
+    int njobs;
+    int bpw;                     // kernel-argument path: blocks per workgroup
+    int wg0[kKernargJobs];       // kernel-argument path: first workgroup of each job
+    const JobDesc *djobs;        // device path: job table
+    const WorkUnit *dunits;      //              one unit per workgroup
+    int tb;                      // blocks per tile: rows folded per barrier pair
+    int groups_max;              // LDS sizing: most groups of any job
+};
+
+size_t lut_lds_bytes(int bits, int group_bytes, int groups_max, int tb);
+// grid_y = activations on the kernel-argument path, 1 on the device path.
+hipError_t launch_lut(const LutLaunch &a, int bits, int group_bytes, int waves, int grid_x, int grid_y, size_t lds,
+                      hipStream_t stream);
+bool lut_geometry_supported(int bits, int group_bytes);
+
 struct RowArgs {
     const uint8_t *idx;
     const uint16_t *norm;

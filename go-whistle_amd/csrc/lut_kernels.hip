@@ -1,0 +1,329 @@
+// gfx950 lut kernel: go-whistle's default CQ product (internal/cq/lut.go),
+// bit for bit, for one or many jobs per launch.
+//
+// Per activation group (lut.go:158-178, 235-282): the plain FWHT of the
+// group, the bound M (cbMax * max|x̂|, or * max(|x̂_2q| + |x̂_2q+1|) for two
+// bits), the integer tables v = RNE(entry * 8191/M) and the step M *
+// lutStep. Per row and group (lut.go:289-313): the exact int32 sum of the
+// looked-up v over the group's index bytes, then y += float32(sum) * (norm *
+// step) in group order from y = 0. Every float operation is the
+// reference's, unfused (-ffp-contract=off) and in its order; the integer
+// sums are exact in any order. The int16 tables hold v itself: the
+// reference's two byte planes (a VPSHUFB/TBL artefact) sum to the same
+// integers (lut.go:16-27).
+//
+// Work split. A workgroup of W wavefronts owns one activation of a range of
+// 64-row blocks of one job.
+//  1. Wavefront w rotates groups w, w+W, ... in registers (a group of G
+//     values is G/64 registers per lane; butterflies below 64 exchange lanes
+//     with shuffles, the others stay in a lane), reduces M across the
+//     wavefront and writes the group's tables (NT tables of 16 int16) to
+//     LDS. Meanwhile the wavefront's first index loads are in flight.
+//  2. After one barrier the (group, block) items of each tile of blocks go
+//     round-robin to the wavefronts. An item is 64 rows' index bytes of one
+//     group: each lane streams its row's bytes with 16-byte loads (a
+//     wavefront load is 1 KiB contiguous in the device layout), double
+//     buffered across items, and looks each nibble up in the LDS tables; all
+//     lanes read the same 16-entry table at once, so the lookups are free of
+//     bank conflicts. The int32 sums meet in LDS.
+//  3. The thread that owns a row folds its groups into y in group order.
+#include "cq_internal.hpp"
+
+#include <hip/hip_fp16.h>
+
+namespace cqhip {
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int BITS, int GB>
+struct LutGeo {
+    static constexpr int G = GB * 8 / BITS;      // weights per group
+    static constexpr int U = GB < 16 ? GB : 16;  // index bytes per lane load
+    static constexpr int UPG = GB / U;           // loads per group
+    static constexpr int NT = 2 * GB;            // 16-entry tables per group
+    static constexpr int E = G >= 64 ? G / 64 : 1;  // rotated values per lane
+};
+
+template <int U>
+__device__ __forceinline__ void load_unit(const uint8_t *p, uint32_t (&w)[4]) {
+    if constexpr (U == 16) {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (U == 8) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        w[0] = v.x; w[1] = v.y; w[2] = 0; w[3] = 0;
+    } else if constexpr (U == 4) {
+        w[0] = *reinterpret_cast<const uint32_t *>(p); w[1] = 0; w[2] = 0; w[3] = 0;
+    } else if constexpr (U == 2) {
+        w[0] = *reinterpret_cast<const uint16_t *>(p); w[1] = 0; w[2] = 0; w[3] = 0;
+    } else {
+        w[0] = *p; w[1] = 0; w[2] = 0; w[3] = 0;
+    }
+}
+
+typedef __attribute__((address_space(3))) const short lds_short;
+
+__device__ __forceinline__ int lds_read_i16(uint32_t addr) { return *(lds_short *)addr; }
+
+// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// Sum of the 2*U looked-up entries of one unit: the low nibble of byte k
+// reads table 2k, the high nibble table 2k+1 (lut.go:301-306). base is the
+// LDS address of the unit's first table, 32-byte aligned, so an entry's
+// address is base | 2*nibble, plus the table's immediate offset 32*(2k or
+// 2k+1).
+template <int U>
+__device__ __forceinline__ int lookup_unit(const uint32_t (&w)[4], uint32_t base) {
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t wd = w[k >> 2];
+        const int sh = (k & 3) * 8;
+        const uint32_t lo = sh == 0 ? (wd << 1) & 0x1eu : (wd >> (sh - 1)) & 0x1eu;
+        const uint32_t hi = (wd >> (sh + 3)) & 0x1eu;
+        s += lds_read_i16((base | lo) + 64 * k) + lds_read_i16((base | hi) + 64 * k + 32);
+    }
+    return s;
+}
+
+__device__ __forceinline__ int rne_int(float e) { return static_cast<int>(rintf(e)); }
+
+__device__ __forceinline__ uint32_t pack16(int lo, int hi) {
+    return (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
+}
+
+template <int BITS, int GB, bool DEV>
+__global__ __launch_bounds__(1024) void lut_kernel(LutLaunch a) {
+    using Gm = LutGeo<BITS, GB>;
+    constexpr int G = Gm::G, U = Gm::U, UPG = Gm::UPG, NT = Gm::NT, E = Gm::E;
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int W = blockDim.x >> 6;
+
+    const JobDesc *J;
+    int b0, bc, act;
+    if constexpr (DEV) {
+        const WorkUnit u = a.dunits[blockIdx.x];
+        J = a.djobs + u.job;
+        b0 = u.blk;
+        bc = u.nb;
+        act = u.act;
+    } else {
+        int j = 0;
+#pragma unroll
+        for (int k = 1; k < kKernargJobs; ++k)
+            if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.wg0[k]) j = k;
+        J = &a.jobs[j];
+        b0 = (static_cast<int>(blockIdx.x) - a.wg0[j]) * a.bpw;
+        bc = min(a.bpw, J->nblk - b0);
+        act = blockIdx.y;
+    }
+    const int groups = J->groups, units = J->units, blk0 = J->blk0 + b0;
+    const uint8_t *idx = J->idx;
+    const float *x = J->x + static_cast<long long>(act) * J->x_stride;
+
+    short *tab = reinterpret_cast<short *>(smem);
+    int *part = reinterpret_cast<int *>(smem + static_cast<size_t>(a.groups_max) * NT * 16 * sizeof(short));
+    float *steps = reinterpret_cast<float *>(part + static_cast<size_t>(a.groups_max) * a.tb * 64);
+
+    // Items of a tile: k -> group k / nbt, block k % nbt; wavefront w takes
+    // k = w, w + W, ...
+    auto item_ptr = [&](int t0, int nbt, int k) -> const uint8_t * {
+        const int g = k / nbt, bb = k - (k / nbt) * nbt;
+        return idx + (static_cast<size_t>(blk0 + t0 + bb) * units + static_cast<size_t>(g) * UPG) * 64 * U +
+               static_cast<size_t>(lane) * U;
+    };
+    uint32_t bufA[UPG][4], bufB[UPG][4];
+    auto load_item = [&](const uint8_t *p, uint32_t (&buf)[UPG][4]) {
+#pragma unroll
+        for (int u = 0; u < UPG; ++u) load_unit<U>(p + static_cast<size_t>(u) * 64 * U, buf[u]);
+    };
+    auto compute_item = [&](int nbt, int k, const uint32_t (&buf)[UPG][4]) {
+        const int g = k / nbt, bb = k - (k / nbt) * nbt;
+        const uint32_t tg = lds_addr(tab + static_cast<size_t>(g) * NT * 16);
+        int s = 0;
+#pragma unroll
+        for (int u = 0; u < UPG; ++u) s += lookup_unit<U>(buf[u], tg + u * 2 * U * 16 * 2);
+        part[(g * a.tb + bb) * 64 + lane] = s;
+    };
+
+    // The first tile's first item is in flight while the tables are built.
+    const int nbt0 = min(a.tb, bc);
+    if (w < groups * nbt0) load_item(item_ptr(0, nbt0, w), bufA);
+
+    // 1. Rotation, bound and tables of groups w, w+W, ...
+    for (int g = w; g < groups; g += W) {
+        float v[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = G >= 64 ? e * 64 + lane : lane;
+            const int col = g * G + i;
+            v[e] = (i < G && col < J->in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
+        }
+#pragma unroll
+        for (int h = 1; h < G; h <<= 1) {  // stages h = 1, 2, ..., G/2 (kernel.go:384-393)
+            if (h < 64) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const float p = __shfl_xor(v[e], h);
+                    v[e] = (lane & h) ? p - v[e] : v[e] + p;  // a - b on the upper lane, a + b on the lower
+                }
+            } else {
+                const int d = h / 64;
+#pragma unroll
+                for (int e = 0; e < E; ++e)
+                    if (!(e & d)) {
+                        const float p = v[e], q = v[e + d];
+                        v[e] = p + q;
+                        v[e + d] = p - q;
+                    }
+            }
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            if constexpr (BITS == 4) {
+                mx = fmaxf(mx, fabsf(v[e]));
+            } else {
+                const float p = __shfl_xor(v[e], 1);
+                const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                mx = fmaxf(mx, s2);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        const float m = J->cb_max * mx;
+        const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+        if (lane == 0) steps[g] = m * J->lut_step;
+        short *tg = tab + static_cast<size_t>(g) * NT * 16;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = G >= 64 ? e * 64 + lane : lane;
+            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
+                if (i < G) {
+                    const float av = v[e] * inv;
+                    uint32_t q[8];
+#pragma unroll
+                    for (int c = 0; c < 16; c += 2) q[c / 2] = pack16(rne_int(J->cb[c] * av), rne_int(J->cb[c + 1] * av));
+                    uint4 *dst = reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i) * 16);
+                    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+                    dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+                }
+            } else {  // lutTables2Generic (lut.go:239-258): the even lane writes codes 0-7, the odd 8-15
+                const float p = __shfl_xor(v[e], 1);
+                if (i < G) {
+                    const bool odd = lane & 1;
+                    const float av = (odd ? p : v[e]) * inv, bv = (odd ? v[e] : p) * inv;
+                    const int c0 = odd ? 8 : 0;
+                    uint32_t q[4];
+#pragma unroll
+                    for (int cc = 0; cc < 8; cc += 2) {
+                        const int c = c0 + cc;
+                        const float l0 = J->cb[c & 3] * av, h0 = J->cb[c >> 2] * bv;
+                        const float l1 = J->cb[(c + 1) & 3] * av, h1 = J->cb[(c + 1) >> 2] * bv;
+                        q[cc / 2] = pack16(rne_int(l0 + h0), rne_int(l1 + h1));
+                    }
+                    *reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i / 2) * 16 + c0) = make_uint4(q[0], q[1], q[2], q[3]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2./3. Tiles of tb blocks: lookups, then the fold.
+    for (int t0 = 0; t0 < bc; t0 += a.tb) {
+        const int nbt = min(a.tb, bc - t0);
+        const int items = groups * nbt;
+        if (t0 > 0 && w < items) load_item(item_ptr(t0, nbt, w), bufA);
+        for (int k = w; k < items; k += 2 * W) {
+            const int k1 = k + W, k2 = k + 2 * W;
+            if (k1 < items) load_item(item_ptr(t0, nbt, k1), bufB);
+            compute_item(nbt, k, bufA);
+            if (k1 < items) {
+                if (k2 < items) load_item(item_ptr(t0, nbt, k2), bufA);
+                compute_item(nbt, k1, bufB);
+            }
+        }
+        __syncthreads();
+        for (int t = tid; t < nbt * 64; t += blockDim.x) {
+            const int blk = blk0 + t0 + (t >> 6), ln = t & 63;
+            const int r = blk * 64 + ln;
+            if (r >= J->row0 && r < J->row0 + J->out) {
+                float acc = 0.0f;
+                for (int g = 0; g < groups; ++g) {
+                    const float n = __half2float(__ushort_as_half(J->norm[(static_cast<size_t>(blk) * groups + g) * 64 + ln]));
+                    const float coef = n * steps[g];
+                    const float prod = static_cast<float>(part[(g * a.tb + (t >> 6)) * 64 + ln]) * coef;
+                    acc = acc + prod;
+                }
+                J->y[static_cast<long long>(act) * J->y_stride + (r - J->row0)] = acc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int BITS, int GB>
+hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, hipStream_t s) {
+    const bool dev = a.dunits != nullptr;
+    const void *fn = dev ? reinterpret_cast<const void *>(&lut_kernel<BITS, GB, true>)
+                         : reinterpret_cast<const void *>(&lut_kernel<BITS, GB, false>);
+    static bool attr[2] = {false, false};  // idempotent attribute write; a race is benign
+    if (!attr[dev]) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr[dev] = true;
+    }
+    if (dev)
+        hipLaunchKernelGGL((lut_kernel<BITS, GB, true>), dim3(gx), dim3(64 * waves), lds, s, a);
+    else
+        hipLaunchKernelGGL((lut_kernel<BITS, GB, false>), dim3(gx, gy), dim3(64 * waves), lds, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t lut_lds_bytes(int bits, int group_bytes, int groups_max, int tb) {
+    (void)bits;
+    return static_cast<size_t>(groups_max) * (2 * group_bytes * 16 * sizeof(short) + static_cast<size_t>(tb) * 64 * 4 + 4);
+}
+
+bool lut_geometry_supported(int bits, int gb) {
+    if (bits == 4) return gb == 4 || gb == 8 || gb == 16 || gb == 32 || gb == 64 || gb == 128 || gb == 256;
+    if (bits == 2) return gb == 2 || gb == 4 || gb == 8 || gb == 16 || gb == 32 || gb == 64 || gb == 128 || gb == 256;
+    return false;
+}
+
+hipError_t launch_lut(const LutLaunch &a, int bits, int gb, int waves, int gx, int gy, size_t lds, hipStream_t s) {
+    if (gx <= 0 || gy <= 0) return hipSuccess;
+    if (bits == 4) {
+        switch (gb) {
+            case 4: return launch_t<4, 4>(a, waves, gx, gy, lds, s);
+            case 8: return launch_t<4, 8>(a, waves, gx, gy, lds, s);
+            case 16: return launch_t<4, 16>(a, waves, gx, gy, lds, s);
+            case 32: return launch_t<4, 32>(a, waves, gx, gy, lds, s);
+            case 64: return launch_t<4, 64>(a, waves, gx, gy, lds, s);
+            case 128: return launch_t<4, 128>(a, waves, gx, gy, lds, s);
+            case 256: return launch_t<4, 256>(a, waves, gx, gy, lds, s);
+        }
+    } else if (bits == 2) {
+        switch (gb) {
+            case 2: return launch_t<2, 2>(a, waves, gx, gy, lds, s);
+            case 4: return launch_t<2, 4>(a, waves, gx, gy, lds, s);
+            case 8: return launch_t<2, 8>(a, waves, gx, gy, lds, s);
+            case 16: return launch_t<2, 16>(a, waves, gx, gy, lds, s);
+            case 32: return launch_t<2, 32>(a, waves, gx, gy, lds, s);
+            case 64: return launch_t<2, 64>(a, waves, gx, gy, lds, s);
+            case 128: return launch_t<2, 128>(a, waves, gx, gy, lds, s);
+            case 256: return launch_t<2, 256>(a, waves, gx, gy, lds, s);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace cqhip

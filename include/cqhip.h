@@ -99,6 +99,21 @@ int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream);
  * (internal/decoder/decoder.go:269-275) in one launch. */
 int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n, void *stream);
 
+/* Batch plans (no reference counterpart; the device-resident form of many
+ * independent Matrix.GEMM calls): job k multiplies ms[k] by rows[k]
+ * activations at device xs[k] into device ys[k], as cq_gemm_dev would, bit
+ * for bit. cq_batch_new validates the jobs and uploads a device job table
+ * once; cq_batch_run queues one lut-kernel launch per kernel geometry (index
+ * width and group size) on `stream`, and can be captured in a HIP graph. The
+ * matrices and buffers must outlive the plan's runs. Jobs on Exact views or
+ * on groups the lut kernel does not hold in LDS return CQ_ERR_UNSUPPORTED. */
+typedef struct cq_batch cq_batch;
+int cq_batch_new(int n, cq_matrix *const *ms, float *const *ys, const float *const *xs, const int *rows,
+                 cq_batch **plan);
+int cq_batch_run(const cq_batch *plan, void *stream);
+int cq_batch_launches(const cq_batch *plan);
+void cq_batch_free(cq_batch *plan);
+
 /* ---- int8 KV numerics (internal/needle/int8.go) ------------------------- */
 
 /* QuantizeRows (int8.go:116-121, Append :125-141): x is rows of cols

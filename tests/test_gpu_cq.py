@@ -267,3 +267,56 @@ def test_device_pointer_api_and_row_gather():
     got = dst.cpu().numpy().reshape(5, 512)
     for i, r in enumerate([3, 999, 0, 512, 3]):
         assert same_bits(got[i], o.row(r))
+
+
+def test_batch_plan_matches_gemm():
+    # Many independent products in one plan: every output equals the
+    # matrix's own GEMM bit for bit, including Rows views and several rows.
+    import torch
+
+    g = synth.rng(4242)
+    specs = [(512, 512, 4), (2048, 512, 4), (512, 2048, 4), (700, 512, 2), (130, 2048, 2), (64, 256, 4)]
+    mats, os_, xs, ys, rows = [], [], [], [], []
+    for k, (out, inp, bits) in enumerate(specs):
+        p = synth.random_packed(g, out, inp, 128, bits, sigma=0.05)
+        m = cq.New(p)
+        if k == 3:
+            m = m.Rows(33, 650)
+        r = 1 if k % 2 == 0 else 3
+        mats.append(m)
+        os_.append(orc.OMatrix.new(p) if k != 3 else orc.OMatrix.new(p).rows(33, 650))
+        xs.append(torch.from_numpy(synth.activations(g, r, inp)).cuda())
+        ys.append(torch.full((r * m.Out(),), float("nan"), dtype=torch.float32, device="cuda"))
+        rows.append(r)
+    b = cq.Batch(mats, ys, xs, rows)
+    assert b.launches() == 2  # one per (bits, group) geometry
+    for rep in range(2):
+        b.run()
+        torch.cuda.synchronize()
+        for k in range(len(specs)):
+            want = os_[k].gemm(xs[k].cpu().numpy(), rows[k], orc.LUT)
+            assert same_bits(ys[k].cpu().numpy(), want), (rep, k)
+
+
+def test_batch_plan_in_a_graph():
+    import torch
+
+    g = synth.rng(99)
+    mats = [cq.New(synth.random_packed(g, 1024, 512, 128, 4, sigma=0.05)) for _ in range(3)]
+    xs = [torch.from_numpy(synth.activations(g, 1, 512)).cuda() for _ in range(3)]
+    ys = [torch.zeros(1024, dtype=torch.float32, device="cuda") for _ in range(3)]
+    b = cq.Batch(mats, ys, xs)
+    b.run()
+    torch.cuda.synchronize()
+    want = [y.clone() for y in ys]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        b.run()
+    for rep in range(3):
+        for y in ys:
+            y.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for y, w in zip(ys, want):
+            assert torch.equal(y.view(torch.int32), w.view(torch.int32)), rep
