@@ -12,7 +12,7 @@ resident in HBM before the timed region.
 
 value = weight bytes (packed index + FP16 norms) of all GEMVs of a step /
 step time, in GB/s. The roofline object is the step's dominant launch, the
-4-bit one (HIP events around it on its stream). detail holds per-shape
+4-bit one (HIP events around it on its stream, inside steps). detail holds per-shape
 rates and the rate of one launch per GEMV (a captured graph of 8 * copies
 launches). The cpu_baseline is the C restatement of the reference's lut
 kernel (oracle/), one thread, on a bounded sample of the same sweep.
@@ -86,6 +86,8 @@ def main():
     ap.add_argument("--copies", type=int, default=0, help="device copies of the sweep (0: > 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the step's 4-bit launch and a 512 MiB device copy (for rocprofv3 counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported"}))
@@ -124,10 +126,36 @@ def main():
         for b in BITS:
             plans[b].run()
 
+    if args.roofline_only:
+        src = torch.empty(128 * 2 ** 20, dtype=torch.float32, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            plans[4].run()
+            plans[2].run()
+            dst.copy_(src)  # calibration: 512 MiB read, 512 MiB written
+        torch.cuda.synchronize()
+        print(json.dumps({"roofline_only": True, "launches": args.steps, "copy_bytes": src.numel() * 4,
+                          "algorithmic_bytes_4bit_launch": sum(algorithmic_bytes(packs[k].Out, packs[k].In, 4)
+                                                               for c, k in by_bits[4])}))
+        return
+
     for _ in range(args.warmup):
         step()
     ms = timed(step, args.steps)
     value = sweep_bytes * copies / (ms / 1e3) / 1e9
+
+    # Roofline: the step's 4-bit launch, events around it inside steps.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for e0, e1 in ev:
+        e0.record()
+        plans[4].run()
+        e1.record()
+        plans[2].run()
+    torch.cuda.synchronize()
+    dur_s = sum(e0.elapsed_time(e1) for e0, e1 in ev) / len(ev) / 1e3
+    alg = sum(algorithmic_bytes(packs[k].Out, packs[k].In, 4) for c, k in by_bits[4])
+    achieved = alg / dur_s / 1e9
 
     # One launch per GEMV: a captured graph of the whole sweep.
     def per_launch():
@@ -153,11 +181,6 @@ def main():
         wb = weight_bytes(p.Out, p.In, p.Bits)
         detail[f"{p.Out}x{p.In}_cq{p.Bits}"] = {"us_per_gemv": round(msk * 1e3 / copies, 3),
                                                  "weight_GBps": round(wb * copies / msk / 1e6, 1)}
-
-    # Roofline: the 4-bit launch of the step, timed on its own.
-    dur_s = timed(plans[4].run, max(3, args.steps)) / 1e3
-    alg = sum(algorithmic_bytes(packs[k].Out, packs[k].In, 4) for c, k in by_bits[4])
-    achieved = alg / dur_s / 1e9
 
     line = {
         "metric": "CQ LUT GEMV HBM GB/s (% of peak) + decode tokens/sec, batch 1 and 256",

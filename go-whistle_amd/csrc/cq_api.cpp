@@ -209,19 +209,23 @@ void fill_job(JobDesc &j, const cq_matrix *m, const float *x, float *y, int rows
     j.lut_step = s.lut_step;
 }
 
-constexpr int kLutTile = 4;  // blocks per tile of the lut kernel
+constexpr int kLutTile = 4;     // blocks per tile of the lut kernel
+constexpr int kLutWaves = 4;    // wavefronts per workgroup
+constexpr int kLutChunk = 4;    // groups per LDS chunk
+constexpr int kLutMaxBpw = 16;  // most blocks per workgroup
 
-int lut_waves(int groups_max) { return std::min(8, std::max(4, groups_max)); }
+int lut_chunk(int groups_max) { return std::min(kLutChunk, std::max(1, groups_max)); }
 
-// The lut kernel runs a geometry whose tables for every group fit in LDS.
+// The lut kernel runs a geometry whose chunk of tables fits in LDS.
 bool lut_fits(const CqStore &s) {
     return lut_geometry_supported(s.width, s.group_bytes) &&
-           lut_lds_bytes(s.width, s.group_bytes, s.groups, kLutTile) <= std::min<size_t>(device_info().max_lds, 128 * 1024);
+           lut_lds_bytes(s.width, s.group_bytes, lut_chunk(s.groups), kLutTile, kLutMaxBpw) <=
+               std::min<size_t>(device_info().max_lds, 128 * 1024);
 }
 
 int blocks_per_workgroup(long long blocks) {
     const long long want = 4LL * device_info().cus;
-    return static_cast<int>(std::min<long long>(16, std::max<long long>(1, blocks / want)));
+    return static_cast<int>(std::min<long long>(kLutMaxBpw, std::max<long long>(1, blocks / want)));
 }
 
 // One launch of the lut kernel for up to kKernargJobs views of one geometry
@@ -247,8 +251,9 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
         wg += (a.jobs[k].nblk + a.bpw - 1) / a.bpw;
     }
     a.tb = kLutTile;
-    a.groups_max = groups_max;
-    const size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, groups_max, a.tb);
+    a.gc = lut_chunk(groups_max);
+    a.bpw_max = a.bpw;
+    const size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, a.gc, a.tb, a.bpw);
     for (int r0 = 0; r0 < rows; r0 += 65535) {
         LutLaunch b = a;
         const int nr = std::min(65535, rows - r0);
@@ -256,7 +261,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
             b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
             b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
         }
-        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, lut_waves(groups_max), wg, nr, lds, stream), "lut launch");
+        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, kLutWaves, wg, nr, lds, stream), "lut launch");
     }
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;
@@ -668,12 +673,13 @@ int cq_batch_new(int n, cq_matrix *const *ms, float *const *ys, const float *con
         std::memset(&L.args, 0, sizeof L.args);
         L.bits = cls.first.first;
         L.gb = cls.first.second;
-        L.waves = lut_waves(groups_max);
+        L.waves = kLutWaves;
         L.args.djobs = static_cast<const JobDesc *>(dj);
         L.args.dunits = static_cast<const WorkUnit *>(du);
         L.args.tb = kLutTile;
-        L.args.groups_max = groups_max;
-        L.lds = lut_lds_bytes(L.bits, L.gb, groups_max, kLutTile);
+        L.args.gc = lut_chunk(groups_max);
+        L.args.bpw_max = bpw;
+        L.lds = lut_lds_bytes(L.bits, L.gb, L.args.gc, kLutTile, bpw);
         L.grid = static_cast<int>(units.size());
         b->launches.push_back(L);
     }

@@ -91,10 +91,11 @@ struct LutLaunch {
     const JobDesc *djobs;        // device path: job table
     const WorkUnit *dunits;      //              one unit per workgroup
     int tb;                      // blocks per tile: rows folded per barrier pair
-    int groups_max;              // LDS sizing: most groups of any job
+    int gc;                      // groups per LDS chunk
+    int bpw_max;                 // LDS sizing: most blocks of any workgroup
 };
 
-size_t lut_lds_bytes(int bits, int group_bytes, int groups_max, int tb);
+size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw);
 // grid_y = activations on the kernel-argument path, 1 on the device path.
 hipError_t launch_lut(const LutLaunch &a, int bits, int group_bytes, int waves, int grid_x, int grid_y, size_t lds,
                       hipStream_t stream);

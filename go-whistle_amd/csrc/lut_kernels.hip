@@ -14,11 +14,13 @@
 //
 // Work split. A workgroup of W wavefronts owns one activation of a range of
 // 64-row blocks of one job.
-//  1. Wavefront w rotates groups w, w+W, ... in registers (a group of G
-//     values is G/64 registers per lane; butterflies below 64 exchange lanes
-//     with shuffles, the others stay in a lane), reduces M across the
-//     wavefront and writes the group's tables (NT tables of 16 int16) to
-//     LDS. Meanwhile the wavefront's first index loads are in flight.
+// The groups go in chunks of gc, so LDS holds one chunk's tables whatever
+// the input width; per chunk:
+//  1. Wavefront w rotates the chunk's groups w, w+W, ... in registers (a
+//     group of G values is G/64 registers per lane; butterflies below 64
+//     exchange lanes with shuffles, the others stay in a lane), reduces M
+//     across the wavefront and writes the group's tables (NT tables of 16
+//     int16) to LDS. Meanwhile the chunk's first index loads are in flight.
 //  2. After one barrier the (group, block) items of each tile of blocks go
 //     round-robin to the wavefronts. An item is 64 rows' index bytes of one
 //     group: each lane streams its row's bytes with 16-byte loads (a
@@ -26,7 +28,8 @@
 //     buffered across items, and looks each nibble up in the LDS tables; all
 //     lanes read the same 16-entry table at once, so the lookups are free of
 //     bank conflicts. The int32 sums meet in LDS.
-//  3. The thread that owns a row folds its groups into y in group order.
+//  3. The thread that owns a row folds the chunk's groups into the row's y
+//     (in LDS) in group order; y goes out after the last chunk.
 #include "cq_internal.hpp"
 
 #include <hip/hip_fp16.h>
@@ -64,7 +67,12 @@ __device__ __forceinline__ void load_unit(const uint8_t *p, uint32_t (&w)[4]) {
 
 typedef __attribute__((address_space(3))) const short lds_short;
 
-__device__ __forceinline__ int lds_read_i16(uint32_t addr) { return *(lds_short *)addr; }
+__device__ __forceinline__ int lds_read_i16(uint32_t addr) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wint-to-pointer-cast"
+    return *(lds_short *)addr;  // LDS pointers are 32-bit
+#pragma clang diagnostic pop
+}
 
 // LDS byte address of a shared-memory pointer.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -127,15 +135,19 @@ __global__ __launch_bounds__(1024) void lut_kernel(LutLaunch a) {
     const uint8_t *idx = J->idx;
     const float *x = J->x + static_cast<long long>(act) * J->x_stride;
 
+    // LDS: tables of a chunk of gc groups, the chunk's int32 sums of a tile,
+    // the chunk's steps, and y of the workgroup's rows (folded chunk by chunk).
+    const int gc = a.gc, tb = a.tb;
     short *tab = reinterpret_cast<short *>(smem);
-    int *part = reinterpret_cast<int *>(smem + static_cast<size_t>(a.groups_max) * NT * 16 * sizeof(short));
-    float *steps = reinterpret_cast<float *>(part + static_cast<size_t>(a.groups_max) * a.tb * 64);
+    int *part = reinterpret_cast<int *>(smem + static_cast<size_t>(gc) * NT * 16 * sizeof(short));
+    float *steps = reinterpret_cast<float *>(part + static_cast<size_t>(gc) * tb * 64);
+    float *yacc = steps + gc;
 
-    // Items of a tile: k -> group k / nbt, block k % nbt; wavefront w takes
-    // k = w, w + W, ...
-    auto item_ptr = [&](int t0, int nbt, int k) -> const uint8_t * {
-        const int g = k / nbt, bb = k - (k / nbt) * nbt;
-        return idx + (static_cast<size_t>(blk0 + t0 + bb) * units + static_cast<size_t>(g) * UPG) * 64 * U +
+    // Items of a tile within a chunk: k -> chunk group k / nbt, block
+    // k % nbt; wavefront w takes k = w, w + W, ...
+    auto item_ptr = [&](int g0, int t0, int nbt, int k) -> const uint8_t * {
+        const int gi = k / nbt, bb = k - (k / nbt) * nbt;
+        return idx + (static_cast<size_t>(blk0 + t0 + bb) * units + static_cast<size_t>(g0 + gi) * UPG) * 64 * U +
                static_cast<size_t>(lane) * U;
     };
     uint32_t bufA[UPG][4], bufB[UPG][4];
@@ -144,127 +156,139 @@ __global__ __launch_bounds__(1024) void lut_kernel(LutLaunch a) {
         for (int u = 0; u < UPG; ++u) load_unit<U>(p + static_cast<size_t>(u) * 64 * U, buf[u]);
     };
     auto compute_item = [&](int nbt, int k, const uint32_t (&buf)[UPG][4]) {
-        const int g = k / nbt, bb = k - (k / nbt) * nbt;
-        const uint32_t tg = lds_addr(tab + static_cast<size_t>(g) * NT * 16);
+        const int gi = k / nbt, bb = k - (k / nbt) * nbt;
+        const uint32_t tg = lds_addr(tab + static_cast<size_t>(gi) * NT * 16);
         int s = 0;
 #pragma unroll
         for (int u = 0; u < UPG; ++u) s += lookup_unit<U>(buf[u], tg + u * 2 * U * 16 * 2);
-        part[(g * a.tb + bb) * 64 + lane] = s;
+        part[(gi * tb + bb) * 64 + lane] = s;
     };
 
-    // The first tile's first item is in flight while the tables are built.
-    const int nbt0 = min(a.tb, bc);
-    if (w < groups * nbt0) load_item(item_ptr(0, nbt0, w), bufA);
+    for (int t = tid; t < bc * 64; t += blockDim.x) yacc[t] = 0.0f;
 
-    // 1. Rotation, bound and tables of groups w, w+W, ...
-    for (int g = w; g < groups; g += W) {
-        float v[E];
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int i = G >= 64 ? e * 64 + lane : lane;
-            const int col = g * G + i;
-            v[e] = (i < G && col < J->in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
-        }
-#pragma unroll
-        for (int h = 1; h < G; h <<= 1) {  // stages h = 1, 2, ..., G/2 (kernel.go:384-393)
-            if (h < 64) {
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const float p = __shfl_xor(v[e], h);
-                    v[e] = (lane & h) ? p - v[e] : v[e] + p;  // a - b on the upper lane, a + b on the lower
-                }
-            } else {
-                const int d = h / 64;
-#pragma unroll
-                for (int e = 0; e < E; ++e)
-                    if (!(e & d)) {
-                        const float p = v[e], q = v[e + d];
-                        v[e] = p + q;
-                        v[e + d] = p - q;
-                    }
-            }
-        }
-        float mx = 0.0f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            if constexpr (BITS == 4) {
-                mx = fmaxf(mx, fabsf(v[e]));
-            } else {
-                const float p = __shfl_xor(v[e], 1);
-                const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
-                mx = fmaxf(mx, s2);
-            }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        const float m = J->cb_max * mx;
-        const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
-        if (lane == 0) steps[g] = m * J->lut_step;
-        short *tg = tab + static_cast<size_t>(g) * NT * 16;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int i = G >= 64 ? e * 64 + lane : lane;
-            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
-                if (i < G) {
-                    const float av = v[e] * inv;
-                    uint32_t q[8];
-#pragma unroll
-                    for (int c = 0; c < 16; c += 2) q[c / 2] = pack16(rne_int(J->cb[c] * av), rne_int(J->cb[c + 1] * av));
-                    uint4 *dst = reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i) * 16);
-                    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
-                    dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
-                }
-            } else {  // lutTables2Generic (lut.go:239-258): the even lane writes codes 0-7, the odd 8-15
-                const float p = __shfl_xor(v[e], 1);
-                if (i < G) {
-                    const bool odd = lane & 1;
-                    const float av = (odd ? p : v[e]) * inv, bv = (odd ? v[e] : p) * inv;
-                    const int c0 = odd ? 8 : 0;
-                    uint32_t q[4];
-#pragma unroll
-                    for (int cc = 0; cc < 8; cc += 2) {
-                        const int c = c0 + cc;
-                        const float l0 = J->cb[c & 3] * av, h0 = J->cb[c >> 2] * bv;
-                        const float l1 = J->cb[(c + 1) & 3] * av, h1 = J->cb[(c + 1) >> 2] * bv;
-                        q[cc / 2] = pack16(rne_int(l0 + h0), rne_int(l1 + h1));
-                    }
-                    *reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i / 2) * 16 + c0) = make_uint4(q[0], q[1], q[2], q[3]);
-                }
-            }
-        }
-    }
-    __syncthreads();
+    for (int g0 = 0; g0 < groups; g0 += gc) {
+        const int gch = min(gc, groups - g0);
+        // The chunk's first item is in flight while its tables are built.
+        const int nbt0 = min(tb, bc);
+        if (w < gch * nbt0) load_item(item_ptr(g0, 0, nbt0, w), bufA);
 
-    // 2./3. Tiles of tb blocks: lookups, then the fold.
-    for (int t0 = 0; t0 < bc; t0 += a.tb) {
-        const int nbt = min(a.tb, bc - t0);
-        const int items = groups * nbt;
-        if (t0 > 0 && w < items) load_item(item_ptr(t0, nbt, w), bufA);
-        for (int k = w; k < items; k += 2 * W) {
-            const int k1 = k + W, k2 = k + 2 * W;
-            if (k1 < items) load_item(item_ptr(t0, nbt, k1), bufB);
-            compute_item(nbt, k, bufA);
-            if (k1 < items) {
-                if (k2 < items) load_item(item_ptr(t0, nbt, k2), bufA);
-                compute_item(nbt, k1, bufB);
+        // 1. Rotation, bound and tables of the chunk's groups w, w+W, ...
+        for (int gi = w; gi < gch; gi += W) {
+            const int g = g0 + gi;
+            float v[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int i = G >= 64 ? e * 64 + lane : lane;
+                const int col = g * G + i;
+                v[e] = (i < G && col < J->in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
+            }
+#pragma unroll
+            for (int h = 1; h < G; h <<= 1) {  // stages h = 1, 2, ..., G/2 (kernel.go:384-393)
+                if (h < 64) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        const float p = __shfl_xor(v[e], h);
+                        v[e] = (lane & h) ? p - v[e] : v[e] + p;  // a - b on the upper lane, a + b on the lower
+                    }
+                } else {
+                    const int d = h / 64;
+#pragma unroll
+                    for (int e = 0; e < E; ++e)
+                        if (!(e & d)) {
+                            const float p = v[e], q = v[e + d];
+                            v[e] = p + q;
+                            v[e + d] = p - q;
+                        }
+                }
+            }
+            float mx = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if constexpr (BITS == 4) {
+                    mx = fmaxf(mx, fabsf(v[e]));
+                } else {
+                    const float p = __shfl_xor(v[e], 1);
+                    const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                    mx = fmaxf(mx, s2);
+                }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float m = J->cb_max * mx;
+            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+            if (lane == 0) steps[gi] = m * J->lut_step;
+            short *tg = tab + static_cast<size_t>(gi) * NT * 16;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int i = G >= 64 ? e * 64 + lane : lane;
+                if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
+                    if (i < G) {
+                        const float av = v[e] * inv;
+                        uint32_t q[8];
+#pragma unroll
+                        for (int c = 0; c < 16; c += 2)
+                            q[c / 2] = pack16(rne_int(J->cb[c] * av), rne_int(J->cb[c + 1] * av));
+                        uint4 *dst = reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i) * 16);
+                        dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+                        dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+                    }
+                } else {  // lutTables2Generic (lut.go:239-258): the even lane writes codes 0-7, the odd 8-15
+                    const float p = __shfl_xor(v[e], 1);
+                    if (i < G) {
+                        const bool odd = lane & 1;
+                        const float av = (odd ? p : v[e]) * inv, bv = (odd ? v[e] : p) * inv;
+                        const int c0 = odd ? 8 : 0;
+                        uint32_t q[4];
+#pragma unroll
+                        for (int cc = 0; cc < 8; cc += 2) {
+                            const int c = c0 + cc;
+                            const float l0 = J->cb[c & 3] * av, h0 = J->cb[c >> 2] * bv;
+                            const float l1 = J->cb[(c + 1) & 3] * av, h1 = J->cb[(c + 1) >> 2] * bv;
+                            q[cc / 2] = pack16(rne_int(l0 + h0), rne_int(l1 + h1));
+                        }
+                        *reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i / 2) * 16 + c0) =
+                            make_uint4(q[0], q[1], q[2], q[3]);
+                    }
+                }
             }
         }
         __syncthreads();
-        for (int t = tid; t < nbt * 64; t += blockDim.x) {
-            const int blk = blk0 + t0 + (t >> 6), ln = t & 63;
-            const int r = blk * 64 + ln;
-            if (r >= J->row0 && r < J->row0 + J->out) {
-                float acc = 0.0f;
-                for (int g = 0; g < groups; ++g) {
-                    const float n = __half2float(__ushort_as_half(J->norm[(static_cast<size_t>(blk) * groups + g) * 64 + ln]));
-                    const float coef = n * steps[g];
-                    const float prod = static_cast<float>(part[(g * a.tb + (t >> 6)) * 64 + ln]) * coef;
+
+        // 2./3. Tiles of tb blocks: lookups, then the chunk's groups folded
+        // into y in group order.
+        for (int t0 = 0; t0 < bc; t0 += tb) {
+            const int nbt = min(tb, bc - t0);
+            const int items = gch * nbt;
+            if (t0 > 0 && w < items) load_item(item_ptr(g0, t0, nbt, w), bufA);
+            for (int k = w; k < items; k += 2 * W) {
+                const int k1 = k + W, k2 = k + 2 * W;
+                if (k1 < items) load_item(item_ptr(g0, t0, nbt, k1), bufB);
+                compute_item(nbt, k, bufA);
+                if (k1 < items) {
+                    if (k2 < items) load_item(item_ptr(g0, t0, nbt, k2), bufA);
+                    compute_item(nbt, k1, bufB);
+                }
+            }
+            __syncthreads();
+            for (int t = tid; t < nbt * 64; t += blockDim.x) {
+                const int blk = blk0 + t0 + (t >> 6), ln = t & 63;
+                float acc = yacc[t0 * 64 + t];
+                for (int gi = 0; gi < gch; ++gi) {
+                    const float n =
+                        __half2float(__ushort_as_half(J->norm[(static_cast<size_t>(blk) * groups + g0 + gi) * 64 + ln]));
+                    const float coef = n * steps[gi];
+                    const float prod = static_cast<float>(part[(gi * tb + (t >> 6)) * 64 + ln]) * coef;
                     acc = acc + prod;
                 }
-                J->y[static_cast<long long>(act) * J->y_stride + (r - J->row0)] = acc;
+                yacc[t0 * 64 + t] = acc;
             }
+            __syncthreads();
         }
-        __syncthreads();
+    }
+
+    for (int t = tid; t < bc * 64; t += blockDim.x) {
+        const int r = blk0 * 64 + t;
+        if (r >= J->row0 && r < J->row0 + J->out) J->y[static_cast<long long>(act) * J->y_stride + (r - J->row0)] = yacc[t];
     }
 }
 
@@ -288,9 +312,10 @@ hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, h
 
 }  // namespace
 
-size_t lut_lds_bytes(int bits, int group_bytes, int groups_max, int tb) {
+size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw) {
     (void)bits;
-    return static_cast<size_t>(groups_max) * (2 * group_bytes * 16 * sizeof(short) + static_cast<size_t>(tb) * 64 * 4 + 4);
+    return static_cast<size_t>(gc) * (2 * group_bytes * 16 * sizeof(short) + static_cast<size_t>(tb) * 64 * 4 + 4) +
+           static_cast<size_t>(bpw) * 64 * 4;
 }
 
 bool lut_geometry_supported(int bits, int gb) {
