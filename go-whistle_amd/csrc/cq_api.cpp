@@ -649,19 +649,34 @@ int cq_batch_new(int n, cq_matrix *const *ms, float *const *ys, const float *con
     for (auto &cls : classes) {
         std::vector<JobDesc> jobs;
         std::vector<WorkUnit> units;
-        long long blocks = 0;
-        int groups_max = 0;
-        for (int k : cls.second) blocks += static_cast<long long>((ms[k]->row0 + ms[k]->out + 63) / 64 - ms[k]->row0 / 64) * rows[k];
-        const int bpw = blocks_per_workgroup(blocks);
+        // Workgroups get about equal index bytes: total / (4 per CU), in whole
+        // 64-row blocks (at most kLutMaxBpw), heaviest units first.
+        long long bytes = 0;
+        for (int k : cls.second)
+            bytes += static_cast<long long>((ms[k]->row0 + ms[k]->out + 63) / 64 - ms[k]->row0 / 64) * 64 *
+                     ms[k]->st->row_bytes * rows[k];
+        const long long target = std::max<long long>(1, bytes / (4LL * device_info().cus));
+        int bpw = 1;
+        std::vector<std::pair<long long, WorkUnit>> weighted;
         for (int k : cls.second) {
             JobDesc j;
             fill_job(j, ms[k], xs[k], ys[k], rows[k]);
-            groups_max = std::max(groups_max, j.groups);
+            const long long blk_bytes = 64LL * ms[k]->st->row_bytes;
+            const int b = static_cast<int>(std::min<long long>(kLutMaxBpw, std::max<long long>(1, target / blk_bytes)));
+            bpw = std::max(bpw, b);
             const int ji = static_cast<int>(jobs.size());
             jobs.push_back(j);
             for (int act = 0; act < rows[k]; ++act)
-                for (int blk = 0; blk < j.nblk; blk += bpw) units.push_back({ji, blk, std::min(bpw, j.nblk - blk), act});
+                for (int blk = 0; blk < j.nblk; blk += b) {
+                    const int nb = std::min(b, j.nblk - blk);
+                    weighted.push_back({nb * blk_bytes, WorkUnit{ji, blk, nb, act}});
+                }
         }
+        std::stable_sort(weighted.begin(), weighted.end(),
+                         [](const auto &p, const auto &q) { return p.first > q.first; });
+        for (auto &wu : weighted) units.push_back(wu.second);
+        int groups_max = 0;
+        for (auto &j : jobs) groups_max = std::max(groups_max, j.groups);
         void *dj = nullptr, *du = nullptr;
         HIP_TRY(hipMalloc(&dj, align256(jobs.size() * sizeof(JobDesc))), "hipMalloc batch jobs");
         b->dev_mem.push_back(dj);

@@ -84,16 +84,49 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // LDS address of the unit's first table, 32-byte aligned, so an entry's
 // address is base | 2*nibble, plus the table's immediate offset 32*(2k or
 // 2k+1).
+// base | byte B of t, in one VALU op (an SDWA byte select).
+template <int B>
+__device__ __forceinline__ uint32_t or_byte(uint32_t base, uint32_t t) {
+    uint32_t r;
+    if constexpr (B == 0)
+        asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(r) : "v"(base), "v"(t));
+    else if constexpr (B == 1)
+        asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(r) : "v"(base), "v"(t));
+    else if constexpr (B == 2)
+        asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(r) : "v"(base), "v"(t));
+    else
+        asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(r) : "v"(base), "v"(t));
+    return r;
+}
+
+template <int U, int Q>
+__device__ __forceinline__ int lookup_word(uint32_t wd, uint32_t base) {
+    // 2 * low and 2 * high nibble of each of the word's bytes: each entry
+    // address is then one byte-select OR with the table base.
+    const uint32_t te = (wd << 1) & 0x1e1e1e1eu, to = (wd >> 3) & 0x1e1e1e1eu;
+    int s = 0;
+    constexpr int k0 = 4 * Q;
+    s += lds_read_i16(or_byte<0>(base, te) + 64 * (k0 + 0)) + lds_read_i16(or_byte<0>(base, to) + 64 * (k0 + 0) + 32);
+    if constexpr (k0 + 1 < U)
+        s += lds_read_i16(or_byte<1>(base, te) + 64 * (k0 + 1)) + lds_read_i16(or_byte<1>(base, to) + 64 * (k0 + 1) + 32);
+    if constexpr (k0 + 2 < U)
+        s += lds_read_i16(or_byte<2>(base, te) + 64 * (k0 + 2)) + lds_read_i16(or_byte<2>(base, to) + 64 * (k0 + 2) + 32);
+    if constexpr (k0 + 3 < U)
+        s += lds_read_i16(or_byte<3>(base, te) + 64 * (k0 + 3)) + lds_read_i16(or_byte<3>(base, to) + 64 * (k0 + 3) + 32);
+    return s;
+}
+
 template <int U>
 __device__ __forceinline__ int lookup_unit(const uint32_t (&w)[4], uint32_t base) {
-    int s = 0;
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-        const uint32_t wd = w[k >> 2];
-        const int sh = (k & 3) * 8;
-        const uint32_t lo = sh == 0 ? (wd << 1) & 0x1eu : (wd >> (sh - 1)) & 0x1eu;
-        const uint32_t hi = (wd >> (sh + 3)) & 0x1eu;
-        s += lds_read_i16((base | lo) + 64 * k) + lds_read_i16((base | hi) + 64 * k + 32);
+    int s = lookup_word<U, 0>(w[0], base);
+    if constexpr (U > 4) s += lookup_word<U, 1>(w[1], base);
+    if constexpr (U > 8) {
+        s += lookup_word<U, 2>(w[2], base);
+        s += lookup_word<U, 3>(w[3], base);
     }
     return s;
 }
