@@ -78,6 +78,57 @@ def cpu_baseline(gw, packs, seconds):
                       f"{el:.1f} s"}
 
 
+def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
+    """Greedy decode of the synthetic 8-layer decoder (d 512, 8 heads, FFN
+    2048, vocab 16384, 1500-frame int8 cross memory per stream), 200 tokens
+    at batch 1 and 256: one captured step graph replayed per token."""
+    from go_whistle_amd import decoder as dec
+
+    cfg = dec.DecoderConfig()
+    model = dec.make_model(7, cfg)
+    res = {"model": "synthetic Whistle-shaped decoder: 8 layers, d 512, 8x64 heads, FFN 2048 (CQ2), attention "
+                    "CQ4, tied CQ4 head 16384x512, int8 self/cross KV, 1500 frames", "tokens": tokens}
+    for batch in (1, 256):
+        d = dec.Decoder(model, batch)
+        d.set_memory(7, "numpy" if batch == 1 else "device")
+        first = list(range(1, batch + 1))
+        d.reset(first)
+        g = d.capture()
+        for _ in range(3):
+            g.replay()
+        d.reset(first)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(tokens):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        res[f"batch{batch}"] = {"tokens_per_s": round(batch * tokens / ms * 1e3, 1),
+                                "ms_per_step": round(ms / tokens, 4)}
+        del d, g
+        torch.cuda.empty_cache()
+    if with_cpu:
+        if ROOT not in sys.path:
+            sys.path.insert(0, ROOT)
+        from oracle import decoder_ref
+
+        ref = decoder_ref.RefDecoder(model)
+        ks, vs = zip(*[dec.memory_states(7, cfg, 0, l) for l in range(cfg.layers)])
+        ref.memory(ks, vs)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            n += len(ref.decode(1, 10))
+            el = time.perf_counter() - t0
+            if el >= cpu_seconds:
+                break
+        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"{n} greedy tokens at batch 1 (runs of 10 from position 0), oracle "
+                                         f"decoder, 1 thread, {el:.1f} s"}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -86,6 +137,8 @@ def main():
     ap.add_argument("--copies", type=int, default=0, help="device copies of the sweep (0: > 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-tokens", type=int, default=200)
+    ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the step's 4-bit launch and a 512 MiB device copy (for rocprofv3 counters)")
     args = ap.parse_args()
@@ -207,6 +260,10 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gw, packs, args.cpu_seconds)
+    if not args.no_decode:
+        del plans, mats
+        torch.cuda.empty_cache()
+        line["decode"] = decode_leg(gw, torch, args.decode_tokens, args.cpu_seconds, not args.no_cpu)
     print(json.dumps(line))
 
 

@@ -37,7 +37,7 @@ SIGNATURES = {
     "cq_gemm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "cq_gemms_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p]),
     "cq_row_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
-    "cq_row_gather_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "cq_row_gather_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "cq_batch_new": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p), POINTER(c_int),
                              POINTER(c_void_p)]),
     "cq_batch_run": (c_int, [c_void_p, c_void_p]),
@@ -48,6 +48,13 @@ SIGNATURES = {
     "kv_attend_int8_dev": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p,
                                    c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_longlong, c_longlong, c_void_p,
                                    c_int, c_float, c_int, c_int, c_void_p]),
+    "kv_append_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_longlong, c_longlong, c_void_p,
+                              c_int, c_void_p]),
+    "nd_zcrmsnorm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "nd_rope_dev": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "nd_argmax_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "nd_silu_dev": (c_int, [c_void_p, c_longlong, c_void_p]),
+    "nd_add_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_void_p]),
 }
 
 _lib = None

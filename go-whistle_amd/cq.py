@@ -132,9 +132,9 @@ class Matrix:
     def row_dev(self, dst, r):
         check(lib().cq_row_dev(self._h, c_void_p(dst.data_ptr()), r, _stream()))
 
-    def row_gather_dev(self, dst, rows_i32):
+    def row_gather_dev(self, dst, rows_i32, scale=1.0):
         check(lib().cq_row_gather_dev(self._h, c_void_p(dst.data_ptr()), c_void_p(rows_i32.data_ptr()),
-                                      int(rows_i32.numel()), _stream()))
+                                      int(rows_i32.numel()), float(scale), _stream()))
 
 
 def New(p: Packed) -> Matrix:

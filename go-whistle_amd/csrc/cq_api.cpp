@@ -346,6 +346,7 @@ int row_args(const cq_matrix *m, RowArgs &a) {
     for (int c = 0; c < 16; ++c) a.cb[c] = c < s.ncb ? s.cb[c] : 0.0f;
     a.inv_sqrt = s.inv_sqrt;
     a.nrows = s.out;
+    a.scale = 1.0f;
     if (static_cast<size_t>(s.group) * 4 > device_info().max_lds)
         return fail(CQ_ERR_UNSUPPORTED, "cq: Row of group %d", s.group);
     return CQ_OK;
@@ -574,7 +575,7 @@ int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream) {
     return CQ_OK;
 }
 
-int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n, void *stream) {
+int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n, float scale, void *stream) {
     if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
     if (n < 0) return fail(CQ_ERR_MISUSE, "cq: gather of %d rows", n);
     if (m->row0 != 0) return fail(CQ_ERR_UNSUPPORTED, "cq: row gather on a Rows view");
@@ -584,6 +585,7 @@ int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n
     a.dst = dst;
     a.rows = rows;
     a.n = n;
+    a.scale = scale;
     HIP_TRY(launch_rows(a, static_cast<hipStream_t>(stream)), "row gather launch");
     return CQ_OK;
 }
@@ -772,6 +774,51 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
                  kv_stride, s_stride, spans, nk_max, scale, quant_q, batch};
     HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");
+    return CQ_OK;
+}
+
+// ---- decode-step float blocks -------------------------------------------------
+
+int nd_zcrmsnorm_dev(float *dst, const float *x, const float *gain, int rows, int dim, void *stream) {
+    if (rows < 0 || dim <= 0) return fail(CQ_ERR_MISUSE, "needle: ZCRMSNorm of %d rows of %d", rows, dim);
+    HIP_TRY(launch_zc_rmsnorm(dst, x, gain, rows, dim, static_cast<hipStream_t>(stream)), "norm launch");
+    return CQ_OK;
+}
+
+int nd_rope_dev(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
+                const int32_t *pos, int rows_per_pos, void *stream) {
+    if (rows < 0 || heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || rows_per_pos <= 0)
+        return fail(CQ_ERR_MISUSE, "needle: RoPE of %d rows, %d heads of %d", rows, heads, head_dim);
+    HIP_TRY(launch_rope(x, rows, heads, head_dim, cos_t, sin_t, pos, rows_per_pos, static_cast<hipStream_t>(stream)),
+            "rope launch");
+    return CQ_OK;
+}
+
+int nd_argmax_dev(int32_t *out, const float *v, int rows, int n, void *stream) {
+    if (rows < 0 || n <= 0) return fail(CQ_ERR_MISUSE, "decoder: argmax of %d rows of %d", rows, n);
+    HIP_TRY(launch_argmax(out, v, rows, n, static_cast<hipStream_t>(stream)), "argmax launch");
+    return CQ_OK;
+}
+
+int nd_silu_dev(float *x, long long n, void *stream) {
+    if (n < 0) return fail(CQ_ERR_MISUSE, "needle: SiLU of %lld values", n);
+    HIP_TRY(launch_silu(x, n, static_cast<hipStream_t>(stream)), "silu launch");
+    return CQ_OK;
+}
+
+int nd_add_dev(float *x, const float *y, long long n, void *stream) {
+    if (n < 0) return fail(CQ_ERR_MISUSE, "needle: add of %lld values", n);
+    HIP_TRY(launch_add(x, y, n, static_cast<hipStream_t>(stream)), "add launch");
+    return CQ_OK;
+}
+
+int kv_append_dev(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
+                  long long s_stride, const int32_t *pos, int cap, void *stream) {
+    if (width <= 0 || cols % width != 0)
+        return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);
+    if (batch < 0 || cap < 0) return fail(CQ_ERR_MISUSE, "needle: append of %d streams", batch);
+    HIP_TRY(launch_append(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, static_cast<hipStream_t>(stream)),
+            "append launch");
     return CQ_OK;
 }
 

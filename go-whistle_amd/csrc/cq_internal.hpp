@@ -111,6 +111,7 @@ struct RowArgs {
     int in, group, groups, row_bytes, width, units, unit_bytes;
     float cb[16];
     float inv_sqrt;
+    float scale;           // dst = scale * Row (1 for Row itself)
 };
 hipError_t launch_rows(const RowArgs &a, hipStream_t stream);
 
@@ -132,5 +133,15 @@ struct AttendArgs {
     int batch;
 };
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream);
+
+// decode-step float blocks (step_kernels.hip)
+hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int rows, int dim, hipStream_t s);
+hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
+                       const int32_t *pos, int rows_per_pos, hipStream_t s);
+hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, hipStream_t s);
+hipError_t launch_silu(float *x, long long n, hipStream_t s);
+hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s);
+hipError_t launch_append(int8_t *q, float *sc, const float *x, int batch, int cols, int width, long long q_stride,
+                         long long s_stride, const int32_t *pos, int cap, hipStream_t s);
 
 }  // namespace cqhip

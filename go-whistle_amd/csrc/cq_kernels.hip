@@ -424,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void rows_kernel(RowArgs a) {
     }
     for (int k = threadIdx.x; k < G; k += blockDim.x) {
         const int col = g * G + k;
-        if (col < a.in) dst[col] = buf[k];
+        if (col < a.in) dst[col] = buf[k] * a.scale;  // x1 is exact; the embedding's scale (decoder.go:269-275)
     }
 }
 

@@ -1,0 +1,227 @@
+// gfx950 kernels for the float blocks between the CQ products of a decode
+// step, each bit for bit the reference's arithmetic:
+//   zc_rmsnorm_kernel  ZCRMSNorm.Apply (internal/needle/norm.go:53-66, 84-109):
+//                      mean(x²) in float64 as four partial sums over i mod 4,
+//                      each in order, rounded to float32; rms =
+//                      float32(sqrt(float64(ms + 1e-6))); y = (gain·x) / rms.
+//   rope_kernel        Rope.apply (internal/needle/rope.go:69-81): per head,
+//                      [x1·cos − x2·sin, x2·cos + x1·sin], products rounded.
+//   argmax_kernel      argmax (internal/decoder/greedy.go:181-191): the first
+//                      index of the largest value.
+//   silu_kernel        x·σ(x) with σ from the amd64 exponent kernel's lane
+//                      (exp_amd64.s:84-112) on non-positive arguments: the
+//                      synthetic decoder's FFN activation (no reference
+//                      counterpart; defined so that CPU and GPU agree bit for bit).
+//   add_kernel         x += y (the residual adds, decoder.go / block.go).
+//   append_kernel      Int8Rows.Append (internal/needle/int8.go:125-141) of one
+//                      row per stream at the stream's position.
+#include "cq_internal.hpp"
+
+#include <climits>
+
+namespace cqhip {
+namespace {
+
+__global__ __launch_bounds__(64) void zc_rmsnorm_kernel(float *dst, const float *x, const float *gain, int dim) {
+    const int r = blockIdx.x, lane = threadIdx.x;
+    const float *row = x + static_cast<long long>(r) * dim;
+    float *out = dst + static_cast<long long>(r) * dim;
+    __shared__ double part[4];
+    __shared__ float rms_sh;
+    // meanSquare (norm.go:91-109): s_k over i = k, k+4, ... (the full words
+    // of four), then the tail into s0, then (s0 + s1 + s2 + s3) / n.
+    if (lane < 4) {
+        double s = 0.0;
+        const int full = dim & ~3;
+        for (int i = lane; i < full; i += 4) {
+            const double v = static_cast<double>(row[i]);
+            s = s + v * v;
+        }
+        if (lane == 0)
+            for (int i = full; i < dim; ++i) {
+                const double v = static_cast<double>(row[i]);
+                s = s + v * v;
+            }
+        part[lane] = s;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        const double s = ((part[0] + part[1]) + part[2]) + part[3];
+        const float ms = static_cast<float>(s / static_cast<double>(dim));
+        const float e = ms + 1e-6f;
+        rms_sh = static_cast<float>(sqrt(static_cast<double>(e)));
+    }
+    __syncthreads();
+    const float rms = rms_sh;
+    for (int c = lane; c < dim; c += 64) {
+        const float gx = gain[c] * row[c];
+        out[c] = gx / rms;
+    }
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(float *x, int heads, int head_dim, const float *cos_t,
+                                                   const float *sin_t, const int32_t *pos, int rows_per_pos) {
+    const int r = blockIdx.x;
+    const int half = head_dim / 2;
+    const int p = pos[r / rows_per_pos];
+    const float *cs = cos_t + static_cast<long long>(p) * half, *sn = sin_t + static_cast<long long>(p) * half;
+    float *row = x + static_cast<long long>(r) * heads * head_dim;
+    for (int e = threadIdx.x; e < heads * half; e += blockDim.x) {
+        const int h = e / half, i = e % half;
+        float *xh = row + h * head_dim;
+        const float a = xh[i], b = xh[i + half];
+        const float ac = a * cs[i], bs = b * sn[i], bc = b * cs[i], as = a * sn[i];
+        xh[i] = ac - bs;
+        xh[i + half] = bc + as;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *v, int n) {
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const float *row = v + static_cast<long long>(r) * n;
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int i = tid; i < n; i += blockDim.x) {
+        const float x = row[i];
+        if (bi == INT_MAX || x > best) {  // the first of this thread's values that beats the rest
+            best = x;
+            bi = i;
+        }
+    }
+    __shared__ float sb[256];
+    __shared__ int si[256];
+    sb[tid] = best;
+    si[tid] = bi;
+    __syncthreads();
+    for (int off = blockDim.x / 2; off > 0; off >>= 1) {
+        if (tid < off) {
+            const float ob = sb[tid + off];
+            const int oi = si[tid + off];
+            // larger value wins; on equal values the smaller index (first)
+            if (oi != INT_MAX && (si[tid] == INT_MAX || ob > sb[tid] || (ob == sb[tid] && oi < si[tid]))) {
+                sb[tid] = ob;
+                si[tid] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) out[r] = si[0] == INT_MAX ? 0 : si[0];
+}
+
+// One lane of the amd64 exponent kernel (exp_amd64.s:84-112), for x <= 0.
+__device__ __forceinline__ float exp_lane(float x) {
+    const float log2e = 0x1.715476p+0f, ln2hi = 0x1.63p-1f, ln2lo = -0x1.bd0106p-13f;
+    const float c6 = 0x1.a0d2cep-13f, c5 = 0x1.6e879cp-10f, c4 = 0x1.111210p-7f;
+    const float c3 = 0x1.555382p-5f, c2 = 0x1.555554p-3f, c1 = 0x1p-1f;
+    const float lo = -0x1.5d51ecp+6f;
+    const bool lt = x < lo;
+    const float xc = (x != x) ? x : (lo > x ? lo : x);
+    const float k = rintf(xc * log2e);
+    float r = fmaf(-k, ln2hi, xc);
+    r = fmaf(-k, ln2lo, r);
+    const float r2 = r * r;
+    float p = c6;
+    p = fmaf(p, r, c5);
+    p = fmaf(p, r, c4);
+    p = fmaf(p, r, c3);
+    p = fmaf(p, r, c2);
+    p = fmaf(p, r, c1);
+    float yv = fmaf(p, r2, r);
+    yv = yv + 1.0f;
+    const int ki = (k != k || k >= 2147483648.0f || k < -2147483648.0f) ? INT_MIN : static_cast<int>(k);
+    const float e = __uint_as_float(__float_as_uint(yv) + (static_cast<unsigned>(ki) << 23));
+    return lt ? 0.0f : e;
+}
+
+__global__ __launch_bounds__(256) void silu_kernel(float *x, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    float s;
+    if (v >= 0.0f) {
+        const float e = exp_lane(-v);
+        const float d = 1.0f + e;
+        s = 1.0f / d;
+    } else {
+        const float e = exp_lane(v);
+        const float d = 1.0f + e;
+        s = e / d;
+    }
+    x[i] = v * s;
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float *x, const float *y, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = x[i] + y[i];
+}
+
+// Int8Rows.Append of stream b's row at its position pos[b]: QuantizeRow
+// per chunk of width (int8.go:36-55), one wavefront per chunk.
+__global__ __launch_bounds__(256) void append_kernel(int8_t *q, float *s, const float *x, int cols, int width,
+                                                     long long q_stride, long long s_stride, const int32_t *pos,
+                                                     int cap) {
+    const int b = blockIdx.y, lane = threadIdx.x & 63;
+    const int c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+    const int chunks = cols / width;
+    const int p = pos[b];
+    if (c >= chunks || p < 0 || p >= cap) return;
+    const float *xc = x + static_cast<long long>(b) * cols + static_cast<long long>(c) * width;
+    float m = 0.0f;
+    for (int i = lane; i < width; i += 64) m = fmaxf(m, fabsf(xc[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+    int8_t *qc = q + b * q_stride + static_cast<long long>(p) * cols + static_cast<long long>(c) * width;
+    for (int i = lane; i < width; i += 64) {
+        float r = rintf(xc[i] / sc);
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        qc[i] = static_cast<int8_t>(static_cast<int>(r));
+    }
+    if (lane == 0) s[b * s_stride + static_cast<long long>(p) * chunks + c] = sc;
+}
+
+unsigned blocks_for(long long n, int t) { return static_cast<unsigned>((n + t - 1) / t); }
+
+}  // namespace
+
+hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int rows, int dim, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(zc_rmsnorm_kernel, dim3(rows), dim3(64), 0, s, dst, x, gain, dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
+                       const int32_t *pos, int rows_per_pos, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3(rows), dim3(256), 0, s, x, heads, head_dim, cos_t, sin_t, pos, rows_per_pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, out, v, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu(float *x, long long n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(silu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_append(int8_t *q, float *sc, const float *x, int batch, int cols, int width, long long q_stride,
+                         long long s_stride, const int32_t *pos, int cap, hipStream_t s) {
+    if (batch <= 0) return hipSuccess;
+    const int chunks = cols / width;
+    hipLaunchKernelGGL(append_kernel, dim3(blocks_for(chunks, 4), batch), dim3(256), 0, s, q, sc, x, cols, width,
+                       q_stride, s_stride, pos, cap);
+    return hipGetLastError();
+}
+
+}  // namespace cqhip

@@ -1,0 +1,303 @@
+"""A synthetic Whistle-shaped decoder on the device, for greedy decoding.
+
+The configuration is the one the benchmark names: 8 layers, d_model 512,
+8 heads of 64, FFN 2048, vocabulary 16384, cross-attention over 1500
+frames, an int8 self- and cross-KV cache, CQ-packed linears (4-bit
+attention, 2-bit FFN) and a 4-bit embedding tied to the head. Whistle's
+real decoder (internal/decoder) has mHC, engram and a float Monarch MLP;
+this one keeps the CQ, int8 and float pieces of its decode step that the
+quantized path serves:
+
+  x = E.Row(token) * scale                          decoder.go:269-275
+  per layer:
+    h = ZCRMSNorm(x); q, k, v = GEMMs(Wq, Wk, Wv; h)  norm.go, kernel.go:134
+    RoPE(q), RoPE(k) at the position                 rope.go:69-81
+    append int8 k, v; a = AttendInt8(q, 0..pos)      int8.go:125-141, 208-272
+    x += Wo a
+    h = ZCRMSNorm(x); a = AttendInt8(Wcq h, memory); x += Wco a
+    h = ZCRMSNorm(x); x += W2 SiLU(W1 h)
+  logits = E ZCRMSNorm(x); token = argmax           decoder.go:507-523, greedy.go:181-191
+
+with the int8 query (Int8.Act) and amd64's softmax exponent. Every step is
+bit for bit the same arithmetic as the C restatement in oracle/, so the
+greedy tokens match exactly. The cross memory of each stream is its own
+1500 x 512 keys and values drawn N(0, 1) and quantised per head on the
+device (the projected encoder states; their projection is the batched
+encoder workload, not part of the decode step).
+
+All state lives on the device; step() queues one token's launches on
+torch's current stream and can be captured in a HIP graph.
+"""
+
+from dataclasses import dataclass, field
+import math
+
+import numpy as np
+
+from . import cq, needle, synth
+from ._lib import check, lib
+
+
+@dataclass
+class DecoderConfig:
+    vocab: int = 16384
+    dim: int = 512
+    heads: int = 8
+    head_dim: int = 64
+    ffn: int = 2048
+    layers: int = 8
+    frames: int = 1500
+    max_pos: int = 256
+    attn_bits: int = 4
+    ffn_bits: int = 2
+    group: int = 128
+    theta: float = 1e5
+
+
+LAYER_MATS = ("wq", "wk", "wv", "wo", "wcq", "wco", "w1", "w2")
+
+
+@dataclass
+class Model:
+    cfg: DecoderConfig
+    emb: cq.Packed
+    layers: list  # per layer: dict name -> Packed
+    gains: np.ndarray  # [layers*3 + 1, dim]: attn, cross, ffn per layer, then final
+    rope_cos: np.ndarray
+    rope_sin: np.ndarray
+    scale: np.float32 = field(default=np.float32(0))
+
+
+def _share(p, cb):
+    p.Codebook = cb
+    return p
+
+
+def rope_tables(head_dim, n, theta):
+    """NewRope (internal/needle/rope.go:17-44): float32 frequencies, float64
+    cos/sin of float32 angles, rounded to float32."""
+    half = head_dim // 2
+    freqs = np.zeros(half, np.float32)
+    for i in range(half):
+        e = np.float32(2 * i) / np.float32(head_dim)
+        freqs[i] = np.float32(1) / np.float32(math.pow(theta, float(e)))
+    cos = np.zeros((n, half), np.float32)
+    sin = np.zeros((n, half), np.float32)
+    for t in range(n):
+        ang = (np.float32(t) * freqs).astype(np.float64)
+        cos[t] = np.cos(ang).astype(np.float32)
+        sin[t] = np.sin(ang).astype(np.float32)
+    return cos, sin
+
+
+def make_model(seed, cfg=DecoderConfig()):
+    """Seeded weights: one zero-mean codebook per index width (as a .cact file holds),
+    uniform indices, FP16 norms 2^-3..2^1 (the embedding's 0.5..0.56, so
+    that no row outscores the others for every input), gains 1 + N(0, 0.1)."""
+    g = synth.rng(seed)
+
+    def symmetric(n):  # N(0, 0.05) magnitudes mirrored: a zero-mean codebook, as Lloyd-Max levels are
+        m = np.abs(g.standard_normal(n // 2) * 0.05).astype(np.float32)
+        return np.sort(np.concatenate([-m, m])).astype(np.float32)
+
+    cb4, cb2 = symmetric(16), symmetric(4)
+
+    def packed(out, inp, bits, exps=(12, 16), mants=1024):
+        p = synth.random_packed(g, out, inp, cfg.group, bits, sigma=0.05)
+        groups = (inp + cfg.group - 1) // cfg.group
+        exp = g.integers(exps[0], exps[1], size=out * groups).astype(np.uint16)
+        man = g.integers(0, mants, size=out * groups).astype(np.uint16)
+        p.Norms = ((exp << 10) | man).astype("<u2").view(np.uint8)
+        return _share(p, cb4 if bits == 4 else cb2)
+
+    d, f = cfg.dim, cfg.ffn
+    emb = packed(cfg.vocab, d, cfg.attn_bits, exps=(14, 15), mants=128)  # rows of about equal norm
+    layers = []
+    for _ in range(cfg.layers):
+        layers.append({"wq": packed(d, d, cfg.attn_bits), "wk": packed(d, d, cfg.attn_bits),
+                       "wv": packed(d, d, cfg.attn_bits), "wo": packed(d, d, cfg.attn_bits),
+                       "wcq": packed(d, d, cfg.attn_bits), "wco": packed(d, d, cfg.attn_bits),
+                       "w1": packed(f, d, cfg.ffn_bits), "w2": packed(d, f, cfg.ffn_bits)})
+    scales = (g.standard_normal((cfg.layers * 3 + 1, d)) * 0.1).astype(np.float32)
+    gains = (np.float32(1) + scales).astype(np.float32)  # NewZCRMSNorm (norm.go:22-30)
+    cos, sin = rope_tables(cfg.head_dim, cfg.max_pos, cfg.theta)
+    # The unscaled input (Whistle's InputScale off, decoder.go:322-326): with
+    # sqrt(d), a random tied embedding makes every token its own argmax.
+    return Model(cfg=cfg, emb=emb, layers=layers, gains=gains, rope_cos=cos, rope_sin=sin, scale=np.float32(1))
+
+
+def memory_states(seed, cfg, stream, layer):
+    """One stream's cross keys and values for one layer, N(0, 1), [frames, dim]."""
+    g = synth.rng((seed * 1000003 + stream) * 131 + layer)
+    k = g.standard_normal(cfg.frames * cfg.dim).astype(np.float32)
+    v = g.standard_normal(cfg.frames * cfg.dim).astype(np.float32)
+    return k, v
+
+
+def _ptr(t):
+    from ctypes import c_void_p
+
+    return c_void_p(t.data_ptr())
+
+
+class Decoder:
+    """The model on the device for `batch` streams decoding in lockstep."""
+
+    def __init__(self, model, batch, device="cuda"):
+        import torch
+
+        self.model, self.cfg, self.batch = model, model.cfg, batch
+        c, B = model.cfg, batch
+        self.emb = cq.New(model.emb)
+        self.mats = [{n: cq.New(p[n]) for n in LAYER_MATS} for p in model.layers]
+        f32, i8, i32 = torch.float32, torch.int8, torch.int32
+        z = lambda *shape, dt=f32: torch.zeros(*shape, dtype=dt, device=device)
+        self.gains = torch.from_numpy(model.gains).to(device)
+        self.cos = torch.from_numpy(model.rope_cos).to(device)
+        self.sin = torch.from_numpy(model.rope_sin).to(device)
+        self.tok = z(B, dt=i32)
+        self.pos = z(B, dt=i32)
+        self.spans_self = z(B, 4, dt=i32)
+        self.spans_cross = z(B, 4, dt=i32)
+        self.spans_cross[:, 3] = c.frames
+        self.x, self.h = z(B, c.dim), z(B, c.dim)
+        self.q, self.k, self.v = z(B, c.dim), z(B, c.dim), z(B, c.dim)
+        self.att, self.o = z(B, c.dim), z(B, c.dim)
+        self.u = z(B, c.ffn)
+        self.logits = z(B, c.vocab)
+        hk = c.dim // c.head_dim
+        self.self_k = [z(B, c.max_pos, c.dim, dt=i8) for _ in range(c.layers)]
+        self.self_ks = [z(B, c.max_pos, hk) for _ in range(c.layers)]
+        self.self_v = [z(B, c.max_pos, c.dim, dt=i8) for _ in range(c.layers)]
+        self.self_vs = [z(B, c.max_pos, hk) for _ in range(c.layers)]
+        self.cross_k = [z(B, c.frames, c.dim, dt=i8) for _ in range(c.layers)]
+        self.cross_ks = [z(B, c.frames, hk) for _ in range(c.layers)]
+        self.cross_v = [z(B, c.frames, c.dim, dt=i8) for _ in range(c.layers)]
+        self.cross_vs = [z(B, c.frames, hk) for _ in range(c.layers)]
+
+    def set_memory(self, seed, generator="numpy"):
+        """Quantises each stream's cross keys and values (QuantizeRows per
+        head, bit for bit) into the int8 memory. generator "numpy" draws
+        them with memory_states; "device" draws them on the GPU (torch's
+        seeded Philox) for large batches."""
+        import torch
+
+        c = self.cfg
+        tmp_k = torch.empty(c.frames * c.dim, dtype=torch.float32, device=self.x.device)
+        tmp_v = torch.empty_like(tmp_k)
+        gen = torch.Generator(device=self.x.device)
+        for layer in range(c.layers):
+            for b in range(self.batch):
+                if generator == "numpy":
+                    k, v = memory_states(seed, c, b, layer)
+                    tmp_k.copy_(torch.from_numpy(k))
+                    tmp_v.copy_(torch.from_numpy(v))
+                else:
+                    gen.manual_seed((seed * 1000003 + b) * 131 + layer)
+                    torch.randn(tmp_k.shape, generator=gen, out=tmp_k, device=tmp_k.device)
+                    torch.randn(tmp_v.shape, generator=gen, out=tmp_v, device=tmp_v.device)
+                needle.quantize_rows_dev(self.cross_k[layer][b], self.cross_ks[layer][b], tmp_k, c.frames, c.dim,
+                                         c.head_dim)
+                needle.quantize_rows_dev(self.cross_v[layer][b], self.cross_vs[layer][b], tmp_v, c.frames, c.dim,
+                                         c.head_dim)
+        torch.cuda.synchronize()
+
+    def memory_states_device(self, seed, stream, layer):
+        """The keys and values set_memory(generator="device") drew for one
+        stream and layer, copied to the host."""
+        import torch
+
+        c = self.cfg
+        gen = torch.Generator(device=self.x.device)
+        gen.manual_seed((seed * 1000003 + stream) * 131 + layer)
+        k = torch.randn(c.frames * c.dim, generator=gen, device=self.x.device)
+        v = torch.randn(c.frames * c.dim, generator=gen, device=self.x.device)
+        return k.cpu().numpy(), v.cpu().numpy()
+
+    def reset(self, tokens):
+        import torch
+
+        self.tok.copy_(torch.as_tensor(np.asarray(tokens, np.int32), device=self.tok.device))
+        self.pos.zero_()
+
+    def _attend(self, layer, cross, s):
+        c, B = self.cfg, self.batch
+        hk = c.dim // c.head_dim
+        if cross:
+            kq, ks, vq, vs, spans, n = (self.cross_k[layer], self.cross_ks[layer], self.cross_v[layer],
+                                        self.cross_vs[layer], self.spans_cross, c.frames)
+        else:
+            kq, ks, vq, vs, spans, n = (self.self_k[layer], self.self_ks[layer], self.self_v[layer],
+                                        self.self_vs[layer], self.spans_self, c.max_pos)
+        check(lib().kv_attend_int8_dev(_ptr(self.att), 0, _ptr(self.q), 0, 1, c.heads, _ptr(kq), _ptr(ks), c.dim,
+                                       c.head_dim, _ptr(vq), _ptr(vs), c.dim, c.head_dim, n * c.dim, n * hk,
+                                       _ptr(spans), n, float(np.float32(math.sqrt(c.head_dim))), 1, B, s))
+
+    def step(self):
+        """One greedy token for every stream: reads tok and pos, writes the
+        next token to tok and advances pos."""
+        import torch
+
+        c, B, L = self.cfg, self.batch, lib()
+        s = cq._stream()
+        D, hk = c.dim, c.dim // c.head_dim
+        torch.add(self.pos, 1, out=self.spans_self[:, 3])  # keys 0..pos after this step's append
+        self.emb.row_gather_dev(self.x, self.tok, float(self.model.scale))
+        for l in range(c.layers):
+            m = self.mats[l]
+            check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * l]), B, D, s))
+            cq.gemms_dev([m["wq"], m["wk"], m["wv"]], [self.q, self.k, self.v], self.h, B)
+            for t in (self.q, self.k):
+                check(L.nd_rope_dev(_ptr(t), B, c.heads, c.head_dim, _ptr(self.cos), _ptr(self.sin), _ptr(self.pos),
+                                    1, s))
+            for src, cq_, cs_ in ((self.k, self.self_k[l], self.self_ks[l]), (self.v, self.self_v[l], self.self_vs[l])):
+                check(L.kv_append_dev(_ptr(cq_), _ptr(cs_), _ptr(src), B, D, c.head_dim, c.max_pos * D,
+                                      c.max_pos * hk, _ptr(self.pos), c.max_pos, s))
+            self._attend(l, False, s)
+            m["wo"].gemm_dev(self.o, self.att, B)
+            check(L.nd_add_dev(_ptr(self.x), _ptr(self.o), B * D, s))
+            check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * l + 1]), B, D, s))
+            m["wcq"].gemm_dev(self.q, self.h, B)
+            self._attend(l, True, s)
+            m["wco"].gemm_dev(self.o, self.att, B)
+            check(L.nd_add_dev(_ptr(self.x), _ptr(self.o), B * D, s))
+            check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * l + 2]), B, D, s))
+            m["w1"].gemm_dev(self.u, self.h, B)
+            check(L.nd_silu_dev(_ptr(self.u), B * c.ffn, s))
+            m["w2"].gemm_dev(self.o, self.u, B)
+            check(L.nd_add_dev(_ptr(self.x), _ptr(self.o), B * D, s))
+        check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * c.layers]), B, D, s))
+        self.emb.gemm_dev(self.logits, self.h, B)
+        check(L.nd_argmax_dev(_ptr(self.tok), _ptr(self.logits), B, c.vocab, s))
+        self.pos.add_(1)
+
+    def decode(self, first_tokens, n, graph=True):
+        """Greedy-decodes n tokens after first_tokens; returns [batch, n]."""
+        import torch
+
+        self.reset(first_tokens)
+        out = torch.zeros(self.batch, n, dtype=torch.int32, device=self.tok.device)
+        if not graph:
+            for i in range(n):
+                self.step()
+                out[:, i] = self.tok
+            return out
+        g = self.capture()
+        for i in range(n):
+            g.replay()
+            out[:, i] = self.tok
+        return out
+
+    def capture(self):
+        """A HIP graph of one step (the state it reads is on the device)."""
+        import torch
+
+        pos0, tok0 = self.pos.clone(), self.tok.clone()
+        self.step()  # kernel attributes are set outside the capture
+        torch.cuda.synchronize()
+        self.pos.copy_(pos0)
+        self.tok.copy_(tok0)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        return g  # capturing runs nothing: the state is as before

@@ -94,10 +94,11 @@ int cq_gemms(int n, cq_matrix *const *ms, float *const *dsts, const size_t *dst_
 int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream);
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream);
 int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream);
-/* Rows gathered by index: dst[i] = Row(rows[i]) for i < n, rows a device
- * int32 array: the decoder's token-embedding lookup for several streams
- * (internal/decoder/decoder.go:269-275) in one launch. */
-int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n, void *stream);
+/* Rows gathered by index: dst[i] = scale * Row(rows[i]) for i < n, rows a
+ * device int32 array: the decoder's scaled token-embedding lookup for
+ * several streams (internal/decoder/decoder.go:269-275) in one launch. A
+ * listed row outside the matrix gives zeros. */
+int cq_row_gather_dev(const cq_matrix *m, float *dst, const int32_t *rows, int n, float scale, void *stream);
 
 /* Batch plans (no reference counterpart; the device-resident form of many
  * independent Matrix.GEMM calls): job k multiplies ms[k] by rows[k]
@@ -140,6 +141,36 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
                        const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
                        int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
                        float scale, int quant_q, int batch, void *stream);
+
+/* Int8Rows.Append (int8.go:125-141) on a device KV cache for `batch`
+ * streams: stream b's row x + b*cols is quantised per chunk of width
+ * (QuantizeRow, bit for bit) into codes q + b*q_stride + pos[b]*cols and
+ * scales s + b*s_stride + pos[b]*(cols/width); pos is a device array, and a
+ * position outside [0, cap) is skipped. */
+int kv_append_dev(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
+                  long long s_stride, const int32_t *pos, int cap, void *stream);
+
+/* ---- float blocks of a decode step, on device memory -------------------- */
+
+/* ZCRMSNorm.Apply (internal/needle/norm.go:53-66, meanSquare :91-109):
+ * dst = gain * x / sqrt(mean(x^2) + 1e-6) per row of dim, mean in float64
+ * as the reference sums it; gain = 1 + scale (NewZCRMSNorm, norm.go:22-30).
+ * dst may be x. */
+int nd_zcrmsnorm_dev(float *dst, const float *x, const float *gain, int rows, int dim, void *stream);
+/* Rope.apply (internal/needle/rope.go:69-81) in place on rows of heads
+ * vectors of head_dim: row r uses position pos[r / rows_per_pos] of the
+ * (positions x head_dim/2) cos/sin tables (NewRope, rope.go:17-44). */
+int nd_rope_dev(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
+                const int32_t *pos, int rows_per_pos, void *stream);
+/* argmax (internal/decoder/greedy.go:181-191) of each row of n: the first
+ * index of the largest value. */
+int nd_argmax_dev(int32_t *out, const float *v, int rows, int n, void *stream);
+/* x = x * sigmoid(x), sigmoid from the amd64 exponent kernel's arithmetic
+ * (exp_amd64.s:84-112) on non-positive arguments. No reference
+ * counterpart: the synthetic decoder's FFN activation. */
+int nd_silu_dev(float *x, long long n, void *stream);
+/* x += y elementwise (the residual adds). */
+int nd_add_dev(float *x, const float *y, long long n, void *stream);
 
 #ifdef __cplusplus
 }

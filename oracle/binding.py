@@ -57,6 +57,12 @@ def lib():
             "orc_dots_f32_i8": (None, [POINTER(c_float), c_int, POINTER(c_float), c_int, POINTER(c_int8), c_int]),
             "orc_exp_sub_sum": (c_float, [POINTER(c_float), c_int, c_float, c_int]),
             "orc_softmax": (None, [POINTER(c_float), c_int, c_int]),
+            "orc_exp_lane": (c_float, [c_float]),
+            "orc_zc_rmsnorm": (None, [POINTER(c_float), POINTER(c_float), POINTER(c_float), c_int, c_int]),
+            "orc_rope": (None, [POINTER(c_float), c_int, c_int, c_int, POINTER(c_float), POINTER(c_float),
+                                POINTER(c_int32)]),
+            "orc_argmax": (None, [POINTER(c_int32), POINTER(c_float), c_int, c_int]),
+            "orc_silu": (None, [POINTER(c_float), ctypes.c_long]),
             "orc_attend_int8_spans": (c_int, [POINTER(c_float), POINTER(c_float), c_int, c_int, POINTER(c_int8),
                                               POINTER(c_float), c_int, c_int, POINTER(c_int8), POINTER(c_float), c_int,
                                               c_int, c_int, POINTER(c_int32), c_float, c_int, c_int, POINTER(c_float)]),
@@ -214,3 +220,32 @@ def attend_int8_spans(q, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, nk, s
     if rc:
         raise OracleError(f"attend: {rc}")
     return (out, probs) if want_probs else out
+
+
+def zc_rmsnorm(x, gain, dim):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    gain = np.ascontiguousarray(gain, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_zc_rmsnorm(fp(out), fp(x), fp(gain), x.size // dim, dim)
+    return out
+
+
+def rope(x, heads, head_dim, cos_t, sin_t, pos):
+    x = np.array(x, dtype=np.float32)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    lib().orc_rope(fp(x), pos.size, heads, head_dim, fp(np.ascontiguousarray(cos_t, np.float32)),
+                   fp(np.ascontiguousarray(sin_t, np.float32)), i32p(pos))
+    return x
+
+
+def argmax(v, rows, n):
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.zeros(rows, np.int32)
+    lib().orc_argmax(i32p(out), fp(v), rows, n)
+    return out
+
+
+def silu(x):
+    x = np.array(x, dtype=np.float32)
+    lib().orc_silu(fp(x), x.size)
+    return x

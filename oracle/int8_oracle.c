@@ -110,7 +110,7 @@ static float exp_sub_sum_generic(float *s, int n, float m) {
 }
 
 /* One lane of exp_amd64.s:84-112 (constants exp_amd64.s:7-51). */
-static float exp_lane(float x) {
+float orc_exp_lane(float x) {
     /* exp_amd64.s:7-51, bit for bit */
     const float log2e = 0x1.715476p+0f;  /* 0x3FB8AA3B */
     const float ln2hi = 0x1.63p-1f;      /* 0x3F318000 */
@@ -146,7 +146,7 @@ static float exp_sub_sum_avx2(float *s, int n8, float m) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int i = 0; i < n8; i += 8)
         for (int l = 0; l < 8; l++) {
-            float e = exp_lane(s[i + l] - m);
+            float e = orc_exp_lane(s[i + l] - m);
             s[i + l] = e;
             acc[l] = acc[l] + e;
         }

@@ -102,6 +102,17 @@ int orc_attend_int8_spans(float *out, const float *q, int t, int heads, const in
                           int k_cols, int qk, const int8_t *vq, const float *vs, int v_cols, int vd, int nk,
                           const int32_t *spans, float scale, int quant_q, int exp_variant, float *probs);
 
+/* One lane of the amd64 exponent kernel (exp_amd64.s:84-112). */
+float orc_exp_lane(float x);
+
+/* ---- decode-step float blocks (step_oracle.c) --------------------------- */
+
+void orc_zc_rmsnorm(float *dst, const float *x, const float *gain, int rows, int dim); /* norm.go:53-66 */
+void orc_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
+              const int32_t *pos);                                                    /* rope.go:69-81 */
+void orc_argmax(int32_t *out, const float *v, int rows, int n);                          /* greedy.go:181-191 */
+void orc_silu(float *x, long n);
+
 #ifdef __cplusplus
 }
 #endif

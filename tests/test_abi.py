@@ -18,7 +18,7 @@ from conftest import ROOT, gpu_available
 def declared(header):
     text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b((?:cq|kv)_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b((?:cq|kv|nd)_\w+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():

@@ -1,0 +1,133 @@
+"""GPU parity of the decode step with the CPU oracle, through the C ABI:
+the float blocks (ZCRMSNorm, RoPE, argmax, SiLU, the residual add, the int8
+append) bit for bit, and greedy decoding of the synthetic decoder with
+identical tokens and bit-identical logits, at batch 1 (the full model, 200
+tokens) and for streams of a batched run."""
+
+import numpy as np
+import pytest
+
+from go_whistle_amd import decoder as dec
+from go_whistle_amd import needle, synth
+from go_whistle_amd._lib import check, lib
+from oracle import binding as orc
+from oracle import decoder_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _p(t):
+    from ctypes import c_void_p
+
+    return c_void_p(t.data_ptr())
+
+
+def _s():
+    import torch
+    from ctypes import c_void_p
+
+    return c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def same(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_step_blocks_bit_exact():
+    import torch
+
+    g = synth.rng(11)
+    rows, dim = 7, 512
+    x = (g.standard_normal(rows * dim) * 2).astype(np.float32)
+    gain = (1 + g.standard_normal(dim) * 0.1).astype(np.float32)
+    xd, yd, gd = _t(x), torch.zeros(rows * dim, device="cuda"), _t(gain)
+    check(lib().nd_zcrmsnorm_dev(_p(yd), _p(xd), _p(gd), rows, dim, _s()))
+    cos, sin = dec.rope_tables(64, 300, 1e5)
+    pos = np.array([0, 1, 5, 63, 100, 200, 299], np.int32)
+    rd, cd, sd, pd = _t(x.copy()), _t(cos), _t(sin), _t(pos)  # held: a freed temporary's block is reused
+    check(lib().nd_rope_dev(_p(rd), rows, 8, 64, _p(cd), _p(sd), _p(pd), 1, _s()))
+    v = g.standard_normal((5, 16384)).astype(np.float32)
+    v[1, 3], v[1, 16000] = 40, 40
+    v[2] = 1.5
+    v[3, 16383] = 30
+    am, vd = torch.zeros(5, dtype=torch.int32, device="cuda"), _t(v)
+    check(lib().nd_argmax_dev(_p(am), _p(vd), 5, 16384, _s()))
+    u = np.concatenate([np.linspace(-40, 40, 4001), (g.standard_normal(3000) * 5)]).astype(np.float32)
+    ud = _t(u)
+    check(lib().nd_silu_dev(_p(ud), u.size, _s()))
+    a, b = g.standard_normal(1000).astype(np.float32), g.standard_normal(1000).astype(np.float32)
+    ad, bd = _t(a), _t(b)
+    check(lib().nd_add_dev(_p(ad), _p(bd), 1000, _s()))
+    torch.cuda.synchronize()
+    assert same(yd.cpu().numpy(), orc.zc_rmsnorm(x, gain, dim))
+    assert same(rd.cpu().numpy(), orc.rope(x, 8, 64, cos, sin, pos))
+    assert list(am.cpu().numpy()) == list(orc.argmax(v, 5, 16384))
+    assert list(am.cpu().numpy())[1:4] == [3, 0, 16383]
+    assert same(ud.cpu().numpy(), orc.silu(u))
+    assert same(ad.cpu().numpy(), (a + b).astype(np.float32))
+
+
+def test_append_at_positions():
+    import torch
+
+    g = synth.rng(12)
+    B, cap, cols, width = 3, 10, 512, 64
+    x = g.standard_normal(B * cols).astype(np.float32)
+    q = torch.zeros(B, cap, cols, dtype=torch.int8, device="cuda")
+    s = torch.zeros(B, cap, cols // width, device="cuda")
+    pos = np.array([0, 4, 9], np.int32)
+    xd, pd = _t(x), _t(pos)
+    check(lib().kv_append_dev(_p(q), _p(s), _p(xd), B, cols, width, cap * cols, cap * cols // width, _p(pd), cap,
+                              _s()))
+    torch.cuda.synchronize()
+    qh, sh = q.cpu().numpy(), s.cpu().numpy()
+    for b in range(B):
+        wq, ws = orc.quantize_rows(x[b * cols:(b + 1) * cols], cols, width)
+        assert np.array_equal(qh[b, pos[b]], wq) and same(sh[b, pos[b]], ws)
+        others = [p for p in range(cap) if p != pos[b]]
+        assert not qh[b, others].any()
+
+
+def _run(cfg, seed, batch, first, n, check_streams, generator="numpy"):
+    model = dec.make_model(seed, cfg)
+    d = dec.Decoder(model, batch)
+    d.set_memory(seed, generator)
+    toks = d.decode(first, n).cpu().numpy()
+    logits = d.logits.cpu().numpy()
+    ref = decoder_ref.RefDecoder(model)
+    for b in check_streams:
+        if generator == "numpy":
+            ks, vs = zip(*[dec.memory_states(seed, cfg, b, l) for l in range(cfg.layers)])
+        else:
+            ks, vs = zip(*[d.memory_states_device(seed, b, l) for l in range(cfg.layers)])
+        ref.memory(ks, vs)
+        want, wl = ref.decode(first[b], n, want_logits=True)
+        assert list(toks[b]) == want, (b, list(toks[b]), want)
+        assert same(logits[b], wl[-1]), b
+    return toks
+
+
+def test_small_decoder_batch_bit_exact():
+    cfg = dec.DecoderConfig(vocab=4096, layers=2, frames=100, max_pos=64)
+    toks = _run(cfg, 5, 3, [1, 2, 3], 24, [0, 1, 2])
+    assert len(set(toks[0].tolist())) > 1
+
+
+def test_full_decoder_batch1_200_tokens():
+    cfg = dec.DecoderConfig()
+    print("full decoder, batch 1, 200 tokens", flush=True)
+    toks = _run(cfg, 7, 1, [1], 200, [0])
+    assert len(set(toks[0].tolist())) > 5
+
+
+def test_full_decoder_batch256_streams():
+    cfg = dec.DecoderConfig()
+    print("full decoder, batch 256, 40 tokens", flush=True)
+    _run(cfg, 9, 256, list(range(256)), 40, [0, 131, 255], generator="device")

@@ -1,0 +1,62 @@
+"""Pins the oracle's decode-step float blocks: ZCRMSNorm (norm.go:53-109)
+against float64 and a closed form, RoPE (rope.go:69-81) against the float64
+rotation and the identity at position 0, argmax (greedy.go:181-191)
+against numpy's first-index argmax with ties, SiLU against float64."""
+
+import numpy as np
+import pytest
+
+from go_whistle_amd import decoder as dec
+from go_whistle_amd import synth
+from oracle import binding as orc
+
+
+def test_zc_rmsnorm_vs_float64_and_constant_row():
+    g = synth.rng(1)
+    x = (g.standard_normal(5 * 512) * 3).astype(np.float32)
+    gain = (1 + g.standard_normal(512) * 0.1).astype(np.float32)
+    y = orc.zc_rmsnorm(x, gain, 512).reshape(5, 512)
+    x64 = x.reshape(5, 512).astype(np.float64)
+    want = gain * x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    assert np.max(np.abs(y - want) / np.abs(want).max()) < 4e-7
+    # a constant row c: mean square c^2 exactly, y = gain * c / float32(sqrt(c^2 + 1e-6))
+    c = np.float32(2.0)
+    y = orc.zc_rmsnorm(np.full(512, c, np.float32), np.ones(512, np.float32), 512)
+    rms = np.float32(np.sqrt(np.float64(np.float32(np.float32(4.0) + np.float32(1e-6)))))
+    assert np.all(y == np.float32(c / rms))
+
+
+def test_rope_identity_and_float64_rotation():
+    cos, sin = dec.rope_tables(64, 16, 1e5)
+    assert np.all(cos[0] == 1) and np.all(sin[0] == 0)
+    g = synth.rng(2)
+    x = g.standard_normal(8 * 64).astype(np.float32)
+    assert np.array_equal(orc.rope(x, 8, 64, cos, sin, [0]), x)
+    y = orc.rope(x, 8, 64, cos, sin, [7]).reshape(8, 64)
+    xx = x.reshape(8, 64).astype(np.float64)
+    c64, s64 = cos[7].astype(np.float64), sin[7].astype(np.float64)
+    want = np.concatenate([xx[:, :32] * c64 - xx[:, 32:] * s64, xx[:, 32:] * c64 + xx[:, :32] * s64], axis=1)
+    assert np.max(np.abs(y - want)) < 1e-6 * np.abs(xx).max() * 4
+    # the tables: angle t / theta^(2i/d) (rope.go:33-41)
+    t, i = 7, 5
+    ang = 7 / (1e5 ** (2 * i / 64))
+    assert abs(cos[t, i] - np.cos(ang)) < 1e-6 and abs(sin[t, i] - np.sin(ang)) < 1e-6
+
+
+def test_argmax_first_on_ties():
+    g = synth.rng(3)
+    v = g.standard_normal((4, 1000)).astype(np.float32)
+    v[1, 17] = v[1, 900] = 50
+    v[2, :] = 0
+    v[3, 999] = 9
+    got = orc.argmax(v, 4, 1000)
+    assert list(got) == [int(np.argmax(v[0])), 17, 0, 999]
+
+
+def test_silu_vs_float64():
+    x = np.concatenate([np.linspace(-30, 30, 20001), [0.0, -0.0, 1e-30, -1e-30, 80.0, -80.0]]).astype(np.float32)
+    got = orc.silu(x).astype(np.float64)
+    xx = x.astype(np.float64)
+    want = xx / (1 + np.exp(-xx))
+    err = np.abs(got - want)
+    assert np.all(err <= 4 * 2.0 ** -23 * np.abs(want) + 1e-37)
