@@ -139,6 +139,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (prints its JSON)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the step's 4-bit launch and a 512 MiB device copy (for rocprofv3 counters)")
     args = ap.parse_args()
@@ -152,6 +153,9 @@ def main():
     gw = _package()
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
+    if args.decode_only:
+        print(json.dumps({"decode": decode_leg(gw, torch, args.decode_tokens, args.cpu_seconds, not args.no_cpu)}))
+        return
 
     g = gw.synth.rng(20261201)
     packs = [gw.synth.random_packed(g, o, i, GROUP, b, sigma=0.05) for b in BITS for (o, i) in SHAPES]

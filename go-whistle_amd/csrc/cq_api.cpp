@@ -764,15 +764,20 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
     const int kv_heads = k_cols / qk;
     if (heads <= 0 || heads % kv_heads != 0 || v_cols != kv_heads * vd)
         return fail(CQ_ERR_MISUSE, "needle: %d heads over %d KV heads (values %d of %d)", heads, kv_heads, v_cols, vd);
-    if (qk > 256 || qk % 4 != 0 || k_cols % 4 != 0)
-        return fail(CQ_ERR_UNSUPPORTED, "needle: int8 attention with head width %d", qk);
+    if (qk > 256 || qk % 4 != 0 || k_cols % 4 != 0 || vd > 192)
+        return fail(CQ_ERR_UNSUPPORTED, "needle: int8 attention with head widths %d and %d", qk, vd);
     if (t < 0 || batch < 0 || nk_max < 0) return fail(CQ_ERR_MISUSE, "needle: bad attention sizes");
-    const size_t lds = sizeof(float) * static_cast<size_t>(nk_max) + 64 * static_cast<size_t>(vd);
-    if (lds > device_info().max_lds) return fail(CQ_ERR_UNSUPPORTED, "needle: %d keys exceed LDS", nk_max);
+    if (nk_max > 8192) return fail(CQ_ERR_UNSUPPORTED, "needle: %d keys exceed LDS", nk_max);
     if (out_stride == 0) out_stride = static_cast<long long>(t) * heads * vd;  // dense streams
     if (q_stride == 0) q_stride = static_cast<long long>(t) * heads * qk;
+    // Value codes in LDS: all of a stream's rows at once (their loads overlap
+    // the logits) when the launch has few workgroups and they fit in 96 KiB;
+    // else two buffers of 256 rows, for more workgroups per CU.
+    const long long wgs = static_cast<long long>(heads) * t * batch;
+    const int fit = static_cast<int>(96 * 1024 / vd);
+    const int vchunk = (wgs <= 2LL * device_info().cus && nk_max <= fit) ? std::max(1, nk_max) : std::min(256, fit / 2);
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
-                 kv_stride, s_stride, spans, nk_max, scale, quant_q, batch};
+                 kv_stride, s_stride, spans, nk_max, vchunk, scale, quant_q, batch};
     HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");
     return CQ_OK;
 }

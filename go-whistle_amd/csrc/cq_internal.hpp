@@ -128,6 +128,7 @@ struct AttendArgs {
     long long kv_stride, s_stride;
     const int32_t *spans;
     int nk_max;            // key rows each stream's arrays hold; spans must lie in [0, nk_max)
+    int vchunk;            // set by the launcher: value rows per LDS chunk
     float scale;
     int quant_q;
     int batch;

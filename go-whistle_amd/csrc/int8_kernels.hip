@@ -20,10 +20,12 @@
 //      then every value divided by the sum;
 //   3. the weights times the value scales, and axpysI8 (int8kernel.go:
 //      360-368): per output, one key after the other, each product rounded
-//      before the add. One thread per output carries that chain; the value
-//      codes of 64 keys at a time are staged in LDS by the workgroup.
+//      before the add. One thread per output carries that chain over LDS
+//      chunks of value codes, which the workgroup's other wavefronts stage
+//      with 16-byte loads one chunk ahead.
 #include "cq_internal.hpp"
 
+#include <algorithm>
 #include <climits>
 
 namespace cqhip {
@@ -78,7 +80,6 @@ __device__ __forceinline__ float exp_lane(float x) {
 __device__ __forceinline__ float exp_generic(float d) { return static_cast<float>(exp(static_cast<double>(d))); }
 
 constexpr int kAttThreads = 256;
-constexpr int kVStage = 64;  // keys of value codes staged per round
 
 __device__ __forceinline__ float block_max(float v, float *red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -92,6 +93,13 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return r;
 }
 
+__device__ __forceinline__ int dot4_i8(int a, int b, int acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        acc += static_cast<int>(static_cast<int8_t>(a >> (8 * e))) * static_cast<int>(static_cast<int8_t>(b >> (8 * e)));
+    return acc;
+}
+
 __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int h = blockIdx.x, i = blockIdx.y, b = blockIdx.z;
@@ -103,10 +111,10 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const int n = len0 + len1;
     if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
 
-    float *s = reinterpret_cast<float *>(smem);                 // n logits / weights
-    int8_t *vstage = reinterpret_cast<int8_t *>(s + a.nk_max);  // kVStage rows of vd codes
+    float *s = reinterpret_cast<float *>(smem);  // n logits, then weights
+    int8_t *vbuf = reinterpret_cast<int8_t *>(s + ((a.nk_max + 3) & ~3));  // value codes: one or two chunks
     __shared__ float red[8];
-    __shared__ int8_t q8[256];
+    __shared__ __align__(16) int8_t q8[256];
     __shared__ float sq_sh, sum_sh;
 
     const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
@@ -114,6 +122,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const float *ks = a.ks + b * a.s_stride;
     const int8_t *vq = a.vq + b * a.kv_stride;
     const float *vs = a.vs + b * a.s_stride;
+    auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
 
     // QuantizeRow of the query head (int8.go:226-228).
     if (a.quant_q) {
@@ -131,36 +140,79 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     }
     const float sq = a.quant_q ? sq_sh : 0.0f;
 
-    // 1. Logits.
-    for (int j = tid; j < n; j += kAttThreads) {
-        const int key = j < len0 ? lo0 + j : lo1 + (j - len0);
+    // Value codes: staged into LDS from the start, so their loads overlap
+    // the logits and the softmax. All n rows when they fit (vchunk >= n),
+    // else chunks of vchunk rows, two buffers, staged one chunk ahead.
+    const bool aligned = (a.kv_stride & 15) == 0 && (reinterpret_cast<uintptr_t>(a.kq) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.vq) & 15) == 0;
+    const bool wide = aligned && (a.qk & 15) == 0 && (a.k_cols & 15) == 0;
+    const int vchunk = a.vchunk;
+    const int nchunks = (n + vchunk - 1) / vchunk;
+    const bool wide_v = aligned && (a.vd & 15) == 0 && (a.v_cols & 15) == 0;
+    auto stage = [&](int c, int8_t *buf, int t0, int nt) {
+        const int j0 = c * vchunk, cnt = min(vchunk, n - j0);
+        if (wide_v) {
+            const int per = a.vd / 16;
+            for (int e = t0; e < cnt * per; e += nt) {
+                const int jj = e / per, part = e - (e / per) * per;
+                const int4 w = *reinterpret_cast<const int4 *>(vq + static_cast<long long>(key_of(j0 + jj)) * a.v_cols +
+                                                               kv * a.vd + part * 16);
+                *reinterpret_cast<int4 *>(buf + jj * a.vd + part * 16) = w;
+            }
+        } else {
+            for (int e = t0; e < cnt * a.vd; e += nt) {
+                const int jj = e / a.vd, d = e - (e / a.vd) * a.vd;
+                buf[jj * a.vd + d] = vq[static_cast<long long>(key_of(j0 + jj)) * a.v_cols + kv * a.vd + d];
+            }
+        }
+    };
+    if (nchunks > 0) stage(0, vbuf, tid, kAttThreads);
+
+    // 1. Logits, one thread per key (int8Logits / dotsF32I8), two keys at a
+    // time so that their loads are in flight together.
+    auto logit = [&](int j) -> float {
+        const int key = key_of(j);
         const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
         const float sk = ks[static_cast<long long>(key) * kv_heads + kv];
-        float lg;
         if (a.quant_q) {
-            int dot = 0;
-            for (int c = 0; c < a.qk; c += 4) {
-                const int w = *reinterpret_cast<const int *>(krow + c);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dot += static_cast<int>(q8[c + e]) * static_cast<int>(static_cast<int8_t>(w >> (8 * e)));
+            int dot = 0;  // exact in any order
+            if (wide) {
+                for (int c = 0; c < a.qk; c += 16) {
+                    const int4 kw = *reinterpret_cast<const int4 *>(krow + c);
+                    const int4 qw = *reinterpret_cast<const int4 *>(q8 + c);
+                    dot = dot4_i8(kw.x, qw.x, dot);
+                    dot = dot4_i8(kw.y, qw.y, dot);
+                    dot = dot4_i8(kw.z, qw.z, dot);
+                    dot = dot4_i8(kw.w, qw.w, dot);
+                }
+            } else {
+                for (int c = 0; c < a.qk; c += 4)
+                    dot = dot4_i8(*reinterpret_cast<const int *>(krow + c), *reinterpret_cast<const int *>(q8 + c), dot);
             }
             const float scl = sq * sk;
             const float t1 = static_cast<float>(dot) * scl;
-            lg = t1 / a.scale;
-        } else {
-            float dot = 0.0f;
-            for (int c = 0; c < a.qk; c += 4) {
-                const int w = *reinterpret_cast<const int *>(krow + c);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float pr = qi[c + e] * static_cast<float>(static_cast<int8_t>(w >> (8 * e)));
-                    dot = dot + pr;
-                }
-            }
-            const float t1 = dot * sk;
-            lg = t1 / a.scale;
+            return t1 / a.scale;
         }
-        s[j] = lg;
+        float dot = 0.0f;  // in order
+        for (int c = 0; c < a.qk; c += 4) {
+            const int w = *reinterpret_cast<const int *>(krow + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float pr = qi[c + e] * static_cast<float>(static_cast<int8_t>(w >> (8 * e)));
+                dot = dot + pr;
+            }
+        }
+        const float t1 = dot * sk;
+        return t1 / a.scale;
+    };
+    {
+        int j = tid;
+        for (; j + kAttThreads < n; j += 2 * kAttThreads) {
+            const float l0 = logit(j), l1 = logit(j + kAttThreads);
+            s[j] = l0;
+            s[j + kAttThreads] = l1;
+        }
+        if (j < n) s[j] = logit(j);
     }
     __syncthreads();
 
@@ -175,9 +227,17 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         s[j] = (kernel_path && j < n8) ? exp_lane(d) : exp_generic(d);
     }
     __syncthreads();
-    if (tid < 8 && kernel_path) {
+    if (tid < 8 && kernel_path) {  // lane tid of the 8-lane sum, elements in order
         float acc = 0.0f;
-        for (int j = tid; j < n8; j += 8) acc = acc + s[j];
+        int j = tid;
+        for (; j + 24 < n8; j += 32) {
+            const float e0 = s[j], e1 = s[j + 8], e2 = s[j + 16], e3 = s[j + 24];
+            acc = acc + e0;
+            acc = acc + e1;
+            acc = acc + e2;
+            acc = acc + e3;
+        }
+        for (; j < n8; j += 8) acc = acc + s[j];
         red[tid] = acc;
     }
     __syncthreads();
@@ -201,30 +261,43 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     __syncthreads();
     const float sum = sum_sh;
     for (int j = tid; j < n; j += kAttThreads) {
-        const int key = j < len0 ? lo0 + j : lo1 + (j - len0);
         const float p = s[j] / sum;
-        s[j] = p * vs[static_cast<long long>(key) * kv_heads + kv];
+        s[j] = p * vs[static_cast<long long>(key_of(j)) * kv_heads + kv];
     }
-    __syncthreads();
 
-    // 3. axpysI8 per output, keys in order.
+    // 3. axpysI8 per output, keys in order: the first ceil(vd/64)
+    // wavefronts carry the chains over LDS chunks of value codes; with more
+    // than one chunk the other wavefronts stage the next one meanwhile.
+    const int chain_threads = ((a.vd + 63) / 64) * 64;
+    __syncthreads();
     float acc = 0.0f;
-    for (int j0 = 0; j0 < n; j0 += kVStage) {
-        const int cnt = min(kVStage, n - j0);
-        for (int e = tid; e < cnt * a.vd; e += kAttThreads) {
-            const int jj = e / a.vd, d = e % a.vd;
-            const int j = j0 + jj;
-            const int key = j < len0 ? lo0 + j : lo1 + (j - len0);
-            vstage[e] = vq[static_cast<long long>(key) * a.v_cols + kv * a.vd + d];
-        }
-        __syncthreads();
-        if (tid < a.vd) {
-            for (int jj = 0; jj < cnt; ++jj) {
-                const float pr = s[j0 + jj] * static_cast<float>(vstage[jj * a.vd + tid]);
-                acc = acc + pr;
+    for (int c = 0; c < nchunks; ++c) {
+        int8_t *cur = vbuf + (c & 1) * vchunk * a.vd;
+        if (tid < chain_threads) {
+            if (tid < a.vd) {
+                const int j0 = c * vchunk, cnt = min(vchunk, n - j0);
+                int jj = 0;
+                for (; jj + 3 < cnt; jj += 4) {
+                    const float w0 = s[j0 + jj], w1 = s[j0 + jj + 1], w2 = s[j0 + jj + 2], w3 = s[j0 + jj + 3];
+                    const float c0 = static_cast<float>(cur[jj * a.vd + tid]);
+                    const float c1 = static_cast<float>(cur[(jj + 1) * a.vd + tid]);
+                    const float c2 = static_cast<float>(cur[(jj + 2) * a.vd + tid]);
+                    const float c3 = static_cast<float>(cur[(jj + 3) * a.vd + tid]);
+                    const float p0 = w0 * c0, p1 = w1 * c1, p2 = w2 * c2, p3 = w3 * c3;
+                    acc = acc + p0;
+                    acc = acc + p1;
+                    acc = acc + p2;
+                    acc = acc + p3;
+                }
+                for (; jj < cnt; ++jj) {
+                    const float pr = s[j0 + jj] * static_cast<float>(cur[jj * a.vd + tid]);
+                    acc = acc + pr;
+                }
             }
+        } else if (c + 1 < nchunks) {
+            stage(c + 1, vbuf + ((c + 1) & 1) * vchunk * a.vd, tid - chain_threads, kAttThreads - chain_threads);
         }
-        __syncthreads();
+        if (nchunks > 1) __syncthreads();
     }
     if (tid < a.vd) a.out[b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * a.vd + tid] = acc;
 }
@@ -248,8 +321,19 @@ hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long c
 
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
     if (a.t <= 0 || a.heads <= 0 || a.batch <= 0) return hipSuccess;
-    const size_t lds = sizeof(float) * static_cast<size_t>(a.nk_max) + static_cast<size_t>(kVStage) * a.vd;
-    hipLaunchKernelGGL(attend_kernel, dim3(a.heads, a.t, a.batch), dim3(kAttThreads), lds, stream, a);
+    const AttendArgs &b = a;
+    const bool one_chunk = a.vchunk >= a.nk_max;
+    const size_t vbytes = (one_chunk ? 1 : 2) * static_cast<size_t>(a.vchunk) * a.vd;
+    const size_t lds = sizeof(float) * static_cast<size_t>((a.nk_max + 3) & ~3) + vbytes;
+    static bool attr = false;
+    if (!attr) {
+        // dynamic LDS beside the kernel's static arrays: 96 KiB of values + up to 8192 logits
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(attend_kernel, dim3(a.heads, a.t, a.batch), dim3(kAttThreads), lds, stream, b);
     return hipGetLastError();
 }
 

@@ -23,25 +23,34 @@ namespace cqhip {
 namespace {
 
 __global__ __launch_bounds__(64) void zc_rmsnorm_kernel(float *dst, const float *x, const float *gain, int dim) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    double *sq = reinterpret_cast<double *>(smem);  // the row's squares, exact in float64
     const int r = blockIdx.x, lane = threadIdx.x;
     const float *row = x + static_cast<long long>(r) * dim;
     float *out = dst + static_cast<long long>(r) * dim;
     __shared__ double part[4];
     __shared__ float rms_sh;
+    for (int i = lane; i < dim; i += 64) {
+        const double v = static_cast<double>(row[i]);
+        sq[i] = v * v;
+    }
+    __syncthreads();
     // meanSquare (norm.go:91-109): s_k over i = k, k+4, ... (the full words
     // of four), then the tail into s0, then (s0 + s1 + s2 + s3) / n.
     if (lane < 4) {
         double s = 0.0;
         const int full = dim & ~3;
-        for (int i = lane; i < full; i += 4) {
-            const double v = static_cast<double>(row[i]);
-            s = s + v * v;
+        int i = lane;
+        for (; i + 12 < full; i += 16) {
+            const double a0 = sq[i], a1 = sq[i + 4], a2 = sq[i + 8], a3 = sq[i + 12];
+            s = s + a0;
+            s = s + a1;
+            s = s + a2;
+            s = s + a3;
         }
+        for (; i < full; i += 4) s = s + sq[i];
         if (lane == 0)
-            for (int i = full; i < dim; ++i) {
-                const double v = static_cast<double>(row[i]);
-                s = s + v * v;
-            }
+            for (int t = full; t < dim; ++t) s = s + sq[t];
         part[lane] = s;
     }
     __syncthreads();
@@ -186,7 +195,7 @@ unsigned blocks_for(long long n, int t) { return static_cast<unsigned>((n + t - 
 
 hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int rows, int dim, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(zc_rmsnorm_kernel, dim3(rows), dim3(64), 0, s, dst, x, gain, dim);
+    hipLaunchKernelGGL(zc_rmsnorm_kernel, dim3(rows), dim3(64), sizeof(double) * dim, s, dst, x, gain, dim);
     return hipGetLastError();
 }
 
