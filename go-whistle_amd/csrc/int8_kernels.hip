@@ -152,12 +152,27 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     auto stage = [&](int c, int8_t *buf, int t0, int nt) {
         const int j0 = c * vchunk, cnt = min(vchunk, n - j0);
         if (wide_v) {
-            const int per = a.vd / 16;
-            for (int e = t0; e < cnt * per; e += nt) {
-                const int jj = e / per, part = e - (e / per) * per;
-                const int4 w = *reinterpret_cast<const int4 *>(vq + static_cast<long long>(key_of(j0 + jj)) * a.v_cols +
+            // eight 16-byte loads in flight per thread before their LDS stores
+            const int per = a.vd / 16, total = cnt * per;
+            for (int e0 = t0; e0 < total; e0 += 8 * nt) {
+                int4 w[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int e = e0 + u * nt;
+                    if (e < total) {
+                        const int jj = e / per, part = e - (e / per) * per;
+                        w[u] = *reinterpret_cast<const int4 *>(vq + static_cast<long long>(key_of(j0 + jj)) * a.v_cols +
                                                                kv * a.vd + part * 16);
-                *reinterpret_cast<int4 *>(buf + jj * a.vd + part * 16) = w;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int e = e0 + u * nt;
+                    if (e < total) {
+                        const int jj = e / per, part = e - (e / per) * per;
+                        *reinterpret_cast<int4 *>(buf + jj * a.vd + part * 16) = w[u];
+                    }
+                }
             }
         } else {
             for (int e = t0; e < cnt * a.vd; e += nt) {
@@ -168,8 +183,8 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     };
     if (nchunks > 0) stage(0, vbuf, tid, kAttThreads);
 
-    // 1. Logits, one thread per key (int8Logits / dotsF32I8), two keys at a
-    // time so that their loads are in flight together.
+    // 1. Logits, one thread per key (int8Logits / dotsF32I8), four keys at
+    // a time so that their loads are in flight together.
     auto logit = [&](int j) -> float {
         const int key = key_of(j);
         const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
@@ -207,12 +222,15 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     };
     {
         int j = tid;
-        for (; j + kAttThreads < n; j += 2 * kAttThreads) {
-            const float l0 = logit(j), l1 = logit(j + kAttThreads);
+        for (; j + 3 * kAttThreads < n; j += 4 * kAttThreads) {
+            const float l0 = logit(j), l1 = logit(j + kAttThreads), l2 = logit(j + 2 * kAttThreads),
+                        l3 = logit(j + 3 * kAttThreads);
             s[j] = l0;
             s[j + kAttThreads] = l1;
+            s[j + 2 * kAttThreads] = l2;
+            s[j + 3 * kAttThreads] = l3;
         }
-        if (j < n) s[j] = logit(j);
+        for (; j < n; j += kAttThreads) s[j] = logit(j);
     }
     __syncthreads();
 
