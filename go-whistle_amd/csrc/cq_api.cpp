@@ -776,8 +776,9 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
     const long long wgs = static_cast<long long>(heads) * t * batch;
     const int fit = static_cast<int>(96 * 1024 / vd);
     const int vchunk = (wgs <= 2LL * device_info().cus && nk_max <= fit) ? std::max(1, nk_max) : std::min(256, fit / 2);
+    const int resident = wgs <= 2LL * device_info().cus ? 1 : 0;
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
-                 kv_stride, s_stride, spans, nk_max, vchunk, scale, quant_q, batch};
+                 kv_stride, s_stride, spans, nk_max, vchunk, resident, scale, quant_q, batch};
     HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");
     return CQ_OK;
 }

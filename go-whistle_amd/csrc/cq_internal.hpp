@@ -128,7 +128,8 @@ struct AttendArgs {
     long long kv_stride, s_stride;
     const int32_t *spans;
     int nk_max;            // key rows each stream's arrays hold; spans must lie in [0, nk_max)
-    int vchunk;            // set by the launcher: value rows per LDS chunk
+    int vchunk;            // value rows per LDS chunk (general kernel)
+    int resident;          // 1: few workgroups, keep every value row of a stream in LDS
     float scale;
     int quant_q;
     int batch;

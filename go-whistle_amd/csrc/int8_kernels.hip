@@ -320,6 +320,376 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     if (tid < a.vd) a.out[b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * a.vd + tid] = acc;
 }
 
+
+// s_waitcnt vmcnt(K), every other counter left alone (gfx9 encoding).
+template <int K>
+__device__ __forceinline__ void wait_vm_const() {
+    __builtin_amdgcn_s_waitcnt((K & 15) | ((K >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wait until at most k of this wavefront's vector-memory loads are in flight
+// (loads retire in order). Counts above 24 wait for 24, which is stricter.
+__device__ __forceinline__ void wait_vm(int k) {
+    switch (k < 0 ? 0 : k) {
+#define CQ_WAIT_CASE(K) \
+    case K: wait_vm_const<K>(); break;
+        CQ_WAIT_CASE(0) CQ_WAIT_CASE(1) CQ_WAIT_CASE(2) CQ_WAIT_CASE(3) CQ_WAIT_CASE(4) CQ_WAIT_CASE(5)
+        CQ_WAIT_CASE(6) CQ_WAIT_CASE(7) CQ_WAIT_CASE(8) CQ_WAIT_CASE(9) CQ_WAIT_CASE(10) CQ_WAIT_CASE(11)
+        CQ_WAIT_CASE(12) CQ_WAIT_CASE(13) CQ_WAIT_CASE(14) CQ_WAIT_CASE(15) CQ_WAIT_CASE(16) CQ_WAIT_CASE(17)
+        CQ_WAIT_CASE(18) CQ_WAIT_CASE(19) CQ_WAIT_CASE(20) CQ_WAIT_CASE(21) CQ_WAIT_CASE(22) CQ_WAIT_CASE(23)
+#undef CQ_WAIT_CASE
+    default: wait_vm_const<24>(); break;
+    }
+}
+
+// Byte offset of an LDS location, as M0 and the LDS instructions take it.
+__device__ __forceinline__ unsigned lds_offset(const void *p) {
+    return static_cast<unsigned>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char *)(p)));
+}
+
+// One 16-byte global load per lane straight into LDS: lane l's bytes land
+// at lds + 16 * l (global_load_lds_dwordx4, M0 = lds). Issued as inline
+// assembly so that the compiler does not wait for it before every later LDS
+// read; its completion is the caller's wait_vm before a barrier.
+__device__ __forceinline__ void dma16(const void *src, unsigned lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+// Geometry of the streamed attention kernel: value heads of VD codes,
+// chunks of JC keys.
+template <int VD, int JC>
+struct StreamGeo {
+    static constexpr int kKpt = JC == 64 ? 6 : 4;       // keys per thread per round of logits
+    static constexpr int kCW = VD / 64;                 // chain wavefronts: one output per lane
+    static constexpr int kPW = kAttThreads / 64 - kCW;  // product wavefronts
+    static constexpr int kJC = JC;                      // keys per chunk
+    static constexpr int kPitch = JC + 4;               // floats per product row (16 B times an odd number)
+    static constexpr int kSeg = VD / 16;                // 16-byte pieces per value row
+    static constexpr int kPieces = JC * kSeg;           // pieces per chunk = product items per chunk
+    static constexpr int kDma = kPieces / 64;           // wavefront-wide LDS-DMA loads per chunk
+    static_assert(kDma * 64 == kPieces, "a chunk is whole wavefront loads");
+    static_assert((kPitch / 4) % 2 == 1, "product rows 16 B times an odd number apart");
+};
+
+constexpr int kStreamQk = 64;  // widest key head the streamed kernel holds in registers
+
+// AttendInt8Spans for one (stream, query row, head) per workgroup, value
+// heads of 64 or 128 codes, key heads of at most 64 codes, 16-byte aligned
+// rows. Same arithmetic as attend_kernel; the work is ordered for latency:
+//   - the query and the first keys of every thread are loaded together,
+//     the keys into registers (kKpt keys per thread at a time);
+//   - value rows stream from HBM straight into an LDS ring of chunks of JC
+//     keys (global_load_lds, issued up to rs chunks ahead, all of the stream
+//     when `rs` covers it), laid out [16-byte piece][key]; the first chunks
+//     are issued after the logits, under the softmax;
+//   - the product wavefronts turn a chunk into float32 products
+//     fl(w_j * code_jd), stored [d][key] in one of two LDS buffers;
+//   - meanwhile each chain lane d adds the previous chunk's products of its
+//     output in key order, four per 16-byte LDS read, a chunk's reads
+//     issued at once.
+// With `swz`, workgroup w serves stream (w mod 8) + 8 * (w / (8 * heads * t))
+// (one stream's heads on one XCD, whose L2 then holds the 128-byte lines
+// its heads share); otherwise stream w / (heads * t).
+template <int VD, int JC>
+__global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a, int rs, int swz) {
+    using G = StreamGeo<VD, JC>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int per = a.heads * a.t;
+    const int w = blockIdx.x;
+    int b, r;
+    if (swz) {
+        const int full = (a.batch & ~7) * per;
+        if (w < full) {
+            b = (w & 7) + 8 * (w / (8 * per));
+            r = (w >> 3) % per;
+        } else {
+            const int w2 = w - full, rem = a.batch & 7;
+            b = (a.batch & ~7) + w2 % rem;
+            r = w2 / rem;
+        }
+    } else {
+        b = w / per;
+        r = w - b * per;
+    }
+    const int h = r % a.heads, i = r / a.heads;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the DMA's LDS base goes to M0
+    const int kv_heads = a.k_cols / a.qk;
+    const int kv = h / (a.heads / kv_heads);
+    const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
+    const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
+    const int n = len0 + len1;
+    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
+    float *outp = a.out + b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * VD;
+    if (n == 0) {
+        if (tid < VD) outp[tid] = 0.0f;
+        return;
+    }
+
+    const int nk_pad = (a.nk_max + 3) & ~3;
+    float *s = reinterpret_cast<float *>(smem);  // logits, exponentials, then weights
+    float *vsb = s + nk_pad;                     // value scales of the keys
+    float *P = vsb + nk_pad;                     // two product buffers [VD][kPitch]
+    int8_t *ring = reinterpret_cast<int8_t *>(P + 2 * VD * G::kPitch);
+    __shared__ float red[8];
+    __shared__ __align__(16) int8_t q8[kStreamQk];
+    __shared__ __align__(16) float qf[kStreamQk];
+    __shared__ float sq_sh, sum_sh;
+
+    const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
+    const int8_t *kq = a.kq + b * a.kv_stride;
+    const float *ks = a.ks + b * a.s_stride;
+    const int8_t *vq = a.vq + b * a.kv_stride;
+    const float *vs = a.vs + b * a.s_stride;
+    auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
+
+    const int nch = (n + G::kJC - 1) / G::kJC;
+    const bool producer = wave >= G::kCW;
+    const int pw = wave - G::kCW, ptid = tid - 64 * G::kCW;
+    const int lw = producer ? (G::kDma - pw + G::kPW - 1) / G::kPW : 0;  // this wavefront's DMA loads per chunk
+
+    // Chunk c of value rows into ring slot c % rs: piece p = (segment,
+    // key) lands at p * 16; keys past the stream's end re-read its first key.
+    auto dma = [&](int c) {
+        const int j0 = c * G::kJC, cnt = min(G::kJC, n - j0);
+        int8_t *slot = ring + (c % rs) * (G::kJC * VD);
+        for (int u = pw; u < G::kDma; u += G::kPW) {
+            const int p = u * 64 + lane;
+            const int seg = p / G::kJC, jj = p - seg * G::kJC;
+            const int key = key_of(j0 + (jj < cnt ? jj : 0));
+            dma16(vq + static_cast<long long>(key) * a.v_cols + kv * VD + seg * 16, lds_offset(slot + u * 64 * 16));
+        }
+    };
+
+    // 1. The query, then the first four keys of this thread, in flight together.
+    const int kpieces = a.qk / 16;
+    const float qv = tid < a.qk ? qi[tid] : 0.0f;
+    constexpr int KPT = G::kKpt;
+    int4 kw[KPT][kStreamQk / 16];
+    float skr[KPT], vsr[KPT];
+    auto kload = [&](int g, int j) {
+        const int key = key_of(j);
+        const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
+#pragma unroll
+        for (int p = 0; p < kStreamQk / 16; ++p)
+            if (p < kpieces) kw[g][p] = *reinterpret_cast<const int4 *>(krow + 16 * p);
+        skr[g] = ks[static_cast<long long>(key) * kv_heads + kv];
+        vsr[g] = vs[static_cast<long long>(key) * kv_heads + kv];
+    };
+    auto logit = [&](int g) -> float {
+        if (a.quant_q) {
+            int dot = 0;  // exact in any order
+#pragma unroll
+            for (int p = 0; p < kStreamQk / 16; ++p)
+                if (p < kpieces) {
+                    const int4 qw = *reinterpret_cast<const int4 *>(q8 + 16 * p);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].x, qw.x, dot, false);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].y, qw.y, dot, false);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].z, qw.z, dot, false);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].w, qw.w, dot, false);
+                }
+            const float scl = sq_sh * skr[g];
+            const float t1 = static_cast<float>(dot) * scl;
+            return t1 / a.scale;
+        }
+        float dot = 0.0f;  // in order
+#pragma unroll
+        for (int p = 0; p < kStreamQk / 16; ++p)
+            if (p < kpieces) {
+                const int cw[4] = {kw[g][p].x, kw[g][p].y, kw[g][p].z, kw[g][p].w};
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float pr = qf[16 * p + e] * static_cast<float>(static_cast<int8_t>(cw[e >> 2] >> (8 * (e & 3))));
+                    dot = dot + pr;
+                }
+            }
+        const float t1 = dot * skr[g];
+        return t1 / a.scale;
+    };
+#pragma unroll
+    for (int g = 0; g < KPT; ++g)
+        if (tid + g * kAttThreads < n) kload(g, tid + g * kAttThreads);
+
+    // QuantizeRow of the query head (int8.go:226-228).
+    if (tid < a.qk) qf[tid] = qv;
+    if (a.quant_q) {
+        const float m = block_max(tid < a.qk ? fabsf(qv) : 0.0f, red);
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+        if (tid < a.qk) {
+            float rq = rintf(qv / sc);
+            rq = fminf(fmaxf(rq, -128.0f), 127.0f);
+            q8[tid] = static_cast<int8_t>(static_cast<int>(rq));
+        }
+        if (tid == 0) sq_sh = sc;
+    }
+    __syncthreads();
+
+    // Logits (int8Logits / dotsF32I8), KPT keys per thread per round; the
+    // keys' value scales go to LDS beside them.
+    for (int j0 = 0; j0 < n; j0 += KPT * kAttThreads) {
+        if (j0 > 0) {
+#pragma unroll
+            for (int g = 0; g < KPT; ++g)
+                if (j0 + tid + g * kAttThreads < n) kload(g, j0 + tid + g * kAttThreads);
+        }
+#pragma unroll
+        for (int g = 0; g < KPT; ++g) {
+            const int j = j0 + tid + g * kAttThreads;
+            if (j < n) {
+                s[j] = logit(g);
+                vsb[j] = vsr[g];
+            }
+        }
+    }
+    __syncthreads();
+
+    // The first rs chunks of value rows start streaming now, under the
+    // softmax. The compiler's own loads are drained first: loads retire in
+    // order, so any wait for one of them issued later would also wait for
+    // the value rows queued behind it.
+    wait_vm_const<0>();
+    if (producer) {
+        const int c0 = min(rs, nch);
+        for (int c = 0; c < c0; ++c) dma(c);
+    }
+
+    // 2. softmaxInPlace with amd64's expSubSum. The eight lane sums read
+    // the exponentials from a copy transposed to [lane][index] in the
+    // product buffers (free until step 3) when it fits.
+    float m = -INFINITY;
+    for (int j = tid; j < n; j += kAttThreads) m = fmaxf(m, s[j]);
+    m = block_max(m, red);
+    const int n8 = n & ~7;
+    const bool kernel_path = n8 > 0;
+    const int r8 = ((n8 >> 3) + 3) & ~3;
+    const bool transposed = kernel_path && 8 * r8 <= 2 * VD * G::kPitch;
+    for (int j = tid; j < n8; j += kAttThreads) {
+        const float e = exp_lane(s[j] - m);
+        s[j] = e;
+        if (transposed) P[(j & 7) * r8 + (j >> 3)] = e;
+    }
+    for (int j = n8 + tid; j < n; j += kAttThreads) s[j] = exp_generic(s[j] - m);
+    __syncthreads();
+    if (tid < 8 && kernel_path) {  // lane tid of the 8-lane sum, elements in order
+        float acc = 0.0f;
+        if (transposed) {
+            const float *row = P + tid * r8;
+            const int cnt = n8 >> 3;
+            int k = 0;
+            for (; k + 16 <= cnt; k += 16) {
+                const float4 v0 = *reinterpret_cast<const float4 *>(row + k);
+                const float4 v1 = *reinterpret_cast<const float4 *>(row + k + 4);
+                const float4 v2 = *reinterpret_cast<const float4 *>(row + k + 8);
+                const float4 v3 = *reinterpret_cast<const float4 *>(row + k + 12);
+                acc = acc + v0.x; acc = acc + v0.y; acc = acc + v0.z; acc = acc + v0.w;
+                acc = acc + v1.x; acc = acc + v1.y; acc = acc + v1.z; acc = acc + v1.w;
+                acc = acc + v2.x; acc = acc + v2.y; acc = acc + v2.z; acc = acc + v2.w;
+                acc = acc + v3.x; acc = acc + v3.y; acc = acc + v3.z; acc = acc + v3.w;
+            }
+            for (; k < cnt; ++k) acc = acc + row[k];
+        } else {
+            for (int j = tid; j < n8; j += 8) acc = acc + s[j];
+        }
+        red[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float sum;
+        if (kernel_path) {
+            const float x0 = red[0] + red[4], x1 = red[1] + red[5], x2 = red[2] + red[6], x3 = red[3] + red[7];
+            const float h0 = x0 + x1, h1 = x2 + x3;
+            sum = h0 + h1;
+            if (n8 != n) {
+                float tail = 0.0f;
+                for (int j = n8; j < n; ++j) tail = tail + s[j];
+                sum = sum + tail;
+            }
+        } else {
+            sum = 0.0f;
+            for (int j = 0; j < n; ++j) sum = sum + s[j];
+        }
+        sum_sh = sum;
+    }
+    __syncthreads();
+    const float sum = sum_sh;
+    for (int j = tid; j < n; j += kAttThreads) {
+        const float p = s[j] / sum;
+        s[j] = p * vsb[j];
+    }
+
+    // 3. axpysI8 per output, keys in order, over the chunk pipeline. Before
+    // the barrier that opens iteration c, chunk c + 1 has landed in the ring.
+    auto produce = [&](int c) {
+        const int j0 = c * G::kJC, cnt = min(G::kJC, n - j0);
+        const int8_t *slot = ring + (c % rs) * (G::kJC * VD);
+        float *pb = P + (c & 1) * (VD * G::kPitch);
+        for (int e = ptid; e < G::kPieces; e += 64 * G::kPW) {
+            const int seg = e / G::kJC, jj = e - seg * G::kJC;
+            if (jj < cnt) {
+                const int4 c4 = *reinterpret_cast<const int4 *>(slot + e * 16);
+                const float wj = s[j0 + jj];
+                float *col = pb + seg * 16 * G::kPitch + jj;
+                const int cw[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float code = static_cast<float>(static_cast<int8_t>(cw[q] >> (8 * k)));
+                        col[(4 * q + k) * G::kPitch] = wj * code;
+                    }
+            }
+        }
+    };
+    const int hi0 = min(rs, nch) - 1;  // the last chunk issued so far
+    if (producer) wait_vm(lw * hi0);   // chunk 0 has landed
+    __syncthreads();                   // weights in LDS
+    if (producer) {
+        produce(0);
+        if (nch > 1) wait_vm(lw * (hi0 - 1));
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+        if (producer) {
+            if (c + rs < nch) dma(c + rs);  // slot c % rs was last read producing chunk c
+            if (c + 1 < nch) produce(c + 1);
+            if (c + 2 < nch) wait_vm(lw * (min(c + rs, nch - 1) - (c + 2)));
+        } else {
+            const int cnt = min(G::kJC, n - c * G::kJC);
+            const float *row = P + (c & 1) * (VD * G::kPitch) + tid * G::kPitch;
+            if (cnt == G::kJC) {  // a full chunk: every read issued, then the adds
+                float4 v[G::kJC / 4];
+#pragma unroll
+                for (int q = 0; q < G::kJC / 4; ++q) v[q] = *reinterpret_cast<const float4 *>(row + 4 * q);
+#pragma unroll
+                for (int q = 0; q < G::kJC / 4; ++q) {
+                    acc = acc + v[q].x;
+                    acc = acc + v[q].y;
+                    acc = acc + v[q].z;
+                    acc = acc + v[q].w;
+                }
+            } else {  // the last chunk: eight keys per round of reads
+                int jj = 0;
+                for (; jj + 8 <= cnt; jj += 8) {
+                    const float4 v0 = *reinterpret_cast<const float4 *>(row + jj);
+                    const float4 v1 = *reinterpret_cast<const float4 *>(row + jj + 4);
+                    acc = acc + v0.x;
+                    acc = acc + v0.y;
+                    acc = acc + v0.z;
+                    acc = acc + v0.w;
+                    acc = acc + v1.x;
+                    acc = acc + v1.y;
+                    acc = acc + v1.z;
+                    acc = acc + v1.w;
+                }
+                for (; jj < cnt; ++jj) acc = acc + row[jj];
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < VD) outp[tid] = acc;
+}
+
 }  // namespace
 
 hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
@@ -337,8 +707,60 @@ hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long c
     return hipSuccess;
 }
 
+template <int VD, int JC>
+hipError_t launch_attend_stream(const AttendArgs &a, int rs, size_t lds, hipStream_t stream) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_stream_kernel<VD, JC>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const long long wgs = static_cast<long long>(a.heads) * a.t * a.batch;
+    hipLaunchKernelGGL((attend_stream_kernel<VD, JC>), dim3(static_cast<unsigned>(wgs)), dim3(kAttThreads), lds,
+                       stream, a, rs, a.batch >= 8 ? 1 : 0);
+    return hipGetLastError();
+}
+
+// Ring slots and LDS bytes of the streamed kernel: every value row of a
+// stream when the launch is small and they fit, else a ring within ~50 KiB
+// (three workgroups per CU).
+template <int VD, int JC>
+bool stream_plan(const AttendArgs &a, bool resident, int &rs, size_t &lds) {
+    using G = StreamGeo<VD, JC>;
+    const size_t nk_pad = (static_cast<size_t>(a.nk_max) + 3) & ~size_t(3);
+    const size_t fixed = 8 * nk_pad + 2 * sizeof(float) * VD * G::kPitch;
+    const size_t slot = static_cast<size_t>(JC) * VD;
+    const int nch_max = (a.nk_max + JC - 1) / JC;
+    if (resident) {
+        rs = std::max(nch_max, 2);
+        lds = fixed + slot * rs;
+        return lds <= 150 * 1024;
+    }
+    const long long room = 50 * 1024 - static_cast<long long>(fixed);
+    rs = static_cast<int>(std::min(8LL, std::max(2LL, room / static_cast<long long>(slot))));
+    lds = fixed + slot * rs;
+    return lds <= 150 * 1024;
+}
+
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
     if (a.t <= 0 || a.heads <= 0 || a.batch <= 0) return hipSuccess;
+    const bool aligned = (a.kv_stride & 15) == 0 && (reinterpret_cast<uintptr_t>(a.kq) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.vq) & 15) == 0;
+    const bool stream_ok = aligned && (a.qk & 15) == 0 && a.qk <= kStreamQk && (a.k_cols & 15) == 0 &&
+                           (a.v_cols & 15) == 0;
+    int rs = 0;
+    size_t slds = 0;
+    if (stream_ok && a.vd == 64) {
+        if (a.resident && stream_plan<64, 64>(a, true, rs, slds))
+            return launch_attend_stream<64, 64>(a, rs, slds, stream);
+        if (stream_plan<64, 32>(a, false, rs, slds)) return launch_attend_stream<64, 32>(a, rs, slds, stream);
+    }
+    if (stream_ok && a.vd == 128) {
+        if (a.resident && stream_plan<128, 64>(a, true, rs, slds))
+            return launch_attend_stream<128, 64>(a, rs, slds, stream);
+        if (stream_plan<128, 32>(a, false, rs, slds)) return launch_attend_stream<128, 32>(a, rs, slds, stream);
+    }
     const AttendArgs &b = a;
     const bool one_chunk = a.vchunk >= a.nk_max;
     const size_t vbytes = (one_chunk ? 1 : 2) * static_cast<size_t>(a.vchunk) * a.vd;

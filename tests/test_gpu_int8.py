@@ -2,7 +2,11 @@
 ABI: QuantizeRows codes and scales bit for bit, and AttendInt8Spans bit for
 bit with amd64's softmax exponent, for decode self-attention over a causal
 KV cache (1..448 keys), cross-attention over 1500 frames, GQA, windows with
-a sink, and many streams at once."""
+a sink, and many streams at once. The launch picks between a kernel that
+streams 16-byte-aligned value heads of 64 or 128 codes through LDS (all of
+a stream's rows at once for small launches, a ring of chunks for large
+ones) and a general kernel for other widths and alignments; every case
+below names the path it reaches."""
 
 import math
 
@@ -126,6 +130,79 @@ def test_many_streams():
         want = orc.attend_int8_spans(qs[b], 1, heads, kqs[b], kss[b], heads * qk, qk, vqs[b], vss[b], heads * vd, vd,
                                      nk, spans[b:b + 1], 8.0, True, 1)
         assert same_bits(got[b * heads * vd:(b + 1) * heads * vd], want), b
+
+
+def _streams_case(seed, batch, nk, heads, kv_heads, qk, vd, spans, quant_q, pad=0):
+    """`batch` independent caches of nk rows with random codes and scales,
+    in one device buffer per operand with a stream stride of
+    nk * kv_heads * max(qk, vd) + pad codes; each stream's output is checked
+    against the oracle bit for bit."""
+    g = synth.rng(seed)
+    width = max(qk, vd)
+    stride = nk * kv_heads * width + pad
+    kq = g.integers(-128, 128, size=batch * stride, dtype=np.int8)
+    vq = g.integers(-128, 128, size=batch * stride, dtype=np.int8)
+    ks = (g.random(batch * nk * kv_heads) * 0.05 + 1e-4).astype(np.float32)
+    vs = (g.random(batch * nk * kv_heads) * 0.05 + 1e-4).astype(np.float32)
+    q = g.standard_normal(batch * heads * qk).astype(np.float32)
+    spans = np.asarray(spans, np.int32).reshape(batch, 4)
+    got = _attend_gpu(q, 1, heads, kq, ks, kv_heads * qk, qk, vq, vs, kv_heads * vd, vd, spans, nk,
+                      np.float32(math.sqrt(qk)), quant_q, batch=batch, q_stride=heads * qk, kv_stride=stride,
+                      s_stride=nk * kv_heads, out_stride=heads * vd)
+    for b in range(batch):
+        kb = kq[b * stride: b * stride + nk * kv_heads * qk]
+        vb = vq[b * stride: b * stride + nk * kv_heads * vd]
+        sl = slice(b * nk * kv_heads, (b + 1) * nk * kv_heads)
+        want = orc.attend_int8_spans(q[b * heads * qk:(b + 1) * heads * qk], 1, heads, kb, ks[sl], kv_heads * qk, qk,
+                                     vb, vs[sl], kv_heads * vd, vd, nk, spans[b:b + 1], np.float32(math.sqrt(qk)),
+                                     quant_q, 1)
+        assert same_bits(got[b * heads * vd:(b + 1) * heads * vd], want), (b, spans[b])
+
+
+def _lengths(nk, batch, seed):
+    # chunk edges of the streamed kernel (48 and 64 keys), empty and full streams
+    edge = [0, 1, 7, 8, 9, 47, 48, 49, 63, 64, 65, 95, 96, 97, 191, 192, 193, nk - 1, nk]
+    g = synth.rng(seed)
+    return [edge[b] if b < len(edge) else int(g.integers(0, nk + 1)) for b in range(batch)]
+
+
+@pytest.mark.parametrize("quant_q", [True, False])
+def test_streamed_ring_of_chunks(quant_q):
+    # 72 streams x 8 heads = 576 workgroups: value rows go through a ring
+    # of chunks, refilled ahead of the products (cross-attention shape).
+    batch, nk, heads = 72, 1500, 8
+    spans = []
+    for b, n in enumerate(_lengths(nk, batch, 5)):
+        if b % 5 == 4 and n > 120:  # attention sink plus a window
+            spans.append([0, 4, n - 100, n])
+        else:
+            spans.append([0, 0, 0, n])
+    _streams_case(72, batch, nk, heads, heads, 64, 64, spans, quant_q)
+
+
+def test_streamed_all_rows_resident():
+    # 16 streams x 8 heads: every value row of a stream in LDS at once.
+    batch, nk = 16, 1500
+    spans = [[0, 0, 0, n] for n in _lengths(nk, batch, 6)]
+    _streams_case(16, batch, nk, 8, 8, 64, 64, spans, True)
+
+
+@pytest.mark.parametrize("batch", [3, 160])
+def test_streamed_value_heads_of_128(batch):
+    # vd 128 (two chain wavefronts), GQA 4 heads over 2 KV heads; 3 streams
+    # keep every row resident, 160 streams use the ring.
+    nk = 300
+    spans = [[0, 0, 0, n] for n in _lengths(nk, batch, 7)]
+    _streams_case(128 + batch, batch, nk, 4, 2, 64, 128, spans, True)
+
+
+@pytest.mark.parametrize("qk,vd,pad", [(20, 40, 0), (64, 64, 8), (48, 96, 0)])
+def test_general_kernel_shapes(qk, vd, pad):
+    # widths other than 64/128 codes, or streams off 16-byte alignment,
+    # take the general kernel
+    batch, nk = 5, 200
+    spans = [[0, 0, 0, n] for n in _lengths(nk, batch, 8)]
+    _streams_case(qk + vd + pad, batch, nk, 4, 4, qk, vd, spans, True, pad=pad)
 
 
 def test_attend_misuse():
