@@ -12,7 +12,8 @@ resident in HBM before the timed region.
 
 value = weight bytes (packed index + FP16 norms) of all GEMVs of a step /
 step time, in GB/s. The roofline object is the step's dominant launch, the
-4-bit one (HIP events around it on its stream, inside steps). detail holds per-shape
+4-bit one (HIP events on its stream around 4 back-to-back launches, inside
+steps). detail holds per-shape
 rates and the rate of one launch per GEMV (a captured graph of 8 * copies
 launches). The cpu_baseline is the C restatement of the reference's lut
 kernel (oracle/), one thread, on a bounded sample of the same sweep.
@@ -31,6 +32,8 @@ HBM_PEAK_GBS = 8000.0
 SHAPES = [(512, 512), (2048, 512), (512, 2048), (16384, 512)]
 BITS = (4, 2)
 GROUP = 128
+ROOF_REPS = 4
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "lut_kernel_4bit_sweep_pmc.txt")
 
 
 def _package():
@@ -52,6 +55,19 @@ def weight_bytes(out, inp, bits):
 
 def algorithmic_bytes(out, inp, bits):
     return weight_bytes(out, inp, bits) + 4 * inp + 4 * out + 4 * (1 << bits)
+
+
+def pmc_traffic():
+    """HBM bytes per 4-bit sweep launch from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter
+    reads for a plain copy of known size), or None without it."""
+    try:
+        for line in open(PMC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1].split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(gw, packs, seconds):
@@ -201,18 +217,22 @@ def main():
     ms = timed(step, args.steps)
     value = sweep_bytes * copies / (ms / 1e3) / 1e9
 
-    # Roofline: the step's 4-bit launch, events around it inside steps.
+    # Roofline: the step's 4-bit launch, HIP events on the plans' stream
+    # around ROOF_REPS back-to-back launches inside each step (the copies
+    # exceed the MALL, so repeats stream from HBM too).
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     for e0, e1 in ev:
         e0.record()
-        plans[4].run()
+        for _ in range(ROOF_REPS):
+            plans[4].run()
         e1.record()
         plans[2].run()
     torch.cuda.synchronize()
-    dur_s = sum(e0.elapsed_time(e1) for e0, e1 in ev) / len(ev) / 1e3
+    dur_s = sum(e0.elapsed_time(e1) for e0, e1 in ev) / len(ev) / ROOF_REPS / 1e3
     alg = sum(algorithmic_bytes(packs[k].Out, packs[k].In, 4) for c, k in by_bits[4])
     achieved = alg / dur_s / 1e9
+    traffic = pmc_traffic()
 
     # One launch per GEMV: a captured graph of the whole sweep.
     def per_launch():
@@ -257,7 +277,7 @@ def main():
                    "copies": copies, "gemvs_per_step": copies * len(packs),
                    "weight_bytes_per_step": sweep_bytes * copies, "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "lut_kernel<4,64,dev>: the step's 4-bit batch launch",
                      "launch_us": round(dur_s * 1e6, 3), "algorithmic_bytes": alg},
         "detail": detail,
