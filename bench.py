@@ -94,6 +94,46 @@ def cpu_baseline(gw, packs, seconds):
                       f"{el:.1f} s"}
 
 
+INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA, ops/s
+
+
+def batched_gemm_leg(gw, torch, reps=5):
+    """The encoder's batched CQ GEMMs: X [M x In] ~N(0, 1) times 4/2-bit
+    2048x512 and 512x2048 (FFN up/down), M in {375, 1500, 12000}, through
+    cq_gemm_dev (which picks the lut kernel or its MFMA form). Flops are the
+    dense equivalent 2*M*Out*In; for the MFMA form, mfma_util is the int8 MFMA
+    work it issues (one 32x32x32 product per 64-row block, 64-activation tile,
+    position and 32x32 quadrant) over the time, against 5.0 POP/s."""
+    g = gw.synth.rng(31)
+    out = {}
+    for bits in (4, 2):
+        for (o, i) in ((2048, 512), (512, 2048)):
+            m = gw.cq.New(gw.synth.random_packed(g, o, i, GROUP, bits, sigma=0.05))
+            for M in (375, 1500, 12000):
+                x = torch.randn(M, i, device="cuda")
+                y = torch.empty(M, o, device="cuda")
+                m.gemm_dev(y, x, M)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    m.gemm_dev(y, x, M)
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / reps
+                path = m.gemm_path(M)
+                rec = {"path": path, "us": round(us, 2), "dense_TFLOPs": round(2.0 * M * o * i / us / 1e6, 2)}
+                if path == "lut-mfma":
+                    positions = (i // GROUP) * (2 * GROUP * bits // 8)
+                    mfmas = -(-o // 64) * -(-M // 64) * positions * 4
+                    ops = mfmas * 2 * 32 * 32 * 32
+                    rec["mfma_TOPs"] = round(ops / us / 1e6, 1)
+                    rec["mfma_util"] = round(ops / (us * 1e-6) / INT8_PEAK_OPS, 4)
+                out[f"cq{bits}_{o}x{i}_M{M}"] = rec
+                del x, y
+    return out
+
+
 def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
     """Greedy decode of the synthetic 8-layer decoder (d 512, 8 heads, FFN
     2048, vocab 16384, 1500-frame int8 cross memory per stream), 200 tokens
@@ -155,6 +195,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM leg")
+    ap.add_argument("--gemm-only", action="store_true", help="run only the batched GEMM leg (prints its JSON)")
     ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (prints its JSON)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the step's 4-bit launch and a 512 MiB device copy (for rocprofv3 counters)")
@@ -169,6 +211,9 @@ def main():
     gw = _package()
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
+    if args.gemm_only:
+        print(json.dumps({"batched_gemm": batched_gemm_leg(gw, torch)}))
+        return
     if args.decode_only:
         print(json.dumps({"decode": decode_leg(gw, torch, args.decode_tokens, args.cpu_seconds, not args.no_cpu)}))
         return
@@ -284,6 +329,8 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gw, packs, args.cpu_seconds)
+    if not args.no_gemm:
+        line["batched_gemm"] = batched_gemm_leg(gw, torch)
     if not args.no_decode:
         del plans, mats
         torch.cuda.empty_cache()

@@ -35,6 +35,8 @@ SIGNATURES = {
     "cq_gemms": (c_int, [c_int, POINTER(c_void_p), POINTER(POINTER(c_float)), POINTER(c_size_t), POINTER(c_float),
                          c_size_t, c_int]),
     "cq_gemm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "cq_gemm_mfma_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "cq_gemm_path": (c_char_p, [c_void_p, c_int]),
     "cq_gemms_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p]),
     "cq_row_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "cq_row_gather_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p]),

@@ -129,6 +129,14 @@ class Matrix:
     def gemm_dev(self, y, x, rows):
         check(lib().cq_gemm_dev(self._h, c_void_p(y.data_ptr()), c_void_p(x.data_ptr()), rows, _stream()))
 
+    def gemm_mfma_dev(self, y, x, rows):
+        """The MFMA form of the lut product, whatever the grid size."""
+        check(lib().cq_gemm_mfma_dev(self._h, c_void_p(y.data_ptr()), c_void_p(x.data_ptr()), rows, _stream()))
+
+    def gemm_path(self, rows):
+        """The kernel gemm_dev runs for `rows` activations."""
+        return lib().cq_gemm_path(self._h, rows).decode()
+
     def row_dev(self, dst, r):
         check(lib().cq_row_dev(self._h, c_void_p(dst.data_ptr()), r, _stream()))
 

@@ -267,10 +267,63 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     return CQ_OK;
 }
 
+constexpr int kMfmaMinRows = 64;  // activations from which the MFMA form can run
+
+// The MFMA form pays when its grid fills a good part of the chip; below that
+// the lut kernel's workgroup per activation spreads wider.
+bool mfma_pays(cq_matrix *const *ms, int n, int rows) {
+    if (rows < kMfmaMinRows) return false;
+    const int rpw = mfma_rows_per_workgroup() / kBlockRows;
+    long long wgs = 0;
+    for (int k = 0; k < n; ++k) {
+        const int nblk = (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
+        wgs += (nblk + rpw - 1) / rpw;
+    }
+    const int ta = mfma_activations_per_workgroup();
+    wgs *= (rows + ta - 1) / ta;
+    return wgs * 8 >= 3LL * device_info().cus;
+}
+
+// One launch of the MFMA form of the lut kernel for up to kKernargJobs views
+// of one geometry and the same activations.
+int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+    const CqStore &s0 = *ms[0]->st;
+    LutLaunch a;
+    std::memset(&a, 0, sizeof a);
+    const int rpw = mfma_rows_per_workgroup() / kBlockRows;  // blocks per workgroup
+    int wg = 0;
+    for (int k = 0; k < n; ++k) {
+        if (ms[k]->out == 0) continue;
+        JobDesc &j = a.jobs[a.njobs];
+        fill_job(j, ms[k], x, dsts[k], rows);
+        a.wg0[a.njobs] = wg;
+        wg += (j.nblk + rpw - 1) / rpw;
+        ++a.njobs;
+    }
+    if (a.njobs == 0 || rows == 0) return CQ_OK;
+    const int ta = mfma_activations_per_workgroup();
+    const int max_rows = 65535 * ta;
+    for (int r0 = 0; r0 < rows; r0 += max_rows) {
+        LutLaunch b = a;
+        const int nr = std::min(max_rows, rows - r0);
+        for (int k = 0; k < b.njobs; ++k) {
+            b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
+            b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
+            b.jobs[k].rows = nr;
+        }
+        HIP_TRY(launch_lut_mfma(b, s0.width, wg, (nr + ta - 1) / ta, stream), "lut mfma launch");
+    }
+    for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
+    return CQ_OK;
+}
+
 // Launches the product of up to kMaxMatrices views sharing their tables.
 int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
     const CqStore &s0 = *ms[0]->st;
     const int mode = uses_lut(ms[0]) ? kModeLut : kModeExact;
+    if (mode == kModeLut && n <= kKernargJobs && mfma_geometry_supported(s0.width, s0.group) &&
+        mfma_pays(ms, n, rows))
+        return run_mfma(ms, n, dsts, x, rows, stream);
     if (mode == kModeLut && lut_fits(s0) && n <= kKernargJobs) return run_lut(ms, n, dsts, x, rows, stream);
     int rc = check_geometry(s0, mode);
     if (rc) return rc;
@@ -482,6 +535,25 @@ int cq_exact(const cq_matrix *m, cq_matrix **view) {
 }
 
 const char *cq_kernel_name(const cq_matrix *m) { return m && uses_lut(m) ? "lut" : "nibble4"; }
+
+int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream) {
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "cq: GEMM of %d rows", rows);
+    if (!uses_lut(m) || !mfma_geometry_supported(m->st->width, m->st->group))
+        return fail(CQ_ERR_UNSUPPORTED, "cq: the MFMA form needs a lut matrix of group 128 (group %d, %s)",
+                    m->st->group, m->exact ? "exact" : "lut");
+    if (rows == 0 || m->out == 0) return CQ_OK;
+    if (!dst || !x) return fail(CQ_ERR_MISUSE, "cq: nil device pointer");
+    cq_matrix *mm = const_cast<cq_matrix *>(m);
+    return run_mfma(&mm, 1, &dst, x, rows, static_cast<hipStream_t>(stream));
+}
+
+const char *cq_gemm_path(const cq_matrix *m, int rows) {
+    if (!m || !uses_lut(m)) return "nibble4";
+    cq_matrix *mm = const_cast<cq_matrix *>(m);
+    if (mfma_geometry_supported(m->st->width, m->st->group) && mfma_pays(&mm, 1, rows)) return "lut-mfma";
+    return "lut";
+}
 
 int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream) {
     if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");

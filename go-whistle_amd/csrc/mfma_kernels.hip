@@ -1,0 +1,346 @@
+// gfx950 MFMA form of go-whistle's lut product (internal/cq/lut.go) for
+// many activations at once, bit for bit the lut kernel's result.
+//
+// For one group g of an activation t, the lut product of row r is the exact
+// integer S = sum_j v_t[j][idx(r, j)] over the group's nibble positions j
+// (4-bit: one index per position, 128 positions; 2-bit: one pair of indices
+// per position, 64 positions), with v the int14 table entries
+// RNE(entry * 8191/M) (lut.go:235-282). Written with a one-hot expansion of
+// the indices, S is an integer matrix product over K = (position, code):
+//
+//   S[t][r] = sum_{j, c} V[t][(j, c)] * OneHot[(j, c)][r],   OneHot = [idx(r, j) == c]
+//
+// V does not fit int8, so it is split: v = 64 * h + l with l = v & 63 in
+// [0, 63] and h = v >> 6 in [-128, 127]. Per position the K dimension holds
+// both planes, l's 16 codes then h's 16 codes, and the one-hot holds 1 in
+// the l half and 64 in the h half, so one v_mfma_i32_32x32x32_i8 per
+// position sums 64 * h + l = v exactly in int32. The float fold is the lut
+// kernel's: y += float32(S) * (norm * step), groups in order from y = 0,
+// unfused.
+//
+// A table entry is RNE(f) for |f| <= 8191.5; f + 1.5 * 2^23 rounds to that
+// integer (round to nearest even, exact for |f| < 2^22), and its bit pattern
+// is 0x4B400000 + RNE(f), whose bits 0-5 are l and bits 6-13 are h.
+//
+// Work split: a workgroup of 8 wavefronts owns 64 activations and 512 weight
+// rows (one 64-row block per wavefront, two 32-row MFMA tiles). Per group:
+//   1. the activations' groups are rotated (the plain FWHT in the lut
+//      kernel's stage order) and scaled by 8191/M into LDS, 8 per wavefront;
+//   2. per chunk of 8 positions, every thread builds one table's two int8
+//      planes in LDS [position][plane][activation][16 codes] (the next chunk
+//      while the MFMAs run on the current one);
+//   3. each wavefront streams its rows' index bytes (16-byte loads in the
+//      lut layout), turns each nibble into a 16-byte one-hot in registers and
+//      runs 4 MFMAs per position (2 activation tiles x 2 row tiles);
+//   4. the int32 sums are folded into float32 y in registers.
+// MFMA roles: A = table planes (rows = activations), B = one-hot (columns =
+// weight rows), so a result row of 32 weight rows is 128 contiguous bytes
+// of y.
+#include "cq_internal.hpp"
+
+#include <hip/hip_fp16.h>
+
+namespace cqhip {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+template <int BITS>
+struct MfmaGeo {
+    static constexpr int G = 128;           // weights per group
+    static constexpr int GB = G * BITS / 8;  // index bytes per row and group: 64 or 32
+    static constexpr int NJ = 2 * GB;        // nibble positions (tables) per group: 128 or 64
+    static constexpr int KS = GB;            // K-steps per group: 2 positions x 16 codes each
+    static constexpr int CK = 8;             // positions per LDS chunk of tables
+    static constexpr int NCH = NJ / CK;      // chunks per group
+    static constexpr int UPG = GB / 16;      // 16-byte index loads per row and group
+    static constexpr int TA = 64;            // activations per workgroup
+    static constexpr int AP = G + 1;         // LDS pitch of an activation's scaled group (odd: no bank conflicts)
+};
+
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaThreads = 64 * kMfmaWaves;
+constexpr float kRneMagic = 12582912.0f;  // 1.5 * 2^23
+
+__device__ __forceinline__ uint32_t rne_bits(float f) { return __float_as_uint(f + kRneMagic); }
+
+// Byte 0 of each of four words, in order.
+__device__ __forceinline__ uint32_t bytes0(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3) {
+    const uint32_t p01 = __builtin_amdgcn_perm(e1, e0, 0x05010400u);  // e0.b0 e1.b0 e0.b1 e1.b1
+    const uint32_t p23 = __builtin_amdgcn_perm(e3, e2, 0x05010400u);  // e2.b0 e3.b0 e2.b1 e3.b1
+    return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+}
+
+// Four entries' bit patterns -> the l plane's 4 bytes (v & 63) and the h
+// plane's 4 bytes ((v >> 6) & 255).
+__device__ __forceinline__ void planes4(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, uint32_t &lo,
+                                        uint32_t &hi) {
+    lo = bytes0(e0, e1, e2, e3) & 0x3f3f3f3fu;
+    hi = bytes0(e0 >> 6, e1 >> 6, e2 >> 6, e3 >> 6);
+}
+
+// 16-byte one-hot of a nibble n holding `val` (1 or 64) at byte n.
+__device__ __forceinline__ i32x4 one_hot(uint32_t n, unsigned long long val) {
+    const unsigned long long one = val << ((n & 7u) << 3);
+    const bool low = n < 8u;
+    const unsigned long long lo = low ? one : 0ull, hi = low ? 0ull : one;
+    i32x4 r;
+    r.x = static_cast<int>(lo);
+    r.y = static_cast<int>(lo >> 32);
+    r.z = static_cast<int>(hi);
+    r.w = static_cast<int>(hi >> 32);
+    return r;
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
+    using M = MfmaGeo<BITS>;
+    constexpr int G = M::G, TA = M::TA, AP = M::AP, CK = M::CK;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float *av = reinterpret_cast<float *>(smem);                    // [TA][AP] scaled rotated groups
+    float *stp = av + TA * AP;                                       // [TA] steps of the group
+    int8_t *tab = reinterpret_cast<int8_t *>(stp + TA);              // [2][CK][2][TA][16] table planes
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
+
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kKernargJobs; ++k)
+        if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.wg0[k]) jb = k;
+    const JobDesc &J = a.jobs[jb];
+    const int blk = (static_cast<int>(blockIdx.x) - a.wg0[jb]) * kMfmaWaves + w;  // this wavefront's block
+    const bool rows_here = blk < J.nblk;
+    const int gblk = J.blk0 + blk;
+    const int t0 = blockIdx.y * TA;
+    const int groups = J.groups;
+
+    i32x16 acc[2][2];     // [activation tile][row tile]
+    float yv[2][2][16];   // [activation tile][row tile][element]
+#pragma unroll
+    for (int at = 0; at < 2; ++at)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) yv[at][rt][i] = 0.0f;
+
+    auto build = [&](int c, int buf) {
+        for (int e = tid; e < TA * CK; e += kMfmaThreads) {
+            const int t = e % TA, jc = e / TA;
+            const int j = c * CK + jc;
+            uint32_t b[16];
+            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
+                const float x = av[t * AP + j];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const float f = J.cb[q] * x;
+                    b[q] = rne_bits(f);
+                }
+            } else {  // lutTables2Generic (lut.go:239-258): code q = hi << 2 | lo
+                const float x0 = av[t * AP + 2 * j], x1 = av[t * AP + 2 * j + 1];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const float l = J.cb[q & 3] * x0, h = J.cb[q >> 2] * x1;
+                    const float s = l + h;
+                    b[q] = rne_bits(s);
+                }
+            }
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) planes4(b[4 * q], b[4 * q + 1], b[4 * q + 2], b[4 * q + 3], lo[q], hi[q]);
+            int8_t *dst = tab + ((static_cast<size_t>(buf) * CK + jc) * 2 * TA + t) * 16;
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4 *>(dst + TA * 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        }
+    };
+
+    // The wavefront's rows' index bytes of group g, unit u (lut layout:
+    // 16-byte units of a 64-row block side by side); word q of a unit holds
+    // the index bytes of chunk 4u + q.
+    auto load_unit = [&](int g, int u, uint32_t (&d)[2][4]) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            if (rows_here) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(
+                    J.idx + ((static_cast<size_t>(gblk) * J.units + g * M::UPG + u) * 64 + rt * 32 + l32) * 16);
+                d[rt][0] = v.x; d[rt][1] = v.y; d[rt][2] = v.z; d[rt][3] = v.w;
+            } else {
+                d[rt][0] = d[rt][1] = d[rt][2] = d[rt][3] = 0u;
+            }
+        }
+    };
+
+    for (int g = 0; g < groups; ++g) {
+        uint32_t cur[2][4], nxt[2][4];
+        load_unit(g, 0, nxt);
+        float nrm[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+            nrm[rt] = rows_here ? __half2float(__ushort_as_half(
+                                      J.norm[(static_cast<size_t>(gblk) * groups + g) * 64 + rt * 32 + l32]))
+                                : 0.0f;
+
+        // 1. Rotation and bound of the group of each activation (lut.go:158-178).
+        for (int tt = w; tt < TA; tt += kMfmaWaves) {
+            const int t = t0 + tt;
+            float v[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int col = g * G + e * 64 + lane;
+                v[e] = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
+            }
+#pragma unroll
+            for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float p = __shfl_xor(v[e], h);
+                    v[e] = (lane & h) ? p - v[e] : v[e] + p;
+                }
+            }
+            {  // stage h = 64 within the lane
+                const float p = v[0], q = v[1];
+                v[0] = p + q;
+                v[1] = p - q;
+            }
+            float mx = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                if constexpr (BITS == 4) {
+                    mx = fmaxf(mx, fabsf(v[e]));
+                } else {
+                    const float p = __shfl_xor(v[e], 1);
+                    const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                    mx = fmaxf(mx, s2);
+                }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float m = J.cb_max * mx;
+            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[e] * inv;
+            if (lane == 0) stp[tt] = m * J.lut_step;
+        }
+        __syncthreads();
+        build(0, 0);
+#pragma unroll
+        for (int at = 0; at < 2; ++at)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) acc[at][rt] = i32x16{};
+        __syncthreads();
+
+        // 2./3. Chunks of CK positions (one index word per row): the next
+        // chunk's tables are built while this chunk's MFMAs run.
+        const unsigned long long val = half ? 64ull : 1ull;
+        for (int u = 0; u < M::UPG; ++u) {
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cur[rt][q] = nxt[rt][q];
+            if (u + 1 < M::UPG) load_unit(g, u + 1, nxt);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = 4 * u + q;
+                if (c + 1 < M::NCH) build(c + 1, (c + 1) & 1);
+                if (rows_here) {
+                    // lane half 0 reads a position's l plane, half 1 its h plane
+                    const int8_t *tb = tab + (static_cast<size_t>(c & 1) * CK * 2 + half) * TA * 16;
+                    i32x4 A[2][2];  // [position parity][activation tile]
+#pragma unroll
+                    for (int at = 0; at < 2; ++at)
+                        A[0][at] = *reinterpret_cast<const i32x4 *>(tb + (at * 32 + l32) * 16);
+#pragma unroll
+                    for (int jc = 0; jc < CK; ++jc) {
+                        if (jc + 1 < CK) {
+#pragma unroll
+                            for (int at = 0; at < 2; ++at)
+                                A[(jc + 1) & 1][at] = *reinterpret_cast<const i32x4 *>(
+                                    tb + (static_cast<size_t>(jc + 1) * 2 * TA + at * 32 + l32) * 16);
+                        }
+#pragma unroll
+                        for (int rt = 0; rt < 2; ++rt) {
+                            // position jc: index byte jc / 2 of the chunk's word, nibble jc % 2
+                            const uint32_t n = (cur[rt][q] >> (4 * jc)) & 15u;
+                            const i32x4 B = one_hot(n, val);
+#pragma unroll
+                            for (int at = 0; at < 2; ++at)
+                                acc[at][rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[jc & 1][at], B, acc[at][rt], 0, 0, 0);
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+
+        // 4. Fold group g into y, in group order (lut.go:297-310).
+        if (rows_here) {
+#pragma unroll
+            for (int at = 0; at < 2; ++at)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int tt = at * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+                    const float step = stp[tt];
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) {
+                        const int s = acc[at][rt][i];
+                        const float coef = nrm[rt] * step;
+                        const float prod = static_cast<float>(s) * coef;
+                        yv[at][rt][i] = yv[at][rt][i] + prod;
+                    }
+                }
+        }
+        __syncthreads();  // av and stp are rewritten by the next group
+    }
+
+    if (rows_here) {
+#pragma unroll
+        for (int at = 0; at < 2; ++at)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int t = t0 + at * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+                if (t >= J.rows) continue;
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const int r = gblk * 64 + rt * 32 + l32;
+                    if (r >= J.row0 && r < J.row0 + J.out)
+                        J.y[static_cast<long long>(t) * J.y_stride + (r - J.row0)] = yv[at][rt][i];
+                }
+            }
+    }
+}
+
+template <int BITS>
+size_t mfma_lds_bytes() {
+    using M = MfmaGeo<BITS>;
+    return sizeof(float) * (M::TA * M::AP + M::TA) + static_cast<size_t>(2) * M::CK * 2 * M::TA * 16;
+}
+
+template <int BITS>
+hipError_t launch_mfma_t(const LutLaunch &a, int wg, int act_tiles, hipStream_t s) {
+    static bool attr = false;
+    const size_t lds = mfma_lds_bytes<BITS>();
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_mfma_kernel<BITS>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(lut_mfma_kernel<BITS>, dim3(wg, act_tiles), dim3(kMfmaThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool mfma_geometry_supported(int bits, int group) { return group == 128 && (bits == 2 || bits == 4); }
+
+int mfma_rows_per_workgroup() { return 64 * kMfmaWaves; }
+
+int mfma_activations_per_workgroup() { return MfmaGeo<4>::TA; }
+
+hipError_t launch_lut_mfma(const LutLaunch &a, int bits, int wg, int act_tiles, hipStream_t s) {
+    if (wg <= 0 || act_tiles <= 0) return hipSuccess;
+    if (bits == 4) return launch_mfma_t<4>(a, wg, act_tiles, s);
+    if (bits == 2) return launch_mfma_t<2>(a, wg, act_tiles, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace cqhip

@@ -92,6 +92,16 @@ int cq_gemms(int n, cq_matrix *const *ms, float *const *dsts, const size_t *dst_
  * memory, work is queued on `stream` (a hipStream_t; NULL = the null
  * stream) and the call returns without waiting. */
 int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream);
+/* The same product, always in the MFMA form of the lut kernel (one-hot
+ * indices times int8 table planes on v_mfma_i32_32x32x32_i8, exact int32
+ * sums, the lut fold), bit for bit cq_gemm_dev's result. No counterpart in
+ * the reference: the encoder's batched products (many frames at once) call
+ * it; cq_gemm_dev picks it by itself when its grid is large enough. Group
+ * 128, 2 or 4 bits, not an Exact view; else CQ_ERR_UNSUPPORTED. */
+int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream);
+/* The kernel cq_gemm_dev runs for `rows` activations: "lut", "lut-mfma" or
+ * "nibble4". */
+const char *cq_gemm_path(const cq_matrix *m, int rows);
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream);
 int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream);
 /* Rows gathered by index: dst[i] = scale * Row(rows[i]) for i < n, rows a
