@@ -690,6 +690,317 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
     if (tid < VD) outp[tid] = acc;
 }
 
+// Max over the NW wavefronts of a workgroup.
+template <int NW>
+__device__ __forceinline__ float block_max_nw(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    if constexpr (NW == 1) {
+        return __shfl(v, 0);
+    } else {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        if (lane == 0) red[wave] = v;
+        __syncthreads();
+        float r = red[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) r = fmaxf(r, red[w]);
+        __syncthreads();
+        return r;
+    }
+}
+
+// A workgroup barrier, kept for a single wavefront too: it is also what
+// orders one lane's LDS writes before another lane's reads for the compiler.
+template <int NW>
+__device__ __forceinline__ void block_sync() {
+    __syncthreads();
+}
+
+constexpr int kChainVd = 64;  // value codes per head of the chain kernel: one per lane of wavefront 0
+
+// AttendInt8Spans for one (stream, query row, head) per workgroup of NW
+// wavefronts, value heads of 64 codes, key heads of at most 64 codes,
+// 16-byte aligned rows. Same arithmetic as attend_kernel. Lane d of
+// wavefront 0 carries output d's in-order chain (axpysI8) and forms each
+// product itself: per key one LDS byte read, a sign-extending convert, the
+// rounded multiply by the key's weight (read four at a time) and the add.
+// Value rows stream from HBM straight into LDS (global_load_lds, 16-byte
+// pieces, rows [key][64 codes]): with RES every row of the stream, issued by
+// all wavefronts under the logits' tail and the softmax; otherwise a ring of
+// rs chunks of JC keys that wavefront 0 refills behind the chain. The
+// logits and the softmax are spread over the NW wavefronts.
+template <int NW, int JC, bool RES>
+__global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int rs, int swz) {
+    constexpr int NT = 64 * NW;
+    constexpr int KPT = 6;                  // keys per thread per round of logits
+    constexpr int LPC = JC / 16;            // wavefront DMA loads per chunk (16 keys of 64 codes each)
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int per = a.heads * a.t;
+    const int w = blockIdx.x;
+    int b, r;
+    if (swz) {
+        const int full = (a.batch & ~7) * per;
+        if (w < full) {
+            b = (w & 7) + 8 * (w / (8 * per));
+            r = (w >> 3) % per;
+        } else {
+            const int w2 = w - full, rem = a.batch & 7;
+            b = (a.batch & ~7) + w2 % rem;
+            r = w2 / rem;
+        }
+    } else {
+        b = w / per;
+        r = w - b * per;
+    }
+    const int h = r % a.heads, i = r / a.heads;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kv_heads = a.k_cols / a.qk;
+    const int kv = h / (a.heads / kv_heads);
+    const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
+    const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
+    const int n = len0 + len1;
+    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
+    float *outp = a.out + b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * kChainVd;
+    if (n == 0) {
+        if (tid < kChainVd) outp[tid] = 0.0f;
+        return;
+    }
+
+    const int nk_pad = (a.nk_max + 3) & ~3;
+    float *s = reinterpret_cast<float *>(smem);   // logits, exponentials, then weights
+    float *tt = s + nk_pad;                       // exponentials transposed to [lane][index]
+    const int r8max = ((a.nk_max >> 3) + 3) & ~3;
+    int8_t *ring = reinterpret_cast<int8_t *>(tt + 8 * r8max);
+    __shared__ float red[8];
+    __shared__ __align__(16) int8_t q8[kStreamQk];
+    __shared__ __align__(16) float qf[kStreamQk];
+    __shared__ float sq_sh, sum_sh;
+
+    const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
+    const int8_t *kq = a.kq + b * a.kv_stride;
+    const float *ks = a.ks + b * a.s_stride;
+    const int8_t *vq = a.vq + b * a.kv_stride;
+    const float *vs = a.vs + b * a.s_stride;
+    auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
+    const int nch = (n + JC - 1) / JC;
+
+    // Wavefront-wide DMA load u (16 keys) of chunk c into ring slot c % rs.
+    auto dma = [&](int c, int u) {
+        const int j0 = c * JC, cnt = min(JC, n - j0);
+        int8_t *slot = ring + (c % rs) * (JC * kChainVd);
+        const int p = u * 64 + lane;
+        const int jj = p >> 2, seg = p & 3;
+        const int key = key_of(j0 + (jj < cnt ? jj : 0));
+        dma16(vq + static_cast<long long>(key) * a.v_cols + kv * kChainVd + seg * 16, lds_offset(slot + u * 64 * 16));
+    };
+
+    // 1. The query, then each thread's first KPT keys, in flight together.
+    const int kpieces = a.qk / 16;
+    const float qv = tid < a.qk ? qi[tid] : 0.0f;
+    int4 kw[KPT][kStreamQk / 16];
+    float skr[KPT];
+    auto kload = [&](int g, int j) {
+        const int key = key_of(j);
+        const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
+#pragma unroll
+        for (int p = 0; p < kStreamQk / 16; ++p)
+            if (p < kpieces) kw[g][p] = *reinterpret_cast<const int4 *>(krow + 16 * p);
+        skr[g] = ks[static_cast<long long>(key) * kv_heads + kv];
+    };
+    auto logit = [&](int g) -> float {
+        if (a.quant_q) {
+            int dot = 0;  // exact in any order
+#pragma unroll
+            for (int p = 0; p < kStreamQk / 16; ++p)
+                if (p < kpieces) {
+                    const int4 qw = *reinterpret_cast<const int4 *>(q8 + 16 * p);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].x, qw.x, dot, false);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].y, qw.y, dot, false);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].z, qw.z, dot, false);
+                    dot = __builtin_amdgcn_sdot4(kw[g][p].w, qw.w, dot, false);
+                }
+            const float scl = sq_sh * skr[g];
+            const float t1 = static_cast<float>(dot) * scl;
+            return t1 / a.scale;
+        }
+        float dot = 0.0f;  // in order
+#pragma unroll
+        for (int p = 0; p < kStreamQk / 16; ++p)
+            if (p < kpieces) {
+                const int cw[4] = {kw[g][p].x, kw[g][p].y, kw[g][p].z, kw[g][p].w};
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float pr = qf[16 * p + e] * static_cast<float>(static_cast<int8_t>(cw[e >> 2] >> (8 * (e & 3))));
+                    dot = dot + pr;
+                }
+            }
+        const float t1 = dot * skr[g];
+        return t1 / a.scale;
+    };
+#pragma unroll
+    for (int g = 0; g < KPT; ++g)
+        if (tid + g * NT < n) kload(g, tid + g * NT);
+
+    // QuantizeRow of the query head (int8.go:226-228); qk <= 64 <= NT.
+    if (tid < a.qk) qf[tid] = qv;
+    if (a.quant_q) {
+        const float m = block_max_nw<NW>(tid < a.qk ? fabsf(qv) : 0.0f, red);
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+        if (tid < a.qk) {
+            float rq = rintf(qv / sc);
+            rq = fminf(fmaxf(rq, -128.0f), 127.0f);
+            q8[tid] = static_cast<int8_t>(static_cast<int>(rq));
+        }
+        if (tid == 0) sq_sh = sc;
+    }
+    __syncthreads();
+
+    // Logits (int8Logits / dotsF32I8), KPT keys per thread per round.
+    for (int j0 = 0; j0 < n; j0 += KPT * NT) {
+        if (j0 > 0) {
+#pragma unroll
+            for (int g = 0; g < KPT; ++g)
+                if (j0 + tid + g * NT < n) kload(g, j0 + tid + g * NT);
+        }
+#pragma unroll
+        for (int g = 0; g < KPT; ++g) {
+            const int j = j0 + tid + g * NT;
+            if (j < n) s[j] = logit(g);
+        }
+    }
+
+    // Value rows start streaming now (the compiler's own loads drained
+    // first: loads retire in order).
+    wait_vm_const<0>();
+    if constexpr (RES) {
+        for (int u = wave; u < nch * LPC; u += NW) dma(u / LPC, u % LPC);
+    } else {
+        const int c0 = min(rs, nch);
+        for (int c = 0; c < c0; ++c)
+            for (int u = 0; u < LPC; ++u) dma(c, u);
+    }
+    __syncthreads();
+
+    // 2. softmaxInPlace with amd64's expSubSum; the eight lane sums read a
+    // copy transposed to [lane][index].
+    float m0 = -INFINITY;
+    for (int j = tid; j < n; j += NT) m0 = fmaxf(m0, s[j]);
+    const float m = block_max_nw<NW>(m0, red);
+    const int n8 = n & ~7;
+    const bool kernel_path = n8 > 0;
+    const int r8 = ((n8 >> 3) + 3) & ~3;
+    for (int j = tid; j < n8; j += NT) {
+        const float e = exp_lane(s[j] - m);
+        s[j] = e;
+        tt[(j & 7) * r8 + (j >> 3)] = e;
+    }
+    for (int j = n8 + tid; j < n; j += NT) s[j] = exp_generic(s[j] - m);
+    block_sync<NW>();
+    if (tid < 8 && kernel_path) {  // lane tid of the 8-lane sum, elements in order
+        float acc = 0.0f;
+        const float *row = tt + tid * r8;
+        const int cnt = n8 >> 3;
+        int k = 0;
+        for (; k + 16 <= cnt; k += 16) {
+            const float4 v0 = *reinterpret_cast<const float4 *>(row + k);
+            const float4 v1 = *reinterpret_cast<const float4 *>(row + k + 4);
+            const float4 v2 = *reinterpret_cast<const float4 *>(row + k + 8);
+            const float4 v3 = *reinterpret_cast<const float4 *>(row + k + 12);
+            acc = acc + v0.x; acc = acc + v0.y; acc = acc + v0.z; acc = acc + v0.w;
+            acc = acc + v1.x; acc = acc + v1.y; acc = acc + v1.z; acc = acc + v1.w;
+            acc = acc + v2.x; acc = acc + v2.y; acc = acc + v2.z; acc = acc + v2.w;
+            acc = acc + v3.x; acc = acc + v3.y; acc = acc + v3.z; acc = acc + v3.w;
+        }
+        for (; k < cnt; ++k) acc = acc + row[k];
+        red[tid] = acc;
+    }
+    block_sync<NW>();
+    if (tid == 0) {
+        float sum;
+        if (kernel_path) {
+            const float x0 = red[0] + red[4], x1 = red[1] + red[5], x2 = red[2] + red[6], x3 = red[3] + red[7];
+            const float h0 = x0 + x1, h1 = x2 + x3;
+            sum = h0 + h1;
+            if (n8 != n) {
+                float tail = 0.0f;
+                for (int j = n8; j < n; ++j) tail = tail + s[j];
+                sum = sum + tail;
+            }
+        } else {
+            sum = 0.0f;
+            for (int j = 0; j < n; ++j) sum = sum + s[j];
+        }
+        sum_sh = sum;
+    }
+    block_sync<NW>();
+    const float sum = sum_sh;
+    for (int j = tid; j < n; j += NT) {
+        const float p = s[j] / sum;
+        s[j] = p * vs[static_cast<long long>(key_of(j)) * kv_heads + kv];
+    }
+    if constexpr (RES) wait_vm_const<0>();  // this wavefront's value rows have landed
+    __syncthreads();                         // weights and (RES) every value row in LDS
+    if (wave != 0) return;
+
+    // 3. axpysI8 (int8kernel.go:360-368): lane d adds fl(w_j * code_jd) in key order.
+    float acc = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+        if constexpr (!RES) wait_vm(LPC * (min(c + rs, nch) - 1 - c));  // chunk c has landed
+        const int j0 = c * JC, cnt = min(JC, n - j0);
+        const int8_t *slot = ring + (c % rs) * (JC * kChainVd) + lane;
+        const float *wj = s + j0;
+        int jj = 0;
+        // Blocks of 32 keys: every code and weight read issued, then the
+        // products and the adds in key order.
+        for (; jj + 32 <= cnt; jj += 32) {
+            float cd[32];
+            float4 wv[8];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) cd[k] = static_cast<float>(slot[(jj + k) * kChainVd]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) wv[q] = *reinterpret_cast<const float4 *>(wj + jj + 4 * q);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float p0 = wv[q].x * cd[4 * q], p1 = wv[q].y * cd[4 * q + 1];
+                const float p2 = wv[q].z * cd[4 * q + 2], p3 = wv[q].w * cd[4 * q + 3];
+                acc = acc + p0;
+                acc = acc + p1;
+                acc = acc + p2;
+                acc = acc + p3;
+            }
+        }
+        for (; jj + 8 <= cnt; jj += 8) {
+            const float4 w0 = *reinterpret_cast<const float4 *>(wj + jj);
+            const float4 w1 = *reinterpret_cast<const float4 *>(wj + jj + 4);
+            float cd[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cd[k] = static_cast<float>(slot[(jj + k) * kChainVd]);
+            const float p0 = w0.x * cd[0], p1 = w0.y * cd[1], p2 = w0.z * cd[2], p3 = w0.w * cd[3];
+            const float p4 = w1.x * cd[4], p5 = w1.y * cd[5], p6 = w1.z * cd[6], p7 = w1.w * cd[7];
+            acc = acc + p0;
+            acc = acc + p1;
+            acc = acc + p2;
+            acc = acc + p3;
+            acc = acc + p4;
+            acc = acc + p5;
+            acc = acc + p6;
+            acc = acc + p7;
+        }
+        for (; jj < cnt; ++jj) {
+            const float pr = wj[jj] * static_cast<float>(slot[jj * kChainVd]);
+            acc = acc + pr;
+        }
+        if constexpr (!RES) {
+            if (c + rs < nch) {
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this chunk's slot reads are done
+                for (int u = 0; u < LPC; ++u) dma(c + rs, u);
+            }
+        }
+    }
+    if (lane < kChainVd) outp[lane] = acc;
+}
+
 }  // namespace
 
 hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
@@ -743,12 +1054,45 @@ bool stream_plan(const AttendArgs &a, bool resident, int &rs, size_t &lds) {
     return lds <= 150 * 1024;
 }
 
+template <int NW, int JC, bool RES>
+hipError_t launch_attend_chain(const AttendArgs &a, int rs, size_t lds, hipStream_t stream) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_chain_kernel<NW, JC, RES>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const long long wgs = static_cast<long long>(a.heads) * a.t * a.batch;
+    hipLaunchKernelGGL((attend_chain_kernel<NW, JC, RES>), dim3(static_cast<unsigned>(wgs)), dim3(64 * NW), lds,
+                       stream, a, rs, a.batch >= 8 ? 1 : 0);
+    return hipGetLastError();
+}
+
+// LDS of the chain kernel: logits, their transposed copy, and rs chunks of
+// JC value rows.
+size_t chain_lds(const AttendArgs &a, int jc, int rs) {
+    const size_t nk_pad = (static_cast<size_t>(a.nk_max) + 3) & ~size_t(3);
+    const size_t r8 = ((static_cast<size_t>(a.nk_max) >> 3) + 3) & ~size_t(3);
+    return 4 * nk_pad + 4 * 8 * r8 + static_cast<size_t>(rs) * jc * kChainVd;
+}
+
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
     if (a.t <= 0 || a.heads <= 0 || a.batch <= 0) return hipSuccess;
     const bool aligned = (a.kv_stride & 15) == 0 && (reinterpret_cast<uintptr_t>(a.kq) & 15) == 0 &&
                          (reinterpret_cast<uintptr_t>(a.vq) & 15) == 0;
     const bool stream_ok = aligned && (a.qk & 15) == 0 && a.qk <= kStreamQk && (a.k_cols & 15) == 0 &&
                            (a.v_cols & 15) == 0;
+    if (stream_ok && a.vd == kChainVd) {
+        if (a.resident) {
+            const int rs = std::max(1, (a.nk_max + 63) / 64);
+            const size_t lds = chain_lds(a, 64, rs);
+            if (lds <= 150 * 1024) return launch_attend_chain<4, 64, true>(a, rs, lds, stream);
+        }
+        const int rs = 4;
+        const size_t lds = chain_lds(a, 32, rs);
+        if (lds <= 150 * 1024) return launch_attend_chain<1, 32, false>(a, rs, lds, stream);
+    }
     int rs = 0;
     size_t slds = 0;
     if (stream_ok && a.vd == 64) {

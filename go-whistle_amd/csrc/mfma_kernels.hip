@@ -65,19 +65,20 @@ constexpr float kRneMagic = 12582912.0f;  // 1.5 * 2^23
 
 __device__ __forceinline__ uint32_t rne_bits(float f) { return __float_as_uint(f + kRneMagic); }
 
-// Byte 0 of each of four words, in order.
-__device__ __forceinline__ uint32_t bytes0(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3) {
-    const uint32_t p01 = __builtin_amdgcn_perm(e1, e0, 0x05010400u);  // e0.b0 e1.b0 e0.b1 e1.b1
-    const uint32_t p23 = __builtin_amdgcn_perm(e3, e2, 0x05010400u);  // e2.b0 e3.b0 e2.b1 e3.b1
-    return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
-}
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // Four entries' bit patterns -> the l plane's 4 bytes (v & 63) and the h
-// plane's 4 bytes ((v >> 6) & 255).
+// plane's 4 bytes ((v >> 6) & 255): the entries' low halfwords are paired,
+// shifted right by 6 two at a time (bits 6-13 land in each halfword's low
+// byte), and the wanted bytes gathered.
 __device__ __forceinline__ void planes4(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, uint32_t &lo,
                                         uint32_t &hi) {
-    lo = bytes0(e0, e1, e2, e3) & 0x3f3f3f3fu;
-    hi = bytes0(e0 >> 6, e1 >> 6, e2 >> 6, e3 >> 6);
+    const uint32_t q01 = __builtin_amdgcn_perm(e1, e0, 0x05040100u);  // e0.lo16 | e1.lo16 << 16
+    const uint32_t q23 = __builtin_amdgcn_perm(e3, e2, 0x05040100u);  // e2.lo16 | e3.lo16 << 16
+    lo = __builtin_amdgcn_perm(q23, q01, 0x06040200u) & 0x3f3f3f3fu;  // byte 0 of each halfword
+    const u16x2 r01 = __builtin_bit_cast(u16x2, q01) >> static_cast<unsigned short>(6);
+    const u16x2 r23 = __builtin_bit_cast(u16x2, q23) >> static_cast<unsigned short>(6);
+    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, r23), __builtin_bit_cast(uint32_t, r01), 0x06040200u);
 }
 
 // 16-byte one-hot of a nibble n holding `val` (1 or 64) at byte n.
