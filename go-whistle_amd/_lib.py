@@ -52,6 +52,14 @@ SIGNATURES = {
                                    c_int, c_float, c_int, c_int, c_void_p]),
     "kv_append_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_longlong, c_longlong, c_void_p,
                               c_int, c_void_p]),
+    "kv_append_rope_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_longlong, c_longlong,
+                                   c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "kv_attend_int8_rope_dev": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p,
+                                        c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_longlong, c_longlong,
+                                        c_void_p, c_int, c_float, c_int, c_int, c_void_p, c_void_p, c_void_p,
+                                        c_void_p]),
+    "cq_gemms_fused_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p, c_void_p,
+                                   c_int, c_void_p]),
     "nd_zcrmsnorm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "nd_rope_dev": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "nd_argmax_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),

@@ -178,6 +178,19 @@ def gemms_dev(ms, ys, x, rows):
     check(lib().cq_gemms_dev(n, hs, ds, c_void_p(x.data_ptr()), rows, _stream()))
 
 
+def gemms_fused_dev(ms, ys, x, rows, norm_gain=None, resid=None, act=0):
+    """gemms_dev with the input rows ZCRMSNorm'ed by norm_gain first, and
+    the output y = resid + product (one matrix) or y = silu(product) (act 1)."""
+    n = len(ms)
+    if n != len(ys):
+        raise CQPanic(f"cq: GEMMs of {n} matrices into {len(ys)} outputs")
+    hs = (c_void_p * max(n, 1))(*[m.handle for m in ms])
+    ds = (c_void_p * max(n, 1))(*[c_void_p(y.data_ptr()) for y in ys])
+    ptr = lambda t: c_void_p(t.data_ptr()) if t is not None else None
+    check(lib().cq_gemms_fused_dev(n, hs, ds, c_void_p(x.data_ptr()), rows, ptr(norm_gain), ptr(resid), act,
+                                   _stream()))
+
+
 class Batch:
     """A plan of independent products on device tensors (cq_batch_*): job k
     is ms[k].GEMM of rows[k] activations xs[k] into ys[k]. run() queues one

@@ -209,6 +209,23 @@ void fill_job(JobDesc &j, const cq_matrix *m, const float *x, float *y, int rows
     j.lut_step = s.lut_step;
 }
 
+// A fused prologue/epilogue request (see JobDesc).
+struct Fuse {
+    const float *ngain = nullptr;
+    const float *resid = nullptr;
+    long long resid_stride = 0;
+    int act = 0;
+    bool any() const { return ngain || resid || act; }
+};
+
+void apply_fuse(JobDesc &j, const Fuse *f) {
+    if (!f) return;
+    j.ngain = f->ngain;
+    j.resid = f->resid;
+    j.resid_stride = f->resid_stride;
+    j.act = f->act;
+}
+
 constexpr int kLutTile = 4;     // blocks per tile of the lut kernel
 constexpr int kLutWaves = 4;    // wavefronts per workgroup
 constexpr int kLutChunk = 4;    // groups per LDS chunk
@@ -230,7 +247,8 @@ int blocks_per_workgroup(long long blocks) {
 
 // One launch of the lut kernel for up to kKernargJobs views of one geometry
 // and the same activations.
-int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
+            const Fuse *fz = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     LutLaunch a;
     std::memset(&a, 0, sizeof a);
@@ -240,6 +258,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
         if (ms[k]->out == 0) continue;
         JobDesc &j = a.jobs[a.njobs++];
         fill_job(j, ms[k], x, dsts[k], rows);
+        apply_fuse(j, fz);
         blocks += static_cast<long long>(j.nblk) * rows;
         groups_max = std::max(groups_max, j.groups);
     }
@@ -260,6 +279,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
         for (int k = 0; k < b.njobs; ++k) {
             b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
             b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
+            if (b.jobs[k].resid) b.jobs[k].resid += static_cast<long long>(r0) * b.jobs[k].resid_stride;
         }
         HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, kLutWaves, wg, nr, lds, stream), "lut launch");
     }
@@ -286,7 +306,8 @@ bool mfma_pays(cq_matrix *const *ms, int n, int rows) {
 
 // One launch of the MFMA form of the lut kernel for up to kKernargJobs views
 // of one geometry and the same activations.
-int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
+             const Fuse *fz = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     LutLaunch a;
     std::memset(&a, 0, sizeof a);
@@ -296,6 +317,7 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
         if (ms[k]->out == 0) continue;
         JobDesc &j = a.jobs[a.njobs];
         fill_job(j, ms[k], x, dsts[k], rows);
+        apply_fuse(j, fz);
         a.wg0[a.njobs] = wg;
         wg += (j.nblk + rpw - 1) / rpw;
         ++a.njobs;
@@ -309,6 +331,7 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
         for (int k = 0; k < b.njobs; ++k) {
             b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
             b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
+            if (b.jobs[k].resid) b.jobs[k].resid += static_cast<long long>(r0) * b.jobs[k].resid_stride;
             b.jobs[k].rows = nr;
         }
         HIP_TRY(launch_lut_mfma(b, s0.width, wg, (nr + ta - 1) / ta, stream), "lut mfma launch");
@@ -318,13 +341,17 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
 }
 
 // Launches the product of up to kMaxMatrices views sharing their tables.
-int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
+                const Fuse *fz = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     const int mode = uses_lut(ms[0]) ? kModeLut : kModeExact;
     if (mode == kModeLut && n <= kKernargJobs && mfma_geometry_supported(s0.width, s0.group) &&
         mfma_pays(ms, n, rows))
-        return run_mfma(ms, n, dsts, x, rows, stream);
-    if (mode == kModeLut && lut_fits(s0) && n <= kKernargJobs) return run_lut(ms, n, dsts, x, rows, stream);
+        return run_mfma(ms, n, dsts, x, rows, stream, fz);
+    if (mode == kModeLut && lut_fits(s0) && n <= kKernargJobs) return run_lut(ms, n, dsts, x, rows, stream, fz);
+    if (fz && fz->any())
+        return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel (this is %s, group bytes %d)",
+                    mode == kModeLut ? "lut" : "exact", s0.group_bytes);
     int rc = check_geometry(s0, mode);
     if (rc) return rc;
     ProdArgs a;
@@ -370,14 +397,15 @@ int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x,
 // cq.GEMMs on device pointers: one launch per run of up to kMaxMatrices
 // matrices that share their tables and kernel, else one launch per matrix
 // (each gives the same bits either way: kernel.go:127-133).
-int gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+int gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, hipStream_t stream,
+              const Fuse *fz = nullptr) {
     int k = 0;
     while (k < n) {
         int e = k + 1;
         while (e < n && e - k < kMaxMatrices && uses_lut(ms[e]) == uses_lut(ms[k]) &&
                shares_tables(*ms[k]->st, *ms[e]->st))
             ++e;
-        int rc = run_product(ms + k, e - k, dsts + k, x, rows, stream);
+        int rc = run_product(ms + k, e - k, dsts + k, x, rows, stream, fz);
         if (rc) return rc;
         k = e;
     }
@@ -571,6 +599,28 @@ int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x
             return fail(CQ_ERR_MISUSE, "cq: GEMMs over matrices of different input widths");
     if (rows == 0 || n == 0) return CQ_OK;
     return gemms_dev(n, ms, dsts, x, rows, static_cast<hipStream_t>(stream));
+}
+
+int cq_gemms_fused_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows,
+                       const float *norm_gain, const float *resid, int act, void *stream) {
+    if (n < 0 || (n > 0 && (!ms || !dsts))) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d matrices", n);
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d rows", rows);
+    if (act != 0 && act != 1) return fail(CQ_ERR_MISUSE, "cq: activation %d", act);
+    if (resid && (n != 1 || act != 0))
+        return fail(CQ_ERR_MISUSE, "cq: a residual add takes one matrix and no activation");
+    for (int k = 0; k < n; ++k) {
+        if (!ms[k] || ms[k]->st->in != ms[0]->st->in)
+            return fail(CQ_ERR_MISUSE, "cq: GEMMs over matrices of different input widths");
+        if (!uses_lut(ms[k]))
+            return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel, not %s", cq_kernel_name(ms[k]));
+    }
+    if (rows == 0 || n == 0) return CQ_OK;
+    Fuse f;
+    f.ngain = norm_gain;
+    f.resid = resid;
+    f.resid_stride = resid ? ms[0]->out : 0;
+    f.act = act;
+    return gemms_dev(n, ms, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
 }
 
 int cq_gemm(const cq_matrix *m, float *dst, size_t dst_len, const float *x, size_t x_len, int rows) {
@@ -827,10 +877,13 @@ int kv_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, in
     return CQ_OK;
 }
 
-int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+static int attend_impl(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
                        const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
                        int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
-                       float scale, int quant_q, int batch, void *stream) {
+                       float scale, int quant_q, int batch, const float *rope_cos, const float *rope_sin,
+                       const int32_t *qpos, void *stream) {
+    if (rope_cos && (!rope_sin || !qpos || qk % 2 != 0))
+        return fail(CQ_ERR_MISUSE, "needle: RoPE of query heads of %d", qk);
     if (qk <= 0 || vd <= 0 || k_cols % qk != 0)
         return fail(CQ_ERR_MISUSE, "needle: int8 keys of %d in chunks of %d", k_cols, qk);
     const int kv_heads = k_cols / qk;
@@ -850,9 +903,28 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
     const int vchunk = (wgs <= 2LL * device_info().cus && nk_max <= fit) ? std::max(1, nk_max) : std::min(256, fit / 2);
     const int resident = wgs <= 2LL * device_info().cus ? 1 : 0;
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
-                 kv_stride, s_stride, spans, nk_max, vchunk, resident, scale, quant_q, batch};
+                 kv_stride, s_stride, spans, nk_max, vchunk, resident, scale, quant_q, batch,
+                 rope_cos, rope_sin, qpos};
     HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");
     return CQ_OK;
+}
+
+int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                       const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                       int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
+                       float scale, int quant_q, int batch, void *stream) {
+    return attend_impl(out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, kv_stride,
+                       s_stride, spans, nk_max, scale, quant_q, batch, nullptr, nullptr, nullptr, stream);
+}
+
+int kv_attend_int8_rope_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                            const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                            int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans,
+                            int nk_max, float scale, int quant_q, int batch, const float *cos_t, const float *sin_t,
+                            const int32_t *qpos, void *stream) {
+    if (!cos_t) return fail(CQ_ERR_MISUSE, "needle: RoPE tables missing");
+    return attend_impl(out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, kv_stride,
+                       s_stride, spans, nk_max, scale, quant_q, batch, cos_t, sin_t, qpos, stream);
 }
 
 // ---- decode-step float blocks -------------------------------------------------
@@ -890,14 +962,30 @@ int nd_add_dev(float *x, const float *y, long long n, void *stream) {
     return CQ_OK;
 }
 
-int kv_append_dev(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
-                  long long s_stride, const int32_t *pos, int cap, void *stream) {
+static int append_impl(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
+                       long long s_stride, const int32_t *pos, int cap, const float *cos_t, const float *sin_t,
+                       void *stream) {
     if (width <= 0 || cols % width != 0)
         return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);
     if (batch < 0 || cap < 0) return fail(CQ_ERR_MISUSE, "needle: append of %d streams", batch);
-    HIP_TRY(launch_append(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, static_cast<hipStream_t>(stream)),
+    if (width > 256) return fail(CQ_ERR_UNSUPPORTED, "needle: append in chunks of %d (at most 256)", width);
+    if (cos_t && (!sin_t || width % 2 != 0)) return fail(CQ_ERR_MISUSE, "needle: RoPE of heads of %d", width);
+    HIP_TRY(launch_append(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, cos_t, sin_t,
+                          static_cast<hipStream_t>(stream)),
             "append launch");
     return CQ_OK;
+}
+
+int kv_append_dev(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
+                  long long s_stride, const int32_t *pos, int cap, void *stream) {
+    return append_impl(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, nullptr, nullptr, stream);
+}
+
+int kv_append_rope_dev(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
+                       long long s_stride, const int32_t *pos, int cap, const float *cos_t, const float *sin_t,
+                       void *stream) {
+    if (!cos_t) return fail(CQ_ERR_MISUSE, "needle: RoPE tables missing");
+    return append_impl(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, cos_t, sin_t, stream);
 }
 
 }  // extern "C"

@@ -73,6 +73,14 @@ struct JobDesc {
     int rows;              // activations
     float cb[16];
     float cb_max, lut_step;
+    // Fused prologue and epilogue (null / 0: none). ngain: each activation
+    // row is first ZCRMSNorm'ed with this gain (length in). resid: y = resid
+    // + product, resid rows resid_stride floats apart (may be y itself).
+    // act 1: y = silu(product).
+    const float *ngain;
+    const float *resid;
+    long long resid_stride;
+    int act;
 };
 
 // A workgroup's share of a job: blocks [blk, blk + nb) (counted from the
@@ -141,6 +149,10 @@ struct AttendArgs {
     float scale;
     int quant_q;
     int batch;
+    // RoPE of the query heads before they are quantised (null: none): row
+    // qpos[b * t + i] of the tables, pairs (j, j + qk/2).
+    const float *rope_cos, *rope_sin;
+    const int32_t *qpos;
 };
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream);
 
@@ -152,6 +164,7 @@ hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, hipStrea
 hipError_t launch_silu(float *x, long long n, hipStream_t s);
 hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s);
 hipError_t launch_append(int8_t *q, float *sc, const float *x, int batch, int cols, int width, long long q_stride,
-                         long long s_stride, const int32_t *pos, int cap, hipStream_t s);
+                         long long s_stride, const int32_t *pos, int cap, const float *cos_t, const float *sin_t,
+                         hipStream_t s);
 
 }  // namespace cqhip

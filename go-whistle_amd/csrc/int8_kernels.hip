@@ -24,6 +24,7 @@
 //      chunks of value codes, which the workgroup's other wavefronts stage
 //      with 16-byte loads one chunk ahead.
 #include "cq_internal.hpp"
+#include "cq_device.hpp"
 
 #include <algorithm>
 #include <climits>
@@ -51,35 +52,21 @@ __global__ __launch_bounds__(256) void quantize_kernel(int8_t *q, float *s, cons
     if (lane == 0) s[c] = sc;
 }
 
-// One lane of the amd64 kernel's exponent (exp_amd64.s:84-112), constants
-// bit for bit (exp_amd64.s:7-51).
-__device__ __forceinline__ float exp_lane(float x) {
-    const float log2e = 0x1.715476p+0f, ln2hi = 0x1.63p-1f, ln2lo = -0x1.bd0106p-13f;
-    const float c6 = 0x1.a0d2cep-13f, c5 = 0x1.6e879cp-10f, c4 = 0x1.111210p-7f;
-    const float c3 = 0x1.555382p-5f, c2 = 0x1.555554p-3f, c1 = 0x1p-1f;
-    const float lo = -0x1.5d51ecp+6f;
-    const bool lt = x < lo;
-    const float xc = (x != x) ? x : (lo > x ? lo : x);
-    const float k = rintf(xc * log2e);
-    float r = fmaf(-k, ln2hi, xc);
-    r = fmaf(-k, ln2lo, r);
-    const float r2 = r * r;
-    float p = c6;
-    p = fmaf(p, r, c5);
-    p = fmaf(p, r, c4);
-    p = fmaf(p, r, c3);
-    p = fmaf(p, r, c2);
-    p = fmaf(p, r, c1);
-    float yv = fmaf(p, r2, r);
-    yv = yv + 1.0f;
-    const int ki = (k != k || k >= 2147483648.0f || k < -2147483648.0f) ? INT_MIN : static_cast<int>(k);
-    const float e = __uint_as_float(__float_as_uint(yv) + (static_cast<unsigned>(ki) << 23));
-    return lt ? 0.0f : e;
-}
-
 __device__ __forceinline__ float exp_generic(float d) { return static_cast<float>(exp(static_cast<double>(d))); }
 
 constexpr int kAttThreads = 256;
+
+// Element c of query head qi, after RoPE at table row p when a.rope_cos is
+// set (rope.go:69-81; pairs (j, j + qk/2)).
+__device__ __forceinline__ float query_value(const AttendArgs &a, const float *qi, int p, int c) {
+    if (!a.rope_cos) return qi[c];
+    const int half = a.qk / 2;
+    const int j = c < half ? c : c - half;
+    float o1, o2;
+    rope_pair(qi[j], qi[j + half], a.rope_cos[static_cast<long long>(p) * half + j],
+              a.rope_sin[static_cast<long long>(p) * half + j], o1, o2);
+    return c < half ? o1 : o2;
+}
 
 __device__ __forceinline__ float block_max(float v, float *red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -115,6 +102,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     int8_t *vbuf = reinterpret_cast<int8_t *>(s + ((a.nk_max + 3) & ~3));  // value codes: one or two chunks
     __shared__ float red[8];
     __shared__ __align__(16) int8_t q8[256];
+    __shared__ float qg[256];
     __shared__ float sq_sh, sum_sh;
 
     const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
@@ -124,14 +112,18 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const float *vs = a.vs + b * a.s_stride;
     auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
 
-    // QuantizeRow of the query head (int8.go:226-228).
+    // The query head (after RoPE when asked), then QuantizeRow of it
+    // (int8.go:226-228).
+    const int qp = a.rope_cos ? a.qpos[static_cast<long long>(b) * a.t + i] : 0;
+    for (int c = tid; c < a.qk; c += kAttThreads) qg[c] = query_value(a, qi, qp, c);
+    __syncthreads();
     if (a.quant_q) {
         float m = 0.0f;
-        for (int c = tid; c < a.qk; c += kAttThreads) m = fmaxf(m, fabsf(qi[c]));
+        for (int c = tid; c < a.qk; c += kAttThreads) m = fmaxf(m, fabsf(qg[c]));
         m = block_max(m, red);
         const float sc = m > 0.0f ? m / 127.0f : 1.0f;
         for (int c = tid; c < a.qk; c += kAttThreads) {
-            float r = rintf(qi[c] / sc);
+            float r = rintf(qg[c] / sc);
             r = fminf(fmaxf(r, -128.0f), 127.0f);
             q8[c] = static_cast<int8_t>(static_cast<int>(r));
         }
@@ -213,7 +205,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
             const int w = *reinterpret_cast<const int *>(krow + c);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float pr = qi[c + e] * static_cast<float>(static_cast<int8_t>(w >> (8 * e)));
+                const float pr = qg[c + e] * static_cast<float>(static_cast<int8_t>(w >> (8 * e)));
                 dot = dot + pr;
             }
         }
@@ -463,7 +455,8 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
 
     // 1. The query, then the first four keys of this thread, in flight together.
     const int kpieces = a.qk / 16;
-    const float qv = tid < a.qk ? qi[tid] : 0.0f;
+    const int qp = a.rope_cos ? a.qpos[static_cast<long long>(b) * a.t + i] : 0;
+    const float qv = tid < a.qk ? query_value(a, qi, qp, tid) : 0.0f;
     constexpr int KPT = G::kKpt;
     int4 kw[KPT][kStreamQk / 16];
     float skr[KPT], vsr[KPT];
@@ -797,7 +790,8 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
 
     // 1. The query, then each thread's first KPT keys, in flight together.
     const int kpieces = a.qk / 16;
-    const float qv = tid < a.qk ? qi[tid] : 0.0f;
+    const int qp = a.rope_cos ? a.qpos[static_cast<long long>(b) * a.t + i] : 0;
+    const float qv = tid < a.qk ? query_value(a, qi, qp, tid) : 0.0f;
     int4 kw[KPT][kStreamQk / 16];
     float skr[KPT];
     auto kload = [&](int g, int j) {

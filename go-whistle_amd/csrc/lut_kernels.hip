@@ -31,6 +31,7 @@
 //  3. The thread that owns a row folds the chunk's groups into the row's y
 //     (in LDS) in group order; y goes out after the last chunk.
 #include "cq_internal.hpp"
+#include "cq_device.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -168,6 +169,15 @@ __global__ __launch_bounds__(1024) void lut_kernel(LutLaunch a) {
     const uint8_t *idx = J->idx;
     const float *x = J->x + static_cast<long long>(act) * J->x_stride;
 
+    // Fused ZCRMSNorm of the activation row (norm.go:53-109): its divisor,
+    // from four float64 partial sums on lanes 0-3 of every wavefront.
+    float rms = 1.0f;
+    if (J->ngain) {
+        const double part = lane < 4 ? zc_partial(x, J->in, lane) : 0.0;
+        const double p0 = __shfl(part, 0), p1 = __shfl(part, 1), p2 = __shfl(part, 2), p3 = __shfl(part, 3);
+        rms = zc_rms(p0, p1, p2, p3, J->in);
+    }
+
     // LDS: tables of a chunk of gc groups, the chunk's int32 sums of a tile,
     // the chunk's steps, and y of the workgroup's rows (folded chunk by chunk).
     const int gc = a.gc, tb = a.tb;
@@ -213,7 +223,12 @@ __global__ __launch_bounds__(1024) void lut_kernel(LutLaunch a) {
             for (int e = 0; e < E; ++e) {
                 const int i = G >= 64 ? e * 64 + lane : lane;
                 const int col = g * G + i;
-                v[e] = (i < G && col < J->in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
+                float xv = (i < G && col < J->in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
+                if (J->ngain && i < G && col < J->in) {
+                    const float gx = J->ngain[col] * xv;
+                    xv = gx / rms;
+                }
+                v[e] = xv;
             }
 #pragma unroll
             for (int h = 1; h < G; h <<= 1) {  // stages h = 1, 2, ..., G/2 (kernel.go:384-393)
@@ -321,7 +336,14 @@ __global__ __launch_bounds__(1024) void lut_kernel(LutLaunch a) {
 
     for (int t = tid; t < bc * 64; t += blockDim.x) {
         const int r = blk0 * 64 + t;
-        if (r >= J->row0 && r < J->row0 + J->out) J->y[static_cast<long long>(act) * J->y_stride + (r - J->row0)] = yacc[t];
+        if (r >= J->row0 && r < J->row0 + J->out) {
+            float out = yacc[t];
+            if (J->resid)
+                out = J->resid[static_cast<long long>(act) * J->resid_stride + (r - J->row0)] + out;
+            else if (J->act == 1)
+                out = silu_value(out);
+            J->y[static_cast<long long>(act) * J->y_stride + (r - J->row0)] = out;
+        }
     }
 }
 

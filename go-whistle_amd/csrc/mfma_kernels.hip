@@ -37,6 +37,7 @@
 // weight rows), so a result row of 32 weight rows is 128 contiguous bytes
 // of y.
 #include "cq_internal.hpp"
+#include "cq_device.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -115,6 +116,21 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
     const int t0 = blockIdx.y * TA;
     const int groups = J.groups;
 
+    // Fused ZCRMSNorm of the activation rows (norm.go:53-109): divisors of
+    // the workgroup's activations, four float64 partial sums each.
+    __shared__ double zpart[4 * TA];
+    __shared__ float zrms[TA];
+    if (J.ngain) {
+        for (int e = tid; e < 4 * TA; e += kMfmaThreads) {
+            const int t = t0 + e / 4;
+            zpart[e] = t < J.rows ? zc_partial(J.x + static_cast<long long>(t) * J.x_stride, J.in, e % 4) : 0.0;
+        }
+        __syncthreads();
+        for (int e = tid; e < TA; e += kMfmaThreads)
+            zrms[e] = zc_rms(zpart[4 * e], zpart[4 * e + 1], zpart[4 * e + 2], zpart[4 * e + 3], J.in);
+        __syncthreads();
+    }
+
     i32x16 acc[2][2];     // [activation tile][row tile]
     float yv[2][2][16];   // [activation tile][row tile][element]
 #pragma unroll
@@ -187,7 +203,12 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const int col = g * G + e * 64 + lane;
-                v[e] = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
+                float xv = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
+                if (J.ngain && t < J.rows && col < J.in) {
+                    const float gx = J.ngain[col] * xv;
+                    xv = gx / zrms[tt];
+                }
+                v[e] = xv;
             }
 #pragma unroll
             for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
@@ -302,8 +323,14 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
                     const int r = gblk * 64 + rt * 32 + l32;
-                    if (r >= J.row0 && r < J.row0 + J.out)
-                        J.y[static_cast<long long>(t) * J.y_stride + (r - J.row0)] = yv[at][rt][i];
+                    if (r >= J.row0 && r < J.row0 + J.out) {
+                        float out = yv[at][rt][i];
+                        if (J.resid)
+                            out = J.resid[static_cast<long long>(t) * J.resid_stride + (r - J.row0)] + out;
+                        else if (J.act == 1)
+                            out = silu_value(out);
+                        J.y[static_cast<long long>(t) * J.y_stride + (r - J.row0)] = out;
+                    }
                 }
             }
     }

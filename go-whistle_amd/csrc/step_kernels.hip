@@ -8,14 +8,15 @@
 //                      [x1·cos − x2·sin, x2·cos + x1·sin], products rounded.
 //   argmax_kernel      argmax (internal/decoder/greedy.go:181-191): the first
 //                      index of the largest value.
-//   silu_kernel        x·σ(x) with σ from the amd64 exponent kernel's lane
-//                      (exp_amd64.s:84-112) on non-positive arguments: the
-//                      synthetic decoder's FFN activation (no reference
-//                      counterpart; defined so that CPU and GPU agree bit for bit).
+//   silu_kernel        silu_value (cq_device.hpp): the synthetic decoder's FFN
+//                      activation (no reference counterpart; defined so that
+//                      CPU and GPU agree bit for bit).
 //   add_kernel         x += y (the residual adds, decoder.go / block.go).
 //   append_kernel      Int8Rows.Append (internal/needle/int8.go:125-141) of one
-//                      row per stream at the stream's position.
+//                      row per stream at the stream's position, optionally
+//                      after RoPE of each head at that position.
 #include "cq_internal.hpp"
+#include "cq_device.hpp"
 
 #include <climits>
 
@@ -117,46 +118,10 @@ __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *
     if (tid == 0) out[r] = si[0] == INT_MAX ? 0 : si[0];
 }
 
-// One lane of the amd64 exponent kernel (exp_amd64.s:84-112), for x <= 0.
-__device__ __forceinline__ float exp_lane(float x) {
-    const float log2e = 0x1.715476p+0f, ln2hi = 0x1.63p-1f, ln2lo = -0x1.bd0106p-13f;
-    const float c6 = 0x1.a0d2cep-13f, c5 = 0x1.6e879cp-10f, c4 = 0x1.111210p-7f;
-    const float c3 = 0x1.555382p-5f, c2 = 0x1.555554p-3f, c1 = 0x1p-1f;
-    const float lo = -0x1.5d51ecp+6f;
-    const bool lt = x < lo;
-    const float xc = (x != x) ? x : (lo > x ? lo : x);
-    const float k = rintf(xc * log2e);
-    float r = fmaf(-k, ln2hi, xc);
-    r = fmaf(-k, ln2lo, r);
-    const float r2 = r * r;
-    float p = c6;
-    p = fmaf(p, r, c5);
-    p = fmaf(p, r, c4);
-    p = fmaf(p, r, c3);
-    p = fmaf(p, r, c2);
-    p = fmaf(p, r, c1);
-    float yv = fmaf(p, r2, r);
-    yv = yv + 1.0f;
-    const int ki = (k != k || k >= 2147483648.0f || k < -2147483648.0f) ? INT_MIN : static_cast<int>(k);
-    const float e = __uint_as_float(__float_as_uint(yv) + (static_cast<unsigned>(ki) << 23));
-    return lt ? 0.0f : e;
-}
-
 __global__ __launch_bounds__(256) void silu_kernel(float *x, long long n) {
     const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float v = x[i];
-    float s;
-    if (v >= 0.0f) {
-        const float e = exp_lane(-v);
-        const float d = 1.0f + e;
-        s = 1.0f / d;
-    } else {
-        const float e = exp_lane(v);
-        const float d = 1.0f + e;
-        s = e / d;
-    }
-    x[i] = v * s;
+    x[i] = silu_value(x[i]);
 }
 
 __global__ __launch_bounds__(256) void add_kernel(float *x, const float *y, long long n) {
@@ -165,26 +130,59 @@ __global__ __launch_bounds__(256) void add_kernel(float *x, const float *y, long
 }
 
 // Int8Rows.Append of stream b's row at its position pos[b]: QuantizeRow
-// per chunk of width (int8.go:36-55), one wavefront per chunk.
+// per chunk of width (int8.go:36-55), one wavefront per chunk. With cos_t,
+// each chunk (a head) is first rotated by RoPE at pos[b] (rope.go:69-81):
+// value i < width/2 pairs with i + width/2.
 __global__ __launch_bounds__(256) void append_kernel(int8_t *q, float *s, const float *x, int cols, int width,
                                                      long long q_stride, long long s_stride, const int32_t *pos,
-                                                     int cap) {
+                                                     int cap, const float *cos_t, const float *sin_t) {
     const int b = blockIdx.y, lane = threadIdx.x & 63;
     const int c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
     const int chunks = cols / width;
     const int p = pos[b];
     if (c >= chunks || p < 0 || p >= cap) return;
     const float *xc = x + static_cast<long long>(b) * cols + static_cast<long long>(c) * width;
+    float v[4];  // width <= 256
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = lane + 64 * k;
+        v[k] = i < width ? xc[i] : 0.0f;
+    }
+    if (cos_t) {
+        const int half = width / 2;
+        const float *cs = cos_t + static_cast<long long>(p) * half, *sn = sin_t + static_cast<long long>(p) * half;
+        float rv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = lane + 64 * k;
+            rv[k] = v[k];
+            if (i < width) {
+                const int j = i < half ? i : i - half;
+                const float a = xc[j], bb = xc[j + half];
+                float o1, o2;
+                rope_pair(a, bb, cs[j], sn[j], o1, o2);
+                rv[k] = i < half ? o1 : o2;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = rv[k];
+    }
     float m = 0.0f;
-    for (int i = lane; i < width; i += 64) m = fmaxf(m, fabsf(xc[i]));
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (lane + 64 * k < width) m = fmaxf(m, fabsf(v[k]));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     const float sc = m > 0.0f ? m / 127.0f : 1.0f;
     int8_t *qc = q + b * q_stride + static_cast<long long>(p) * cols + static_cast<long long>(c) * width;
-    for (int i = lane; i < width; i += 64) {
-        float r = rintf(xc[i] / sc);
-        r = fminf(fmaxf(r, -128.0f), 127.0f);
-        qc[i] = static_cast<int8_t>(static_cast<int>(r));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = lane + 64 * k;
+        if (i < width) {
+            float r = rintf(v[k] / sc);
+            r = fminf(fmaxf(r, -128.0f), 127.0f);
+            qc[i] = static_cast<int8_t>(static_cast<int>(r));
+        }
     }
     if (lane == 0) s[b * s_stride + static_cast<long long>(p) * chunks + c] = sc;
 }
@@ -225,11 +223,12 @@ hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s) {
 }
 
 hipError_t launch_append(int8_t *q, float *sc, const float *x, int batch, int cols, int width, long long q_stride,
-                         long long s_stride, const int32_t *pos, int cap, hipStream_t s) {
+                         long long s_stride, const int32_t *pos, int cap, const float *cos_t, const float *sin_t,
+                         hipStream_t s) {
     if (batch <= 0) return hipSuccess;
     const int chunks = cols / width;
     hipLaunchKernelGGL(append_kernel, dim3(blocks_for(chunks, 4), batch), dim3(256), 0, s, q, sc, x, cols, width,
-                       q_stride, s_stride, pos, cap);
+                       q_stride, s_stride, pos, cap, cos_t, sin_t);
     return hipGetLastError();
 }
 

@@ -48,10 +48,29 @@ def quantize_rows_dev(q, s, x, rows, cols, width):
 
 
 def attend_int8_dev(out, q, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, spans, nk_max, scale, quant_q,
-                    batch=1, out_stride=0, q_stride=0, kv_stride=0, s_stride=0):
-    """AttendInt8Spans on device tensors for `batch` streams (see cqhip.h)."""
-    check(lib().kv_attend_int8_dev(c_void_p(out.data_ptr()), out_stride, c_void_p(q.data_ptr()), q_stride, t, heads,
-                                   c_void_p(kq.data_ptr()), c_void_p(ks.data_ptr()), k_cols, qk,
-                                   c_void_p(vq.data_ptr()), c_void_p(vs.data_ptr()), v_cols, vd, kv_stride, s_stride,
-                                   c_void_p(spans.data_ptr()), nk_max, float(scale), 1 if quant_q else 0, batch,
-                                   _stream()))
+                    batch=1, out_stride=0, q_stride=0, kv_stride=0, s_stride=0, rope=None):
+    """AttendInt8Spans on device tensors for `batch` streams (see cqhip.h).
+    rope = (cos, sin, qpos): the query heads are first rotated by RoPE at
+    row qpos[b*t + i] of the tables."""
+    args = [c_void_p(out.data_ptr()), out_stride, c_void_p(q.data_ptr()), q_stride, t, heads,
+            c_void_p(kq.data_ptr()), c_void_p(ks.data_ptr()), k_cols, qk, c_void_p(vq.data_ptr()),
+            c_void_p(vs.data_ptr()), v_cols, vd, kv_stride, s_stride, c_void_p(spans.data_ptr()), nk_max, float(scale),
+            1 if quant_q else 0, batch]
+    if rope is None:
+        check(lib().kv_attend_int8_dev(*args, _stream()))
+    else:
+        cos, sin, qpos = rope
+        check(lib().kv_attend_int8_rope_dev(*args, c_void_p(cos.data_ptr()), c_void_p(sin.data_ptr()),
+                                            c_void_p(qpos.data_ptr()), _stream()))
+
+
+def append_dev(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, rope=None):
+    """Int8Rows.Append of one row per stream at pos[b] (see cqhip.h); rope =
+    (cos, sin): each chunk is first rotated by RoPE at row pos[b]."""
+    args = [c_void_p(q.data_ptr()), c_void_p(s.data_ptr()), c_void_p(x.data_ptr()), batch, cols, width, q_stride,
+            s_stride, c_void_p(pos.data_ptr()), cap]
+    if rope is None:
+        check(lib().kv_append_dev(*args, _stream()))
+    else:
+        cos, sin = rope
+        check(lib().kv_append_rope_dev(*args, c_void_p(cos.data_ptr()), c_void_p(sin.data_ptr()), _stream()))

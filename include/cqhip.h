@@ -103,6 +103,16 @@ int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, v
  * "nibble4". */
 const char *cq_gemm_path(const cq_matrix *m, int rows);
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream);
+/* cq_gemms_dev with the decode step's neighbours fused into the product
+ * (no reference counterpart: one launch instead of three, results bit for
+ * bit those of the separate steps). norm_gain non-null: every input row is
+ * first ZCRMSNorm.Apply'd with that gain (internal/needle/norm.go:53-109).
+ * resid non-null (n = 1): dst = resid + product, the residual add of the
+ * decoder's layer body (resid may be dst). act 1 (no resid): dst =
+ * silu(product), the synthetic decoder's FFN activation (as nd_silu_dev).
+ * lut matrices only. */
+int cq_gemms_fused_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows,
+                       const float *norm_gain, const float *resid, int act, void *stream);
 int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream);
 /* Rows gathered by index: dst[i] = scale * Row(rows[i]) for i < n, rows a
  * device int32 array: the decoder's scaled token-embedding lookup for
@@ -151,6 +161,15 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
                        const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
                        int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
                        float scale, int quant_q, int batch, void *stream);
+/* The same with the query heads first rotated by RoPE (Rope.apply,
+ * internal/needle/rope.go:69-81) at row qpos[b*t + i] of the (positions x
+ * qk/2) cos/sin tables: Attention.Extend's rotated query
+ * (internal/needle/attention.go:345-415) without a separate pass. */
+int kv_attend_int8_rope_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                            const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                            int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans,
+                            int nk_max, float scale, int quant_q, int batch, const float *cos_t, const float *sin_t,
+                            const int32_t *qpos, void *stream);
 
 /* Int8Rows.Append (int8.go:125-141) on a device KV cache for `batch`
  * streams: stream b's row x + b*cols is quantised per chunk of width
@@ -159,6 +178,12 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
  * position outside [0, cap) is skipped. */
 int kv_append_dev(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
                   long long s_stride, const int32_t *pos, int cap, void *stream);
+/* The same with each chunk (a key head) first rotated by RoPE (rope.go:
+ * 69-81) at row pos[b] of the (positions x width/2) cos/sin tables: the
+ * rotated key appended (attention.go:345-415). width <= 256, even. */
+int kv_append_rope_dev(int8_t *q, float *s, const float *x, int batch, int cols, int width, long long q_stride,
+                       long long s_stride, const int32_t *pos, int cap, const float *cos_t, const float *sin_t,
+                       void *stream);
 
 /* ---- float blocks of a decode step, on device memory -------------------- */
 
