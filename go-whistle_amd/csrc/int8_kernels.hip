@@ -995,6 +995,270 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     if (lane < kChainVd) outp[lane] = acc;
 }
 
+// One 4-byte global load per active lane straight into LDS: lane l's word
+// lands at lds + 4 * l (global_load_lds_dword, M0 = lds); lanes off in EXEC
+// neither load nor write.
+__device__ __forceinline__ void dma4(const void *src, unsigned lds) {
+    asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+constexpr int kRingJc = 32;                     // keys per ring chunk
+constexpr int kRingSlot = kRingJc * 64 + kRingJc * 4;  // 64 codes per key, then the keys' scales
+
+// AttendInt8Spans for one (stream, query row, head) per single-wavefront
+// workgroup, key and value heads of 64 codes, 16-byte aligned rows: the
+// many-stream form. Key chunks, then value chunks, of 32 keys stream through
+// one LDS ring of RS slots (global_load_lds, refilled behind the reads); a
+// slot holds the chunk's rows [key][64 codes] and the 32 keys' scales, so no
+// load of the kernel waits on its own: every wavefront keeps RS chunks of
+// HBM reads in flight.
+//   1. the query; the logits chunk by chunk, two lanes per key (exact int32
+//      dots, or the float32 query in order);
+//   2. the softmax (amd64's expSubSum) with the eight lane sums read at
+//      stride 8;
+//   3. per value chunk the keys' weights p_j * vscale_j, then lane d's
+//      in-order chain of fl(w_j * code_jd).
+// Same arithmetic as attend_kernel.
+template <int RS>
+__global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) {
+    constexpr int JC = kRingJc, ROW = 64;
+    constexpr int LPC = JC * ROW / 1024 + 1;  // wavefront DMA loads per chunk: 2 of rows, 1 of scales
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int per = a.heads * a.t;
+    const int w = blockIdx.x;
+    int b, r;
+    if (swz) {
+        const int full = (a.batch & ~7) * per;
+        if (w < full) {
+            b = (w & 7) + 8 * (w / (8 * per));
+            r = (w >> 3) % per;
+        } else {
+            const int w2 = w - full, rem = a.batch & 7;
+            b = (a.batch & ~7) + w2 % rem;
+            r = w2 / rem;
+        }
+    } else {
+        b = w / per;
+        r = w - b * per;
+    }
+    const int h = r % a.heads, i = r / a.heads;
+    const int lane = threadIdx.x;
+    const int kv_heads = a.k_cols / a.qk;
+    const int kv = h / (a.heads / kv_heads);
+    const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
+    const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
+    const int n = len0 + len1;
+    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
+    float *outp = a.out + b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * ROW;
+    if (n == 0) {
+        outp[lane] = 0.0f;
+        return;
+    }
+    const int nk_pad = (a.nk_max + 3) & ~3;
+    float *s = reinterpret_cast<float *>(smem);  // logits, exponentials, then weights
+    int8_t *ring = reinterpret_cast<int8_t *>(s + nk_pad);
+    __shared__ float qf[ROW];
+    __shared__ float red[8];
+
+    const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * ROW;
+    const int8_t *kq = a.kq + b * a.kv_stride;
+    const float *ks = a.ks + b * a.s_stride;
+    const int8_t *vq = a.vq + b * a.kv_stride;
+    const float *vs = a.vs + b * a.s_stride;
+    auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
+    const int nch = (n + JC - 1) / JC, total = 2 * nch;  // key chunks, then value chunks
+
+    // Ring chunk g (g < nch: key chunk g, else value chunk g - nch) into
+    // slot g % RS: rows as 16-byte pieces, then the scales (lanes < 32).
+    auto dma = [&](int g) {
+        const bool keys = g < nch;
+        const int c = keys ? g : g - nch;
+        const int j0 = c * JC, cnt = min(JC, n - j0);
+        int8_t *slot = ring + (g % RS) * kRingSlot;
+        const int8_t *base = keys ? kq + kv * ROW : vq + kv * ROW;
+        const long long cols = keys ? a.k_cols : a.v_cols;
+#pragma unroll
+        for (int u = 0; u < LPC - 1; ++u) {
+            const int p = u * 64 + lane;
+            const int jj = p >> 2, seg = p & 3;
+            const int key = key_of(j0 + (jj < cnt ? jj : 0));
+            dma16(base + static_cast<long long>(key) * cols + seg * 16, lds_offset(slot + u * 64 * 16));
+        }
+        const float *sc = keys ? ks : vs;
+        const int key = key_of(j0 + (lane < cnt ? lane : 0));
+        if (lane < JC) dma4(sc + static_cast<long long>(key) * kv_heads + kv, lds_offset(slot + JC * ROW));
+    };
+    // Chunk g has landed: at most the chunks issued after it are in flight.
+    auto wait_chunk = [&](int g) {
+        if (g + RS - 1 < total) wait_vm_const<LPC * (RS - 1)>();
+        else wait_vm(LPC * (total - 1 - g));
+    };
+    auto refill = [&](int g) {  // after chunk g's reads: chunk g + RS into its slot
+        if (g + RS < total) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot's reads are done
+            dma(g + RS);
+        }
+    };
+
+    // 1. The query (the compiler's loads drained before the ring starts:
+    // loads retire in order).
+    const int qp = a.rope_cos ? a.qpos[static_cast<long long>(b) * a.t + i] : 0;
+    const float qv = query_value(a, qi, qp, lane);
+    wait_vm_const<0>();
+    for (int g = 0; g < min(RS, total); ++g) dma(g);
+    qf[lane] = qv;
+    float sq = 0.0f;
+    int4 q4[2];  // this lane's half of the int8 query (32 codes)
+    const int half = lane >> 5;
+    if (a.quant_q) {
+        float m = fabsf(qv);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+        float rq = rintf(qv / sc);
+        rq = fminf(fmaxf(rq, -128.0f), 127.0f);
+        const int code = static_cast<int>(rq) & 255;
+        // gather this lane's 32 query codes (lanes 32*half ..) into 8 words
+        int words[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int c0 = __shfl(code, 32 * half + 4 * k), c1 = __shfl(code, 32 * half + 4 * k + 1);
+            const int c2 = __shfl(code, 32 * half + 4 * k + 2), c3 = __shfl(code, 32 * half + 4 * k + 3);
+            words[k] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+        }
+        q4[0] = make_int4(words[0], words[1], words[2], words[3]);
+        q4[1] = make_int4(words[4], words[5], words[6], words[7]);
+        sq = sc;
+    }
+    __syncthreads();
+
+    // Logits: lane (key jj = lane % 32, half) dots its 32 codes; the halves
+    // add up exactly (int32), the float query sums in order on half 0.
+    for (int g = 0; g < nch; ++g) {
+        wait_chunk(g);
+        const int j0 = g * JC, cnt = min(JC, n - j0);
+        const int jj = lane & 31;
+        const int8_t *slot = ring + (g % RS) * kRingSlot;
+        const int8_t *row = slot + jj * ROW;
+        const float kscale = reinterpret_cast<const float *>(slot + JC * ROW)[jj];
+        float lg = 0.0f;
+        if (a.quant_q) {
+            const int4 k0 = *reinterpret_cast<const int4 *>(row + 32 * half);
+            const int4 k1 = *reinterpret_cast<const int4 *>(row + 32 * half + 16);
+            int dot = 0;
+            dot = __builtin_amdgcn_sdot4(k0.x, q4[0].x, dot, false);
+            dot = __builtin_amdgcn_sdot4(k0.y, q4[0].y, dot, false);
+            dot = __builtin_amdgcn_sdot4(k0.z, q4[0].z, dot, false);
+            dot = __builtin_amdgcn_sdot4(k0.w, q4[0].w, dot, false);
+            dot = __builtin_amdgcn_sdot4(k1.x, q4[1].x, dot, false);
+            dot = __builtin_amdgcn_sdot4(k1.y, q4[1].y, dot, false);
+            dot = __builtin_amdgcn_sdot4(k1.z, q4[1].z, dot, false);
+            dot = __builtin_amdgcn_sdot4(k1.w, q4[1].w, dot, false);
+            dot += __shfl_xor(dot, 32);
+            if (half == 0 && jj < cnt) {
+                const float scl = sq * kscale;
+                const float t1 = static_cast<float>(dot) * scl;
+                lg = t1 / a.scale;
+            }
+        } else if (half == 0 && jj < cnt) {
+            float dot = 0.0f;  // in order
+            for (int c = 0; c < ROW; c += 4) {
+                const int wd = *reinterpret_cast<const int *>(row + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float pr = qf[c + e] * static_cast<float>(static_cast<int8_t>(wd >> (8 * e)));
+                    dot = dot + pr;
+                }
+            }
+            const float t1 = dot * kscale;
+            lg = t1 / a.scale;
+        }
+        if (half == 0 && jj < cnt) s[j0 + jj] = lg;
+        refill(g);
+    }
+    __syncthreads();
+
+    // 2. softmaxInPlace with amd64's expSubSum.
+    float m = -INFINITY;
+    for (int j = lane; j < n; j += 64) m = fmaxf(m, s[j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const int n8 = n & ~7;
+    const bool kernel_path = n8 > 0;
+    for (int j = lane; j < n8; j += 64) s[j] = exp_lane(s[j] - m);
+    for (int j = n8 + lane; j < n; j += 64) s[j] = exp_generic(s[j] - m);
+    __syncthreads();
+    if (lane < 8 && kernel_path) {  // lane k of the 8-lane sum, elements in order
+        float acc = 0.0f;
+        int j = lane;
+        for (; j + 56 < n8; j += 64) {
+            float e[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) e[k] = s[j + 8 * k];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc = acc + e[k];
+        }
+        for (; j < n8; j += 8) acc = acc + s[j];
+        red[lane] = acc;
+    }
+    __syncthreads();
+    float sum;
+    if (kernel_path) {
+        const float x0 = red[0] + red[4], x1 = red[1] + red[5], x2 = red[2] + red[6], x3 = red[3] + red[7];
+        const float h0 = x0 + x1, h1 = x2 + x3;
+        sum = h0 + h1;
+        if (n8 != n) {
+            float tail = 0.0f;
+            for (int j = n8; j < n; ++j) tail = tail + s[j];
+            sum = sum + tail;
+        }
+    } else {
+        sum = 0.0f;
+        for (int j = 0; j < n; ++j) sum = sum + s[j];
+    }
+    __syncthreads();
+
+    // 3. axpysI8 (int8kernel.go:360-368): the chunk's weights, then lane d's
+    // products in key order.
+    float acc = 0.0f;
+    for (int g = nch; g < total; ++g) {
+        wait_chunk(g);
+        const int j0 = (g - nch) * JC, cnt = min(JC, n - j0);
+        const int8_t *sl = ring + (g % RS) * kRingSlot;
+        if (lane < cnt) {
+            const float p = s[j0 + lane] / sum;
+            s[j0 + lane] = p * reinterpret_cast<const float *>(sl + JC * ROW)[lane];
+        }
+        __syncthreads();
+        const int8_t *slot = sl + lane;
+        const float *wj = s + j0;
+        if (cnt == JC) {
+            float cd[JC];
+            float4 wv[JC / 4];
+#pragma unroll
+            for (int k = 0; k < JC; ++k) cd[k] = static_cast<float>(slot[k * ROW]);
+#pragma unroll
+            for (int q = 0; q < JC / 4; ++q) wv[q] = *reinterpret_cast<const float4 *>(wj + 4 * q);
+#pragma unroll
+            for (int q = 0; q < JC / 4; ++q) {
+                const float p0 = wv[q].x * cd[4 * q], p1 = wv[q].y * cd[4 * q + 1];
+                const float p2 = wv[q].z * cd[4 * q + 2], p3 = wv[q].w * cd[4 * q + 3];
+                acc = acc + p0;
+                acc = acc + p1;
+                acc = acc + p2;
+                acc = acc + p3;
+            }
+        } else {
+            for (int jj = 0; jj < cnt; ++jj) {
+                const float pr = wj[jj] * static_cast<float>(slot[jj * ROW]);
+                acc = acc + pr;
+            }
+        }
+        refill(g);
+    }
+    outp[lane] = acc;
+}
+
 }  // namespace
 
 hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
@@ -1063,6 +1327,21 @@ hipError_t launch_attend_chain(const AttendArgs &a, int rs, size_t lds, hipStrea
     return hipGetLastError();
 }
 
+template <int RS>
+hipError_t launch_attend_ring(const AttendArgs &a, size_t lds, hipStream_t stream) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_ring_kernel<RS>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const long long wgs = static_cast<long long>(a.heads) * a.t * a.batch;
+    hipLaunchKernelGGL((attend_ring_kernel<RS>), dim3(static_cast<unsigned>(wgs)), dim3(64), lds, stream, a,
+                       a.batch >= 8 ? 1 : 0);
+    return hipGetLastError();
+}
+
 // LDS of the chain kernel: logits, their transposed copy, and rs chunks of
 // JC value rows.
 size_t chain_lds(const AttendArgs &a, int jc, int rs) {
@@ -1082,6 +1361,13 @@ hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
             const int rs = std::max(1, (a.nk_max + 63) / 64);
             const size_t lds = chain_lds(a, 64, rs);
             if (lds <= 150 * 1024) return launch_attend_chain<4, 64, true>(a, rs, lds, stream);
+        }
+        if (a.qk == kChainVd) {
+            // many streams: key and value chunks through a ring of 6 slots
+            // (eight workgroups per CU at 1500 keys)
+            constexpr int rs = 6;
+            const size_t lds = 4 * ((static_cast<size_t>(a.nk_max) + 3) & ~size_t(3)) + static_cast<size_t>(rs) * kRingSlot;
+            if (lds <= 150 * 1024) return launch_attend_ring<rs>(a, lds, stream);
         }
         const int rs = 4;
         const size_t lds = chain_lds(a, 32, rs);
