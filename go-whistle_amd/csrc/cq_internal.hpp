@@ -98,7 +98,7 @@ struct LutLaunch {
     int wg0[kKernargJobs];       // kernel-argument path: first workgroup of each job
     const JobDesc *djobs;        // device path: job table
     const WorkUnit *dunits;      //              one unit per workgroup
-    int tb;                      // blocks per tile: rows folded per barrier pair
+    int tb;                      // blocks of the lut kernel's term buffer (>= W / 2)
     int gc;                      // groups per LDS chunk
     int bpw_max;                 // LDS sizing: most blocks of any workgroup
 };

@@ -13,23 +13,24 @@
 // integers (lut.go:16-27).
 //
 // Work split. A workgroup of W wavefronts owns one activation of a range of
-// 64-row blocks of one job.
-// The groups go in chunks of gc, so LDS holds one chunk's tables whatever
-// the input width; per chunk:
+// 64-row blocks of one job. The groups go in chunks of gc, so LDS holds one
+// chunk's tables whatever the input width; per chunk:
 //  1. Wavefront w rotates the chunk's groups w, w+W, ... in registers (a
 //     group of G values is G/64 registers per lane; butterflies below 64
 //     exchange lanes with shuffles, the others stay in a lane), reduces M
 //     across the wavefront and writes the group's tables (NT tables of 16
-//     int16) to LDS. Meanwhile the chunk's first index loads are in flight.
-//  2. After one barrier the (group, block) items of each tile of blocks go
-//     round-robin to the wavefronts. An item is 64 rows' index bytes of one
-//     group: each lane streams its row's bytes with 16-byte loads (a
-//     wavefront load is 1 KiB contiguous in the device layout), double
-//     buffered across items, and looks each nibble up in the LDS tables; all
-//     lanes read the same 16-entry table at once, so the lookups are free of
-//     bank conflicts. The int32 sums meet in LDS.
-//  3. The thread that owns a row folds the chunk's groups into the row's y
-//     (in LDS) in group order; y goes out after the last chunk.
+//     int16) to LDS. Meanwhile the wavefront's first index loads are in
+//     flight.
+//  2. After one barrier each wavefront streams its items, a few groups of
+//     16-byte loads ahead (a wavefront load is 1 KiB contiguous in the
+//     device layout): an item is one group of 64 rows of one block, each
+//     lane its row's index bytes, each nibble looked up in the LDS tables
+//     (all lanes read the same 16-entry table at once, free of bank
+//     conflicts). With at least W blocks a wavefront owns whole blocks and
+//     folds y = y + float32(sum) * (norm * step) in a register in group
+//     order; with fewer, wavefronts split a block's groups and one pass
+//     folds their terms from LDS in group order.
+// y goes out after the last chunk (with the fused residual add or SiLU).
 #include "cq_internal.hpp"
 #include "cq_device.hpp"
 
@@ -49,18 +50,37 @@ struct LutGeo {
     static constexpr int E = G >= 64 ? G / 64 : 1;  // rotated values per lane
 };
 
+// Global-memory views of pointers the kernel reads from its job table: as
+// generic pointers their loads would be flat loads, which also count as LDS
+// operations, so every LDS wait would wait for the index stream too.
+// (The host pass of hipcc only parses device code: there the qualifier is
+// left out.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define CQ_GLOBAL __attribute__((address_space(1)))
+#else
+#define CQ_GLOBAL
+#endif
+template <class T>
+__device__ __forceinline__ const CQ_GLOBAL T *gptr(const T *p) {
+    return (const CQ_GLOBAL T *)p;
+}
+template <class T>
+__device__ __forceinline__ CQ_GLOBAL T *gptr_w(T *p) {
+    return (CQ_GLOBAL T *)p;
+}
+
 template <int U>
-__device__ __forceinline__ void load_unit(const uint8_t *p, uint32_t (&w)[4]) {
+__device__ __forceinline__ void load_unit(const CQ_GLOBAL uint8_t *p, uint32_t (&w)[4]) {
     if constexpr (U == 16) {
-        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const CQ_GLOBAL u32x4 *>(p));
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     } else if constexpr (U == 8) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        const uint2 v = *reinterpret_cast<const CQ_GLOBAL uint2 *>(p);
         w[0] = v.x; w[1] = v.y; w[2] = 0; w[3] = 0;
     } else if constexpr (U == 4) {
-        w[0] = *reinterpret_cast<const uint32_t *>(p); w[1] = 0; w[2] = 0; w[3] = 0;
+        w[0] = *reinterpret_cast<const CQ_GLOBAL uint32_t *>(p); w[1] = 0; w[2] = 0; w[3] = 0;
     } else if constexpr (U == 2) {
-        w[0] = *reinterpret_cast<const uint16_t *>(p); w[1] = 0; w[2] = 0; w[3] = 0;
+        w[0] = *reinterpret_cast<const CQ_GLOBAL uint16_t *>(p); w[1] = 0; w[2] = 0; w[3] = 0;
     } else {
         w[0] = *p; w[1] = 0; w[2] = 0; w[3] = 0;
     }
@@ -138,212 +158,333 @@ __device__ __forceinline__ uint32_t pack16(int lo, int hi) {
     return (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
 }
 
-template <int BITS, int GB, bool DEV>
-__global__ __launch_bounds__(1024) void lut_kernel(LutLaunch a) {
+// Rotation, bound, tables and step of group g of the activation row x
+// (lut.go:158-178, 235-282) by one wavefront: the plain FWHT of the group
+// in registers (a group of G values is G/64 registers per lane; butterflies
+// below 64 exchange lanes with shuffles, the others stay in a lane), M
+// reduced across the wavefront, the NT tables of 16 int16 to tg and the
+// step to *step (lane 0). With ngain the row is ZCRMSNorm'ed first (divisor
+// rms).
+template <int BITS, int GB>
+__device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, int g, const float (&cbv)[16],
+                                             float cb_max, float lut_step, const CQ_GLOBAL float *ngain, float rms,
+                                             short *tg, float *step, int lane) {
     using Gm = LutGeo<BITS, GB>;
-    constexpr int G = Gm::G, U = Gm::U, UPG = Gm::UPG, NT = Gm::NT, E = Gm::E;
+    constexpr int G = Gm::G, E = Gm::E;
+    float v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = G >= 64 ? e * 64 + lane : lane;
+        const int col = g * G + i;
+        float xv = (i < G && col < in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
+        if (ngain && i < G && col < in) {
+            const float gx = ngain[col] * xv;
+            xv = gx / rms;
+        }
+        v[e] = xv;
+    }
+#pragma unroll
+    for (int h = 1; h < G; h <<= 1) {  // stages h = 1, 2, ..., G/2 (kernel.go:384-393)
+        if (h < 64) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float p = __shfl_xor(v[e], h);
+                v[e] = (lane & h) ? p - v[e] : v[e] + p;  // a - b on the upper lane, a + b on the lower
+            }
+        } else {
+            const int d = h / 64;
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                if (!(e & d)) {
+                    const float p = v[e], q = v[e + d];
+                    v[e] = p + q;
+                    v[e + d] = p - q;
+                }
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        if constexpr (BITS == 4) {
+            mx = fmaxf(mx, fabsf(v[e]));
+        } else {
+            const float p = __shfl_xor(v[e], 1);
+            const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+            mx = fmaxf(mx, s2);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const float m = cb_max * mx;
+    const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+    if (lane == 0) *step = m * lut_step;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = G >= 64 ? e * 64 + lane : lane;
+        if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
+            if (i < G) {
+                const float av = v[e] * inv;
+                uint32_t q[8];
+#pragma unroll
+                for (int c = 0; c < 16; c += 2)
+                    q[c / 2] = pack16(rne_int(cbv[c] * av), rne_int(cbv[c + 1] * av));
+                uint4 *dst = reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i) * 16);
+                dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+                dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+            }
+        } else {  // lutTables2Generic (lut.go:239-258): the even lane writes codes 0-7, the odd 8-15
+            const float p = __shfl_xor(v[e], 1);
+            if (i < G) {
+                const bool odd = lane & 1;
+                const float av = (odd ? p : v[e]) * inv, bv = (odd ? v[e] : p) * inv;
+                const int c0 = odd ? 8 : 0;
+                const float hlo = odd ? cbv[2] : cbv[0], hhi = odd ? cbv[3] : cbv[1];
+                uint32_t q[4];
+#pragma unroll
+                for (int cc = 0; cc < 8; cc += 2) {
+                    // code c = c0 + cc: c & 3 = cc & 3, c >> 2 = (odd ? 2 : 0) + (cc >> 2)
+                    const float l0 = cbv[cc & 3] * av, h0 = ((cc >> 2) ? hhi : hlo) * bv;
+                    const float l1 = cbv[(cc + 1) & 3] * av, h1 = (((cc + 1) >> 2) ? hhi : hlo) * bv;
+                    q[cc / 2] = pack16(rne_int(l0 + h0), rne_int(l1 + h1));
+                }
+                *reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i / 2) * 16 + c0) =
+                    make_uint4(q[0], q[1], q[2], q[3]);
+            }
+        }
+    }
+}
+
+// One work unit: blocks [b0, b0 + bc) of job J (counted from its blk0) for
+// activation act.
+template <int BITS, int GB>
+__device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, int b0, int bc, int act) {
+    using Gm = LutGeo<BITS, GB>;
+    constexpr int U = Gm::U, UPG = Gm::UPG, NT = Gm::NT;
+    constexpr int DG = UPG >= 8 ? 1 : 8 / UPG;  // groups of index loads in flight per wavefront
 
     extern __shared__ __align__(16) unsigned char smem[];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int W = blockDim.x >> 6;
 
-    const JobDesc *J;
-    int b0, bc, act;
-    if constexpr (DEV) {
+    // The job's fields, read once before any store (later reads through J
+    // could not be hoisted past the stores of y).
+    const int j_in = J->in, j_row0 = J->row0, j_out = J->out, j_act = J->act;
+    const CQ_GLOBAL uint16_t *j_norm = gptr(J->norm);
+    CQ_GLOBAL float *j_y = gptr_w(J->y);
+    const long long j_ystride = J->y_stride, j_rstride = J->resid_stride;
+    const CQ_GLOBAL float *j_ngain = gptr(J->ngain), *j_resid = gptr(J->resid);
+    const float j_cbmax = J->cb_max, j_step = J->lut_step;
+    float cbv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) cbv[c] = J->cb[c];
+    const int groups = J->groups, units = J->units, blk0 = J->blk0 + b0;
+    const CQ_GLOBAL uint8_t *idx = gptr(J->idx);
+    const CQ_GLOBAL float *x = gptr(J->x) + static_cast<long long>(act) * J->x_stride;
+
+    // LDS: tables of a chunk of gc groups, the chunk's steps, y of the
+    // workgroup's rows between chunks, the chunk's float terms of up to tc
+    // blocks (when wavefronts share a block), and the row's norm divisor.
+    const int gc = a.gc, tc = a.tb;
+    short *tab = reinterpret_cast<short *>(smem);
+    float *steps = reinterpret_cast<float *>(smem + static_cast<size_t>(gc) * NT * 16 * sizeof(short));
+    float *yacc = steps + gc;
+    float *term = yacc + static_cast<size_t>(a.bpw_max) * 64;
+    float *misc = term + static_cast<size_t>(gc) * tc * 64;
+
+    // Fused ZCRMSNorm of the activation row (norm.go:53-109): the row goes
+    // through LDS in pieces (one coalesced read each), lanes 0-3 of
+    // wavefront 0 keep the four float64 partial sums in the reference's
+    // order (lane k: elements i = k mod 4 below In & ~3, lane 0 then the
+    // tail), and the divisor is shared through LDS.
+    float rms = 1.0f;
+    if (j_ngain) {
+        float *xs = reinterpret_cast<float *>(smem);
+        const int cap = static_cast<int>(misc - xs) & ~63;
+        const int dim = j_in, full = dim & ~3;
+        double part = 0.0;
+        for (int p0 = 0; p0 < dim; p0 += cap) {
+            const int pn = min(cap, dim - p0);
+#pragma unroll 4
+            for (int t = tid; t < pn; t += blockDim.x) xs[t] = x[p0 + t];
+            __syncthreads();
+            if (tid < 4) {
+                const int lim = min(p0 + pn, full);
+                int i = p0 + tid;
+                for (; i + 60 < lim; i += 64) {
+                    float v[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) v[k] = xs[i - p0 + 4 * k];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) {
+                        const double d = v[k];
+                        part = part + d * d;
+                    }
+                }
+                for (; i < lim; i += 4) {
+                    const double d = xs[i - p0];
+                    part = part + d * d;
+                }
+                if (tid == 0)
+                    for (int t = max(full, p0); t < p0 + pn; ++t) {
+                        const double d = xs[t - p0];
+                        part = part + d * d;
+                    }
+            }
+            __syncthreads();
+        }
+        if (w == 0) {
+            const double p0 = __shfl(part, 0), p1 = __shfl(part, 1), p2 = __shfl(part, 2), p3 = __shfl(part, 3);
+            if (lane == 0) misc[0] = zc_rms(p0, p1, p2, p3, dim);
+        }
+        __syncthreads();
+        rms = misc[0];
+    }
+
+    auto write_out = [&](int bb, int ln, float v) {
+        const int r = (blk0 + bb) * 64 + ln;
+        if (r >= j_row0 && r < j_row0 + j_out) {
+            float out = v;
+            if (j_resid)
+                out = j_resid[static_cast<long long>(act) * j_rstride + (r - j_row0)] + out;
+            else if (j_act == 1)
+                out = silu_value(out);
+            j_y[static_cast<long long>(act) * j_ystride + (r - j_row0)] = out;
+        }
+    };
+
+    // Wavefront roles. With at least as many blocks as wavefronts, wavefront
+    // w owns blocks w, w + W, ... and every group of them, and folds each
+    // row in a register in group order. With fewer, S wavefronts share a
+    // block (groups gs, gs + S, ...), their terms meet in LDS and one pass
+    // folds them in group order.
+    int S = 1;
+    while (S * 2 * bc <= W) S *= 2;
+
+    for (int g0 = 0; g0 < groups; g0 += gc) {
+        const int gch = min(gc, groups - g0);
+        const bool last = g0 + gch >= groups;
+        const int bbs = w / S, gs = w - (w / S) * S;
+        int Q;
+        if (S == 1)
+            Q = w < bc ? ((bc - w + W - 1) / W) * gch : 0;
+        else
+            Q = (bbs < bc && gs < gch) ? (gch - gs + S - 1) / S : 0;
+        // The wavefront's items in order: (block bb, chunk group gi); with
+        // S = 1 the groups of block w, then of block w + W, ...; with S > 1
+        // groups gs, gs + S, ... of block bbs.
+        struct Pos {
+            int bb, gi;
+        };
+        auto next = [&](Pos &p) {
+            if (S == 1) {
+                if (++p.gi == gch) {
+                    p.gi = 0;
+                    p.bb += W;
+                }
+            } else {
+                p.gi += S;
+            }
+        };
+        const Pos first = S == 1 ? Pos{w, 0} : Pos{bbs, gs};
+        uint32_t buf[DG][UPG][4];
+        uint32_t nv[DG];
+        auto load_group = [&](const Pos &p, uint32_t (&bf)[UPG][4], uint32_t &nrm) {
+            const CQ_GLOBAL uint8_t *ip = idx + (static_cast<size_t>(blk0 + p.bb) * units + static_cast<size_t>(g0 + p.gi) * UPG) * 64 * U +
+                                          static_cast<size_t>(lane) * U;
+#pragma unroll
+            for (int u = 0; u < UPG; ++u) load_unit<U>(ip + static_cast<size_t>(u) * 64 * U, bf[u]);
+            nrm = j_norm[(static_cast<size_t>(blk0 + p.bb) * groups + g0 + p.gi) * 64 + lane];
+        };
+        // The first items are in flight while the tables are built; the load
+        // position stops at the last item (repeats past the end keep every
+        // wait of the stream a fixed count).
+        Pos lp = first;
+        int lq = 0;
+        if (Q > 0) {
+#pragma unroll
+            for (int d = 0; d < DG; ++d) {
+                load_group(lp, buf[d], nv[d]);
+                if (lq < Q - 1) {
+                    next(lp);
+                    ++lq;
+                }
+            }
+        }
+
+        // 1. Rotation, bound and tables of the chunk's groups w, w+W, ...
+        for (int gi = w; gi < gch; gi += W)
+            group_tables<BITS, GB>(x, j_in, g0 + gi, cbv, j_cbmax, j_step, j_ngain, rms,
+                                   tab + static_cast<size_t>(gi) * NT * 16, &steps[gi], lane);
+        __syncthreads();
+
+        // 2. The wavefront's items in order, DG groups of loads ahead: the
+        // lookups' exact int32 sum, the term float32(sum) * (norm * step),
+        // folded into the row (or parked for the shared fold).
+        float acc = 0.0f;
+        Pos cp = first;
+        for (int q0 = 0; q0 < Q; q0 += DG) {
+#pragma unroll
+            for (int d = 0; d < DG; ++d) {
+                if (q0 + d < Q) {
+                    const int bb = cp.bb, gi = cp.gi;
+                    const uint32_t tg = lds_addr(tab + static_cast<size_t>(gi) * NT * 16);
+                    int s = 0;
+#pragma unroll
+                    for (int u = 0; u < UPG; ++u) s += lookup_unit<U>(buf[d][u], tg + u * 2 * U * 16 * 2);
+                    const float n = __half2float(__ushort_as_half(static_cast<unsigned short>(nv[d])));
+                    const float coef = n * steps[gi];
+                    const float t = static_cast<float>(s) * coef;
+                    if (S == 1) {
+                        if (gi == 0) acc = g0 == 0 ? 0.0f : yacc[bb * 64 + lane];
+                        acc = acc + t;
+                        if (gi == gch - 1) {
+                            if (last)
+                                write_out(bb, lane, acc);
+                            else
+                                yacc[bb * 64 + lane] = acc;
+                        }
+                    } else {
+                        term[(static_cast<size_t>(gi) * tc + bb) * 64 + lane] = t;
+                    }
+                    next(cp);
+                }
+                load_group(lp, buf[d], nv[d]);
+                if (lq < Q - 1) {
+                    next(lp);
+                    ++lq;
+                }
+            }
+        }
+        if (S > 1) {
+            __syncthreads();
+            for (int t = tid; t < bc * 64; t += blockDim.x) {
+                const int bb = t >> 6, ln = t & 63;
+                float y = g0 == 0 ? 0.0f : yacc[t];
+                for (int gi = 0; gi < gch; ++gi) y = y + term[(static_cast<size_t>(gi) * tc + bb) * 64 + ln];
+                if (last)
+                    write_out(bb, ln, y);
+                else
+                    yacc[t] = y;
+            }
+        }
+        if (!last) __syncthreads();  // tables, steps and terms are rewritten by the next chunk
+    }
+}
+
+template <int BITS, int GB, bool DEV>
+__global__ __launch_bounds__(256, GB >= 256 ? 2 : 4) void lut_kernel(LutLaunch a) {
+    if constexpr (DEV) {  // a batch plan: one unit per workgroup
         const WorkUnit u = a.dunits[blockIdx.x];
-        J = a.djobs + u.job;
-        b0 = u.blk;
-        bc = u.nb;
-        act = u.act;
+        lut_unit<BITS, GB>(a, a.djobs + u.job, u.blk, u.nb, u.act);
     } else {
         int j = 0;
 #pragma unroll
         for (int k = 1; k < kKernargJobs; ++k)
             if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.wg0[k]) j = k;
-        J = &a.jobs[j];
-        b0 = (static_cast<int>(blockIdx.x) - a.wg0[j]) * a.bpw;
-        bc = min(a.bpw, J->nblk - b0);
-        act = blockIdx.y;
-    }
-    const int groups = J->groups, units = J->units, blk0 = J->blk0 + b0;
-    const uint8_t *idx = J->idx;
-    const float *x = J->x + static_cast<long long>(act) * J->x_stride;
-
-    // Fused ZCRMSNorm of the activation row (norm.go:53-109): its divisor,
-    // from four float64 partial sums on lanes 0-3 of every wavefront.
-    float rms = 1.0f;
-    if (J->ngain) {
-        const double part = lane < 4 ? zc_partial(x, J->in, lane) : 0.0;
-        const double p0 = __shfl(part, 0), p1 = __shfl(part, 1), p2 = __shfl(part, 2), p3 = __shfl(part, 3);
-        rms = zc_rms(p0, p1, p2, p3, J->in);
-    }
-
-    // LDS: tables of a chunk of gc groups, the chunk's int32 sums of a tile,
-    // the chunk's steps, and y of the workgroup's rows (folded chunk by chunk).
-    const int gc = a.gc, tb = a.tb;
-    short *tab = reinterpret_cast<short *>(smem);
-    int *part = reinterpret_cast<int *>(smem + static_cast<size_t>(gc) * NT * 16 * sizeof(short));
-    float *steps = reinterpret_cast<float *>(part + static_cast<size_t>(gc) * tb * 64);
-    float *yacc = steps + gc;
-
-    // Items of a tile within a chunk: k -> chunk group k / nbt, block
-    // k % nbt; wavefront w takes k = w, w + W, ...
-    auto item_ptr = [&](int g0, int t0, int nbt, int k) -> const uint8_t * {
-        const int gi = k / nbt, bb = k - (k / nbt) * nbt;
-        return idx + (static_cast<size_t>(blk0 + t0 + bb) * units + static_cast<size_t>(g0 + gi) * UPG) * 64 * U +
-               static_cast<size_t>(lane) * U;
-    };
-    uint32_t bufA[UPG][4], bufB[UPG][4];
-    auto load_item = [&](const uint8_t *p, uint32_t (&buf)[UPG][4]) {
-#pragma unroll
-        for (int u = 0; u < UPG; ++u) load_unit<U>(p + static_cast<size_t>(u) * 64 * U, buf[u]);
-    };
-    auto compute_item = [&](int nbt, int k, const uint32_t (&buf)[UPG][4]) {
-        const int gi = k / nbt, bb = k - (k / nbt) * nbt;
-        const uint32_t tg = lds_addr(tab + static_cast<size_t>(gi) * NT * 16);
-        int s = 0;
-#pragma unroll
-        for (int u = 0; u < UPG; ++u) s += lookup_unit<U>(buf[u], tg + u * 2 * U * 16 * 2);
-        part[(gi * tb + bb) * 64 + lane] = s;
-    };
-
-    for (int t = tid; t < bc * 64; t += blockDim.x) yacc[t] = 0.0f;
-
-    for (int g0 = 0; g0 < groups; g0 += gc) {
-        const int gch = min(gc, groups - g0);
-        // The chunk's first item is in flight while its tables are built.
-        const int nbt0 = min(tb, bc);
-        if (w < gch * nbt0) load_item(item_ptr(g0, 0, nbt0, w), bufA);
-
-        // 1. Rotation, bound and tables of the chunk's groups w, w+W, ...
-        for (int gi = w; gi < gch; gi += W) {
-            const int g = g0 + gi;
-            float v[E];
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const int i = G >= 64 ? e * 64 + lane : lane;
-                const int col = g * G + i;
-                float xv = (i < G && col < J->in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
-                if (J->ngain && i < G && col < J->in) {
-                    const float gx = J->ngain[col] * xv;
-                    xv = gx / rms;
-                }
-                v[e] = xv;
-            }
-#pragma unroll
-            for (int h = 1; h < G; h <<= 1) {  // stages h = 1, 2, ..., G/2 (kernel.go:384-393)
-                if (h < 64) {
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        const float p = __shfl_xor(v[e], h);
-                        v[e] = (lane & h) ? p - v[e] : v[e] + p;  // a - b on the upper lane, a + b on the lower
-                    }
-                } else {
-                    const int d = h / 64;
-#pragma unroll
-                    for (int e = 0; e < E; ++e)
-                        if (!(e & d)) {
-                            const float p = v[e], q = v[e + d];
-                            v[e] = p + q;
-                            v[e + d] = p - q;
-                        }
-                }
-            }
-            float mx = 0.0f;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                if constexpr (BITS == 4) {
-                    mx = fmaxf(mx, fabsf(v[e]));
-                } else {
-                    const float p = __shfl_xor(v[e], 1);
-                    const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
-                    mx = fmaxf(mx, s2);
-                }
-            }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-            const float m = J->cb_max * mx;
-            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
-            if (lane == 0) steps[gi] = m * J->lut_step;
-            short *tg = tab + static_cast<size_t>(gi) * NT * 16;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const int i = G >= 64 ? e * 64 + lane : lane;
-                if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
-                    if (i < G) {
-                        const float av = v[e] * inv;
-                        uint32_t q[8];
-#pragma unroll
-                        for (int c = 0; c < 16; c += 2)
-                            q[c / 2] = pack16(rne_int(J->cb[c] * av), rne_int(J->cb[c + 1] * av));
-                        uint4 *dst = reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i) * 16);
-                        dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
-                        dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
-                    }
-                } else {  // lutTables2Generic (lut.go:239-258): the even lane writes codes 0-7, the odd 8-15
-                    const float p = __shfl_xor(v[e], 1);
-                    if (i < G) {
-                        const bool odd = lane & 1;
-                        const float av = (odd ? p : v[e]) * inv, bv = (odd ? v[e] : p) * inv;
-                        const int c0 = odd ? 8 : 0;
-                        uint32_t q[4];
-#pragma unroll
-                        for (int cc = 0; cc < 8; cc += 2) {
-                            const int c = c0 + cc;
-                            const float l0 = J->cb[c & 3] * av, h0 = J->cb[c >> 2] * bv;
-                            const float l1 = J->cb[(c + 1) & 3] * av, h1 = J->cb[(c + 1) >> 2] * bv;
-                            q[cc / 2] = pack16(rne_int(l0 + h0), rne_int(l1 + h1));
-                        }
-                        *reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i / 2) * 16 + c0) =
-                            make_uint4(q[0], q[1], q[2], q[3]);
-                    }
-                }
-            }
-        }
-        __syncthreads();
-
-        // 2./3. Tiles of tb blocks: lookups, then the chunk's groups folded
-        // into y in group order.
-        for (int t0 = 0; t0 < bc; t0 += tb) {
-            const int nbt = min(tb, bc - t0);
-            const int items = gch * nbt;
-            if (t0 > 0 && w < items) load_item(item_ptr(g0, t0, nbt, w), bufA);
-            for (int k = w; k < items; k += 2 * W) {
-                const int k1 = k + W, k2 = k + 2 * W;
-                if (k1 < items) load_item(item_ptr(g0, t0, nbt, k1), bufB);
-                compute_item(nbt, k, bufA);
-                if (k1 < items) {
-                    if (k2 < items) load_item(item_ptr(g0, t0, nbt, k2), bufA);
-                    compute_item(nbt, k1, bufB);
-                }
-            }
-            __syncthreads();
-            for (int t = tid; t < nbt * 64; t += blockDim.x) {
-                const int blk = blk0 + t0 + (t >> 6), ln = t & 63;
-                float acc = yacc[t0 * 64 + t];
-                for (int gi = 0; gi < gch; ++gi) {
-                    const float n =
-                        __half2float(__ushort_as_half(J->norm[(static_cast<size_t>(blk) * groups + g0 + gi) * 64 + ln]));
-                    const float coef = n * steps[gi];
-                    const float prod = static_cast<float>(part[(gi * tb + (t >> 6)) * 64 + ln]) * coef;
-                    acc = acc + prod;
-                }
-                yacc[t0 * 64 + t] = acc;
-            }
-            __syncthreads();
-        }
-    }
-
-    for (int t = tid; t < bc * 64; t += blockDim.x) {
-        const int r = blk0 * 64 + t;
-        if (r >= J->row0 && r < J->row0 + J->out) {
-            float out = yacc[t];
-            if (J->resid)
-                out = J->resid[static_cast<long long>(act) * J->resid_stride + (r - J->row0)] + out;
-            else if (J->act == 1)
-                out = silu_value(out);
-            J->y[static_cast<long long>(act) * J->y_stride + (r - J->row0)] = out;
-        }
+        const JobDesc *J = &a.jobs[j];
+        const int b0 = (static_cast<int>(blockIdx.x) - a.wg0[j]) * a.bpw;
+        lut_unit<BITS, GB>(a, J, b0, min(a.bpw, J->nblk - b0), blockIdx.y);
     }
 }
 
@@ -370,7 +511,7 @@ hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, h
 size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw) {
     (void)bits;
     return static_cast<size_t>(gc) * (2 * group_bytes * 16 * sizeof(short) + static_cast<size_t>(tb) * 64 * 4 + 4) +
-           static_cast<size_t>(bpw) * 64 * 4;
+           static_cast<size_t>(bpw) * 64 * 4 + 16;
 }
 
 bool lut_geometry_supported(int bits, int gb) {

@@ -298,6 +298,35 @@ def test_batch_plan_matches_gemm():
             assert same_bits(ys[k].cpu().numpy(), want), (rep, k)
 
 
+def test_batch_plan_many_units():
+    # A plan larger than the resident grid: workgroups take byte-balanced
+    # runs of blocks that cross job and activation boundaries (several units
+    # per workgroup, tables rebuilt per unit, multi-chunk inputs). Every
+    # output equals the matrix's own device GEMM bit for bit.
+    import torch
+
+    g = synth.rng(777)
+    specs = [(16384, 512, 4), (2048, 512, 4), (512, 2048, 4), (512, 512, 4), (16384, 512, 2), (512, 2048, 2)]
+    mats, xs, ys, rows = [], [], [], []
+    for k in range(24):
+        out, inp, bits = specs[k % len(specs)]
+        m = cq.New(synth.random_packed(g, out, inp, 128, bits, sigma=0.05))
+        r = 1 + (k % 3 == 1)
+        mats.append(m)
+        xs.append(torch.from_numpy(synth.activations(g, r, inp)).cuda())
+        ys.append(torch.full((r * out,), float("nan"), dtype=torch.float32, device="cuda"))
+        rows.append(r)
+    b = cq.Batch(mats, ys, xs, rows)
+    assert b.launches() == 2
+    b.run()
+    want = [torch.zeros_like(y) for y in ys]
+    for m, w, x, r in zip(mats, want, xs, rows):
+        m.gemm_dev(w, x, r)
+    torch.cuda.synchronize()
+    for k in range(len(mats)):
+        assert torch.equal(ys[k].view(torch.int32), want[k].view(torch.int32)), k
+
+
 def test_batch_plan_in_a_graph():
     import torch
 
