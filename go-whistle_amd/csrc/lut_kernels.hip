@@ -389,27 +389,35 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
         const Pos first = S == 1 ? Pos{w, 0} : Pos{bbs, gs};
         uint32_t buf[DG][UPG][4];
         uint32_t nv[DG];
-        auto load_group = [&](const Pos &p, uint32_t (&bf)[UPG][4], uint32_t &nrm) {
-            const CQ_GLOBAL uint8_t *ip = idx + (static_cast<size_t>(blk0 + p.bb) * units + static_cast<size_t>(g0 + p.gi) * UPG) * 64 * U +
-                                          static_cast<size_t>(lane) * U;
+        // Loads past the wavefront's last item read one 16-byte line of the
+        // activation row instead (kept in L2 by the tables' reads of it): the
+        // stream issues the same loads every turn, so each of its waits is a
+        // fixed count, and no index byte is fetched twice.
+        const CQ_GLOBAL uint8_t *spare = (const CQ_GLOBAL uint8_t *)(reinterpret_cast<uintptr_t>(x) & ~uintptr_t(15));
+        auto load_group = [&](const Pos &p, bool real, uint32_t (&bf)[UPG][4], uint32_t &nrm) {
+            const CQ_GLOBAL uint8_t *ip =
+                real ? idx + (static_cast<size_t>(blk0 + p.bb) * units + static_cast<size_t>(g0 + p.gi) * UPG) * 64 * U +
+                           static_cast<size_t>(lane) * U
+                     : spare;
+            const size_t ustride = real ? static_cast<size_t>(64) * U : 0;
 #pragma unroll
-            for (int u = 0; u < UPG; ++u) load_unit<U>(ip + static_cast<size_t>(u) * 64 * U, bf[u]);
-            nrm = j_norm[(static_cast<size_t>(blk0 + p.bb) * groups + g0 + p.gi) * 64 + lane];
+            for (int u = 0; u < UPG; ++u) load_unit<U>(ip + u * ustride, bf[u]);
+            const CQ_GLOBAL uint16_t *np =
+                real ? j_norm + (static_cast<size_t>(blk0 + p.bb) * groups + g0 + p.gi) * 64 + lane
+                     : (const CQ_GLOBAL uint16_t *)spare;
+            nrm = *np;
         };
-        // The first items are in flight while the tables are built; the load
-        // position stops at the last item (repeats past the end keep every
-        // wait of the stream a fixed count).
+        // The first items are in flight while the tables are built.
         Pos lp = first;
-        int lq = 0;
+        int lq = 0;  // items loaded
+        auto refill = [&](uint32_t (&bf)[UPG][4], uint32_t &nrm) {
+            load_group(lp, lq < Q, bf, nrm);
+            if (lq < Q) next(lp);
+            ++lq;
+        };
         if (Q > 0) {
 #pragma unroll
-            for (int d = 0; d < DG; ++d) {
-                load_group(lp, buf[d], nv[d]);
-                if (lq < Q - 1) {
-                    next(lp);
-                    ++lq;
-                }
-            }
+            for (int d = 0; d < DG; ++d) refill(buf[d], nv[d]);
         }
 
         // 1. Rotation, bound and tables of the chunk's groups w, w+W, ...
@@ -449,11 +457,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
                     }
                     next(cp);
                 }
-                load_group(lp, buf[d], nv[d]);
-                if (lq < Q - 1) {
-                    next(lp);
-                    ++lq;
-                }
+                refill(buf[d], nv[d]);
             }
         }
         if (S > 1) {
