@@ -271,6 +271,12 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     }
     a.tb = kLutTile;
     a.gc = lut_chunk(groups_max);
+    // A launch that fills at most a quarter of the CUs is latency-bound: wide
+    // rows then take their tables in fewer chunks (up to 32 KiB of tables),
+    // each chunk costing a table build and a barrier.
+    if (static_cast<long long>(wg) * rows * 4 <= device_info().cus)
+        while (a.gc * 2 <= groups_max && 2 * a.gc * 2 * s0.group_bytes * 16 * static_cast<int>(sizeof(short)) <= 32 * 1024)
+            a.gc *= 2;
     a.bpw_max = a.bpw;
     const size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, a.gc, a.tb, a.bpw);
     for (int r0 = 0; r0 < rows; r0 += 65535) {
