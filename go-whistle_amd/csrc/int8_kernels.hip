@@ -145,17 +145,17 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         const int j0 = c * vchunk, cnt = min(vchunk, n - j0);
         if (wide_v) {
             // eight 16-byte loads in flight per thread before their LDS stores
+            // (past the end a load repeats the last piece, so the eight stay
+            // in registers; only real pieces are stored)
             const int per = a.vd / 16, total = cnt * per;
             for (int e0 = t0; e0 < total; e0 += 8 * nt) {
                 int4 w[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    const int e = e0 + u * nt;
-                    if (e < total) {
-                        const int jj = e / per, part = e - (e / per) * per;
-                        w[u] = *reinterpret_cast<const int4 *>(vq + static_cast<long long>(key_of(j0 + jj)) * a.v_cols +
-                                                               kv * a.vd + part * 16);
-                    }
+                    const int e = min(e0 + u * nt, total - 1);
+                    const int jj = e / per, part = e - (e / per) * per;
+                    w[u] = *reinterpret_cast<const int4 *>(vq + static_cast<long long>(key_of(j0 + jj)) * a.v_cols +
+                                                           kv * a.vd + part * 16);
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
@@ -366,8 +366,9 @@ struct StreamGeo {
 constexpr int kStreamQk = 64;  // widest key head the streamed kernel holds in registers
 
 // AttendInt8Spans for one (stream, query row, head) per workgroup, value
-// heads of 64 or 128 codes, key heads of at most 64 codes, 16-byte aligned
-// rows. Same arithmetic as attend_kernel; the work is ordered for latency:
+// heads of VD codes (the launcher uses it for 128), key heads of at most 64
+// codes, 16-byte aligned rows. Same arithmetic as attend_kernel; the work is
+// ordered for latency:
 //   - the query and the first keys of every thread are loaded together,
 //     the keys into registers (kKpt keys per thread at a time);
 //   - value rows stream from HBM straight into an LDS ring of chunks of JC
@@ -1373,13 +1374,10 @@ hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
         const size_t lds = chain_lds(a, 32, rs);
         if (lds <= 150 * 1024) return launch_attend_chain<1, 32, false>(a, rs, lds, stream);
     }
+    // (64-code value heads the chain kernel does not fit need more LDS than
+    // the streamed kernel has: they take the general kernel)
     int rs = 0;
     size_t slds = 0;
-    if (stream_ok && a.vd == 64) {
-        if (a.resident && stream_plan<64, 64>(a, true, rs, slds))
-            return launch_attend_stream<64, 64>(a, rs, slds, stream);
-        if (stream_plan<64, 32>(a, false, rs, slds)) return launch_attend_stream<64, 32>(a, rs, slds, stream);
-    }
     if (stream_ok && a.vd == 128) {
         if (a.resident && stream_plan<128, 64>(a, true, rs, slds))
             return launch_attend_stream<128, 64>(a, rs, slds, stream);
