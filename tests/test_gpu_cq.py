@@ -92,7 +92,11 @@ def test_gemm_rows_and_exact(bits, rows):
 def test_gemm_375_frames_and_wide_inputs():
     # q_proj over a 30 s clip and the 2048-wide φ input (cq/bench_test.go:23-38).
     g = synth.rng(375)
-    for out, inp, bits, rows in [(384, 512, 2, 375), (128, 2048, 4, 64), (96, 4096, 4, 3), (64, 8192, 2, 2)]:
+    # small launches take wide rows in chunks of 8 (4-bit) or 16 (2-bit) groups:
+    # 1000 (8 groups, the last padded), 1280 (10: a chunk of 8, then 2) and
+    # 2600 (21: 16, then 5) cover the last chunk's tail
+    for out, inp, bits, rows in [(384, 512, 2, 375), (128, 2048, 4, 64), (96, 4096, 4, 3), (64, 8192, 2, 2),
+                                 (33, 1000, 4, 1), (70, 1280, 4, 2), (200, 1280, 2, 1), (50, 2600, 2, 1)]:
         print(f"gemm {out}x{inp} CQ{bits} rows {rows}", flush=True)
         p = synth.random_packed(g, out, inp, 128, bits)
         m, o = cq.New(p), orc.OMatrix.new(p)
