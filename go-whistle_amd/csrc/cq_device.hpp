@@ -9,6 +9,40 @@
 
 namespace cqhip {
 
+// Lane l's value from lane l ^ H of the wavefront, without the LDS
+// crossbar where a DPP move reaches: quad permutes for H = 1, 2, row shifts
+// within 16 lanes for 4, 8 (lane + H below, lane - H above), a ds_swizzle
+// for 16 and ds_bpermute only for 32. The values move unchanged.
+template <int H>
+__device__ __forceinline__ float xor_lane(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    if constexpr (H == 1) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
+    } else if constexpr (H == 2) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
+    } else if constexpr (H == 4 || H == 8) {
+        const int up = __builtin_amdgcn_update_dpp(0, x, 0x100 + H, 0xF, 0xF, true);  // row_shl: lane + H
+        const int dn = __builtin_amdgcn_update_dpp(0, x, 0x110 + H, 0xF, 0xF, true);  // row_shr: lane - H
+        return __builtin_bit_cast(float, (threadIdx.x & H) ? dn : up);
+    } else if constexpr (H == 16) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(x, 0x401F));  // swizzle(SWAP, 16)
+    } else {
+        return __shfl_xor(v, H);
+    }
+}
+
+// The same for h a power of two below 64 (a constant once loops unroll).
+__device__ __forceinline__ float xor_lane(float v, int h) {
+    switch (h) {
+        case 1: return xor_lane<1>(v);
+        case 2: return xor_lane<2>(v);
+        case 4: return xor_lane<4>(v);
+        case 8: return xor_lane<8>(v);
+        case 16: return xor_lane<16>(v);
+        default: return xor_lane<32>(v);
+    }
+}
+
 // One lane of the amd64 exponent kernel (exp_amd64.s:84-112), constants bit
 // for bit (exp_amd64.s:7-51): Cephes expf with the kernel's fused steps.
 __device__ __forceinline__ float exp_lane(float x) {

@@ -188,7 +188,7 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
         if (h < 64) {
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                const float p = __shfl_xor(v[e], h);
+                const float p = xor_lane(v[e], h);
                 v[e] = (lane & h) ? p - v[e] : v[e] + p;  // a - b on the upper lane, a + b on the lower
             }
         } else {
@@ -208,13 +208,13 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
         if constexpr (BITS == 4) {
             mx = fmaxf(mx, fabsf(v[e]));
         } else {
-            const float p = __shfl_xor(v[e], 1);
+            const float p = xor_lane<1>(v[e]);
             const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
             mx = fmaxf(mx, s2);
         }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, xor_lane(mx, off));
     const float m = cb_max * mx;
     const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
     if (lane == 0) *step = m * lut_step;
@@ -233,7 +233,7 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
                 dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
             }
         } else {  // lutTables2Generic (lut.go:239-258): the even lane writes codes 0-7, the odd 8-15
-            const float p = __shfl_xor(v[e], 1);
+            const float p = xor_lane<1>(v[e]);
             if (i < G) {
                 const bool odd = lane & 1;
                 const float av = (odd ? p : v[e]) * inv, bv = (odd ? v[e] : p) * inv;

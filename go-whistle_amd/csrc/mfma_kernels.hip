@@ -196,51 +196,79 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                                       J.norm[(static_cast<size_t>(gblk) * groups + g) * 64 + rt * 32 + l32]))
                                 : 0.0f;
 
-        // 1. Rotation and bound of the group of each activation (lut.go:158-178).
-        for (int tt = w; tt < TA; tt += kMfmaWaves) {
-            const int t = t0 + tt;
-            float v[2];
+        // 1. Rotation and bound of the group of each activation (lut.go:158-178):
+        // a wavefront's TA / 8 activations together, their loads in flight at
+        // once and their butterflies interleaved.
+        {
+            constexpr int PW = TA / kMfmaWaves;  // activations per wavefront
+            float v[PW][2];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int col = g * G + e * 64 + lane;
-                float xv = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
-                if (J.ngain && t < J.rows && col < J.in) {
-                    const float gx = J.ngain[col] * xv;
-                    xv = gx / zrms[tt];
+            for (int k = 0; k < PW; ++k) {
+                const int tt = w + k * kMfmaWaves, t = t0 + tt;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int col = g * G + e * 64 + lane;
+                    v[k][e] = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
                 }
-                v[e] = xv;
+            }
+            if (J.ngain) {
+#pragma unroll
+                for (int k = 0; k < PW; ++k) {
+                    const int tt = w + k * kMfmaWaves, t = t0 + tt;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int col = g * G + e * 64 + lane;
+                        if (t < J.rows && col < J.in) {
+                            const float gx = J.ngain[col] * v[k][e];
+                            v[k][e] = gx / zrms[tt];
+                        }
+                    }
+                }
             }
 #pragma unroll
             for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
 #pragma unroll
+                for (int k = 0; k < PW; ++k)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float p = xor_lane(v[k][e], h);
+                        v[k][e] = (lane & h) ? p - v[k][e] : v[k][e] + p;
+                    }
+            }
+#pragma unroll
+            for (int k = 0; k < PW; ++k) {  // stage h = 64 within the lane
+                const float p = v[k][0], q = v[k][1];
+                v[k][0] = p + q;
+                v[k][1] = p - q;
+            }
+            float mx[PW];
+#pragma unroll
+            for (int k = 0; k < PW; ++k) {
+                mx[k] = 0.0f;
+#pragma unroll
                 for (int e = 0; e < 2; ++e) {
-                    const float p = __shfl_xor(v[e], h);
-                    v[e] = (lane & h) ? p - v[e] : v[e] + p;
-                }
-            }
-            {  // stage h = 64 within the lane
-                const float p = v[0], q = v[1];
-                v[0] = p + q;
-                v[1] = p - q;
-            }
-            float mx = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                if constexpr (BITS == 4) {
-                    mx = fmaxf(mx, fabsf(v[e]));
-                } else {
-                    const float p = __shfl_xor(v[e], 1);
-                    const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
-                    mx = fmaxf(mx, s2);
+                    if constexpr (BITS == 4) {
+                        mx[k] = fmaxf(mx[k], fabsf(v[k][e]));
+                    } else {
+                        const float p = xor_lane<1>(v[k][e]);
+                        const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                        mx[k] = fmaxf(mx[k], s2);
+                    }
                 }
             }
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-            const float m = J.cb_max * mx;
-            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+            for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-            for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[e] * inv;
-            if (lane == 0) stp[tt] = m * J.lut_step;
+                for (int k = 0; k < PW; ++k) mx[k] = fmaxf(mx[k], xor_lane(mx[k], off));
+#pragma unroll
+            for (int k = 0; k < PW; ++k) {
+                const int tt = w + k * kMfmaWaves;
+                const float m = J.cb_max * mx[k];
+                const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[k][e] * inv;
+                if (lane == 0) stp[tt] = m * J.lut_step;
+            }
         }
         __syncthreads();
         build(0, 0);
