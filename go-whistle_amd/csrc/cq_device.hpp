@@ -43,6 +43,18 @@ __device__ __forceinline__ float xor_lane(float v, int h) {
     }
 }
 
+// Workgroup barrier for LDS only: this wavefront's LDS operations complete
+// (lgkmcnt 0), then s_barrier. Unlike __syncthreads it does not wait for
+// the wavefront's global loads, so loads issued ahead stay in flight across
+// it. The empty asm statements keep the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // One lane of the amd64 exponent kernel (exp_amd64.s:84-112), constants bit
 // for bit (exp_amd64.s:7-51): Cephes expf with the kernel's fused steps.
 __device__ __forceinline__ float exp_lane(float x) {

@@ -26,7 +26,7 @@
 // rows (one 64-row block per wavefront, two 32-row MFMA tiles). Per group:
 //   1. the activations' groups are rotated (the plain FWHT in the lut
 //      kernel's stage order) and scaled by 8191/M into LDS, 8 per wavefront;
-//   2. per chunk of 8 positions, every thread builds one table's two int8
+//   2. per chunk of 16 positions, every thread builds two tables' two int8
 //      planes in LDS [position][plane][activation][16 codes] (the next chunk
 //      while the MFMAs run on the current one);
 //   3. each wavefront streams its rows' index bytes (16-byte loads in the
@@ -53,7 +53,8 @@ struct MfmaGeo {
     static constexpr int GB = G * BITS / 8;  // index bytes per row and group: 64 or 32
     static constexpr int NJ = 2 * GB;        // nibble positions (tables) per group: 128 or 64
     static constexpr int KS = GB;            // K-steps per group: 2 positions x 16 codes each
-    static constexpr int CK = 8;             // positions per LDS chunk of tables
+    static constexpr int CK = 16;            // positions per LDS chunk of tables
+    static constexpr int CW = CK / 8;        // index words per row and chunk (8 positions each)
     static constexpr int NCH = NJ / CK;      // chunks per group
     static constexpr int UPG = GB / 16;      // 16-byte index loads per row and group
     static constexpr int TA = 64;            // activations per workgroup
@@ -186,6 +187,22 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
         }
     };
 
+    // A wavefront's activations' values of group g (TA / 8 of them, two per
+    // lane each): group 0 loaded here, group g + 1 while group g streams.
+    constexpr int PW = TA / kMfmaWaves;  // activations per wavefront
+    float xg[PW][2];
+    auto load_x = [&](int g) {
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int t = t0 + w + k * kMfmaWaves;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int col = g * G + e * 64 + lane;
+                xg[k][e] = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
+            }
+        }
+    };
+    load_x(0);
     for (int g = 0; g < groups; ++g) {
         uint32_t cur[2][4], nxt[2][4];
         load_unit(g, 0, nxt);
@@ -197,20 +214,14 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                                 : 0.0f;
 
         // 1. Rotation and bound of the group of each activation (lut.go:158-178):
-        // a wavefront's TA / 8 activations together, their loads in flight at
-        // once and their butterflies interleaved.
+        // a wavefront's TA / 8 activations together, their butterflies
+        // interleaved.
         {
-            constexpr int PW = TA / kMfmaWaves;  // activations per wavefront
             float v[PW][2];
 #pragma unroll
-            for (int k = 0; k < PW; ++k) {
-                const int tt = w + k * kMfmaWaves, t = t0 + tt;
+            for (int k = 0; k < PW; ++k)
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int col = g * G + e * 64 + lane;
-                    v[k][e] = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
-                }
-            }
+                for (int e = 0; e < 2; ++e) v[k][e] = xg[k][e];
             if (J.ngain) {
 #pragma unroll
                 for (int k = 0; k < PW; ++k) {
@@ -270,17 +281,20 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                 if (lane == 0) stp[tt] = m * J.lut_step;
             }
         }
-        __syncthreads();
+        lds_barrier();
         build(0, 0);
 #pragma unroll
         for (int at = 0; at < 2; ++at)
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) acc[at][rt] = i32x16{};
-        __syncthreads();
+        lds_barrier();
 
-        // 2./3. Chunks of CK positions (one index word per row): the next
+        if (g + 1 < groups) load_x(g + 1);
+
+        // 2./3. Chunks of CK positions (CW index words per row): the next
         // chunk's tables are built while this chunk's MFMAs run.
         const unsigned long long val = half ? 64ull : 1ull;
+        constexpr int CW = M::CW;
         for (int u = 0; u < M::UPG; ++u) {
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
@@ -288,8 +302,8 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                 for (int q = 0; q < 4; ++q) cur[rt][q] = nxt[rt][q];
             if (u + 1 < M::UPG) load_unit(g, u + 1, nxt);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int c = 4 * u + q;
+            for (int q = 0; q < 4 / CW; ++q) {
+                const int c = (4 / CW) * u + q;
                 if (c + 1 < M::NCH) build(c + 1, (c + 1) & 1);
                 if (rows_here) {
                     // lane half 0 reads a position's l plane, half 1 its h plane
@@ -308,8 +322,8 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                         }
 #pragma unroll
                         for (int rt = 0; rt < 2; ++rt) {
-                            // position jc: index byte jc / 2 of the chunk's word, nibble jc % 2
-                            const uint32_t n = (cur[rt][q] >> (4 * jc)) & 15u;
+                            // position jc: word jc / 8 of the chunk, byte (jc % 8) / 2, nibble jc % 2
+                            const uint32_t n = (cur[rt][q * CW + jc / 8] >> (4 * (jc % 8))) & 15u;
                             const i32x4 B = one_hot(n, val);
 #pragma unroll
                             for (int at = 0; at < 2; ++at)
@@ -317,7 +331,7 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                         }
                     }
                 }
-                __syncthreads();
+                lds_barrier();
             }
         }
 
@@ -338,7 +352,7 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                     }
                 }
         }
-        __syncthreads();  // av and stp are rewritten by the next group
+        lds_barrier();  // av and stp are rewritten by the next group
     }
 
     if (rows_here) {
