@@ -60,6 +60,9 @@ SIGNATURES = {
                                         c_void_p]),
     "cq_gemms_fused_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p, c_void_p,
                                    c_int, c_void_p]),
+    "cq_gemms_append_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p,
+                                    POINTER(c_void_p), POINTER(c_void_p), c_longlong, c_longlong, c_void_p, c_int,
+                                    POINTER(c_void_p), POINTER(c_void_p), c_void_p]),
     "nd_zcrmsnorm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "nd_rope_dev": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "nd_argmax_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),

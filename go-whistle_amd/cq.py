@@ -191,6 +191,28 @@ def gemms_fused_dev(ms, ys, x, rows, norm_gain=None, resid=None, act=0):
                                    _stream()))
 
 
+def gemms_append_dev(ms, ys, x, rows, caches, q_stride, s_stride, pos, cap, norm_gain=None):
+    """gemms_fused_dev (norm_gain only) whose product k is also appended to
+    an int8 row cache when caches[k] = (codes, scales, rope) is not None:
+    row pos[b] of stream b's cache, each 64-wide head quantized as
+    Int8Rows.Append, after RoPE at pos[b] when rope = (cos, sin) is given.
+    One lut-kernel launch (cq_gemms_append_dev)."""
+    n = len(ms)
+    if not (n == len(ys) == len(caches)):
+        raise CQPanic(f"cq: GEMMs of {n} matrices into {len(ys)} outputs and {len(caches)} caches")
+    ptr = lambda t: c_void_p(t.data_ptr()) if t is not None else None
+    arr = lambda vals: (c_void_p * max(n, 1))(*vals)
+    hs = arr([m.handle for m in ms])
+    ds = arr([ptr(y) for y in ys])
+    kq = arr([ptr(c[0]) if c is not None else None for c in caches])
+    ks = arr([ptr(c[1]) if c is not None else None for c in caches])
+    rope = [c[2] if c is not None and c[2] is not None else None for c in caches]
+    cs = arr([ptr(r[0]) if r is not None else None for r in rope])
+    sn = arr([ptr(r[1]) if r is not None else None for r in rope])
+    check(lib().cq_gemms_append_dev(n, hs, ds, c_void_p(x.data_ptr()), rows, ptr(norm_gain), kq, ks, q_stride,
+                                    s_stride, ptr(pos), cap, cs, sn, _stream()))
+
+
 class Batch:
     """A plan of independent products on device tensors (cq_batch_*): job k
     is ms[k].GEMM of rows[k] activations xs[k] into ys[k]. run() queues one

@@ -215,15 +215,36 @@ struct Fuse {
     const float *resid = nullptr;
     long long resid_stride = 0;
     int act = 0;
-    bool any() const { return ngain || resid || act; }
+    // int8 appends of matrix k of the call (null arrays / entries: none)
+    int8_t *const *app_q = nullptr;
+    float *const *app_s = nullptr;
+    const float *const *app_cos = nullptr;
+    const float *const *app_sin = nullptr;
+    long long app_q_stride = 0, app_s_stride = 0;
+    const int32_t *app_pos = nullptr;
+    int app_cap = 0;
+    bool any() const { return ngain || resid || act || app_q; }
 };
 
-void apply_fuse(JobDesc &j, const Fuse *f) {
+// Job j runs matrix k of the call.
+void apply_fuse(JobDesc &j, const Fuse *f, int k) {
     if (!f) return;
     j.ngain = f->ngain;
     j.resid = f->resid;
     j.resid_stride = f->resid_stride;
     j.act = f->act;
+    if (f->app_q && f->app_q[k]) {
+        j.app_q = f->app_q[k];
+        j.app_s = f->app_s[k];
+        j.app_q_stride = f->app_q_stride;
+        j.app_s_stride = f->app_s_stride;
+        j.app_pos = f->app_pos;
+        j.app_cap = f->app_cap;
+        if (f->app_cos && f->app_cos[k]) {
+            j.app_cos = f->app_cos[k];
+            j.app_sin = f->app_sin[k];
+        }
+    }
 }
 
 constexpr int kLutTile = 4;     // blocks per tile of the lut kernel
@@ -258,7 +279,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
         if (ms[k]->out == 0) continue;
         JobDesc &j = a.jobs[a.njobs++];
         fill_job(j, ms[k], x, dsts[k], rows);
-        apply_fuse(j, fz);
+        apply_fuse(j, fz, k);
         blocks += static_cast<long long>(j.nblk) * rows;
         groups_max = std::max(groups_max, j.groups);
     }
@@ -286,6 +307,11 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
             b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
             b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
             if (b.jobs[k].resid) b.jobs[k].resid += static_cast<long long>(r0) * b.jobs[k].resid_stride;
+            if (b.jobs[k].app_q) {
+                b.jobs[k].app_q += static_cast<long long>(r0) * b.jobs[k].app_q_stride;
+                b.jobs[k].app_s += static_cast<long long>(r0) * b.jobs[k].app_s_stride;
+                b.jobs[k].app_pos += r0;
+            }
         }
         HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, kLutWaves, wg, nr, lds, stream), "lut launch");
     }
@@ -323,7 +349,7 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
         if (ms[k]->out == 0) continue;
         JobDesc &j = a.jobs[a.njobs];
         fill_job(j, ms[k], x, dsts[k], rows);
-        apply_fuse(j, fz);
+        apply_fuse(j, fz, k);
         a.wg0[a.njobs] = wg;
         wg += (j.nblk + rpw - 1) / rpw;
         ++a.njobs;
@@ -627,6 +653,45 @@ int cq_gemms_fused_dev(int n, cq_matrix *const *ms, float *const *dsts, const fl
     f.resid_stride = resid ? ms[0]->out : 0;
     f.act = act;
     return gemms_dev(n, ms, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
+}
+
+int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows,
+                        const float *norm_gain, int8_t *const *kv_q, float *const *kv_s, long long q_stride,
+                        long long s_stride, const int32_t *pos, int cap, const float *const *cos_t,
+                        const float *const *sin_t, void *stream) {
+    if (n < 0 || n > kKernargJobs || (n > 0 && (!ms || !dsts || !kv_q || !kv_s)))
+        return fail(CQ_ERR_MISUSE, "cq: appending GEMMs of %d matrices (at most %d)", n, kKernargJobs);
+    if (rows < 0 || cap < 0) return fail(CQ_ERR_MISUSE, "cq: appending GEMMs of %d rows into %d positions", rows, cap);
+    bool any = false;
+    for (int k = 0; k < n; ++k) {
+        if (!ms[k] || ms[k]->st->in != ms[0]->st->in)
+            return fail(CQ_ERR_MISUSE, "cq: GEMMs over matrices of different input widths");
+        const CqStore &sk = *ms[k]->st, &s0 = *ms[0]->st;  // each workgroup builds its own job's tables
+        if (!uses_lut(ms[k]) || !lut_fits(sk) || sk.group != s0.group || sk.width != s0.width ||
+            sk.group_bytes != s0.group_bytes)
+            return fail(CQ_ERR_UNSUPPORTED, "cq: appending products run one lut kernel over matrices of one geometry");
+        if (!kv_q[k]) continue;
+        any = true;
+        if (!kv_s[k] || ms[k]->row0 % kBlockRows || ms[k]->out % kBlockRows)
+            return fail(CQ_ERR_MISUSE, "cq: append of rows [%d, %d) needs scales and heads of %d rows", ms[k]->row0,
+                        ms[k]->row0 + ms[k]->out, kBlockRows);
+        if (cos_t && cos_t[k] && !(sin_t && sin_t[k])) return fail(CQ_ERR_MISUSE, "cq: RoPE cosines without sines");
+    }
+    if (any && !pos) return fail(CQ_ERR_MISUSE, "cq: append without positions");
+    if (rows == 0 || n == 0) return CQ_OK;
+    Fuse f;
+    f.ngain = norm_gain;
+    if (any) {
+        f.app_q = kv_q;
+        f.app_s = kv_s;
+        f.app_cos = cos_t;
+        f.app_sin = sin_t;
+        f.app_q_stride = q_stride;
+        f.app_s_stride = s_stride;
+        f.app_pos = pos;
+        f.app_cap = cap;
+    }
+    return run_lut(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
 }
 
 int cq_gemm(const cq_matrix *m, float *dst, size_t dst_len, const float *x, size_t x_len, int rows) {

@@ -81,6 +81,18 @@ struct JobDesc {
     const float *resid;
     long long resid_stride;
     int act;
+    // Fused int8 append (app_q null: none; the view's rows and width are
+    // whole 64-row blocks): activation b's output row, each 64-wide block
+    // a head, is quantized into row app_pos[b] of stream b's cache
+    // (codes app_q + b*app_q_stride + p*out, scales app_s + b*app_s_stride
+    // + p*(out/64)) unless that position is outside [0, app_cap); with
+    // app_cos, each head is first rotated by RoPE at that position.
+    int8_t *app_q;
+    float *app_s;
+    long long app_q_stride, app_s_stride;
+    const int32_t *app_pos;
+    const float *app_cos, *app_sin;
+    int app_cap;
 };
 
 // A workgroup's share of a job: blocks [blk, blk + nb) (counted from the

@@ -341,7 +341,40 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
         rms = misc[0];
     }
 
+    // The fused int8 append of a finished block: the whole wavefront holds
+    // its 64 values (lane = row), one head of the cache row. Int8Rows.Append
+    // (int8.go:36-55) with RoPE first (rope.go:69-81: value i < 32 pairs
+    // with i + 32), bit for bit the separate append kernel.
+    int8_t *const j_aq = J->app_q;
+    float *const j_as = J->app_s;
+    const long long j_aqs = J->app_q_stride, j_ass = J->app_s_stride;
+    const int j_apos = j_aq ? J->app_pos[act] : -1;
+    const bool j_app = j_aq && j_apos >= 0 && j_apos < J->app_cap;
+    const CQ_GLOBAL float *j_acos = gptr(J->app_cos), *j_asin = gptr(J->app_sin);
+    auto append_block = [&](int bb, int ln, float v) {
+        const int r0 = (blk0 + bb) * 64 - j_row0;  // view row of the head's first value
+        if (j_acos) {
+            const float o = xor_lane<32>(v);
+            const int jj = ln & 31;
+            const float a = ln < 32 ? v : o, b = ln < 32 ? o : v;
+            float o1, o2;
+            rope_pair(a, b, j_acos[j_apos * 32 + jj], j_asin[j_apos * 32 + jj], o1, o2);
+            v = ln < 32 ? o1 : o2;
+        }
+        float m = fabsf(v);
+#pragma unroll
+        for (int h = 32; h > 0; h >>= 1) m = fmaxf(m, xor_lane(m, h));
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+        float c = rintf(v / sc);
+        c = fminf(fmaxf(c, -128.0f), 127.0f);
+        CQ_GLOBAL int8_t *qp = gptr_w(j_aq) + static_cast<long long>(act) * j_aqs + static_cast<long long>(j_apos) * j_out;
+        qp[r0 + ln] = static_cast<int8_t>(static_cast<int>(c));
+        if (ln == 0)
+            gptr_w(j_as)[static_cast<long long>(act) * j_ass + static_cast<long long>(j_apos) * (j_out >> 6) + (r0 >> 6)] = sc;
+    };
+
     auto write_out = [&](int bb, int ln, float v) {
+        if (j_app) append_block(bb, ln, v);
         const int r = (blk0 + bb) * 64 + ln;
         if (r >= j_row0 && r < j_row0 + j_out) {
             float out = v;

@@ -258,12 +258,17 @@ class Decoder:
         rope = (self.cos, self.sin)
         for l in range(c.layers):
             m = self.mats[l]
-            cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"]], [self.q, self.k, self.v], self.x, B,
-                               norm_gain=self.gains[3 * l])
-            needle.append_dev(self.self_k[l], self.self_ks[l], self.k, B, D, c.head_dim, c.max_pos * D,
-                              c.max_pos * hk, self.pos, c.max_pos, rope=rope)
-            needle.append_dev(self.self_v[l], self.self_vs[l], self.v, B, D, c.head_dim, c.max_pos * D,
-                              c.max_pos * hk, self.pos, c.max_pos)
+            if c.head_dim == 64:  # heads are the lut kernel's 64-row blocks: the appends ride on the product
+                caches = [None, (self.self_k[l], self.self_ks[l], rope), (self.self_v[l], self.self_vs[l], None)]
+                cq.gemms_append_dev([m["wq"], m["wk"], m["wv"]], [self.q, self.k, self.v], self.x, B, caches,
+                                    c.max_pos * D, c.max_pos * hk, self.pos, c.max_pos, norm_gain=self.gains[3 * l])
+            else:
+                cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"]], [self.q, self.k, self.v], self.x, B,
+                                   norm_gain=self.gains[3 * l])
+                needle.append_dev(self.self_k[l], self.self_ks[l], self.k, B, D, c.head_dim, c.max_pos * D,
+                                  c.max_pos * hk, self.pos, c.max_pos, rope=rope)
+                needle.append_dev(self.self_v[l], self.self_vs[l], self.v, B, D, c.head_dim, c.max_pos * D,
+                                  c.max_pos * hk, self.pos, c.max_pos)
             self._attend(l, False, s, rope=(self.cos, self.sin, self.pos))
             cq.gemms_fused_dev([m["wo"]], [self.x], self.att, B, resid=self.x)
             cq.gemms_fused_dev([m["wcq"]], [self.q], self.x, B, norm_gain=self.gains[3 * l + 1])

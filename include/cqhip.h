@@ -113,6 +113,24 @@ int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x
  * lut matrices only. */
 int cq_gemms_fused_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows,
                        const float *norm_gain, const float *resid, int act, void *stream);
+/* cq_gemms_fused_dev (norm_gain only) whose outputs are also appended to
+ * int8 row caches: the decoder's K and V projections followed by
+ * Int8Rows.Append (internal/needle/int8.go:36-55; Attention.Extend's
+ * projections, RoPE and append, internal/needle/cache.go:90-125), one launch instead of
+ * three, results bit for bit kv_append_rope_dev's. No reference
+ * counterpart. For k with kv_q[k] non-null, activation b's product row is
+ * quantized per 64-wide head into row pos[b] of stream b's cache (codes
+ * kv_q[k] + b*q_stride + pos[b]*out, scales kv_s[k] + b*s_stride +
+ * pos[b]*out/64; no append where pos[b] is outside [0, cap)), after RoPE
+ * at pos[b] with the half-width tables cos_t[k], sin_t[k] when cos_t and
+ * cos_t[k] are non-null (internal/needle/rope.go:69-81). dsts[k] still
+ * receives the product. Matrix k's view must cover whole 64-row blocks;
+ * at most 8 lut matrices of one group size and index width (else
+ * CQ_ERR_MISUSE / CQ_ERR_UNSUPPORTED). */
+int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows,
+                        const float *norm_gain, int8_t *const *kv_q, float *const *kv_s, long long q_stride,
+                        long long s_stride, const int32_t *pos, int cap, const float *const *cos_t,
+                        const float *const *sin_t, void *stream);
 int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream);
 /* Rows gathered by index: dst[i] = scale * Row(rows[i]) for i < n, rows a
  * device int32 array: the decoder's scaled token-embedding lookup for

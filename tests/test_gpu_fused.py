@@ -131,6 +131,77 @@ def test_append_with_rope():
     assert same(s1.cpu().numpy(), s2.cpu().numpy())
 
 
+@pytest.mark.parametrize("batch,bits,views", [(1, 4, False), (3, 2, False), (100, 4, False), (256, 4, False),
+                                              (5, 4, True), (300, 2, True)])
+def test_append_epilogue(batch, bits, views):
+    # The K/V appends riding on the qkv product, bit for bit the product
+    # followed by the separate append kernels; batch 1, 100 and 256 cover
+    # the kernel's shared-block (4 and 2 wavefronts a block) and one-wavefront
+    # write paths; views: q, k, v as row views of one fused root.
+    import torch
+
+    heads, hd, cap = 8, 64, 16
+    D = heads * hd
+    g = synth.rng(300 + batch + bits)
+    cos, sin = dec.rope_tables(hd, cap, 1e4)
+    cos, sin = _t(cos), _t(sin)
+    if views:
+        root = cq.New(synth.random_packed(g, 3 * D, D, 128, bits, sigma=0.05))
+        ms = [root.Rows(0, D), root.Rows(D, 2 * D), root.Rows(2 * D, 3 * D)]
+    else:
+        ms = [cq.New(synth.random_packed(g, D, D, 128, bits, sigma=0.05)) for _ in range(3)]
+    x = _t((g.standard_normal((batch, D)) * 2).astype(np.float32))
+    gain = _t((1 + g.standard_normal(D) * 0.1).astype(np.float32))
+    # every stream at its own position, some outside the cache (no append)
+    p = g.integers(0, cap, size=batch).astype(np.int32)
+    p[1::7] = -1
+    p[4::11] = cap
+    pos = _t(p)
+    want_y = [torch.zeros(batch, D, device="cuda") for _ in ms]
+    got_y = [torch.zeros(batch, D, device="cuda") for _ in ms]
+    caches = []
+    for _ in range(2):
+        kq = _t(g.integers(-128, 128, size=(batch, cap, D), dtype=np.int8))
+        ks = _t(g.random((batch, cap, heads)).astype(np.float32))
+        vq = _t(g.integers(-128, 128, size=(batch, cap, D), dtype=np.int8))
+        vs = _t(g.random((batch, cap, heads)).astype(np.float32))
+        caches.append((kq, ks, vq, vs))
+    (kq1, ks1, vq1, vs1), (kq2, ks2, vq2, vs2) = caches
+    kq2.copy_(kq1), ks2.copy_(ks1), vq2.copy_(vq1), vs2.copy_(vs1)
+    cq.gemms_fused_dev(ms, want_y, x, batch, norm_gain=gain)
+    needle.append_dev(kq1, ks1, want_y[1], batch, D, hd, cap * D, cap * heads, pos, cap, rope=(cos, sin))
+    needle.append_dev(vq1, vs1, want_y[2], batch, D, hd, cap * D, cap * heads, pos, cap)
+    cq.gemms_append_dev(ms, got_y, x, batch, [None, (kq2, ks2, (cos, sin)), (vq2, vs2, None)], cap * D,
+                        cap * heads, pos, cap, norm_gain=gain)
+    torch.cuda.synchronize()
+    for a, b in zip(got_y, want_y):
+        assert same(a.cpu().numpy(), b.cpu().numpy())
+    assert np.array_equal(kq2.cpu().numpy(), kq1.cpu().numpy())
+    assert np.array_equal(vq2.cpu().numpy(), vq1.cpu().numpy())
+    assert same(ks2.cpu().numpy(), ks1.cpu().numpy())
+    assert same(vs2.cpu().numpy(), vs1.cpu().numpy())
+
+
+def test_append_epilogue_misuse():
+    import torch
+
+    from go_whistle_amd import CQPanic, CQDeviceError
+
+    g = synth.rng(6)
+    D, cap = 512, 4
+    root = cq.New(synth.random_packed(g, 2 * D, D, 128, 4))
+    z = torch.zeros(D, device="cuda")
+    q8 = torch.zeros(cap * D, dtype=torch.int8, device="cuda")
+    s8 = torch.zeros(cap * 8, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    with pytest.raises(CQPanic):  # heads cut by the view
+        cq.gemms_append_dev([root.Rows(32, D + 32)], [z], z, 1, [(q8, s8, None)], cap * D, cap * 8, pos, cap)
+    with pytest.raises(CQPanic):  # no positions
+        cq.gemms_append_dev([root.Rows(0, D)], [z], z, 1, [(q8, s8, None)], cap * D, cap * 8, None, cap)
+    with pytest.raises(CQDeviceError):  # an Exact view runs no lut kernel
+        cq.gemms_append_dev([root.Rows(0, D).Exact()], [z], z, 1, [(q8, s8, None)], cap * D, cap * 8, pos, cap)
+
+
 @pytest.mark.parametrize("batch,n,vd", [(1, 37, 64), (4, 300, 64), (80, 100, 64), (3, 50, 128), (2, 20, 40)])
 def test_attention_with_query_rope(batch, n, vd):
     # the chain kernel (vd 64, both layouts), the streamed kernel (vd 128)
