@@ -254,13 +254,30 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
     }
 }
 
+// Groups of index loads a wavefront keeps in flight, and wavefronts per
+// SIMD the kernel is built for (its registers fit that many). Eight 16-byte
+// loads ahead (DG = 8 / loads per group) at four or five wavefronts per
+// SIMD; 32-byte groups of 2-bit indices instead keep four loads ahead at six
+// wavefronts per SIMD (measured: a 2-bit sweep launch 53 -> 49 us, where
+// 4-bit groups lose with fewer loads ahead).
+template <int BITS, int GB>
+constexpr int lut_loads_ahead() {
+    constexpr int UPG = LutGeo<BITS, GB>::UPG;
+    if (BITS == 2 && GB == 32) return 2;
+    return UPG >= 8 ? 1 : 8 / UPG;
+}
+template <int BITS, int GB>
+constexpr int lut_waves_per_simd() {
+    return GB >= 256 ? 2 : (BITS == 2 && GB == 32) ? 6 : 4;
+}
+
 // One work unit: blocks [b0, b0 + bc) of job J (counted from its blk0) for
 // activation act.
 template <int BITS, int GB>
 __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, int b0, int bc, int act) {
     using Gm = LutGeo<BITS, GB>;
     constexpr int U = Gm::U, UPG = Gm::UPG, NT = Gm::NT;
-    constexpr int DG = UPG >= 8 ? 1 : 8 / UPG;  // groups of index loads in flight per wavefront
+    constexpr int DG = lut_loads_ahead<BITS, GB>();  // groups of index loads in flight per wavefront
 
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -510,7 +527,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
 }
 
 template <int BITS, int GB, bool DEV>
-__global__ __launch_bounds__(256, GB >= 256 ? 2 : 4) void lut_kernel(LutLaunch a) {
+__global__ __launch_bounds__(256, (lut_waves_per_simd<BITS, GB>())) void lut_kernel(LutLaunch a) {
     if constexpr (DEV) {  // a batch plan: one unit per workgroup
         const WorkUnit u = a.dunits[blockIdx.x];
         lut_unit<BITS, GB>(a, a.djobs + u.job, u.blk, u.nb, u.act);
