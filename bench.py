@@ -70,8 +70,18 @@ def pmc_traffic():
     return None
 
 
+def cpu_threads():
+    """Host cores this process may use, at most 16 (one GPU's share)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
 def cpu_baseline(gw, packs, seconds):
-    """The oracle's lut GEMV (single thread) over the sweep, bounded in time."""
+    """The oracle's lut GEMV over the sweep, bounded in time, three ways: the
+    generic restatement on one thread, its AVX2 form (the reference's amd64
+    path, lut_amd64.s, bit for bit the generic one) on one thread, and the
+    AVX2 form on every host core this process may use, split as the
+    reference splits a GEMV (lut.go:102-201). value is the last: the
+    reference's own CPU path at its own parallelism."""
     if ROOT not in sys.path:
         sys.path.insert(0, ROOT)
     from oracle import binding as orc
@@ -79,19 +89,31 @@ def cpu_baseline(gw, packs, seconds):
     g = gw.synth.rng(99)
     mats = [(orc.OMatrix.new(p), gw.synth.activations(g, 1, p.In), weight_bytes(p.Out, p.In, p.Bits))
             for p in packs]
-    done, t0 = 0, time.perf_counter()
-    passes = 0
-    while True:
-        for m, x, wb in mats:
-            m.gemm(x, 1, orc.LUT)
-            done += wb
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(done / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{passes} passes over the 8-matrix sweep (one copy each), oracle lut GEMV, 1 thread, "
-                      f"{el:.1f} s"}
+    threads = cpu_threads()
+    legs = [("generic_1t", False, 1)]
+    if orc.have_avx2():
+        legs += [("avx2_1t", True, 1), (f"avx2_{threads}t", True, threads)]
+    res = {}
+    for name, avx2, th in legs:
+        orc.set_cpu(avx2, th)
+        done, passes, t0 = 0, 0, time.perf_counter()
+        while True:
+            for m, x, wb in mats:
+                m.gemm(x, 1, orc.LUT)
+                done += wb
+            passes += 1
+            el = time.perf_counter() - t0
+            if el >= seconds / len(legs):
+                break
+        res[name] = (done / el / 1e9, passes, el, th)
+    orc.set_cpu(False, 1)
+    name = legs[-1][0]
+    rate, passes, el, th = res[name]
+    return {"value": round(rate, 4), "unit": "GB/s", "cores": th, "kind": "port",
+            "sample": f"{passes} passes over the 8-matrix sweep (one copy each), oracle lut GEMV, {name} "
+                      f"({'AVX2' if 'avx2' in name else 'generic'}, {th} threads, the reference's split), {el:.1f} s",
+            "legs": {k: {"GBps": round(v[0], 4), "threads": v[3], "passes": v[1], "seconds": round(v[2], 2)}
+                     for k, v in res.items()}}
 
 
 INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA, ops/s
@@ -170,18 +192,24 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
             sys.path.insert(0, ROOT)
         from oracle import decoder_ref
 
+        from oracle import binding as orc
+
         ref = decoder_ref.RefDecoder(model)
         ks, vs = zip(*[dec.memory_states(7, cfg, 0, l) for l in range(cfg.layers)])
         ref.memory(ks, vs)
+        avx2, threads = orc.have_avx2(), cpu_threads()
+        orc.set_cpu(avx2, threads)
         n, t0 = 0, time.perf_counter()
         while True:
             n += len(ref.decode(1, 10))
             el = time.perf_counter() - t0
             if el >= cpu_seconds:
                 break
-        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+        orc.set_cpu(False, 1)
+        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
                                "sample": f"{n} greedy tokens at batch 1 (runs of 10 from position 0), oracle "
-                                         f"decoder, 1 thread, {el:.1f} s"}
+                                         f"decoder, lut products {'AVX2' if avx2 else 'generic'} split over "
+                                         f"{threads} threads as the reference splits them, {el:.1f} s"}
     return res
 
 

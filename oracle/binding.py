@@ -50,6 +50,13 @@ def lib():
             "orc_lut_lookup": (None, [POINTER(c_float), POINTER(c_uint8), POINTER(c_uint8), POINTER(c_float),
                                       POINTER(c_float), c_int, c_int, c_int]),
             "orc_lut_step": (c_float, [c_int]),
+            "orc_have_avx2": (c_int, []),
+            "orc_fwht_avx2": (None, [POINTER(c_float), c_int]),
+            "orc_lut_tables2_avx2": (c_float, [POINTER(c_uint8), POINTER(c_float), c_int, POINTER(c_float), c_float]),
+            "orc_lut_tables4_avx2": (c_float, [POINTER(c_uint8), POINTER(c_float), c_int, POINTER(c_float), c_float]),
+            "orc_lut_lookup_avx2": (None, [POINTER(c_float), POINTER(c_uint8), POINTER(c_uint8), POINTER(c_float),
+                                           POINTER(c_float), c_int, c_int, c_int]),
+            "orc_set_cpu": (c_int, [c_int, c_int]),
             "orc_quantize_row": (c_float, [POINTER(c_int8), POINTER(c_float), c_int]),
             "orc_quantize_rows": (None, [POINTER(c_int8), POINTER(c_float), POINTER(c_float), c_int, c_int, c_int]),
             "orc_dots_i8": (None, [POINTER(c_int32), c_int, POINTER(c_int8), c_int, POINTER(c_int8), c_int]),
@@ -170,10 +177,45 @@ def dequant(p):
     return w.reshape(p.Out, p.In)
 
 
-def fwht(x):
+def fwht(x, avx2=False):
     x = np.array(x, dtype=np.float32)
-    lib().orc_fwht(fp(x), x.size)
+    (lib().orc_fwht_avx2 if avx2 else lib().orc_fwht)(fp(x), x.size)
     return x
+
+
+def have_avx2():
+    return bool(lib().orc_have_avx2())
+
+
+def set_cpu(avx2=False, threads=1):
+    """How lut products run from here on: the generic routines or their AVX2
+    forms (the reference's amd64 path), on one thread or split over threads
+    as gemmLUT splits them. Process-wide."""
+    if lib().orc_set_cpu(int(avx2), int(threads)):
+        raise OracleError("this CPU has no AVX2")
+
+
+def lut_tables(x, cb, cb_max, width, avx2=False):
+    """lutTables2/4 (generic or AVX2) of one rotated group x: (tables, M)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cb = np.ascontiguousarray(cb, dtype=np.float32)
+    n_tab = x.size // 2 if width == 2 else x.size
+    tab = np.zeros(32 * n_tab, dtype=np.uint8)
+    name = f"orc_lut_tables{width}" + ("_avx2" if avx2 else "")
+    m = getattr(lib(), name)(u8p(tab), fp(x), x.size, fp(cb), c_float(cb_max))
+    return tab, np.float32(m)
+
+
+def lut_lookup(idx, tab, norm, steps, blocks, groups, gb, avx2=False):
+    """lutLookup (generic or AVX2) of 32-row blocks: y [blocks * 32]."""
+    y = np.zeros(blocks * 32, dtype=np.float32)
+    idx = np.ascontiguousarray(idx, dtype=np.uint8)
+    tab = np.ascontiguousarray(tab, dtype=np.uint8)
+    norm = np.ascontiguousarray(norm, dtype=np.float32)
+    steps = np.ascontiguousarray(steps, dtype=np.float32)
+    f = lib().orc_lut_lookup_avx2 if avx2 else lib().orc_lut_lookup
+    f(fp(y), u8p(idx), u8p(tab), fp(norm), fp(steps), blocks, groups, gb)
+    return y
 
 
 def quantize_row(x):

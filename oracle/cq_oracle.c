@@ -357,6 +357,41 @@ void orc_lut_lookup(float *y, const uint8_t *idx, const uint8_t *tab, const floa
     }
 }
 
+/* How the lut product runs on this CPU (orc_set_cpu): the generic Go
+ * routines or their AVX2 forms (lut_amd64.go:9-61, bit for bit the same),
+ * on one thread or split as gemmLUT splits it. Process-wide; set it before
+ * the products, not during them. */
+static int g_avx2 = 0, g_threads = 1;
+
+int orc_set_cpu(int avx2, int threads) {
+    if (avx2 && !orc_have_avx2()) return -1;
+    g_avx2 = avx2 != 0;
+    g_threads = threads < 1 ? 1 : threads;
+    return 0;
+}
+
+/* tensor.Parallel(n, grain, fn) of algo-tensor v0.4.0 (not vendored with the
+ * reference; its call sites are lut.go:109-123, 190-194): [0, n) in
+ * contiguous pieces of at least grain items, at most one per worker. The
+ * pieces here are equal to within one item. Each output depends on its own
+ * inputs only (lut.go:95-101), so any split gives the same bits. */
+typedef void (*piece_fn)(void *ctx, int lo, int hi);
+
+static void parallel(int n, int grain, piece_fn fn, void *ctx) {
+    int pieces = grain > 0 ? n / grain : n;
+    if (pieces > g_threads) pieces = g_threads;
+    if (pieces < 1) pieces = 1;
+    if (pieces == 1) {
+        fn(ctx, 0, n);
+        return;
+    }
+#pragma omp parallel for num_threads(pieces) schedule(static, 1)
+    for (int p = 0; p < pieces; p++) fn(ctx, (int)((long long)n * p / pieces), (int)((long long)n * (p + 1) / pieces));
+}
+
+/* lutPieceBytes (lut.go:88-93) */
+enum { LUT_PIECE_BYTES = 1 << 18 };
+
 /* Scratch of one lut product (kernel.go:47-57). */
 typedef struct {
     float *xh;
@@ -373,47 +408,97 @@ static void lut_tables(const orc_matrix *m, lut_scratch *s, const float *x) {
     for (int k = m->in; k < pad; k++) s->xh[k] = 0;
     for (int g = 0; g < m->groups; g++) {
         float *xg = s->xh + (size_t)g * m->group;
-        orc_fwht(xg, m->group);
         uint8_t *tg = s->tab + (size_t)g * tab_bytes;
-        float mm = m->width == 2 ? orc_lut_tables2(tg, xg, m->group, m->st->cb, m->st->cb_max)
-                                 : orc_lut_tables4(tg, xg, m->group, m->st->cb, m->st->cb_max);
+        float mm;
+        if (g_avx2) { /* the group is at least 8 wide (matrix.go:63-65) */
+            orc_fwht_avx2(xg, m->group);
+            mm = m->width == 2 ? orc_lut_tables2_avx2(tg, xg, m->group, m->st->cb, m->st->cb_max)
+                               : orc_lut_tables4_avx2(tg, xg, m->group, m->st->cb, m->st->cb_max);
+        } else {
+            orc_fwht(xg, m->group);
+            mm = m->width == 2 ? orc_lut_tables2(tg, xg, m->group, m->st->cb, m->st->cb_max)
+                               : orc_lut_tables4(tg, xg, m->group, m->st->cb, m->st->cb_max);
+        }
         s->steps[g] = mm * m->st->lut_step;
     }
 }
 
-/* lutApply (lut.go:182-201), unsplit */
-static void lut_apply(const orc_matrix *m, lut_scratch *s, float *y) {
+typedef struct {
+    const orc_matrix *m;
+    lut_scratch *s;
+    size_t ib, nbk;
+    int b0;
+} lookup_job;
+
+static void lookup_piece(void *ctx, int lo, int hi) {
+    const lookup_job *j = ctx;
+    const orc_matrix *m = j->m;
+    const uint8_t *idx = m->st->bidx + (size_t)(j->b0 + lo) * j->ib;
+    const float *norm = m->st->bnorm + (size_t)(j->b0 + lo) * j->nbk;
+    float *y = j->s->y + (size_t)lo * LUT_ROWS;
+    if (g_avx2)
+        orc_lut_lookup_avx2(y, idx, j->s->tab, norm, j->s->steps, hi - lo, m->groups, m->group_bytes);
+    else
+        orc_lut_lookup(y, idx, j->s->tab, norm, j->s->steps, hi - lo, m->groups, m->group_bytes);
+}
+
+/* lutApply (lut.go:182-201): the blocks split over workers when split. */
+static void lut_apply(const orc_matrix *m, lut_scratch *s, float *y, int split) {
     int b0 = m->row0 / LUT_ROWS, b1 = (m->row0 + m->out + LUT_ROWS - 1) / LUT_ROWS;
-    int nb = b1 - b0;
-    size_t ib = (size_t)m->row_bytes * LUT_ROWS, nbk = (size_t)m->groups * LUT_ROWS;
-    orc_lut_lookup(s->y, m->st->bidx + b0 * ib, s->tab, m->st->bnorm + b0 * nbk, s->steps, nb, m->groups,
-                   m->group_bytes);
+    lookup_job j = {m, s, (size_t)m->row_bytes * LUT_ROWS, (size_t)m->groups * LUT_ROWS, b0};
+    if (split)
+        parallel(b1 - b0, (int)((LUT_PIECE_BYTES + j.ib - 1) / j.ib), lookup_piece, &j);
+    else
+        lookup_piece(&j, 0, b1 - b0);
     int off = m->row0 - b0 * LUT_ROWS;
     memcpy(y, s->y + off, sizeof(float) * (size_t)m->out);
 }
 
-/* gemmLUT + lutRun (lut.go:102-156), serial: the reference's split over
- * activations or blocks gives the same bits (lut.go:95-101). */
-static void gemm_lut(orc_matrix *const *ms, int n, float *const *dsts, const float *x, int rows) {
-    const orc_matrix *m0 = ms[0];
-    int nb = 0;
-    for (int k = 0; k < n; k++) {
-        int b0 = ms[k]->row0 / LUT_ROWS, b1 = (ms[k]->row0 + ms[k]->out + LUT_ROWS - 1) / LUT_ROWS;
-        if (b1 - b0 > nb) nb = b1 - b0;
-    }
+typedef struct {
+    orc_matrix *const *ms;
+    int n, nb;
+    float *const *dsts;
+    const float *x;
+    int split;
+} lut_run_job;
+
+/* lutRun (lut.go:128-156) over activations [lo, hi), with its own scratch. */
+static void lut_run(void *ctx, int lo, int hi) {
+    const lut_run_job *r = ctx;
+    const orc_matrix *m0 = r->ms[0];
     lut_scratch s;
     s.xh = malloc(sizeof(float) * (size_t)m0->groups * m0->group);
     s.tab = malloc((size_t)64 * m0->row_bytes);
     s.steps = malloc(sizeof(float) * (size_t)m0->groups);
-    s.y = malloc(sizeof(float) * ((size_t)nb * LUT_ROWS + 1));
-    for (int i = 0; i < rows; i++) {
-        lut_tables(m0, &s, x + (size_t)i * m0->in);
-        for (int k = 0; k < n; k++) lut_apply(ms[k], &s, dsts[k] + (size_t)i * ms[k]->out);
+    s.y = malloc(sizeof(float) * ((size_t)r->nb * LUT_ROWS + 1));
+    for (int i = lo; i < hi; i++) {
+        lut_tables(m0, &s, r->x + (size_t)i * m0->in);
+        for (int k = 0; k < r->n; k++) lut_apply(r->ms[k], &s, r->dsts[k] + (size_t)i * r->ms[k]->out, r->split);
     }
     free(s.xh);
     free(s.tab);
     free(s.steps);
     free(s.y);
+}
+
+/* gemmLUT (lut.go:102-126): over the activations when there are several and
+ * they outnumber the workers or the product is small, else one activation
+ * at a time with each large product's blocks split. */
+static void gemm_lut(orc_matrix *const *ms, int n, float *const *dsts, const float *x, int rows) {
+    long long per = 0;
+    int nb = 0;
+    for (int k = 0; k < n; k++) {
+        int b0 = ms[k]->row0 / LUT_ROWS, b1 = (ms[k]->row0 + ms[k]->out + LUT_ROWS - 1) / LUT_ROWS;
+        if (b1 - b0 > nb) nb = b1 - b0;
+        per += (long long)ms[k]->out * ms[k]->row_bytes;
+    }
+    lut_run_job r = {ms, n, nb, dsts, x, 0};
+    if (rows > 1 && (rows >= g_threads || per < 2LL * LUT_PIECE_BYTES)) {
+        parallel(rows, (int)((LUT_PIECE_BYTES + per - 1) / per), lut_run, &r);
+        return;
+    }
+    r.split = per >= 2LL * LUT_PIECE_BYTES;
+    lut_run(&r, 0, rows);
 }
 
 /* ---- scalar kernels (kernel.go:160-374) --------------------------------- */

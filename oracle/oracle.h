@@ -79,6 +79,20 @@ void orc_lut_lookup(float *y, const uint8_t *idx, const uint8_t *tab, const floa
                     int blocks, int groups, int gb);                                       /* lut.go:289-313 */
 float orc_lut_step(int group);                                                             /* lut.go:213-215 */
 
+/* The AVX2 forms of the lut routines (lut_amd64.s, cq_avx2.c), bit for bit
+ * the generic ones; callable only where orc_have_avx2(). fwht: n a power of
+ * two >= 8; tables: n a multiple of 8. */
+int orc_have_avx2(void);
+void orc_fwht_avx2(float *x, int n);                                                        /* lut_amd64.s:12-75 */
+float orc_lut_tables2_avx2(uint8_t *tab, const float *x, int n, const float *cb, float cb_max); /* :150-197 */
+float orc_lut_tables4_avx2(uint8_t *tab, const float *x, int n, const float *cb, float cb_max); /* :199-233 */
+void orc_lut_lookup_avx2(float *y, const uint8_t *idx, const uint8_t *tab, const float *norm, const float *steps,
+                         int blocks, int groups, int gb);                                   /* :235-378 */
+/* How lut products run from here on: avx2 1 for the AVX2 forms (-1 if the
+ * CPU lacks AVX2), threads > 1 to split them as gemmLUT does
+ * (lut.go:102-201). Process-wide; not to be changed while products run. */
+int orc_set_cpu(int avx2, int threads);
+
 /* ---- internal/needle: int8 numerics ------------------------------------- */
 
 float orc_quantize_row(int8_t *q, const float *x, int n);                /* int8.go:36-55 */
