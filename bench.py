@@ -208,7 +208,7 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
         orc.set_cpu(False, 1)
         res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
                                "sample": f"{n} greedy tokens at batch 1 (runs of 10 from position 0), oracle "
-                                         f"decoder, lut products {'AVX2' if avx2 else 'generic'} split over "
+                                         f"decoder, lut products and int8 attention {'AVX2' if avx2 else 'generic'}, products split over "
                                          f"{threads} threads as the reference splits them, {el:.1f} s"}
     return res
 

@@ -57,6 +57,9 @@ def lib():
             "orc_lut_lookup_avx2": (None, [POINTER(c_float), POINTER(c_uint8), POINTER(c_uint8), POINTER(c_float),
                                            POINTER(c_float), c_int, c_int, c_int]),
             "orc_set_cpu": (c_int, [c_int, c_int]),
+            "orc_dots_i8_avx2": (None, [POINTER(c_int32), c_int, POINTER(c_int8), c_int, POINTER(c_int8), c_int]),
+            "orc_axpys_i8_avx2": (None, [POINTER(c_float), c_int, POINTER(c_float), c_int, POINTER(c_int8), c_int]),
+            "orc_exp_sub_sum_avx2": (c_float, [POINTER(c_float), c_int, c_float]),
             "orc_quantize_row": (c_float, [POINTER(c_int8), POINTER(c_float), c_int]),
             "orc_quantize_rows": (None, [POINTER(c_int8), POINTER(c_float), POINTER(c_float), c_int, c_int, c_int]),
             "orc_dots_i8": (None, [POINTER(c_int32), c_int, POINTER(c_int8), c_int, POINTER(c_int8), c_int]),
@@ -237,6 +240,32 @@ def quantize_rows(x, cols, width):
 def exp_sub_sum(s, m, variant):
     s = np.array(s, dtype=np.float32)
     total = lib().orc_exp_sub_sum(fp(s), s.size, np.float32(m), variant)
+    return s, np.float32(total)
+
+
+def dots_i8(q, k, n, stride, avx2=False):
+    """dotsI8 (int8kernel.go:346-357, or its AVX2 form): n int32 dots of q
+    with the rows of k, stride bytes apart."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    k = np.ascontiguousarray(k, dtype=np.int8)
+    dst = np.zeros(n, dtype=np.int32)
+    (lib().orc_dots_i8_avx2 if avx2 else lib().orc_dots_i8)(i32p(dst), n, i8p(q), q.size, i8p(k), stride)
+    return dst
+
+
+def axpys_i8(out, w, v, stride, avx2=False):
+    """axpysI8 (int8kernel.go:360-368, or its AVX2 form): out += w[j] * v row j."""
+    out = np.array(out, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.int8)
+    (lib().orc_axpys_i8_avx2 if avx2 else lib().orc_axpys_i8)(fp(out), out.size, fp(w), w.size, i8p(v), stride)
+    return out
+
+
+def exp_sub_sum_avx2(s, m):
+    """expSubSumAVX2 on a multiple-of-8 length (exp_amd64.s:68-124)."""
+    s = np.array(s, dtype=np.float32)
+    total = lib().orc_exp_sub_sum_avx2(fp(s), s.size, np.float32(m))
     return s, np.float32(total)
 
 

@@ -36,7 +36,7 @@ enum { ROWS = 32, LUT_Q = 8191, LUT_BIAS = 64 };
 
 int orc_have_avx2(void) {
     __builtin_cpu_init();
-    return __builtin_cpu_supports("avx2");
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
 }
 
 #define AVX2 __attribute__((target("avx2")))

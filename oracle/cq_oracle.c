@@ -363,6 +363,8 @@ void orc_lut_lookup(float *y, const uint8_t *idx, const uint8_t *tab, const floa
  * the products, not during them. */
 static int g_avx2 = 0, g_threads = 1;
 
+int orc_cpu_avx2(void) { return g_avx2; }
+
 int orc_set_cpu(int avx2, int threads) {
     if (avx2 && !orc_have_avx2()) return -1;
     g_avx2 = avx2 != 0;

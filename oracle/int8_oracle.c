@@ -14,6 +14,8 @@
  *                                       published single-precision exp) with the
  *                                       kernel's FMA steps and 8-lane sum
  *   internal/needle/load.go:125-138     softmaxInPlace
+ * With the AVX2 CPU mode (orc_set_cpu) the attention runs the AVX2 forms of
+ * dotsI8, axpysI8 and the exp kernel (int8_avx2.c), bit for bit these.
  *
  * How each part is pinned without running the reference (tests/):
  *   QuantizeRow   the reference's hand vectors (int8_test.go:19-34) and its
@@ -160,7 +162,7 @@ float orc_exp_sub_sum(float *s, int n, float m, int variant) {
     /* exp_amd64.go:13-25 */
     int n8 = n & ~7;
     if (n8 == 0) return exp_sub_sum_generic(s, n, m);
-    float sum = exp_sub_sum_avx2(s, n8, m);
+    float sum = orc_cpu_avx2() ? orc_exp_sub_sum_avx2(s, n8, m) : exp_sub_sum_avx2(s, n8, m);
     if (n8 == n) return sum;
     float tail = exp_sub_sum_generic(s + n8, n - n8, m);
     return sum + tail;
@@ -172,6 +174,23 @@ void orc_softmax(float *s, int n, int variant) {
     for (int i = 0; i < n; i++) m = gomax(m, s[i]);
     float sum = orc_exp_sub_sum(s, n, m, variant);
     for (int i = 0; i < n; i++) s[i] /= sum;
+}
+
+/* dotsI8Kernel / axpysI8Kernel (int8kernel_amd64.go:13-33): the AVX2 forms
+ * for widths that are positive multiples of 16 when the CPU mode asks for
+ * them, the generic loops otherwise; the same bits either way. */
+static void dots_i8(int32_t *dst, int n, const int8_t *q, int width, const int8_t *k, int stride) {
+    if (orc_cpu_avx2() && width > 0 && width % 16 == 0)
+        orc_dots_i8_avx2(dst, n, q, width, k, stride);
+    else
+        orc_dots_i8(dst, n, q, width, k, stride);
+}
+
+static void axpys_i8(float *out, int width, const float *w, int n, const int8_t *v, int stride) {
+    if (orc_cpu_avx2() && width > 0 && width % 16 == 0)
+        orc_axpys_i8_avx2(out, width, w, n, v, stride);
+    else
+        orc_axpys_i8(out, width, w, n, v, stride);
 }
 
 int orc_attend_int8_spans(float *out, const float *q, int t, int heads, const int8_t *kq, const float *ks,
@@ -200,7 +219,7 @@ int orc_attend_int8_spans(float *out, const float *q, int t, int heads, const in
                 o += len;
                 if (quant_q) {
                     /* int8Logits (int8.go:278-285) */
-                    orc_dots_i8(dots, len, q8, qk, kq + (size_t)lo * k_cols + (size_t)kv * qk, k_cols);
+                    dots_i8(dots, len, q8, qk, kq + (size_t)lo * k_cols + (size_t)kv * qk, k_cols);
                     for (int j = 0; j < len; j++) {
                         float sc = sq * ks[(size_t)(lo + j) * kv_heads + kv];
                         float a = (float)dots[j] * sc;
@@ -222,7 +241,7 @@ int orc_attend_int8_spans(float *out, const float *q, int t, int heads, const in
                 const float *vsp = vs + (size_t)lo * kv_heads;
                 if (probs) memcpy(probs + ((size_t)i * heads + h) * nk + lo, sj, sizeof(float) * (size_t)len);
                 for (int j = 0; j < len; j++) sj[j] *= vsp[(size_t)j * kv_heads + kv];
-                orc_axpys_i8(out + ((size_t)i * heads + h) * vd, vd, sj, len,
+                axpys_i8(out + ((size_t)i * heads + h) * vd, vd, sj, len,
                              vq + (size_t)lo * v_cols + (size_t)kv * vd, v_cols);
                 o += len;
             }

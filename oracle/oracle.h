@@ -88,10 +88,19 @@ float orc_lut_tables2_avx2(uint8_t *tab, const float *x, int n, const float *cb,
 float orc_lut_tables4_avx2(uint8_t *tab, const float *x, int n, const float *cb, float cb_max); /* :199-233 */
 void orc_lut_lookup_avx2(float *y, const uint8_t *idx, const uint8_t *tab, const float *norm, const float *steps,
                          int blocks, int groups, int gb);                                   /* :235-378 */
-/* How lut products run from here on: avx2 1 for the AVX2 forms (-1 if the
- * CPU lacks AVX2), threads > 1 to split them as gemmLUT does
- * (lut.go:102-201). Process-wide; not to be changed while products run. */
+/* How lut products and the int8 attention run from here on: avx2 1 for the
+ * AVX2 forms (-1 if the CPU lacks AVX2 or FMA), threads > 1 to split the lut
+ * products as gemmLUT does (lut.go:102-201). Process-wide; not to be changed
+ * while products run. */
 int orc_set_cpu(int avx2, int threads);
+int orc_cpu_avx2(void); /* the mode's avx2 flag */
+/* The AVX2 forms of the int8 attention kernels (int8kernel_amd64.s,
+ * exp_amd64.s; int8_avx2.c), bit for bit the generic ones; widths positive
+ * multiples of 16, n8 a multiple of 8. AttendInt8Spans runs them in the
+ * AVX2 mode. */
+void orc_dots_i8_avx2(int32_t *dst, int n, const int8_t *q, int width, const int8_t *k, int stride);
+void orc_axpys_i8_avx2(float *out, int width, const float *w, int n, const int8_t *v, int stride);
+float orc_exp_sub_sum_avx2(float *s, int n8, float m);
 
 /* ---- internal/needle: int8 numerics ------------------------------------- */
 

@@ -2,8 +2,10 @@
 internal/cq/lut_amd64.s) against the generic restatement, bit for bit, as
 the reference's internal/cq/asm_test.go holds its assembly to the Go code;
 and the products split over threads as gemmLUT splits them (lut.go:102-201)
-against the serial ones, bit for bit, as parallel_test.go:45-168 holds them.
-The AVX2 form and the threads are what bench.py's CPU baseline times."""
+against the serial ones, bit for bit, as parallel_test.go:45-168 holds them;
+and the AVX2 forms of the int8 attention kernels (int8kernel_amd64.s,
+exp_amd64.s) against the generic ones. The AVX2 forms and the threads are
+what bench.py's CPU baseline times."""
 
 import numpy as np
 import pytest
@@ -107,3 +109,48 @@ def test_gemm_activation_split(rows):
         got = [m.gemm(x, rows), v.gemm(x, rows), orc.gemms([m, v], x, rows)]
         assert same(got[0], want[0]) and same(got[1], want[1])
         assert all(same(a, b) for a, b in zip(got[2], want[2]))
+
+
+@pytest.mark.parametrize("width,n", [(16, 1), (64, 37), (128, 300), (48, 9)])
+def test_dots_and_axpys_i8(width, n):
+    # dotsI8 / axpysI8 AVX2 forms (int8kernel_amd64.s) against the generic
+    # loops; stride wider than the row, as in a multi-head cache
+    g = synth.rng(width + n)
+    stride = width * 3
+    q = g.integers(-128, 128, size=width, dtype=np.int8)
+    k = g.integers(-128, 128, size=n * stride, dtype=np.int8)
+    assert np.array_equal(orc.dots_i8(q, k, n, stride, avx2=True), orc.dots_i8(q, k, n, stride))
+    out = g.standard_normal(width).astype(np.float32)
+    w = (g.random(n) * 1e-2).astype(np.float32)
+    assert same(orc.axpys_i8(out, w, k, stride, avx2=True), orc.axpys_i8(out, w, k, stride))
+
+
+@pytest.mark.parametrize("n", [8, 64, 1504])
+def test_exp_sub_sum(n):
+    # expSubSumAVX2 against the lane-by-lane restatement (variant 1); the
+    # inputs reach below the -87.33 flush and include the maximum itself
+    g = synth.rng(n)
+    s = (g.standard_normal(n) * 30).astype(np.float32)
+    m = np.float32(s.max())
+    e0, t0 = orc.exp_sub_sum(s, m, 1)
+    e1, t1 = orc.exp_sub_sum_avx2(s, m)
+    assert same(e0, e1) and same(t0, t1)
+
+
+@pytest.mark.parametrize("quant_q", [True, False])
+def test_attend_int8_avx2_mode(quant_q):
+    # AttendInt8Spans in the AVX2 mode equals the generic run bit for bit:
+    # cross attention over 1500 keys and a two-span self-attention band
+    g = synth.rng(5 if quant_q else 6)
+    heads, qk, nk = 8, 64, 1500
+    cols = heads * qk
+    q = g.standard_normal(2 * cols).astype(np.float32)
+    kq = g.integers(-128, 128, size=nk * cols, dtype=np.int8)
+    vq = g.integers(-128, 128, size=nk * cols, dtype=np.int8)
+    ks = (g.random(nk * heads) * 0.05 + 1e-3).astype(np.float32)
+    vs = (g.random(nk * heads) * 0.05 + 1e-3).astype(np.float32)
+    spans = np.array([[0, 0, 0, nk], [0, 4, 600, 1203]], np.int32)
+    args = (q, 2, heads, kq, ks, cols, qk, vq, vs, cols, qk, nk, spans, np.float32(8.0), quant_q)
+    want = orc.attend_int8_spans(*args)
+    orc.set_cpu(True, 1)
+    assert same(orc.attend_int8_spans(*args), want)
