@@ -367,6 +367,7 @@ int orc_cpu_avx2(void) { return g_avx2; }
 
 int orc_set_cpu(int avx2, int threads) {
     if (avx2 && !orc_have_avx2()) return -1;
+    if (threads > 1 && orc_pool_reserve(threads)) return -2;
     g_avx2 = avx2 != 0;
     g_threads = threads < 1 ? 1 : threads;
     return 0;
@@ -377,18 +378,13 @@ int orc_set_cpu(int avx2, int threads) {
  * contiguous pieces of at least grain items, at most one per worker. The
  * pieces here are equal to within one item. Each output depends on its own
  * inputs only (lut.go:95-101), so any split gives the same bits. */
-typedef void (*piece_fn)(void *ctx, int lo, int hi);
+typedef orc_piece_fn piece_fn;
 
 static void parallel(int n, int grain, piece_fn fn, void *ctx) {
     int pieces = grain > 0 ? n / grain : n;
     if (pieces > g_threads) pieces = g_threads;
     if (pieces < 1) pieces = 1;
-    if (pieces == 1) {
-        fn(ctx, 0, n);
-        return;
-    }
-#pragma omp parallel for num_threads(pieces) schedule(static, 1)
-    for (int p = 0; p < pieces; p++) fn(ctx, (int)((long long)n * p / pieces), (int)((long long)n * (p + 1) / pieces));
+    orc_pool_run(n, pieces, fn, ctx); /* piece p: [n*p/pieces, n*(p+1)/pieces) */
 }
 
 /* lutPieceBytes (lut.go:88-93) */

@@ -94,6 +94,13 @@ void orc_lut_lookup_avx2(float *y, const uint8_t *idx, const uint8_t *tab, const
  * while products run. */
 int orc_set_cpu(int avx2, int threads);
 int orc_cpu_avx2(void); /* the mode's avx2 flag */
+/* The worker pool behind the split (cpu_pool.c): reserve keeps threads - 1
+ * workers (-1 if one cannot start); run calls fn(ctx, lo, hi) on pieces
+ * [n*p/pieces, n*(p+1)/pieces) of [0, n), piece 0 on the caller, and returns
+ * when all are done. One caller thread at a time. */
+typedef void (*orc_piece_fn)(void *ctx, int lo, int hi);
+int orc_pool_reserve(int threads);
+void orc_pool_run(int n, int pieces, orc_piece_fn fn, void *ctx);
 /* The AVX2 forms of the int8 attention kernels (int8kernel_amd64.s,
  * exp_amd64.s; int8_avx2.c), bit for bit the generic ones; widths positive
  * multiples of 16, n8 a multiple of 8. AttendInt8Spans runs them in the
