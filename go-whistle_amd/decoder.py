@@ -20,10 +20,15 @@ quantized path serves:
 
 with the int8 query (Int8.Act) and amd64's softmax exponent. Every step is
 bit for bit the same arithmetic as the C restatement in oracle/, so the
-greedy tokens match exactly. The cross memory of each stream is its own
-1500 x 512 keys and values drawn N(0, 1) and quantised per head on the
-device (the projected encoder states; their projection is the batched
-encoder workload, not part of the decode step).
+greedy tokens match exactly. The cross memory of each stream is built once
+from its own 1500 x 512 encoder states drawn N(0, 1), as cross.project
+does it (cross.go:181-204, without q/k norms or cross RoPE):
+
+  per layer: K, V = GEMMs(Wck, Wcv; enc) over the frames  needle.ApplyShared
+             int8 K, V = QuantizeRows per head             int8.go:116-141
+
+on the device (the batched products take the MFMA form); that build is
+not part of the decode step.
 
 All state lives on the device; step() queues one token's launches on
 torch's current stream and can be captured in a HIP graph.
@@ -54,7 +59,7 @@ class DecoderConfig:
     theta: float = 1e5
 
 
-LAYER_MATS = ("wq", "wk", "wv", "wo", "wcq", "wco", "w1", "w2")
+LAYER_MATS = ("wq", "wk", "wv", "wo", "wcq", "wco", "wck", "wcv", "w1", "w2")
 
 
 @dataclass
@@ -117,6 +122,7 @@ def make_model(seed, cfg=DecoderConfig()):
         layers.append({"wq": packed(d, d, cfg.attn_bits), "wk": packed(d, d, cfg.attn_bits),
                        "wv": packed(d, d, cfg.attn_bits), "wo": packed(d, d, cfg.attn_bits),
                        "wcq": packed(d, d, cfg.attn_bits), "wco": packed(d, d, cfg.attn_bits),
+                       "wck": packed(d, d, cfg.attn_bits), "wcv": packed(d, d, cfg.attn_bits),
                        "w1": packed(f, d, cfg.ffn_bits), "w2": packed(d, f, cfg.ffn_bits)})
     scales = (g.standard_normal((cfg.layers * 3 + 1, d)) * 0.1).astype(np.float32)
     gains = (np.float32(1) + scales).astype(np.float32)  # NewZCRMSNorm (norm.go:22-30)
@@ -126,12 +132,10 @@ def make_model(seed, cfg=DecoderConfig()):
     return Model(cfg=cfg, emb=emb, layers=layers, gains=gains, rope_cos=cos, rope_sin=sin, scale=np.float32(1))
 
 
-def memory_states(seed, cfg, stream, layer):
-    """One stream's cross keys and values for one layer, N(0, 1), [frames, dim]."""
-    g = synth.rng((seed * 1000003 + stream) * 131 + layer)
-    k = g.standard_normal(cfg.frames * cfg.dim).astype(np.float32)
-    v = g.standard_normal(cfg.frames * cfg.dim).astype(np.float32)
-    return k, v
+def encoder_states(seed, cfg, stream):
+    """One stream's encoder output, N(0, 1), [frames, dim]."""
+    g = synth.rng(seed * 1000003 + stream)
+    return g.standard_normal(cfg.frames * cfg.dim).astype(np.float32)
 
 
 def _ptr(t):
@@ -142,9 +146,9 @@ def _ptr(t):
 
 class Decoder:
     """The model on the device for `batch` streams decoding in lockstep.
-    fused: the norms, residual adds, SiLU and RoPE ride in the products,
-    appends and attention (10 launches per layer instead of 19, the same
-    bits)."""
+    fused: the norms, residual adds, SiLU, RoPE and the K/V appends ride in
+    the products and the attention (8 launches per layer instead of 19, the
+    same bits)."""
 
     def __init__(self, model, batch, device="cuda", fused=True):
         import torch
@@ -179,43 +183,42 @@ class Decoder:
         self.cross_vs = [z(B, c.frames, hk) for _ in range(c.layers)]
 
     def set_memory(self, seed, generator="numpy"):
-        """Quantises each stream's cross keys and values (QuantizeRows per
-        head, bit for bit) into the int8 memory. generator "numpy" draws
-        them with memory_states; "device" draws them on the GPU (torch's
-        seeded Philox) for large batches."""
+        """Builds each stream's int8 cross memory from its encoder states
+        (cross.project, cross.go:181-204): per layer K, V = GEMMs(Wck, Wcv)
+        over the frames, then QuantizeRows per head, bit for bit. generator
+        "numpy" draws the states with encoder_states; "device" draws them on
+        the GPU (torch's seeded Philox) for large batches."""
         import torch
 
         c = self.cfg
-        tmp_k = torch.empty(c.frames * c.dim, dtype=torch.float32, device=self.x.device)
-        tmp_v = torch.empty_like(tmp_k)
+        enc = torch.empty(c.frames * c.dim, dtype=torch.float32, device=self.x.device)
+        tmp_k = torch.empty_like(enc)
+        tmp_v = torch.empty_like(enc)
         gen = torch.Generator(device=self.x.device)
-        for layer in range(c.layers):
-            for b in range(self.batch):
-                if generator == "numpy":
-                    k, v = memory_states(seed, c, b, layer)
-                    tmp_k.copy_(torch.from_numpy(k))
-                    tmp_v.copy_(torch.from_numpy(v))
-                else:
-                    gen.manual_seed((seed * 1000003 + b) * 131 + layer)
-                    torch.randn(tmp_k.shape, generator=gen, out=tmp_k, device=tmp_k.device)
-                    torch.randn(tmp_v.shape, generator=gen, out=tmp_v, device=tmp_v.device)
+        for b in range(self.batch):
+            if generator == "numpy":
+                enc.copy_(torch.from_numpy(encoder_states(seed, c, b)))
+            else:
+                gen.manual_seed(seed * 1000003 + b)
+                torch.randn(enc.shape, generator=gen, out=enc, device=enc.device)
+            for layer in range(c.layers):
+                m = self.mats[layer]
+                cq.gemms_dev([m["wck"], m["wcv"]], [tmp_k, tmp_v], enc, c.frames)
                 needle.quantize_rows_dev(self.cross_k[layer][b], self.cross_ks[layer][b], tmp_k, c.frames, c.dim,
                                          c.head_dim)
                 needle.quantize_rows_dev(self.cross_v[layer][b], self.cross_vs[layer][b], tmp_v, c.frames, c.dim,
                                          c.head_dim)
         torch.cuda.synchronize()
 
-    def memory_states_device(self, seed, stream, layer):
-        """The keys and values set_memory(generator="device") drew for one
-        stream and layer, copied to the host."""
+    def encoder_states_device(self, seed, stream):
+        """The encoder states set_memory(generator="device") drew for one
+        stream, copied to the host."""
         import torch
 
         c = self.cfg
         gen = torch.Generator(device=self.x.device)
-        gen.manual_seed((seed * 1000003 + stream) * 131 + layer)
-        k = torch.randn(c.frames * c.dim, generator=gen, device=self.x.device)
-        v = torch.randn(c.frames * c.dim, generator=gen, device=self.x.device)
-        return k.cpu().numpy(), v.cpu().numpy()
+        gen.manual_seed(seed * 1000003 + stream)
+        return torch.randn(c.frames * c.dim, generator=gen, device=self.x.device).cpu().numpy()
 
     def reset(self, tokens):
         import torch

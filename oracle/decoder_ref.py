@@ -2,7 +2,8 @@
 stream at a time: the same operations in the same order as
 go-whistle_amd/decoder.py's device step (embedding Row x sqrt(d),
 ZCRMSNorm, lut GEMMs, RoPE, int8 append and AttendInt8 with the int8 query
-and amd64's exponent, SiLU, tied head, first-index argmax).
+and amd64's exponent, SiLU, tied head, first-index argmax), over a cross
+memory projected from the encoder states and quantised per head.
 
 TEST INFRASTRUCTURE ONLY: the checker for the device decoder and the
 cpu_baseline of bench.py's decode leg.
@@ -21,11 +22,15 @@ class RefDecoder:
         self.emb = orc.OMatrix.new(model.emb)
         self.mats = [{n: orc.OMatrix.new(p[n]) for n in p} for p in model.layers]
 
-    def memory(self, kstates, vstates):
-        """Per layer (k, v) float32 [frames*dim] -> int8 codes and scales."""
+    def memory(self, enc):
+        """The stream's int8 cross memory from its encoder states enc, float32
+        [frames*dim] (cross.project, cross.go:181-204): per layer K, V =
+        GEMMs(Wck, Wcv) over the frames (needle.ApplyShared), QuantizeRows
+        per head."""
         c = self.cfg
         self.mem = []
-        for k, v in zip(kstates, vstates):
+        for w in self.mats:
+            k, v = orc.gemms([w["wck"], w["wcv"]], enc, c.frames)
             kq, ks = orc.quantize_rows(k, c.dim, c.head_dim)
             vq, vs = orc.quantize_rows(v, c.dim, c.head_dim)
             self.mem.append((kq, ks, vq, vs))

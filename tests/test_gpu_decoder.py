@@ -103,11 +103,8 @@ def _run(cfg, seed, batch, first, n, check_streams, generator="numpy"):
     logits = d.logits.cpu().numpy()
     ref = decoder_ref.RefDecoder(model)
     for b in check_streams:
-        if generator == "numpy":
-            ks, vs = zip(*[dec.memory_states(seed, cfg, b, l) for l in range(cfg.layers)])
-        else:
-            ks, vs = zip(*[d.memory_states_device(seed, b, l) for l in range(cfg.layers)])
-        ref.memory(ks, vs)
+        enc = dec.encoder_states(seed, cfg, b) if generator == "numpy" else d.encoder_states_device(seed, b)
+        ref.memory(enc)
         want, wl = ref.decode(first[b], n, want_logits=True)
         assert list(toks[b]) == want, (b, list(toks[b]), want)
         assert same(logits[b], wl[-1]), b
