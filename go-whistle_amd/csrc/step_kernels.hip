@@ -7,7 +7,7 @@
 //   rope_kernel        Rope.apply (internal/needle/rope.go:69-81): per head,
 //                      [x1·cos − x2·sin, x2·cos + x1·sin], products rounded.
 //   argmax_kernel      argmax (internal/decoder/greedy.go:181-191): the first
-//                      index of the largest value.
+//                      index of the largest value (0 when v[0] is NaN).
 //   silu_kernel        silu_value (cq_device.hpp): the synthetic decoder's FFN
 //                      activation (no reference counterpart; defined so that
 //                      CPU and GPU agree bit for bit).
@@ -86,36 +86,73 @@ __global__ __launch_bounds__(256) void rope_kernel(float *x, int heads, int head
     }
 }
 
+// greedy.go's argmax keeps best = 0 and moves to i when v[i] > v[best]: the
+// answer is 0 when v[0] is NaN, else the first index of the largest value
+// that is not NaN (NaN never compares greater; +0 and -0 tie). Each thread
+// takes its values in index order (16-byte loads, eight in flight), NaN
+// never a candidate; candidates combine larger value first, then smaller
+// index, across the wavefront (lane exchanges) and the workgroup (LDS).
+struct ArgmaxCand {
+    float v;
+    int i;  // INT_MAX: none
+};
+
+__device__ __forceinline__ ArgmaxCand argmax_pick(ArgmaxCand a, ArgmaxCand b) {
+    if (b.i == INT_MAX) return a;
+    if (a.i == INT_MAX || b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
 __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *v, int n) {
-    const int r = blockIdx.x, tid = threadIdx.x;
+    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *row = v + static_cast<long long>(r) * n;
-    float best = -INFINITY;
-    int bi = INT_MAX;
-    for (int i = tid; i < n; i += blockDim.x) {
-        const float x = row[i];
-        if (bi == INT_MAX || x > best) {  // the first of this thread's values that beats the rest
-            best = x;
-            bi = i;
-        }
-    }
-    __shared__ float sb[256];
-    __shared__ int si[256];
-    sb[tid] = best;
-    si[tid] = bi;
-    __syncthreads();
-    for (int off = blockDim.x / 2; off > 0; off >>= 1) {
-        if (tid < off) {
-            const float ob = sb[tid + off];
-            const int oi = si[tid + off];
-            // larger value wins; on equal values the smaller index (first)
-            if (oi != INT_MAX && (si[tid] == INT_MAX || ob > sb[tid] || (ob == sb[tid] && oi < si[tid]))) {
-                sb[tid] = ob;
-                si[tid] = oi;
+    ArgmaxCand c{0.0f, INT_MAX};
+    auto take = [&](float x, int i) {
+        if (x == x && (c.i == INT_MAX || x > c.v)) c = ArgmaxCand{x, i};
+    };
+    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+        const int n4 = n >> 2;
+        const float4 *row4 = reinterpret_cast<const float4 *>(row);
+        for (int base = 0; base < n4; base += 8 * 256) {
+            float4 f[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int i4 = base + k * 256 + tid;
+                if (i4 < n4) f[k] = row4[i4];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int i4 = base + k * 256 + tid;
+                if (i4 < n4) {
+                    take(f[k].x, 4 * i4);
+                    take(f[k].y, 4 * i4 + 1);
+                    take(f[k].z, 4 * i4 + 2);
+                    take(f[k].w, 4 * i4 + 3);
+                }
             }
         }
-        __syncthreads();
+    } else {
+        for (int i = tid; i < n; i += 256) take(row[i], i);
     }
-    if (tid == 0) out[r] = si[0] == INT_MAX ? 0 : si[0];
+#pragma unroll
+    for (int h = 32; h > 0; h >>= 1) {
+        ArgmaxCand o;
+        o.v = __shfl_xor(c.v, h);
+        o.i = __shfl_xor(c.i, h);
+        c = argmax_pick(c, o);
+    }
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if (lane == 0) {
+        sv[wave] = c.v;
+        si[wave] = c.i;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w) c = argmax_pick(c, ArgmaxCand{sv[w], si[w]});
+        const bool nan0 = n > 0 && row[0] != row[0];
+        out[r] = (n == 0 || nan0 || c.i == INT_MAX) ? 0 : c.i;
+    }
 }
 
 __global__ __launch_bounds__(256) void silu_kernel(float *x, long long n) {

@@ -95,6 +95,34 @@ def test_append_at_positions():
         assert not qh[b, others].any()
 
 
+@pytest.mark.parametrize("n", [16384, 1001, 5, 4100])
+def test_argmax_edges(n):
+    # greedy.go's argmax on the device against the oracle: ties (first
+    # index), NaN anywhere (never a winner; at index 0 the answer is 0), -0
+    # against +0, -inf rows; n = 1001 and 5 take the scalar path, 4100 a
+    # partial last round of 16-byte loads
+    import torch
+
+    g = synth.rng(n)
+    rows = 8
+    v = g.standard_normal((rows, n)).astype(np.float32)
+    nan = np.float32("nan")
+    v[0, n // 2] = v[0, n - 1] = 60  # tie: first wins
+    v[1, 0] = nan  # answer 0
+    v[2, 1 % n] = nan  # a thread's first value NaN, the true maximum after it
+    v[2, n - 1] = 70
+    v[3, :] = 0.0
+    v[3, 0] = -0.0  # +0 does not beat -0
+    v[4, :] = -np.inf
+    v[5, ::3] = nan
+    v[6, :] = nan
+    v[7, n - 1] = 80
+    am, vd = torch.zeros(rows, dtype=torch.int32, device="cuda"), _t(v)
+    check(lib().nd_argmax_dev(_p(am), _p(vd), rows, n, _s()))
+    torch.cuda.synchronize()
+    assert list(am.cpu().numpy()) == list(orc.argmax(v, rows, n))
+
+
 def _run(cfg, seed, batch, first, n, check_streams, generator="numpy"):
     model = dec.make_model(seed, cfg)
     d = dec.Decoder(model, batch)

@@ -53,6 +53,31 @@ def test_argmax_first_on_ties():
     assert list(got) == [int(np.argmax(v[0])), 17, 0, 999]
 
 
+def test_argmax_nan_and_signed_zero():
+    # greedy.go's loop compares x > v[best] from best = 0: NaN never wins, a
+    # NaN at index 0 is never beaten, and +0 does not beat -0. Stated here
+    # as its closed form: 0 if v[0] is NaN, else the first index of the
+    # largest non-NaN value.
+    nan = np.float32("nan")
+    rows = [
+        [1, nan, 5, 5, 2],
+        [nan, 9, 8, 7, 6],
+        [-0.0, 0.0, -1, -2, -3],
+        [-np.inf, -np.inf, -np.inf, -np.inf, -np.inf],
+        [nan, nan, nan, nan, nan],
+        [3, nan, nan, 3, nan],
+    ]
+    v = np.array(rows, np.float32)
+
+    def closed_form(r):
+        if np.isnan(r[0]):
+            return 0
+        m = np.nanmax(r)
+        return int(np.flatnonzero(r == m)[0])
+
+    assert list(orc.argmax(v, len(rows), 5)) == [closed_form(r) for r in v] == [2, 0, 0, 0, 0, 0]
+
+
 def test_silu_vs_float64():
     x = np.concatenate([np.linspace(-30, 30, 20001), [0.0, -0.0, 1e-30, -1e-30, 80.0, -80.0]]).astype(np.float32)
     got = orc.silu(x).astype(np.float64)
