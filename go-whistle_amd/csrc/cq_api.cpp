@@ -927,6 +927,15 @@ int kv_quantize_rows_dev(int8_t *q, float *s, const float *x, int rows, int cols
     return CQ_OK;
 }
 
+int nd_fake_quant_dev(float *dst, const float *x, long long rows, int cols, int width, void *stream) {
+    if (width <= 0 || cols % width != 0)
+        return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "needle: %lld rows", rows);
+    HIP_TRY(launch_fake_quant(dst, x, rows * (cols / width), width, static_cast<hipStream_t>(stream)),
+            "fake quant launch");
+    return CQ_OK;
+}
+
 int kv_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, int width) {
     if (width <= 0 || cols % width != 0)
         return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);

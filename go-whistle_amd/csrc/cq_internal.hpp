@@ -144,6 +144,7 @@ struct RowArgs {
 hipError_t launch_rows(const RowArgs &a, hipStream_t stream);
 
 // int8 numerics
+hipError_t launch_fake_quant(float *dst, const float *x, long long chunks, int width, hipStream_t stream);
 hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
                                 hipStream_t stream);
 

@@ -52,6 +52,28 @@ __global__ __launch_bounds__(256) void quantize_kernel(int8_t *q, float *s, cons
     if (lane == 0) s[c] = sc;
 }
 
+// fakeQuant (int8.go:57-75): each chunk of width values through QuantizeRow
+// and back, dst = float32(q) * s (the input of a Linear WithInt8Input,
+// quantInput, int8.go:81-88). dst may be x: a chunk's reads for its bound
+// finish before its writes.
+__global__ __launch_bounds__(256) void fake_quant_kernel(float *dst, const float *x, long long chunks, int width) {
+    const int lane = threadIdx.x & 63;
+    const long long c = static_cast<long long>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
+    if (c >= chunks) return;
+    const float *xc = x + c * width;
+    float m = 0.0f;
+    for (int i = lane; i < width; i += 64) m = fmaxf(m, fabsf(xc[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+    float *dc = dst + c * width;
+    for (int i = lane; i < width; i += 64) {
+        float r = rintf(xc[i] / sc);
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        dc[i] = static_cast<float>(static_cast<int>(r)) * sc;  // float32(q): a code of 0 is +0, never -0
+    }
+}
+
 __device__ __forceinline__ float exp_generic(float d) { return static_cast<float>(exp(static_cast<double>(d))); }
 
 constexpr int kAttThreads = 256;
@@ -1261,6 +1283,20 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
 }
 
 }  // namespace
+
+hipError_t launch_fake_quant(float *dst, const float *x, long long chunks, int width, hipStream_t stream) {
+    if (chunks <= 0) return hipSuccess;
+    const long long blocks = (chunks + 3) / 4;
+    for (long long c0 = 0; c0 < blocks; c0 += 1 << 30) {
+        const long long nb = blocks - c0 < (1LL << 30) ? blocks - c0 : (1LL << 30);
+        const long long ch0 = c0 * 4;
+        hipLaunchKernelGGL(fake_quant_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, stream, dst + ch0 * width,
+                           x + ch0 * width, chunks - ch0, width);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
 
 hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
                                 hipStream_t stream) {

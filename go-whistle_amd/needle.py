@@ -1,8 +1,10 @@
-"""go-whistle's int8 KV numerics (internal/needle/int8.go) over libcqhip.
+"""go-whistle's int8 KV numerics (internal/needle/int8.go) and its packed
+Linear (internal/needle/linear.go) over libcqhip.
 
 QuantizeRows / Int8Rows.Append (int8.go:116-141) on host arrays or device
-tensors, and AttendInt8Spans (int8.go:208-272) on device tensors for one
-or many independent streams.
+tensors, AttendInt8Spans (int8.go:208-272) on device tensors for one or
+many independent streams, fakeQuant (int8.go:57-75), and Linear with
+WithInt8Input, Apply and ApplyShared on device tensors.
 """
 
 import ctypes
@@ -74,3 +76,57 @@ def append_dev(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, rope=N
     else:
         cos, sin = rope
         check(lib().kv_append_rope_dev(*args, c_void_p(cos.data_ptr()), c_void_p(sin.data_ptr()), _stream()))
+
+
+def fake_quant_dev(dst, x, rows, cols, width):
+    """fakeQuant (int8.go:57-75) on device tensors: rows of cols values, each
+    chunk of width through QuantizeRow and back; dst may be x."""
+    check(lib().nd_fake_quant_dev(c_void_p(dst.data_ptr()), c_void_p(x.data_ptr()), rows, cols, width, _stream()))
+
+
+class Linear:
+    """needle.Linear over a packed matrix (internal/needle/linear.go:11-145),
+    on device tensors: x rows × In -> dst rows × Out. With WithInt8Input the
+    input rows are first quantised per row (quantInput, int8.go:81-88)."""
+
+    def __init__(self, m, act8=False):
+        self.q, self.act8 = m, bool(act8)
+        self.In, self.Out = m.In(), m.Out()
+
+    def WithInt8Input(self, on):
+        return Linear(self.q, on)
+
+    def Int8Input(self):
+        return self.act8
+
+    def _quant_input(self, x, rows):
+        import torch
+
+        xq = torch.empty(rows * self.In, dtype=torch.float32, device=x.device)
+        fake_quant_dev(xq, x, rows, self.In, self.In)
+        return xq
+
+    def Apply(self, dst, x, rows):
+        """linear.go:82-95."""
+        from . import cq
+
+        if self.act8:
+            x = self._quant_input(x, rows)
+        cq.gemms_dev([self.q], [dst], x, rows)
+
+
+def ApplyShared(dsts, x, rows, *ls):
+    """ApplyShared (linear.go:97-145): each dsts[k] = ls[k].Apply's result bit
+    for bit; the linears that quantise their input share one quantised copy
+    of x, and the packed ones of each kind run through one cq.GEMMs."""
+    from . import cq
+
+    if len(dsts) != len(ls):
+        raise CQPanic(f"needle: ApplyShared of {len(ls)} linears into {len(dsts)} outputs")
+    if not ls:
+        return
+    xq = next((l._quant_input(x, rows) for l in ls if l.act8), None)
+    for quant in (False, True):
+        sel = [k for k, l in enumerate(ls) if l.act8 == quant]
+        if sel:
+            cq.gemms_dev([ls[k].q for k in sel], [dsts[k] for k in sel], xq if quant else x, rows)

@@ -222,6 +222,11 @@ int nd_argmax_dev(int32_t *out, const float *v, int rows, int n, void *stream);
  * (exp_amd64.s:84-112) on non-positive arguments. No reference
  * counterpart: the synthetic decoder's FFN activation. */
 int nd_silu_dev(float *x, long long n, void *stream);
+/* fakeQuant (internal/needle/int8.go:57-75): rows of cols values, each
+ * chunk of width through QuantizeRow and back, dst = float32(q) * s; the
+ * input of a Linear WithInt8Input (quantInput, int8.go:81-88;
+ * internal/needle/linear.go:82-86). dst may be x. */
+int nd_fake_quant_dev(float *dst, const float *x, long long rows, int cols, int width, void *stream);
 /* x += y elementwise (the residual adds). */
 int nd_add_dev(float *x, const float *y, long long n, void *stream);
 

@@ -62,6 +62,7 @@ def lib():
             "orc_exp_sub_sum_avx2": (c_float, [POINTER(c_float), c_int, c_float]),
             "orc_quantize_row": (c_float, [POINTER(c_int8), POINTER(c_float), c_int]),
             "orc_quantize_rows": (None, [POINTER(c_int8), POINTER(c_float), POINTER(c_float), c_int, c_int, c_int]),
+            "orc_fake_quant": (None, [POINTER(c_float), POINTER(c_float), ctypes.c_long, c_int, c_int]),
             "orc_dots_i8": (None, [POINTER(c_int32), c_int, POINTER(c_int8), c_int, POINTER(c_int8), c_int]),
             "orc_axpys_i8": (None, [POINTER(c_float), c_int, POINTER(c_float), c_int, POINTER(c_int8), c_int]),
             "orc_dots_f32_i8": (None, [POINTER(c_float), c_int, POINTER(c_float), c_int, POINTER(c_int8), c_int]),
@@ -235,6 +236,14 @@ def quantize_rows(x, cols, width):
     s = np.zeros(rows * (cols // width), dtype=np.float32)
     lib().orc_quantize_rows(i8p(q), fp(s), fp(x), rows, cols, width)
     return q, s
+
+
+def fake_quant(x, cols, width):
+    """fakeQuant (int8.go:62-75) of rows of cols values in chunks of width."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    dst = np.zeros_like(x)
+    lib().orc_fake_quant(fp(dst), fp(x), x.size // cols, cols, width)
+    return dst
 
 
 def exp_sub_sum(s, m, variant):

@@ -5,6 +5,7 @@
  * Reference files followed (paths relative to the go-whistle repository):
  *   internal/needle/int8.go:36-55       QuantizeRow
  *   internal/needle/int8.go:116-141     QuantizeRows, Int8Rows.Append
+ *   internal/needle/int8.go:62-88       fakeQuant, quantInput (Linear WithInt8Input)
  *   internal/needle/int8.go:208-300     AttendInt8Spans, int8Logits, dotsF32I8
  *   internal/needle/int8kernel.go:346-368  dotsI8Generic, axpysI8Generic
  *   internal/needle/exp.go:21-31        expSubSumGeneric
@@ -63,6 +64,18 @@ void orc_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, 
     /* int8.go:116-141: per chunk of width values */
     int chunks = rows * (cols / width);
     for (int c = 0; c < chunks; c++) s[c] = orc_quantize_row(q + (size_t)c * width, x + (size_t)c * width, width);
+}
+
+void orc_fake_quant(float *dst, const float *x, long rows, int cols, int width) {
+    /* fakeQuant (int8.go:62-75): QuantizeRow per chunk, then float32(q) * s;
+     * dst may be x */
+    long chunks = rows * (cols / width);
+    int8_t *q = malloc((size_t)width + 1);
+    for (long c = 0; c < chunks; c++) {
+        float s = orc_quantize_row(q, x + c * width, width);
+        for (int i = 0; i < width; i++) dst[c * width + i] = (float)q[i] * s;
+    }
+    free(q);
 }
 
 void orc_dots_i8(int32_t *dst, int n, const int8_t *q, int width, const int8_t *k, int stride) {

@@ -113,6 +113,7 @@ float orc_exp_sub_sum_avx2(float *s, int n8, float m);
 
 float orc_quantize_row(int8_t *q, const float *x, int n);                /* int8.go:36-55 */
 void orc_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, int width); /* int8.go:116-141 */
+void orc_fake_quant(float *dst, const float *x, long rows, int cols, int width);          /* int8.go:62-75 */
 void orc_dots_i8(int32_t *dst, int n, const int8_t *q, int width, const int8_t *k, int stride);   /* int8kernel.go:346-357 */
 void orc_axpys_i8(float *out, int width, const float *w, int n, const int8_t *v, int stride);     /* int8kernel.go:360-368 */
 void orc_dots_f32_i8(float *dst, int n, const float *q, int width, const int8_t *k, int stride); /* int8.go:289-300 */

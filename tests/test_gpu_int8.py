@@ -211,3 +211,62 @@ def test_attend_misuse():
     z = torch.zeros(64, dtype=torch.float32, device="cuda")
     with pytest.raises(gw.CQPanic):
         needle.attend_int8_dev(z, z, 1, 8, z, z, 100, 64, z, z, 512, 64, z, 1, 8.0, True)
+
+
+@pytest.mark.parametrize("rows,cols,width", [(1, 512, 512), (37, 2048, 2048), (1500, 512, 64), (5, 96, 48)])
+def test_fake_quant_bit_exact(rows, cols, width):
+    # fakeQuant (int8.go:57-75) on the device against the oracle, in place
+    # and out of place, with zero chunks (scale 1) and wide dynamic range
+    import torch
+
+    g = synth.rng(rows + cols + width)
+    x = (g.standard_normal(rows * cols) * g.choice([1e-6, 1, 1e4], size=rows * cols)).astype(np.float32)
+    x[:width] = 0
+    want = orc.fake_quant(x, cols, width)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty_like(xd)
+    needle.fake_quant_dev(out, xd, rows, cols, width)
+    needle.fake_quant_dev(xd, xd, rows, cols, width)
+    torch.cuda.synchronize()
+    assert same_bits(out.cpu().numpy(), want)
+    assert same_bits(xd.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("rows", [1, 375, 1500])
+def test_linear_int8_input(rows):
+    # needle.Linear WithInt8Input (linear.go:82-95): the mHC phi shape
+    # (CQ4 128x2048) and a 512x512 CQ4, each input row fake-quantised, then
+    # the lut product (its MFMA form when the grid is large), bit for bit
+    # the oracle's; ApplyShared over quantising and plain linears equals
+    # one Apply each (linear.go:97-145)
+    import torch
+
+    g = synth.rng(900 + rows)
+    phi = gw.cq.New(synth.random_packed(g, 128, 2048, 128, 4, sigma=0.05))
+    p2 = synth.random_packed(g, 512, 2048, 128, 4, sigma=0.05)
+    m2 = gw.cq.New(p2)
+    x = (g.standard_normal(rows * 2048) * 2).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    lin_q = needle.Linear(phi).WithInt8Input(True)
+    lin_q2 = needle.Linear(m2, act8=True)
+    lin_p = needle.Linear(m2)
+    assert lin_q.Int8Input() and not lin_p.Int8Input()
+    y = torch.zeros(rows * 128, device="cuda")
+    lin_q.Apply(y, xd, rows)
+    ys = [torch.zeros(rows * 128, device="cuda"), torch.zeros(rows * 512, device="cuda"),
+          torch.zeros(rows * 512, device="cuda")]
+    needle.ApplyShared(ys, xd, rows, lin_q, lin_p, lin_q2)
+    y2q, y2p = torch.zeros(rows * 512, device="cuda"), torch.zeros(rows * 512, device="cuda")
+    lin_q2.Apply(y2q, xd, rows)
+    lin_p.Apply(y2p, xd, rows)
+    torch.cuda.synchronize()
+    xq = orc.fake_quant(x, 2048, 2048)
+    o1 = orc.OMatrix.new(synth.random_packed(synth.rng(900 + rows), 128, 2048, 128, 4, sigma=0.05))
+    want = o1.gemm(xq[: rows * 2048], rows)
+    assert same_bits(y.cpu().numpy(), want)
+    assert same_bits(ys[0].cpu().numpy(), want)
+    assert same_bits(ys[1].cpu().numpy(), y2p.cpu().numpy())
+    assert same_bits(ys[2].cpu().numpy(), y2q.cpu().numpy())
+    o2 = orc.OMatrix.new(p2)
+    assert same_bits(y2q.cpu().numpy(), o2.gemm(xq, rows))
+    assert same_bits(y2p.cpu().numpy(), o2.gemm(x, rows))

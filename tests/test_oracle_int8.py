@@ -48,6 +48,26 @@ def test_quantize_rows_per_chunk():
         assert np.array_equal(q[c * 48:(c + 1) * 48], qc) and s[c] == sc
 
 
+def test_fake_quant_hand_vectors_and_bound():
+    # fakeQuant (int8.go:57-75) is QuantizeRow and back, float32(q) * s:
+    # the hand vectors of int8_test.go:19-34 give exact values, and any row
+    # stays within half a step (plus the divide's rounding) of its input
+    got = orc.fake_quant(np.array([127, 2.5, -2.5, 3.5, -0.5, 1.4999], np.float32), 6, 6)
+    assert list(got) == [127, 2, -2, 4, 0, 1]
+    s = np.float32(np.float32(6.35) / np.float32(127))
+    got = orc.fake_quant(np.array([-6.35, 0.05, 3], np.float32), 3, 3)
+    assert list(got) == [np.float32(-127) * s, np.float32(1) * s, np.float32(60) * s]
+    assert list(orc.fake_quant(np.zeros(4, np.float32), 4, 4)) == [0, 0, 0, 0]
+    g = synth.rng(31)
+    x = (g.standard_normal(3 * 2048) * 3).astype(np.float32)
+    fq = orc.fake_quant(x, 2048, 2048)
+    for r in range(3):
+        xr = x[r * 2048:(r + 1) * 2048]
+        sr = float(np.float32(np.abs(xr).max() / np.float32(127)))
+        d = np.abs(xr.astype(np.float64) - fq[r * 2048:(r + 1) * 2048].astype(np.float64))
+        assert np.all(d <= sr * (0.5 + 128 * 2.0 ** -24) + abs(xr).max() * 2.0 ** -24)
+
+
 @pytest.mark.parametrize("width", [16, 48, 64, 8, 17])
 @pytest.mark.parametrize("n", [1, 5, 375])
 def test_dots_i8_bruteforce(width, n):
