@@ -68,6 +68,8 @@ SIGNATURES = {
     "nd_argmax_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "nd_silu_dev": (c_int, [c_void_p, c_longlong, c_void_p]),
     "nd_fake_quant_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_int, c_int, c_void_p]),
+    "kv_reorder_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                               c_void_p]),
     "nd_add_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_void_p]),
 }
 

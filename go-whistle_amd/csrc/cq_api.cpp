@@ -927,6 +927,24 @@ int kv_quantize_rows_dev(int8_t *q, float *s, const float *x, int rows, int cols
     return CQ_OK;
 }
 
+int kv_reorder_dev(int8_t *q, float *s, int8_t *tmp_q, float *tmp_s, const int32_t *parent, const int32_t *len,
+                   int streams, int cap, int cols, int width, void *stream) {
+    if (width <= 0 || cols % width != 0)
+        return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);
+    if (streams < 0 || cap < 0) return fail(CQ_ERR_MISUSE, "needle: %d streams of %d rows", streams, cap);
+    if (streams == 0 || cap == 0) return CQ_OK;
+    if (!q || !s || !tmp_q || !tmp_s || !parent || !len || tmp_q == q || tmp_s == s)
+        return fail(CQ_ERR_MISUSE, "needle: reorder needs caches, distinct temporaries, parents and lengths");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const int sb = (cols / width) * static_cast<int>(sizeof(float));
+    // through the temporaries: a stream may be another's parent
+    HIP_TRY(launch_gather_rows(tmp_q, q, parent, len, streams, cap, cols, st), "reorder gather");
+    HIP_TRY(launch_gather_rows(tmp_s, s, parent, len, streams, cap, sb, st), "reorder gather");
+    HIP_TRY(launch_gather_rows(q, tmp_q, nullptr, len, streams, cap, cols, st), "reorder copy back");
+    HIP_TRY(launch_gather_rows(s, tmp_s, nullptr, len, streams, cap, sb, st), "reorder copy back");
+    return CQ_OK;
+}
+
 int nd_fake_quant_dev(float *dst, const float *x, long long rows, int cols, int width, void *stream) {
     if (width <= 0 || cols % width != 0)
         return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);

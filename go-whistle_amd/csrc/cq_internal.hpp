@@ -145,6 +145,10 @@ hipError_t launch_rows(const RowArgs &a, hipStream_t stream);
 
 // int8 numerics
 hipError_t launch_fake_quant(float *dst, const float *x, long long chunks, int width, hipStream_t stream);
+// Stream b of dst (cap rows of row_bytes each) <- rows [0, len[b]) of
+// stream idx[b] of src (idx null: stream b); idx, len device int32 arrays.
+hipError_t launch_gather_rows(void *dst, const void *src, const int32_t *idx, const int32_t *len, int streams,
+                              int cap, int row_bytes, hipStream_t stream);
 hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long chunks, int width,
                                 hipStream_t stream);
 

@@ -74,6 +74,31 @@ __global__ __launch_bounds__(256) void fake_quant_kernel(float *dst, const float
     }
 }
 
+// Stream b of dst gets rows [0, len[b]) of stream idx[b] of src (idx null:
+// of stream b; len clamped to the stream's cap rows; idx outside the streams
+// copies nothing), each stream cap rows of row_bytes; 16-byte pieces when
+// every row and stream start is 16-byte aligned. Grid: (pieces per
+// workgroup chunk, streams).
+__global__ __launch_bounds__(256) void gather_rows_kernel(unsigned char *dst, const unsigned char *src,
+                                                          const int32_t *idx, const int32_t *len, int streams,
+                                                          long long stream_bytes, int row_bytes, int vec) {
+    const int b = blockIdx.y;
+    const int from = idx ? idx[b] : b;
+    const int n = len[b];
+    if (from < 0 || from >= streams || n <= 0) return;
+    const long long bytes = min(static_cast<long long>(n) * row_bytes, stream_bytes);  // at most the stream's cap rows
+    const unsigned char *sp = src + from * stream_bytes;
+    unsigned char *dp = dst + b * stream_bytes;
+    const long long step = static_cast<long long>(gridDim.x) * blockDim.x;
+    if (vec) {
+        for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes / 16; i += step)
+            reinterpret_cast<uint4 *>(dp)[i] = reinterpret_cast<const uint4 *>(sp)[i];
+    } else {
+        for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes; i += step)
+            dp[i] = sp[i];
+    }
+}
+
 __device__ __forceinline__ float exp_generic(float d) { return static_cast<float>(exp(static_cast<double>(d))); }
 
 constexpr int kAttThreads = 256;
@@ -1283,6 +1308,20 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
 }
 
 }  // namespace
+
+hipError_t launch_gather_rows(void *dst, const void *src, const int32_t *idx, const int32_t *len, int streams,
+                              int cap, int row_bytes, hipStream_t stream) {
+    if (streams <= 0 || cap <= 0 || row_bytes <= 0) return hipSuccess;
+    const long long stream_bytes = static_cast<long long>(cap) * row_bytes;
+    const int vec = (row_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(src) % 16 == 0) ? 1 : 0;
+    const long long pieces = vec ? stream_bytes / 16 : stream_bytes;
+    const unsigned gx = static_cast<unsigned>(std::min<long long>(64, (pieces + 255) / 256));
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(gx, static_cast<unsigned>(streams)), dim3(256), 0, stream,
+                       static_cast<unsigned char *>(dst), static_cast<const unsigned char *>(src), idx, len, streams,
+                       stream_bytes, row_bytes, vec);
+    return hipGetLastError();
+}
 
 hipError_t launch_fake_quant(float *dst, const float *x, long long chunks, int width, hipStream_t stream) {
     if (chunks <= 0) return hipSuccess;

@@ -319,6 +319,56 @@ class Decoder:
         check(L.nd_argmax_dev(_ptr(self.tok), _ptr(self.logits), B, c.vocab, s))
         self.pos.add_(1)
 
+    def fork(self, parents):
+        """KVCache.Fork for every stream at once (cache.go:62-67), as a beam
+        search reorders its hypotheses: stream b continues from stream
+        parents[b]'s state (its token, position, self-attention rows so far
+        and cross memory), after which every stream extends on its own. The
+        rows are copied (kv_reorder_dev), not shared until written."""
+        import torch
+
+        from ._lib import CQPanic
+
+        c, B = self.cfg, self.batch
+        if len(parents) != B or any(not 0 <= int(p) < B for p in parents):
+            raise CQPanic(f"decoder: fork of {B} streams from parents {list(parents)}")
+        dev = self.tok.device
+        par = torch.as_tensor(np.asarray(parents, np.int32), device=dev)
+        self_len = self.pos.index_select(0, par.long()).to(torch.int32)
+        cross_len = torch.full((B,), c.frames, dtype=torch.int32, device=dev)
+        hk = c.dim // c.head_dim
+        if getattr(self, "_fork_tmp", None) is None:
+            rows = max(c.max_pos, c.frames)
+            self._fork_tmp = (torch.empty(B * rows * c.dim, dtype=torch.int8, device=dev),
+                              torch.empty(B * rows * hk, dtype=torch.float32, device=dev))
+        tq, ts = self._fork_tmp
+        s = cq._stream()
+        for l in range(c.layers):
+            for q, sc, cap, ln in ((self.self_k[l], self.self_ks[l], c.max_pos, self_len),
+                                   (self.self_v[l], self.self_vs[l], c.max_pos, self_len),
+                                   (self.cross_k[l], self.cross_ks[l], c.frames, cross_len),
+                                   (self.cross_v[l], self.cross_vs[l], c.frames, cross_len)):
+                check(lib().kv_reorder_dev(_ptr(q), _ptr(sc), _ptr(tq), _ptr(ts), _ptr(par), _ptr(ln), B, cap, c.dim,
+                                           c.head_dim, s))
+        self.tok.copy_(self.tok.index_select(0, par.long()))
+        self.pos.copy_(self.pos.index_select(0, par.long()))
+
+    def resume(self, n, graph=True):
+        """Greedy-decodes n more tokens from the current state; [batch, n]."""
+        import torch
+
+        out = torch.zeros(self.batch, n, dtype=torch.int32, device=self.tok.device)
+        if not graph:
+            for i in range(n):
+                self.step()
+                out[:, i] = self.tok
+            return out
+        g = self.capture()
+        for i in range(n):
+            g.replay()
+            out[:, i] = self.tok
+        return out
+
     def decode(self, first_tokens, n, graph=True):
         """Greedy-decodes n tokens after first_tokens; returns [batch, n]."""
         import torch

@@ -161,6 +161,17 @@ void cq_batch_free(cq_batch *plan);
  * forms. */
 int kv_quantize_rows(int8_t *q, float *s, const float *x, int rows, int cols, int width);
 int kv_quantize_rows_dev(int8_t *q, float *s, const float *x, int rows, int cols, int width, void *stream);
+/* KVCache.Fork for many streams at once (internal/needle/cache.go:62-67,
+ * Int8Rows.Clip int8.go:155-161; the beams of internal/search/beam.go):
+ * stream b of the int8 cache (codes q, scales s; streams of cap rows of
+ * cols codes, width codes per scale) becomes the first len[b] rows of
+ * stream parent[b], after which every stream extends on its own. parent
+ * and len are device int32 arrays of `streams`; rows past len[b] are left
+ * as they were. The reference shares the rows until one side appends
+ * (copy on write); here they are copied, through the caller's temporaries
+ * tmp_q, tmp_s of the cache's size. No reference counterpart as one call. */
+int kv_reorder_dev(int8_t *q, float *s, int8_t *tmp_q, float *tmp_s, const int32_t *parent, const int32_t *len,
+                   int streams, int cap, int cols, int width, void *stream);
 
 /* AttendInt8Spans (int8.go:208-272) on device memory for `batch`
  * independent streams (beam hypotheses, internal/search/beam.go:508-521).

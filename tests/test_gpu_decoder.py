@@ -123,6 +123,54 @@ def test_argmax_edges(n):
     assert list(am.cpu().numpy()) == list(orc.argmax(v, rows, n))
 
 
+@pytest.mark.parametrize("graph", [True, False])
+def test_fork_continues_as_parent(graph):
+    # KVCache.Fork (cache.go:62-67) for a beam reorder: after 8 tokens, stream
+    # b takes stream parents[b]'s state and must go on exactly as that stream
+    # does without the fork (its self rows, cross memory, token, position)
+    cfg = dec.DecoderConfig(vocab=4096, layers=2, frames=100, max_pos=64)
+    model = dec.make_model(9, cfg)
+    first, parents = [1, 2, 3, 4], [2, 2, 0, 3]
+    whole = dec.Decoder(model, 4)
+    whole.set_memory(9)
+    full = whole.decode(first, 16, graph=graph).cpu().numpy()
+    d = dec.Decoder(model, 4)
+    d.set_memory(9)
+    head = d.decode(first, 8, graph=graph).cpu().numpy()
+    assert np.array_equal(head, full[:, :8])
+    d.fork(parents)
+    tail = d.resume(8, graph=graph).cpu().numpy()
+    for b, p in enumerate(parents):
+        assert list(tail[b]) == list(full[p, 8:]), (b, p)
+    with pytest.raises(Exception):
+        d.fork([0, 1, 2])
+
+
+def test_reorder_rows():
+    # kv_reorder_dev against numpy: stream b <- rows [0, len[b]) of stream
+    # parent[b], the rest untouched, for code rows of 16-byte multiples and
+    # of odd widths (the byte path)
+    import torch
+
+    g = synth.rng(44)
+    for cols, width in ((512, 64), (40, 8)):
+        B, cap = 5, 7
+        q = g.integers(-128, 128, size=(B, cap, cols), dtype=np.int8)
+        s = g.random((B, cap, cols // width)).astype(np.float32)
+        parent = np.array([3, 3, 0, 4, 1], np.int32)
+        ln = np.array([0, 7, 3, 9, 1], np.int32)  # 9 > cap: clamped
+        qd, sd = _t(q), _t(s)
+        tq, ts = torch.empty_like(qd), torch.empty_like(sd)
+        pd, ld = _t(parent), _t(ln)  # held: a freed temporary's block is reused
+        check(lib().kv_reorder_dev(_p(qd), _p(sd), _p(tq), _p(ts), _p(pd), _p(ld), B, cap, cols, width, _s()))
+        torch.cuda.synchronize()
+        wq, ws = q.copy(), s.copy()
+        for b in range(B):
+            n = min(int(ln[b]), cap)
+            wq[b, :n], ws[b, :n] = q[parent[b], :n], s[parent[b], :n]
+        assert np.array_equal(qd.cpu().numpy(), wq) and same(sd.cpu().numpy(), ws)
+
+
 def _run(cfg, seed, batch, first, n, check_streams, generator="numpy"):
     model = dec.make_model(seed, cfg)
     d = dec.Decoder(model, batch)
