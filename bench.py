@@ -75,6 +75,20 @@ def cpu_threads():
     return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
+def cpu_host():
+    """The host CPU's model name, its logical CPU count and the CPUs this
+    process may use."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline(gw, packs, seconds):
     """The oracle's lut GEMV over the sweep, bounded in time, three ways: the
     generic restatement on one thread, its AVX2 form (the reference's amd64
@@ -113,7 +127,8 @@ def cpu_baseline(gw, packs, seconds):
             "sample": f"{passes} passes over the 8-matrix sweep (one copy each), oracle lut GEMV, {name} "
                       f"({'AVX2' if 'avx2' in name else 'generic'}, {th} threads, the reference's split), {el:.1f} s",
             "legs": {k: {"GBps": round(v[0], 4), "threads": v[3], "passes": v[1], "seconds": round(v[2], 2)}
-                     for k, v in res.items()}}
+                     for k, v in res.items()},
+            "host": cpu_host()}
 
 
 INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA, ops/s
@@ -207,6 +222,7 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
                 break
         orc.set_cpu(False, 1)
         res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+                               "host": cpu_host(),
                                "sample": f"{n} greedy tokens at batch 1 (runs of 10 from position 0), oracle "
                                          f"decoder, lut products and int8 attention {'AVX2' if avx2 else 'generic'}, products split over "
                                          f"{threads} threads as the reference splits them, {el:.1f} s"}
