@@ -261,6 +261,14 @@ bool lut_fits(const CqStore &s) {
                std::min<size_t>(device_info().max_lds, 128 * 1024);
 }
 
+// The same number of units of at most b blocks each, as even as possible:
+// 8 blocks at 6 per unit become 4 + 4, not 6 + 2 (a short unit still pays
+// a full build of its activation's tables).
+int balanced_blocks(int nblk, int b) {
+    const int units = (nblk + b - 1) / b;
+    return std::max(1, (nblk + units - 1) / units);
+}
+
 int blocks_per_workgroup(long long blocks) {
     const long long want = 4LL * device_info().cus;
     return static_cast<int>(std::min<long long>(kLutMaxBpw, std::max<long long>(1, blocks / want)));
@@ -284,7 +292,9 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
         groups_max = std::max(groups_max, j.groups);
     }
     if (a.njobs == 0 || rows == 0) return CQ_OK;
-    a.bpw = blocks_per_workgroup(blocks);
+    int nmax = 0;
+    for (int k = 0; k < a.njobs; ++k) nmax = std::max(nmax, a.jobs[k].nblk);
+    a.bpw = balanced_blocks(nmax, blocks_per_workgroup(blocks));
     int wg = 0;
     for (int k = 0; k < a.njobs; ++k) {
         a.wg0[k] = wg;
@@ -857,7 +867,8 @@ int cq_batch_new(int n, cq_matrix *const *ms, float *const *ys, const float *con
             JobDesc j;
             fill_job(j, ms[k], xs[k], ys[k], rows[k]);
             const long long blk_bytes = 64LL * ms[k]->st->row_bytes;
-            const int b = static_cast<int>(std::min<long long>(kLutMaxBpw, std::max<long long>(1, target / blk_bytes)));
+            const int b = balanced_blocks(
+                j.nblk, static_cast<int>(std::min<long long>(kLutMaxBpw, std::max<long long>(1, target / blk_bytes))));
             bpw = std::max(bpw, b);
             const int ji = static_cast<int>(jobs.size());
             jobs.push_back(j);
