@@ -152,10 +152,16 @@ __device__ __forceinline__ int lookup_unit(const uint32_t (&w)[4], uint32_t base
     return s;
 }
 
-__device__ __forceinline__ int rne_int(float e) { return static_cast<int>(rintf(e)); }
+// Two table entries RNE(a), RNE(b) as int16 halves of one word. For |e| <
+// 2^22, e + 1.5 * 2^23 lands where float32 spacing is 1, so the add rounds
+// e to the nearest integer, ties to even, exactly as rintf, and the sum's
+// low 16 bits are that integer in two's complement (|v| <= 8191 here). One
+// byte permute then joins the two low halves.
+constexpr float kRneMagic = 12582912.0f;  // 1.5 * 2^23
 
-__device__ __forceinline__ uint32_t pack16(int lo, int hi) {
-    return (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
+__device__ __forceinline__ uint32_t rne_pair(float a, float b) {
+    const uint32_t ea = __float_as_uint(a + kRneMagic), eb = __float_as_uint(b + kRneMagic);
+    return __builtin_amdgcn_perm(eb, ea, 0x05040100u);  // ea.lo16 | eb.lo16 << 16
 }
 
 // Rotation, bound, tables and step of group g of the activation row x
@@ -227,7 +233,7 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
                 uint32_t q[8];
 #pragma unroll
                 for (int c = 0; c < 16; c += 2)
-                    q[c / 2] = pack16(rne_int(cbv[c] * av), rne_int(cbv[c + 1] * av));
+                    q[c / 2] = rne_pair(cbv[c] * av, cbv[c + 1] * av);
                 uint4 *dst = reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i) * 16);
                 dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
                 dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
@@ -245,7 +251,7 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
                     // code c = c0 + cc: c & 3 = cc & 3, c >> 2 = (odd ? 2 : 0) + (cc >> 2)
                     const float l0 = cbv[cc & 3] * av, h0 = ((cc >> 2) ? hhi : hlo) * bv;
                     const float l1 = cbv[(cc + 1) & 3] * av, h1 = (((cc + 1) >> 2) ? hhi : hlo) * bv;
-                    q[cc / 2] = pack16(rne_int(l0 + h0), rne_int(l1 + h1));
+                    q[cc / 2] = rne_pair(l0 + h0, l1 + h1);
                 }
                 *reinterpret_cast<uint4 *>(tg + static_cast<size_t>(i / 2) * 16 + c0) =
                     make_uint4(q[0], q[1], q[2], q[3]);
