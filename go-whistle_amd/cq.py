@@ -191,6 +191,19 @@ def gemms_fused_dev(ms, ys, x, rows, norm_gain=None, resid=None, act=0):
                                    _stream()))
 
 
+def gemms_gated_dev(ms, ys, x, gate, rows, resid=None):
+    """gemms_dev of x * sigmoid(gate) (Attention.output's gate before
+    outProj.Apply, attention.go:242-260; gate is only read), and y = resid +
+    product when resid is given (one matrix). One launch (cq_gemms_gated_dev)."""
+    n = len(ms)
+    if n != len(ys):
+        raise CQPanic(f"cq: GEMMs of {n} matrices into {len(ys)} outputs")
+    hs = (c_void_p * max(n, 1))(*[m.handle for m in ms])
+    ds = (c_void_p * max(n, 1))(*[c_void_p(y.data_ptr()) for y in ys])
+    ptr = lambda t: c_void_p(t.data_ptr()) if t is not None else None
+    check(lib().cq_gemms_gated_dev(n, hs, ds, c_void_p(x.data_ptr()), ptr(gate), rows, ptr(resid), _stream()))
+
+
 def gemms_append_dev(ms, ys, x, rows, caches, q_stride, s_stride, pos, cap, norm_gain=None):
     """gemms_fused_dev (norm_gain only) whose product k is also appended to
     an int8 row cache when caches[k] = (codes, scales, rope) is not None:

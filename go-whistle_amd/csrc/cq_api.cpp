@@ -215,6 +215,7 @@ struct Fuse {
     const float *resid = nullptr;
     long long resid_stride = 0;
     int act = 0;
+    const float *xgate = nullptr;  // the product is of x * sigmoid(xgate)
     // int8 appends of matrix k of the call (null arrays / entries: none)
     int8_t *const *app_q = nullptr;
     float *const *app_s = nullptr;
@@ -223,7 +224,7 @@ struct Fuse {
     long long app_q_stride = 0, app_s_stride = 0;
     const int32_t *app_pos = nullptr;
     int app_cap = 0;
-    bool any() const { return ngain || resid || act || app_q; }
+    bool any() const { return ngain || resid || act || xgate || app_q; }
 };
 
 // Job j runs matrix k of the call.
@@ -233,6 +234,7 @@ void apply_fuse(JobDesc &j, const Fuse *f, int k) {
     j.resid = f->resid;
     j.resid_stride = f->resid_stride;
     j.act = f->act;
+    j.xgate = f->xgate;
     if (f->app_q && f->app_q[k]) {
         j.app_q = f->app_q[k];
         j.app_s = f->app_s[k];
@@ -665,6 +667,26 @@ int cq_gemms_fused_dev(int n, cq_matrix *const *ms, float *const *dsts, const fl
     return gemms_dev(n, ms, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
 }
 
+int cq_gemms_gated_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, const float *gate, int rows,
+                       const float *resid, void *stream) {
+    if (n < 0 || (n > 0 && (!ms || !dsts))) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d matrices", n);
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d rows", rows);
+    if (!gate && rows > 0 && n > 0) return fail(CQ_ERR_MISUSE, "cq: gated GEMMs without a gate");
+    if (resid && n != 1) return fail(CQ_ERR_MISUSE, "cq: a residual add takes one matrix");
+    for (int k = 0; k < n; ++k) {
+        if (!ms[k] || ms[k]->st->in != ms[0]->st->in)
+            return fail(CQ_ERR_MISUSE, "cq: GEMMs over matrices of different input widths");
+        if (!uses_lut(ms[k]))
+            return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel, not %s", cq_kernel_name(ms[k]));
+    }
+    if (rows == 0 || n == 0) return CQ_OK;
+    Fuse f;
+    f.xgate = gate;
+    f.resid = resid;
+    f.resid_stride = resid ? ms[0]->out : 0;
+    return gemms_dev(n, ms, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
+}
+
 int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows,
                         const float *norm_gain, int8_t *const *kv_q, float *const *kv_s, long long q_stride,
                         long long s_stride, const int32_t *pos, int cap, const float *const *cos_t,
@@ -1068,6 +1090,12 @@ int nd_silu_dev(float *x, long long n, void *stream) {
 int nd_add_dev(float *x, const float *y, long long n, void *stream) {
     if (n < 0) return fail(CQ_ERR_MISUSE, "needle: add of %lld values", n);
     HIP_TRY(launch_add(x, y, n, static_cast<hipStream_t>(stream)), "add launch");
+    return CQ_OK;
+}
+
+int nd_sigmoid_gate_dev(float *out, float *gate, long long n, void *stream) {
+    if (n < 0) return fail(CQ_ERR_MISUSE, "needle: gate of %lld values", n);
+    HIP_TRY(launch_sigmoid_gate(out, gate, n, static_cast<hipStream_t>(stream)), "gate launch");
     return CQ_OK;
 }
 

@@ -97,6 +97,39 @@ __device__ __forceinline__ float silu_value(float v) {
     return v * s;
 }
 
+// exp of a float64 by fdlibm's e_exp.c method (Sun Microsystems, 1993; the
+// steps of Go's portable math.Exp): k = x log2(e) rounded half away from
+// zero, r = hi - lo with hi = x - k ln2_hi and lo = k ln2_lo, exp(r) =
+// 1 - ((lo - r c / (2 - c)) - hi) with c = r - r^2 P(r^2) of degree 5, then
+// y 2^k. Every operation is an IEEE float64 one, unfused, so the CPU
+// restatement returns the same bits; the error is below 1 ulp.
+__device__ __forceinline__ double exp_f64(double x) {
+    const double ln2hi = 6.93147180369123816490e-01, ln2lo = 1.90821492927058770002e-10;
+    const double log2e = 1.44269504088896338700e+00;
+    const double p1 = 1.66666666666666019037e-01, p2 = -2.77777777770155933842e-03;
+    const double p3 = 6.61375632143793436117e-05, p4 = -1.65339022054652515390e-06;
+    const double p5 = 4.13813679705723846039e-08;
+    if (x != x) return x;
+    if (x > 7.09782712893383973096e+02) return __builtin_huge_val();
+    if (x < -7.45133219101941108420e+02) return 0.0;
+    if (x > -3.7252902984619140625e-09 && x < 3.7252902984619140625e-09) return 1.0 + x;  // |x| < 2^-28
+    const double kf = x < 0.0 ? log2e * x - 0.5 : log2e * x + 0.5;
+    const int k = static_cast<int>(kf);  // truncation toward zero
+    const double hi = x - static_cast<double>(k) * ln2hi, lo = static_cast<double>(k) * ln2lo;
+    const double r = hi - lo, t = r * r;
+    const double c = r - t * (p1 + t * (p2 + t * (p3 + t * (p4 + t * p5))));
+    const double y = 1.0 - ((lo - (r * c) / (2.0 - c)) - hi);
+    return ldexp(y, k);
+}
+
+// jax.nn.sigmoid in float32 as the reference computes it,
+// float32(1 / (1 + exp(-float64(x)))) (internal/needle/load.go:120-123,
+// internal/decoder/cross.go:322-325): the attention's output gate.
+__device__ __forceinline__ float gate_sigmoid(float v) {
+    const double e = exp_f64(-static_cast<double>(v));
+    return static_cast<float>(1.0 / (1.0 + e));
+}
+
 // ZCRMSNorm's mean square (norm.go:91-109), partial sum k of four: the
 // float64 squares of row[i] for i = k, k+4, ... below dim & ~3, in order,
 // and for k = 0 the tail after them.

@@ -76,11 +76,13 @@ struct JobDesc {
     // Fused prologue and epilogue (null / 0: none). ngain: each activation
     // row is first ZCRMSNorm'ed with this gain (length in). resid: y = resid
     // + product, resid rows resid_stride floats apart (may be y itself).
-    // act 1: y = silu(product).
+    // act 1: y = silu(product). xgate: the product is of x * sigmoid(xgate)
+    // elementwise (the gated attention output; rows x_stride apart, as x).
     const float *ngain;
     const float *resid;
     long long resid_stride;
     int act;
+    const float *xgate;
     // Fused int8 append (app_q null: none; the view's rows and width are
     // whole 64-row blocks): activation b's output row, each 64-wide block
     // a head, is quantized into row app_pos[b] of stream b's cache
@@ -180,6 +182,7 @@ hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float 
 hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, hipStream_t s);
 hipError_t launch_silu(float *x, long long n, hipStream_t s);
 hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s);
+hipError_t launch_sigmoid_gate(float *out, float *gate, long long n, hipStream_t s);
 hipError_t launch_append(int8_t *q, float *sc, const float *x, int batch, int cols, int width, long long q_stride,
                          long long s_stride, const int32_t *pos, int cap, const float *cos_t, const float *sin_t,
                          hipStream_t s);

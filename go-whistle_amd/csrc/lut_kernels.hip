@@ -170,11 +170,12 @@ __device__ __forceinline__ uint32_t rne_pair(float a, float b) {
 // below 64 exchange lanes with shuffles, the others stay in a lane), M
 // reduced across the wavefront, the NT tables of 16 int16 to tg and the
 // step to *step (lane 0). With ngain the row is ZCRMSNorm'ed first (divisor
-// rms).
+// rms); with xg each value is first gated, x * sigmoid(xg) (Attention.output,
+// internal/needle/attention.go:245-249).
 template <int BITS, int GB>
 __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, int g, const float (&cbv)[16],
                                              float cb_max, float lut_step, const CQ_GLOBAL float *ngain, float rms,
-                                             short *tg, float *step, int lane) {
+                                             const CQ_GLOBAL float *xg, short *tg, float *step, int lane) {
     using Gm = LutGeo<BITS, GB>;
     constexpr int G = Gm::G, E = Gm::E;
     float v[E];
@@ -187,6 +188,7 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
             const float gx = ngain[col] * xv;
             xv = gx / rms;
         }
+        if (xg && i < G && col < in) xv = xv * gate_sigmoid(xg[col]);
         v[e] = xv;
     }
 #pragma unroll
@@ -304,6 +306,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
     const int groups = J->groups, units = J->units, blk0 = J->blk0 + b0;
     const CQ_GLOBAL uint8_t *idx = gptr(J->idx);
     const CQ_GLOBAL float *x = gptr(J->x) + static_cast<long long>(act) * J->x_stride;
+    const CQ_GLOBAL float *xg = J->xgate ? gptr(J->xgate) + static_cast<long long>(act) * J->x_stride : nullptr;
 
     // LDS: tables of a chunk of gc groups, the chunk's steps, y of the
     // workgroup's rows between chunks, the chunk's float terms of up to tc
@@ -478,7 +481,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
 
         // 1. Rotation, bound and tables of the chunk's groups w, w+W, ...
         for (int gi = w; gi < gch; gi += W)
-            group_tables<BITS, GB>(x, j_in, g0 + gi, cbv, j_cbmax, j_step, j_ngain, rms,
+            group_tables<BITS, GB>(x, j_in, g0 + gi, cbv, j_cbmax, j_step, j_ngain, rms, xg,
                                    tab + static_cast<size_t>(gi) * NT * 16, &steps[gi], lane);
         __syncthreads();
 

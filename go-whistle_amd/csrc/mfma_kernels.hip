@@ -198,7 +198,10 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const int col = g * G + e * 64 + lane;
-                xg[k][e] = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
+                float xv = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
+                if (J.xgate && t < J.rows && col < J.in)  // Attention.output's gate (attention.go:245-249)
+                    xv = xv * gate_sigmoid(J.xgate[static_cast<long long>(t) * J.x_stride + col]);
+                xg[k][e] = xv;
             }
         }
     };

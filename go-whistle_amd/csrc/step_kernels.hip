@@ -12,6 +12,9 @@
 //                      activation (no reference counterpart; defined so that
 //                      CPU and GPU agree bit for bit).
 //   add_kernel         x += y (the residual adds, decoder.go / block.go).
+//   sigmoid_gate_kernel  Attention.output's gate (internal/needle/attention.go:
+//                      245-249): gate = sigmoid(gate), out *= gate, with
+//                      sigmoid float32(1 / (1 + exp(-float64(x)))).
 //   append_kernel      Int8Rows.Append (internal/needle/int8.go:125-141) of one
 //                      row per stream at the stream's position, optionally
 //                      after RoPE of each head at that position.
@@ -166,6 +169,14 @@ __global__ __launch_bounds__(256) void add_kernel(float *x, const float *y, long
     if (i < n) x[i] = x[i] + y[i];
 }
 
+__global__ __launch_bounds__(256) void sigmoid_gate_kernel(float *out, float *gate, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float g = gate_sigmoid(gate[i]);
+    gate[i] = g;
+    out[i] = out[i] * g;
+}
+
 // Int8Rows.Append of stream b's row at its position pos[b]: QuantizeRow
 // per chunk of width (int8.go:36-55), one wavefront per chunk. With cos_t,
 // each chunk (a head) is first rotated by RoPE at pos[b] (rope.go:69-81):
@@ -256,6 +267,12 @@ hipError_t launch_silu(float *x, long long n, hipStream_t s) {
 hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_sigmoid_gate(float *out, float *gate, long long n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(sigmoid_gate_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, out, gate, n);
     return hipGetLastError();
 }
 

@@ -10,11 +10,12 @@ quantized path serves:
 
   x = E.Row(token) * scale                          decoder.go:269-275
   per layer:
-    h = ZCRMSNorm(x); q, k, v = GEMMs(Wq, Wk, Wv; h)  norm.go, kernel.go:134
+    h = ZCRMSNorm(x); q, k, v, g = GEMMs(Wq, Wk, Wv, Wg; h)  norm.go, attention.go:265-271
     RoPE(q), RoPE(k) at the position                 rope.go:69-81
     append int8 k, v; a = AttendInt8(q, 0..pos)      int8.go:125-141, 208-272
-    x += Wo a
-    h = ZCRMSNorm(x); a = AttendInt8(Wcq h, memory); x += Wco a
+    x += Wo (a * sigmoid(g))                         attention.go:242-260
+    h = ZCRMSNorm(x); q, g = GEMMs(Wcq, Wcg; h)      cross.go:209-252
+    a = AttendInt8(q, memory); x += Wco (a * sigmoid(g))
     h = ZCRMSNorm(x); x += W2 SiLU(W1 h)
   logits = E ZCRMSNorm(x); token = argmax           decoder.go:507-523, greedy.go:181-191
 
@@ -59,7 +60,7 @@ class DecoderConfig:
     theta: float = 1e5
 
 
-LAYER_MATS = ("wq", "wk", "wv", "wo", "wcq", "wco", "wck", "wcv", "w1", "w2")
+LAYER_MATS = ("wq", "wk", "wv", "wg", "wo", "wcq", "wcg", "wco", "wck", "wcv", "w1", "w2")
 
 
 @dataclass
@@ -123,7 +124,8 @@ def make_model(seed, cfg=DecoderConfig()):
                        "wv": packed(d, d, cfg.attn_bits), "wo": packed(d, d, cfg.attn_bits),
                        "wcq": packed(d, d, cfg.attn_bits), "wco": packed(d, d, cfg.attn_bits),
                        "wck": packed(d, d, cfg.attn_bits), "wcv": packed(d, d, cfg.attn_bits),
-                       "w1": packed(f, d, cfg.ffn_bits), "w2": packed(d, f, cfg.ffn_bits)})
+                       "w1": packed(f, d, cfg.ffn_bits), "w2": packed(d, f, cfg.ffn_bits),
+                       "wg": packed(d, d, cfg.attn_bits), "wcg": packed(d, d, cfg.attn_bits)})
     scales = (g.standard_normal((cfg.layers * 3 + 1, d)) * 0.1).astype(np.float32)
     gains = (np.float32(1) + scales).astype(np.float32)  # NewZCRMSNorm (norm.go:22-30)
     cos, sin = rope_tables(cfg.head_dim, cfg.max_pos, cfg.theta)
@@ -146,9 +148,9 @@ def _ptr(t):
 
 class Decoder:
     """The model on the device for `batch` streams decoding in lockstep.
-    fused: the norms, residual adds, SiLU, RoPE and the K/V appends ride in
-    the products and the attention (8 launches per layer instead of 19, the
-    same bits)."""
+    fused: the norms, residual adds, output gates, SiLU, RoPE and the K/V
+    appends ride in the products and the attention (8 launches per layer
+    instead of 21, the same bits)."""
 
     def __init__(self, model, batch, device="cuda", fused=True):
         import torch
@@ -168,7 +170,7 @@ class Decoder:
         self.spans_cross = z(B, 4, dt=i32)
         self.spans_cross[:, 3] = c.frames
         self.x, self.h = z(B, c.dim), z(B, c.dim)
-        self.q, self.k, self.v = z(B, c.dim), z(B, c.dim), z(B, c.dim)
+        self.q, self.k, self.v, self.g = z(B, c.dim), z(B, c.dim), z(B, c.dim), z(B, c.dim)
         self.att, self.o = z(B, c.dim), z(B, c.dim)
         self.u = z(B, c.ffn)
         self.logits = z(B, c.vocab)
@@ -262,21 +264,23 @@ class Decoder:
         for l in range(c.layers):
             m = self.mats[l]
             if c.head_dim == 64:  # heads are the lut kernel's 64-row blocks: the appends ride on the product
-                caches = [None, (self.self_k[l], self.self_ks[l], rope), (self.self_v[l], self.self_vs[l], None)]
-                cq.gemms_append_dev([m["wq"], m["wk"], m["wv"]], [self.q, self.k, self.v], self.x, B, caches,
-                                    c.max_pos * D, c.max_pos * hk, self.pos, c.max_pos, norm_gain=self.gains[3 * l])
+                caches = [None, (self.self_k[l], self.self_ks[l], rope), (self.self_v[l], self.self_vs[l], None),
+                          None]
+                cq.gemms_append_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.x,
+                                    B, caches, c.max_pos * D, c.max_pos * hk, self.pos, c.max_pos,
+                                    norm_gain=self.gains[3 * l])
             else:
-                cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"]], [self.q, self.k, self.v], self.x, B,
+                cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.x, B,
                                    norm_gain=self.gains[3 * l])
                 needle.append_dev(self.self_k[l], self.self_ks[l], self.k, B, D, c.head_dim, c.max_pos * D,
                                   c.max_pos * hk, self.pos, c.max_pos, rope=rope)
                 needle.append_dev(self.self_v[l], self.self_vs[l], self.v, B, D, c.head_dim, c.max_pos * D,
                                   c.max_pos * hk, self.pos, c.max_pos)
             self._attend(l, False, s, rope=(self.cos, self.sin, self.pos))
-            cq.gemms_fused_dev([m["wo"]], [self.x], self.att, B, resid=self.x)
-            cq.gemms_fused_dev([m["wcq"]], [self.q], self.x, B, norm_gain=self.gains[3 * l + 1])
+            cq.gemms_gated_dev([m["wo"]], [self.x], self.att, self.g, B, resid=self.x)
+            cq.gemms_fused_dev([m["wcq"], m["wcg"]], [self.q, self.g], self.x, B, norm_gain=self.gains[3 * l + 1])
             self._attend(l, True, s)
-            cq.gemms_fused_dev([m["wco"]], [self.x], self.att, B, resid=self.x)
+            cq.gemms_gated_dev([m["wco"]], [self.x], self.att, self.g, B, resid=self.x)
             cq.gemms_fused_dev([m["w1"]], [self.u], self.x, B, norm_gain=self.gains[3 * l + 2], act=1)
             cq.gemms_fused_dev([m["w2"]], [self.x], self.u, B, resid=self.x)
         cq.gemms_fused_dev([self.emb], [self.logits], self.x, B, norm_gain=self.gains[3 * c.layers])
@@ -294,7 +298,7 @@ class Decoder:
         for l in range(c.layers):
             m = self.mats[l]
             check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * l]), B, D, s))
-            cq.gemms_dev([m["wq"], m["wk"], m["wv"]], [self.q, self.k, self.v], self.h, B)
+            cq.gemms_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.h, B)
             for t in (self.q, self.k):
                 check(L.nd_rope_dev(_ptr(t), B, c.heads, c.head_dim, _ptr(self.cos), _ptr(self.sin), _ptr(self.pos),
                                     1, s))
@@ -302,11 +306,13 @@ class Decoder:
                 check(L.kv_append_dev(_ptr(cq_), _ptr(cs_), _ptr(src), B, D, c.head_dim, c.max_pos * D,
                                       c.max_pos * hk, _ptr(self.pos), c.max_pos, s))
             self._attend(l, False, s)
+            check(L.nd_sigmoid_gate_dev(_ptr(self.att), _ptr(self.g), B * D, s))
             m["wo"].gemm_dev(self.o, self.att, B)
             check(L.nd_add_dev(_ptr(self.x), _ptr(self.o), B * D, s))
             check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * l + 1]), B, D, s))
-            m["wcq"].gemm_dev(self.q, self.h, B)
+            cq.gemms_dev([m["wcq"], m["wcg"]], [self.q, self.g], self.h, B)
             self._attend(l, True, s)
+            check(L.nd_sigmoid_gate_dev(_ptr(self.att), _ptr(self.g), B * D, s))
             m["wco"].gemm_dev(self.o, self.att, B)
             check(L.nd_add_dev(_ptr(self.x), _ptr(self.o), B * D, s))
             check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * l + 2]), B, D, s))

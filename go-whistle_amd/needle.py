@@ -84,6 +84,12 @@ def fake_quant_dev(dst, x, rows, cols, width):
     check(lib().nd_fake_quant_dev(c_void_p(dst.data_ptr()), c_void_p(x.data_ptr()), rows, cols, width, _stream()))
 
 
+def sigmoid_gate_dev(out, gate, n):
+    """Attention.output's gate (attention.go:245-249) on device tensors:
+    gate = sigmoid(gate), out *= gate over n values."""
+    check(lib().nd_sigmoid_gate_dev(c_void_p(out.data_ptr()), c_void_p(gate.data_ptr()), n, _stream()))
+
+
 class Linear:
     """needle.Linear over a packed matrix (internal/needle/linear.go:11-145),
     on device tensors: x rows × In -> dst rows × Out. With WithInt8Input the

@@ -113,6 +113,16 @@ int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x
  * lut matrices only. */
 int cq_gemms_fused_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows,
                        const float *norm_gain, const float *resid, int act, void *stream);
+/* The gated attention's output projection: dst = product of (x * gate')
+ * with gate' = sigmoid(gate) elementwise, sigmoid float32(1 / (1 +
+ * exp(-float64(g)))) -- Attention.output (internal/needle/attention.go:
+ * 242-260) and the cross-attention's gate (internal/decoder/cross.go:
+ * 231-252) followed by outProj.Apply, one launch instead of two, bit for bit
+ * nd_sigmoid_gate_dev then cq_gemms_dev. gate has x's layout (rows of the
+ * matrices' input width) and is only read. resid non-null (n = 1): dst =
+ * resid + product (resid may be dst). lut matrices only. */
+int cq_gemms_gated_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, const float *gate, int rows,
+                       const float *resid, void *stream);
 /* cq_gemms_fused_dev (norm_gain only) whose outputs are also appended to
  * int8 row caches: the decoder's K and V projections followed by
  * Int8Rows.Append (internal/needle/int8.go:36-55; Attention.Extend's
@@ -240,6 +250,11 @@ int nd_silu_dev(float *x, long long n, void *stream);
 int nd_fake_quant_dev(float *dst, const float *x, long long rows, int cols, int width, void *stream);
 /* x += y elementwise (the residual adds). */
 int nd_add_dev(float *x, const float *y, long long n, void *stream);
+/* The attention's output gate (internal/needle/attention.go:245-249):
+ * gate[i] = sigmoid(gate[i]), out[i] *= gate[i], sigmoid being jax.nn.sigmoid
+ * in float32 as the reference writes it, float32(1 / (1 + exp(-float64(x))))
+ * (internal/needle/load.go:120-123; internal/decoder/cross.go:240-248). */
+int nd_sigmoid_gate_dev(float *out, float *gate, long long n, void *stream);
 
 #ifdef __cplusplus
 }

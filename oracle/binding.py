@@ -74,6 +74,9 @@ def lib():
                                 POINTER(c_int32)]),
             "orc_argmax": (None, [POINTER(c_int32), POINTER(c_float), c_int, c_int]),
             "orc_silu": (None, [POINTER(c_float), ctypes.c_long]),
+            "orc_exp64": (ctypes.c_double, [ctypes.c_double]),
+            "orc_gate_sigmoid": (c_float, [c_float]),
+            "orc_sigmoid_gate": (None, [POINTER(c_float), POINTER(c_float), ctypes.c_long]),
             "orc_attend_int8_spans": (c_int, [POINTER(c_float), POINTER(c_float), c_int, c_int, POINTER(c_int8),
                                               POINTER(c_float), c_int, c_int, POINTER(c_int8), POINTER(c_float), c_int,
                                               c_int, c_int, POINTER(c_int32), c_float, c_int, c_int, POINTER(c_float)]),
@@ -329,3 +332,24 @@ def silu(x):
     x = np.array(x, dtype=np.float32)
     lib().orc_silu(fp(x), x.size)
     return x
+
+
+def exp64(x):
+    """fdlibm's float64 exp of each value of x."""
+    x = np.asarray(x, np.float64).ravel()
+    return np.array([lib().orc_exp64(float(v)) for v in x], np.float64)
+
+
+def gate_sigmoid(x):
+    """float32(1 / (1 + exp(-float64(x)))) of each value of x."""
+    x = np.asarray(x, np.float32).ravel()
+    return np.array([lib().orc_gate_sigmoid(float(v)) for v in x], np.float32)
+
+
+def sigmoid_gate(out, gate):
+    """Attention.output's gate: returns (out * sigmoid(gate), sigmoid(gate))."""
+    out = np.array(out, dtype=np.float32)
+    gate = np.array(gate, dtype=np.float32)
+    assert out.size == gate.size
+    lib().orc_sigmoid_gate(fp(out), fp(gate), out.size)
+    return out, gate

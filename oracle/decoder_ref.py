@@ -2,7 +2,8 @@
 stream at a time: the same operations in the same order as
 go-whistle_amd/decoder.py's device step (embedding Row x sqrt(d),
 ZCRMSNorm, lut GEMMs, RoPE, int8 append and AttendInt8 with the int8 query
-and amd64's exponent, SiLU, tied head, first-index argmax), over a cross
+and amd64's exponent, the sigmoid output gates, SiLU, tied head,
+first-index argmax), over a cross
 memory projected from the encoder states and quantised per head.
 
 TEST INFRASTRUCTURE ONLY: the checker for the device decoder and the
@@ -48,7 +49,7 @@ class RefDecoder:
             for l in range(c.layers):
                 w = self.mats[l]
                 h = orc.zc_rmsnorm(x, m.gains[3 * l], c.dim)
-                q, k, v = orc.gemms([w["wq"], w["wk"], w["wv"]], h, 1)
+                q, k, v, g = orc.gemms([w["wq"], w["wk"], w["wv"], w["wg"]], h, 1)
                 q = orc.rope(q, c.heads, c.head_dim, m.rope_cos, m.rope_sin, [pos])
                 k = orc.rope(k, c.heads, c.head_dim, m.rope_cos, m.rope_sin, [pos])
                 kc, ksc, vc, vsc = caches[l]
@@ -60,12 +61,14 @@ class RefDecoder:
                 a = orc.attend_int8_spans(q, 1, c.heads, kc[:n_keys * c.dim], ksc[:n_keys * hk], c.dim, c.head_dim,
                                           vc[:n_keys * c.dim], vsc[:n_keys * hk], c.dim, c.head_dim, n_keys,
                                           np.array([[0, 0, 0, n_keys]], np.int32), scale, True, 1)
+                a, _ = orc.sigmoid_gate(a, g)  # Attention.output (attention.go:242-260)
                 x = (x + w["wo"].gemm(a, 1)).astype(np.float32)
                 h = orc.zc_rmsnorm(x, m.gains[3 * l + 1], c.dim)
-                qc = w["wcq"].gemm(h, 1)
+                qc, gc = orc.gemms([w["wcq"], w["wcg"]], h, 1)
                 mk, mks, mv, mvs = self.mem[l]
                 a = orc.attend_int8_spans(qc, 1, c.heads, mk, mks, c.dim, c.head_dim, mv, mvs, c.dim, c.head_dim,
                                           c.frames, np.array([[0, 0, 0, c.frames]], np.int32), scale, True, 1)
+                a, _ = orc.sigmoid_gate(a, gc)  # cross.go:231-252
                 x = (x + w["wco"].gemm(a, 1)).astype(np.float32)
                 h = orc.zc_rmsnorm(x, m.gains[3 * l + 2], c.dim)
                 u = orc.silu(w["w1"].gemm(h, 1))

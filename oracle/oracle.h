@@ -143,6 +143,9 @@ void orc_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, c
               const int32_t *pos);                                                    /* rope.go:69-81 */
 void orc_argmax(int32_t *out, const float *v, int rows, int n);                          /* greedy.go:181-191 */
 void orc_silu(float *x, long n);
+double orc_exp64(double x);                             /* fdlibm e_exp.c; Go's portable math.Exp */
+float orc_gate_sigmoid(float x);                        /* load.go:120-123, cross.go:322-325 */
+void orc_sigmoid_gate(float *out, float *gate, long n); /* attention.go:245-249 */
 
 #ifdef __cplusplus
 }

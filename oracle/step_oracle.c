@@ -8,11 +8,22 @@
  *   internal/needle/rope.go:17-44, 69-81   NewRope (tables built in Python by
  *                                          the same steps), Rope.apply
  *   internal/decoder/greedy.go:181-191     argmax
+ *   internal/needle/attention.go:245-249   Attention.output's gate
+ *   internal/needle/load.go:120-123        sigmoid = float32(1/(1 + exp(-float64(x))))
  *
  * Pinned by tests/test_oracle_step.py: ZCRMSNorm against float64 and a
  * closed form (a constant row); RoPE against the float64 rotation and the
  * identity at position 0; argmax against numpy's first-index argmax with
- * planted ties; SiLU against float64 x*sigmoid(x) within a few ulps.
+ * planted ties; SiLU against float64 x*sigmoid(x) within a few ulps; the
+ * float64 exp against the C library's exp (within 1 ulp, equal in nearly all
+ * cases) and exact powers of e; the gate's sigmoid against float32(1/(1 +
+ * libm exp(-x))) bit for bit and its closed forms (0 -> 0.5, tails 0 and 1).
+ *
+ * The reference's sigmoid calls Go's math.Exp (a dependency outside the
+ * reference: the Go standard library); exp here is fdlibm's method, whose
+ * float64 result is within 1 ulp of Go's, so the float32 sigmoid is the
+ * same except where the float64 value lies within 1 ulp of a float32
+ * rounding midpoint.
  */
 #include <math.h>
 #include <stdint.h>
@@ -86,5 +97,39 @@ void orc_silu(float *x, long n) {
             s = e / d;
         }
         x[i] = v * s;
+    }
+}
+
+double orc_exp64(double x) {
+    /* fdlibm e_exp.c (Sun Microsystems, 1993), the steps of Go's portable
+     * math.Exp: x = k ln2 + r, r = hi - lo, exp(r) = 1 - ((lo - r c/(2 - c)) - hi) */
+    const double ln2hi = 6.93147180369123816490e-01, ln2lo = 1.90821492927058770002e-10;
+    const double log2e = 1.44269504088896338700e+00;
+    const double p1 = 1.66666666666666019037e-01, p2 = -2.77777777770155933842e-03;
+    const double p3 = 6.61375632143793436117e-05, p4 = -1.65339022054652515390e-06;
+    const double p5 = 4.13813679705723846039e-08;
+    if (x != x) return x;
+    if (x > 7.09782712893383973096e+02) return HUGE_VAL;
+    if (x < -7.45133219101941108420e+02) return 0.0;
+    if (x > -3.7252902984619140625e-09 && x < 3.7252902984619140625e-09) return 1.0 + x;
+    double kf = x < 0.0 ? log2e * x - 0.5 : log2e * x + 0.5;
+    int k = (int)kf;
+    double hi = x - (double)k * ln2hi, lo = (double)k * ln2lo;
+    double r = hi - lo, t = r * r;
+    double c = r - t * (p1 + t * (p2 + t * (p3 + t * (p4 + t * p5))));
+    double y = 1.0 - ((lo - (r * c) / (2.0 - c)) - hi);
+    return ldexp(y, k);
+}
+
+float orc_gate_sigmoid(float x) {
+    double e = orc_exp64(-(double)x);
+    return (float)(1.0 / (1.0 + e));
+}
+
+void orc_sigmoid_gate(float *out, float *gate, long n) {
+    /* Attention.output (attention.go:245-249): gate = sigmoid(gate), out *= gate */
+    for (long i = 0; i < n; i++) {
+        gate[i] = orc_gate_sigmoid(gate[i]);
+        out[i] *= gate[i];
     }
 }

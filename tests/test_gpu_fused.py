@@ -245,3 +245,85 @@ def test_decoder_fused_equals_plain():
         out.append((toks, d.logits.cpu().numpy()))
     assert np.array_equal(out[0][0], out[1][0])
     assert same(out[0][1], out[1][1])
+
+
+def test_sigmoid_gate_vs_oracle():
+    """nd_sigmoid_gate_dev against the oracle's Attention.output gate
+    (attention.go:245-249), bit for bit, tails and zeros included."""
+    import torch
+
+    from oracle import binding as orc
+
+    g = synth.rng(91)
+    out = (g.standard_normal(70001) * 3).astype(np.float32)
+    gate = (g.standard_normal(70001) * 8).astype(np.float32)
+    gate[:6] = [0.0, -0.0, 120.0, -120.0, -103.5, 30.0]
+    wo, wg = orc.sigmoid_gate(out, gate)
+    o, gg = _t(out), _t(gate)
+    check(lib().nd_sigmoid_gate_dev(_p(o), _p(gg), out.size, _s()))
+    torch.cuda.synchronize()
+    assert same(gg.cpu().numpy(), wg) and same(o.cpu().numpy(), wo)
+
+
+@pytest.mark.parametrize("rows,shape,bits,resid", [(1, (512, 512), 4, True), (6, (512, 2048), 2, True),
+                                                   (4, (1024, 512), 4, False), (300, (16384, 512), 4, False)])
+def test_gated_product(rows, shape, bits, resid):
+    """cq_gemms_gated_dev (x * sigmoid(gate) inside the product, then the
+    residual add) bit for bit the separate gate, product and add; at 300
+    activations of a 16384-row matrix the MFMA form carries the gate."""
+    import torch
+
+    out, inp = shape
+    g = synth.rng(92 + rows + out)
+    m = cq.New(synth.random_packed(g, out, inp, 128, bits, sigma=0.05))
+    x = _t((g.standard_normal((rows, inp)) * 2).astype(np.float32))
+    gate = _t((g.standard_normal((rows, inp)) * 4).astype(np.float32))
+    r0 = _t(g.standard_normal((rows, out)).astype(np.float32))
+    xw, gw_ = x.clone(), gate.clone()
+    check(lib().nd_sigmoid_gate_dev(_p(xw), _p(gw_), rows * inp, _s()))
+    want = torch.zeros(rows, out, device="cuda")
+    m.gemm_dev(want, xw, rows)
+    if resid:
+        want = r0 + want
+    got = r0.clone() if resid else torch.zeros(rows, out, device="cuda")
+    gate_before = gate.clone()
+    cq.gemms_gated_dev([m], [got], x, gate, rows, resid=got if resid else None)
+    torch.cuda.synchronize()
+    assert same(got.cpu().numpy(), want.cpu().numpy())
+    assert torch.equal(gate, gate_before)  # the gate is only read
+    if rows == 300:
+        assert m.gemm_path(rows) == "lut-mfma"
+
+
+def test_gated_product_vs_oracle():
+    """The gated product against the oracle: gate, then the lut product."""
+    import torch
+
+    from oracle import binding as orc
+
+    g = synth.rng(95)
+    p = synth.random_packed(g, 512, 512, 128, 4, sigma=0.05)
+    m, om = cq.New(p), orc.OMatrix.new(p)
+    x = (g.standard_normal((3, 512)) * 2).astype(np.float32)
+    gate = (g.standard_normal((3, 512)) * 4).astype(np.float32)
+    xw, _ = orc.sigmoid_gate(x, gate)
+    want = om.gemm(xw, 3)
+    got = torch.zeros(3, 512, device="cuda")
+    cq.gemms_gated_dev([m], [got], _t(x), _t(gate), 3)
+    torch.cuda.synchronize()
+    assert same(got.cpu().numpy().ravel(), want)
+
+
+def test_gated_misuse():
+    import torch
+
+    from go_whistle_amd import CQPanic
+
+    g = synth.rng(96)
+    ms = [cq.New(synth.random_packed(g, 512, 512, 128, 4, sigma=0.05)) for _ in range(2)]
+    x = torch.zeros(2, 512, device="cuda")
+    ys = [torch.zeros(2, 512, device="cuda") for _ in ms]
+    with pytest.raises(CQPanic):  # no gate
+        cq.gemms_gated_dev(ms, ys, x, None, 2)
+    with pytest.raises(CQPanic):  # a residual add takes one matrix
+        cq.gemms_gated_dev(ms, ys, x, x, 2, resid=ys[0])

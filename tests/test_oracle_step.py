@@ -3,6 +3,8 @@ against float64 and a closed form, RoPE (rope.go:69-81) against the float64
 rotation and the identity at position 0, argmax (greedy.go:181-191)
 against numpy's first-index argmax with ties, SiLU against float64."""
 
+import math
+
 import numpy as np
 import pytest
 
@@ -85,3 +87,54 @@ def test_silu_vs_float64():
     want = xx / (1 + np.exp(-xx))
     err = np.abs(got - want)
     assert np.all(err <= 4 * 2.0 ** -23 * np.abs(want) + 1e-37)
+
+
+def test_exp64_vs_libm_and_exact_points():
+    """fdlibm's exp against the C library's (Python's math.exp): within 1 ulp
+    everywhere, bit-equal in most cases, and the closed forms exp(0) = 1,
+    exp(k ln 2) = 2^k to 1 ulp, the overflow and underflow edges."""
+    g = np.random.default_rng(11)
+    x = np.concatenate([g.standard_normal(4000) * 4, g.uniform(-740, 705, 4000), g.standard_normal(500) * 1e-9])
+    got = orc.exp64(x)
+    want = np.array([math.exp(v) for v in x])
+    ulps = np.abs(got.view(np.int64) - want.view(np.int64))
+    assert ulps.max() <= 1
+    assert (ulps == 0).mean() > 0.8
+    assert orc.exp64([0.0])[0] == 1.0 and abs(orc.exp64([1.0])[0] - math.e) <= 2.0 ** -51  # 1 ulp of e
+    y = g.uniform(-700, 700, 2000)
+    prod = orc.exp64(y) * orc.exp64(-y)  # exp(y) exp(-y) = 1
+    assert np.all(np.abs(prod - 1.0) <= 3 * 2.0 ** -52)
+    big = orc.exp64([709.0, 710.0, -745.0, -746.0, float("nan")])
+    assert np.isfinite(big[0]) and np.isinf(big[1]) and big[2] > 0 and big[3] == 0 and np.isnan(big[4])
+
+
+def test_gate_sigmoid_bit_exact_and_closed_forms():
+    """The gate's sigmoid (load.go:120-123) against float32(1/(1 + exp(-x)))
+    with the C library's exp, bit for bit, and its fixed points: 0.5 at 0,
+    exactly 1 and 0 in the tails, the smallest subnormal just before 0."""
+    g = np.random.default_rng(12)
+    x = (g.standard_normal(50000) * 8).astype(np.float32)
+    got = orc.gate_sigmoid(x)
+    want = np.array([np.float32(1.0 / (1.0 + math.exp(-float(v)))) for v in x], np.float32)
+    assert np.array_equal(got.view(np.int32), want.view(np.int32))
+    edge = orc.gate_sigmoid([0.0, -0.0, 40.0, 800.0, -103.0, -104.0, float("inf"), float("-inf")])
+    assert list(edge[:4]) == [0.5, 0.5, 1.0, 1.0]
+    assert edge[4] == np.float32(2.0 ** -149) and edge[5] == 0.0 and edge[6] == 1.0 and edge[7] == 0.0
+    # 1 - sigmoid(x) = sigmoid(-x) for float64; in float32 within an ulp of the larger
+    s, t = orc.gate_sigmoid(x[:2000]).astype(np.float64), orc.gate_sigmoid(-x[:2000]).astype(np.float64)
+    assert np.all(np.abs(s + t - 1.0) <= 2.0 ** -23)
+
+
+def test_sigmoid_gate_updates_both():
+    """Attention.output (attention.go:245-249): gate becomes sigmoid(gate),
+    out becomes out * gate, each rounded to float32; a plain restatement of
+    the planted case where the gate is 0 (sigmoid 1/2: out halves exactly)."""
+    out = np.array([3.0, -5.0, 1e-30, 7.0], np.float32)
+    gate = np.zeros(4, np.float32)
+    o, gg = orc.sigmoid_gate(out, gate)
+    assert list(gg) == [0.5] * 4 and list(o) == list(out / 2)
+    g = np.random.default_rng(13)
+    out, gate = g.standard_normal(300).astype(np.float32), g.standard_normal(300).astype(np.float32)
+    o, gg = orc.sigmoid_gate(out, gate)
+    assert np.array_equal(gg, orc.gate_sigmoid(gate))
+    assert np.array_equal(o, (out * gg).astype(np.float32))
