@@ -180,8 +180,9 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
     cfg = dec.DecoderConfig()
     model = dec.make_model(7, cfg)
     res = {"model": "synthetic Whistle-shaped decoder: 8 layers, d 512, 8x64 heads, FFN 2048 (CQ2), attention "
-                    "CQ4, tied CQ4 head 16384x512, int8 self/cross KV; cross memory: 1500 random encoder states "
-                    "through CQ4 K/V projections", "tokens": tokens}
+                    "CQ4 (self q/k/v/gate/o, cross q/gate/o: sigmoid output gates), tied CQ4 head 16384x512, int8 "
+                    "self/cross KV; cross memory: 1500 random encoder states through CQ4 K/V projections",
+           "tokens": tokens}
     for batch in (1, 256):
         d = dec.Decoder(model, batch)
         d.set_memory(7, "numpy" if batch == 1 else "device")
