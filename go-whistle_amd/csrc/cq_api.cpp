@@ -332,6 +332,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
 }
 
 constexpr int kMfmaMinRows = 64;  // activations from which the MFMA form can run
+constexpr int kMfmaTile = 64;     // activations per workgroup of the MFMA form (32 when 64 leaves CUs idle)
 
 // The MFMA form pays when its grid fills a good part of the chip; below that
 // the lut kernel's workgroup per activation spreads wider.
@@ -343,8 +344,7 @@ bool mfma_pays(cq_matrix *const *ms, int n, int rows) {
         const int nblk = (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
         wgs += (nblk + rpw - 1) / rpw;
     }
-    const int ta = mfma_activations_per_workgroup();
-    wgs *= (rows + ta - 1) / ta;
+    wgs *= (rows + kMfmaTile - 1) / kMfmaTile;
     return wgs * 8 >= 3LL * device_info().cus;
 }
 
@@ -367,7 +367,15 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
         ++a.njobs;
     }
     if (a.njobs == 0 || rows == 0) return CQ_OK;
-    const int ta = mfma_activations_per_workgroup();
+    // 32-activation tiles when twice the workgroups of 64 still run in one
+    // round on the CUs (2048 rows at 1500 activations: 96 -> 192 workgroups;
+    // the 16384-row head at 256: 128 -> 256). A 32-activation workgroup
+    // takes about two thirds of a 64-activation one's time (half the MFMAs
+    // and table items, one-hot operands reused by one activation tile
+    // instead of two), so a second round would lose (512 x 2048 at 12000
+    // activations: 482 -> 597 us measured).
+    const long long wg64 = static_cast<long long>(wg) * ((rows + kMfmaTile - 1) / kMfmaTile);
+    const int ta = 2 * wg64 <= device_info().cus ? kMfmaTile / 2 : kMfmaTile;
     const int max_rows = 65535 * ta;
     for (int r0 = 0; r0 < rows; r0 += max_rows) {
         LutLaunch b = a;
@@ -378,7 +386,7 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
             if (b.jobs[k].resid) b.jobs[k].resid += static_cast<long long>(r0) * b.jobs[k].resid_stride;
             b.jobs[k].rows = nr;
         }
-        HIP_TRY(launch_lut_mfma(b, s0.width, wg, (nr + ta - 1) / ta, stream), "lut mfma launch");
+        HIP_TRY(launch_lut_mfma(b, s0.width, ta, wg, (nr + ta - 1) / ta, stream), "lut mfma launch");
     }
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;

@@ -125,11 +125,11 @@ bool lut_geometry_supported(int bits, int group_bytes);
 
 // MFMA form of the lut product for many activations (mfma_kernels.hip):
 // one launch for up to kKernargJobs views of one geometry; grid x covers
-// the jobs' 256-row tiles (wg0), grid y the 64-activation tiles.
+// the jobs' 512-row tiles (wg0), grid y the tiles of ta activations (64 or
+// 32).
 bool mfma_geometry_supported(int bits, int group);
 int mfma_rows_per_workgroup();
-int mfma_activations_per_workgroup();
-hipError_t launch_lut_mfma(const LutLaunch &a, int bits, int wg, int act_tiles, hipStream_t s);
+hipError_t launch_lut_mfma(const LutLaunch &a, int bits, int ta, int wg, int act_tiles, hipStream_t s);
 
 struct RowArgs {
     const uint8_t *idx;

@@ -22,16 +22,18 @@
 // integer (round to nearest even, exact for |f| < 2^22), and its bit pattern
 // is 0x4B400000 + RNE(f), whose bits 0-5 are l and bits 6-13 are h.
 //
-// Work split: a workgroup of 8 wavefronts owns 64 activations and 512 weight
-// rows (one 64-row block per wavefront, two 32-row MFMA tiles). Per group:
+// Work split: a workgroup of 8 wavefronts owns TA activations (64, or 32
+// when 64 would leave CUs idle) and 512 weight rows (one 64-row block per
+// wavefront, two 32-row MFMA tiles, TA / 32 activation tiles). Per group:
 //   1. the activations' groups are rotated (the plain FWHT in the lut
-//      kernel's stage order) and scaled by 8191/M into LDS, 8 per wavefront;
+//      kernel's stage order) and scaled by 8191/M into LDS, TA / 8 per
+//      wavefront;
 //   2. per chunk of 16 positions, every thread builds two tables' two int8
 //      planes in LDS [position][plane][activation][16 codes] (the next chunk
 //      while the MFMAs run on the current one);
 //   3. each wavefront streams its rows' index bytes (16-byte loads in the
 //      lut layout), turns each nibble into a 16-byte one-hot in registers and
-//      runs 4 MFMAs per position (2 activation tiles x 2 row tiles);
+//      runs 2 * TA / 32 MFMAs per position (activation tiles x 2 row tiles);
 //   4. the int32 sums are folded into float32 y in registers.
 // MFMA roles: A = table planes (rows = activations), B = one-hot (columns =
 // weight rows), so a result row of 32 weight rows is 128 contiguous bytes
@@ -57,7 +59,6 @@ struct MfmaGeo {
     static constexpr int CW = CK / 8;        // index words per row and chunk (8 positions each)
     static constexpr int NCH = NJ / CK;      // chunks per group
     static constexpr int UPG = GB / 16;      // 16-byte index loads per row and group
-    static constexpr int TA = 64;            // activations per workgroup
     static constexpr int AP = G + 1;         // LDS pitch of an activation's scaled group (odd: no bank conflicts)
 };
 
@@ -96,10 +97,11 @@ __device__ __forceinline__ i32x4 one_hot(uint32_t n, unsigned long long val) {
     return r;
 }
 
-template <int BITS>
+template <int BITS, int TA>
 __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
     using M = MfmaGeo<BITS>;
-    constexpr int G = M::G, TA = M::TA, AP = M::AP, CK = M::CK;
+    constexpr int G = M::G, AP = M::AP, CK = M::CK;
+    constexpr int AT = TA / 32;  // activation tiles per wavefront
     extern __shared__ __align__(16) unsigned char smem[];
     float *av = reinterpret_cast<float *>(smem);                    // [TA][AP] scaled rotated groups
     float *stp = av + TA * AP;                                       // [TA] steps of the group
@@ -132,10 +134,10 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
         __syncthreads();
     }
 
-    i32x16 acc[2][2];     // [activation tile][row tile]
-    float yv[2][2][16];   // [activation tile][row tile][element]
+    i32x16 acc[AT][2];     // [activation tile][row tile]
+    float yv[AT][2][16];   // [activation tile][row tile][element]
 #pragma unroll
-    for (int at = 0; at < 2; ++at)
+    for (int at = 0; at < AT; ++at)
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
         lds_barrier();
         build(0, 0);
 #pragma unroll
-        for (int at = 0; at < 2; ++at)
+        for (int at = 0; at < AT; ++at)
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) acc[at][rt] = i32x16{};
         lds_barrier();
@@ -311,15 +313,15 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                 if (rows_here) {
                     // lane half 0 reads a position's l plane, half 1 its h plane
                     const int8_t *tb = tab + (static_cast<size_t>(c & 1) * CK * 2 + half) * TA * 16;
-                    i32x4 A[2][2];  // [position parity][activation tile]
+                    i32x4 A[2][AT];  // [position parity][activation tile]
 #pragma unroll
-                    for (int at = 0; at < 2; ++at)
+                    for (int at = 0; at < AT; ++at)
                         A[0][at] = *reinterpret_cast<const i32x4 *>(tb + (at * 32 + l32) * 16);
 #pragma unroll
                     for (int jc = 0; jc < CK; ++jc) {
                         if (jc + 1 < CK) {
 #pragma unroll
-                            for (int at = 0; at < 2; ++at)
+                            for (int at = 0; at < AT; ++at)
                                 A[(jc + 1) & 1][at] = *reinterpret_cast<const i32x4 *>(
                                     tb + (static_cast<size_t>(jc + 1) * 2 * TA + at * 32 + l32) * 16);
                         }
@@ -329,7 +331,7 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
                             const uint32_t n = (cur[rt][q * CW + jc / 8] >> (4 * (jc % 8))) & 15u;
                             const i32x4 B = one_hot(n, val);
 #pragma unroll
-                            for (int at = 0; at < 2; ++at)
+                            for (int at = 0; at < AT; ++at)
                                 acc[at][rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[jc & 1][at], B, acc[at][rt], 0, 0, 0);
                         }
                     }
@@ -341,7 +343,7 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
         // 4. Fold group g into y, in group order (lut.go:297-310).
         if (rows_here) {
 #pragma unroll
-            for (int at = 0; at < 2; ++at)
+            for (int at = 0; at < AT; ++at)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int tt = at * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
 
     if (rows_here) {
 #pragma unroll
-        for (int at = 0; at < 2; ++at)
+        for (int at = 0; at < AT; ++at)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int t = t0 + at * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
@@ -381,23 +383,23 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
     }
 }
 
-template <int BITS>
+template <int BITS, int TA>
 size_t mfma_lds_bytes() {
     using M = MfmaGeo<BITS>;
-    return sizeof(float) * (M::TA * M::AP + M::TA) + static_cast<size_t>(2) * M::CK * 2 * M::TA * 16;
+    return sizeof(float) * (TA * M::AP + TA) + static_cast<size_t>(2) * M::CK * 2 * TA * 16;
 }
 
-template <int BITS>
+template <int BITS, int TA>
 hipError_t launch_mfma_t(const LutLaunch &a, int wg, int act_tiles, hipStream_t s) {
-    static bool attr = false;
-    const size_t lds = mfma_lds_bytes<BITS>();
+    static bool attr = false;  // idempotent attribute write; a race is benign
+    const size_t lds = mfma_lds_bytes<BITS, TA>();
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_mfma_kernel<BITS>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_mfma_kernel<BITS, TA>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL(lut_mfma_kernel<BITS>, dim3(wg, act_tiles), dim3(kMfmaThreads), lds, s, a);
+    hipLaunchKernelGGL((lut_mfma_kernel<BITS, TA>), dim3(wg, act_tiles), dim3(kMfmaThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -407,12 +409,15 @@ bool mfma_geometry_supported(int bits, int group) { return group == 128 && (bits
 
 int mfma_rows_per_workgroup() { return 64 * kMfmaWaves; }
 
-int mfma_activations_per_workgroup() { return MfmaGeo<4>::TA; }
-
-hipError_t launch_lut_mfma(const LutLaunch &a, int bits, int wg, int act_tiles, hipStream_t s) {
+hipError_t launch_lut_mfma(const LutLaunch &a, int bits, int ta, int wg, int act_tiles, hipStream_t s) {
     if (wg <= 0 || act_tiles <= 0) return hipSuccess;
-    if (bits == 4) return launch_mfma_t<4>(a, wg, act_tiles, s);
-    if (bits == 2) return launch_mfma_t<2>(a, wg, act_tiles, s);
+    if (ta == 64) {
+        if (bits == 4) return launch_mfma_t<4, 64>(a, wg, act_tiles, s);
+        if (bits == 2) return launch_mfma_t<2, 64>(a, wg, act_tiles, s);
+    } else if (ta == 32) {
+        if (bits == 4) return launch_mfma_t<4, 32>(a, wg, act_tiles, s);
+        if (bits == 2) return launch_mfma_t<2, 32>(a, wg, act_tiles, s);
+    }
     return hipErrorInvalidValue;
 }
 

@@ -47,7 +47,7 @@ def _norm(x, gain, rows, dim):
 
 
 @pytest.mark.parametrize("rows,shape,bits", [(1, (512, 512), 4), (5, (2048, 512), 2), (256, (16384, 512), 4),
-                                             (3, (300, 640), 4)])
+                                             (3, (300, 640), 4), (2048, (16384, 512), 2)])
 def test_norm_prologue(rows, shape, bits):
     import torch
 
@@ -63,7 +63,7 @@ def test_norm_prologue(rows, shape, bits):
     torch.cuda.synchronize()
     for a, b in zip(got, want):
         assert same(a.cpu().numpy(), b.cpu().numpy())
-    if rows == 256:
+    if rows >= 256:  # 32-activation tiles at 256, 64 at 2048
         assert ms[0].gemm_path(rows) == "lut-mfma"
 
 
@@ -266,7 +266,8 @@ def test_sigmoid_gate_vs_oracle():
 
 
 @pytest.mark.parametrize("rows,shape,bits,resid", [(1, (512, 512), 4, True), (6, (512, 2048), 2, True),
-                                                   (4, (1024, 512), 4, False), (300, (16384, 512), 4, False)])
+                                                   (4, (1024, 512), 4, False), (300, (16384, 512), 4, False),
+                                                   (2048, (16384, 512), 4, True)])
 def test_gated_product(rows, shape, bits, resid):
     """cq_gemms_gated_dev (x * sigmoid(gate) inside the product, then the
     residual add) bit for bit the separate gate, product and add; at 300
@@ -291,7 +292,7 @@ def test_gated_product(rows, shape, bits, resid):
     torch.cuda.synchronize()
     assert same(got.cpu().numpy(), want.cpu().numpy())
     assert torch.equal(gate, gate_before)  # the gate is only read
-    if rows == 300:
+    if rows >= 300:
         assert m.gemm_path(rows) == "lut-mfma"
 
 
