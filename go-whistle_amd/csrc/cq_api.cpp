@@ -250,7 +250,6 @@ void apply_fuse(JobDesc &j, const Fuse *f, int k) {
 }
 
 constexpr int kLutTile = 4;     // blocks per tile of the lut kernel
-constexpr int kLutWaves = 4;    // wavefronts per workgroup
 constexpr int kLutChunk = 4;    // groups per LDS chunk
 constexpr int kLutMaxBpw = 16;  // most blocks per workgroup
 
@@ -297,17 +296,15 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     int nmax = 0;
     for (int k = 0; k < a.njobs; ++k) nmax = std::max(nmax, a.jobs[k].nblk);
     a.bpw = balanced_blocks(nmax, blocks_per_workgroup(blocks));
-    int wg = 0;
-    for (int k = 0; k < a.njobs; ++k) {
-        a.wg0[k] = wg;
-        wg += (a.jobs[k].nblk + a.bpw - 1) / a.bpw;
-    }
+    const int wg = (nmax + a.bpw - 1) / a.bpw;  // grid x: the units of the largest job (grid z: the jobs)
+    long long units = 0;
+    for (int k = 0; k < a.njobs; ++k) units += (a.jobs[k].nblk + a.bpw - 1) / a.bpw;
     a.tb = kLutTile;
     a.gc = lut_chunk(groups_max);
     // A launch that fills at most a quarter of the CUs is latency-bound: wide
     // rows then take their tables in fewer chunks (up to 32 KiB of tables),
     // each chunk costing a table build and a barrier.
-    if (static_cast<long long>(wg) * rows * 4 <= device_info().cus)
+    if (units * rows * 4 <= device_info().cus)
         while (a.gc * 2 <= groups_max && 2 * a.gc * 2 * s0.group_bytes * 16 * static_cast<int>(sizeof(short)) <= 32 * 1024)
             a.gc *= 2;
     a.bpw_max = a.bpw;

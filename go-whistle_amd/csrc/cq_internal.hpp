@@ -104,6 +104,7 @@ struct WorkUnit {
 };
 
 constexpr int kKernargJobs = 8;
+constexpr int kLutWaves = 4;  // wavefronts per workgroup of the lut kernel
 
 struct LutLaunch {
     JobDesc jobs[kKernargJobs];  // kernel-argument jobs (when dunits is null)

@@ -36,6 +36,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <cstddef>
+
 namespace cqhip {
 namespace {
 
@@ -279,10 +281,45 @@ constexpr int lut_waves_per_simd() {
     return GB >= 256 ? 2 : (BITS == 2 && GB == 32) ? 6 : 4;
 }
 
-// One work unit: blocks [b0, b0 + bc) of job J (counted from its blk0) for
+// A JobDesc held one dword per lane (lane i: dword i), fetched by one vector
+// load: the wavefront pays a single memory round trip for every field of
+// its job. Scalar loads of the same fields went out in three or four
+// dependent rounds (the compiler spreads them to spare scalar registers),
+// each about a microsecond at batch 1 where a product takes a few.
+static_assert(sizeof(JobDesc) <= 256, "a JobDesc must fit one dword per lane");
+struct JobRegs {
+    uint32_t d;
+    template <class T>
+    __device__ __forceinline__ T get(size_t off) const {
+        const uint32_t lo = __builtin_amdgcn_readlane(d, static_cast<int>(off / 4));
+        if constexpr (sizeof(T) == 8) {
+            const uint32_t hi = __builtin_amdgcn_readlane(d, static_cast<int>(off / 4 + 1));
+            return __builtin_bit_cast(T, static_cast<uint64_t>(lo) | static_cast<uint64_t>(hi) << 32);
+        } else {
+            return __builtin_bit_cast(T, lo);
+        }
+    }
+};
+__device__ __forceinline__ JobRegs job_regs(const JobDesc *J, int lane) {
+    const CQ_GLOBAL uint32_t *w = gptr(reinterpret_cast<const uint32_t *>(J));
+    return JobRegs{lane * 4 < static_cast<int>(sizeof(JobDesc)) ? w[lane] : 0u};
+}
+// The same fields by scalar loads through a pointer: the batch plans' job
+// table, which lives in device memory behind the unit table (measured
+// faster there than the vector fetch).
+struct JobPtr {
+    const JobDesc *J;
+    template <class T>
+    __device__ __forceinline__ T get(size_t off) const {
+        return *reinterpret_cast<const T *>(reinterpret_cast<const char *>(J) + off);
+    }
+};
+#define JOB(jr, T, field) ((jr).template get<T>(offsetof(JobDesc, field)))
+
+// One work unit: blocks [b0, b0 + bc) of job jr (counted from its blk0) for
 // activation act.
-template <int BITS, int GB>
-__device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, int b0, int bc, int act) {
+template <int BITS, int GB, class JS>
+__device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b0, int bc, int act, int W) {
     using Gm = LutGeo<BITS, GB>;
     constexpr int U = Gm::U, UPG = Gm::UPG, NT = Gm::NT;
     constexpr int DG = lut_loads_ahead<BITS, GB>();  // groups of index loads in flight per wavefront
@@ -290,23 +327,24 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int W = blockDim.x >> 6;
 
-    // The job's fields, read once before any store (later reads through J
-    // could not be hoisted past the stores of y).
-    const int j_in = J->in, j_row0 = J->row0, j_out = J->out, j_act = J->act;
-    const CQ_GLOBAL uint16_t *j_norm = gptr(J->norm);
-    CQ_GLOBAL float *j_y = gptr_w(J->y);
-    const long long j_ystride = J->y_stride, j_rstride = J->resid_stride;
-    const CQ_GLOBAL float *j_ngain = gptr(J->ngain), *j_resid = gptr(J->resid);
-    const float j_cbmax = J->cb_max, j_step = J->lut_step;
+    // The job's fields, taken once before any store.
+    const int j_in = JOB(jr, int, in), j_row0 = JOB(jr, int, row0), j_out = JOB(jr, int, out);
+    const int j_act = JOB(jr, int, act);
+    const CQ_GLOBAL uint16_t *j_norm = gptr(JOB(jr, const uint16_t *, norm));
+    CQ_GLOBAL float *j_y = gptr_w(JOB(jr, float *, y));
+    const long long j_ystride = JOB(jr, long long, y_stride), j_rstride = JOB(jr, long long, resid_stride);
+    const CQ_GLOBAL float *j_ngain = gptr(JOB(jr, const float *, ngain)), *j_resid = gptr(JOB(jr, const float *, resid));
+    const float j_cbmax = JOB(jr, float, cb_max), j_step = JOB(jr, float, lut_step);
     float cbv[16];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) cbv[c] = J->cb[c];
-    const int groups = J->groups, units = J->units, blk0 = J->blk0 + b0;
-    const CQ_GLOBAL uint8_t *idx = gptr(J->idx);
-    const CQ_GLOBAL float *x = gptr(J->x) + static_cast<long long>(act) * J->x_stride;
-    const CQ_GLOBAL float *xg = J->xgate ? gptr(J->xgate) + static_cast<long long>(act) * J->x_stride : nullptr;
+    for (int c = 0; c < 16; ++c) cbv[c] = jr.template get<float>(offsetof(JobDesc, cb) + 4 * c);
+    const int groups = JOB(jr, int, groups), units = JOB(jr, int, units), blk0 = JOB(jr, int, blk0) + b0;
+    const CQ_GLOBAL uint8_t *idx = gptr(JOB(jr, const uint8_t *, idx));
+    const long long j_xstride = JOB(jr, long long, x_stride);
+    const CQ_GLOBAL float *x = gptr(JOB(jr, const float *, x)) + static_cast<long long>(act) * j_xstride;
+    const float *j_xgate = JOB(jr, const float *, xgate);
+    const CQ_GLOBAL float *xg = j_xgate ? gptr(j_xgate) + static_cast<long long>(act) * j_xstride : nullptr;
 
     // LDS: tables of a chunk of gc groups, the chunk's steps, y of the
     // workgroup's rows between chunks, the chunk's float terms of up to tc
@@ -332,7 +370,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
         for (int p0 = 0; p0 < dim; p0 += cap) {
             const int pn = min(cap, dim - p0);
 #pragma unroll 4
-            for (int t = tid; t < pn; t += blockDim.x) xs[t] = x[p0 + t];
+            for (int t = tid; t < pn; t += 64 * W) xs[t] = x[p0 + t];
             __syncthreads();
             if (tid < 4) {
                 const int lim = min(p0 + pn, full);
@@ -371,12 +409,12 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
     // its 64 values (lane = row), one head of the cache row. Int8Rows.Append
     // (int8.go:36-55) with RoPE first (rope.go:69-81: value i < 32 pairs
     // with i + 32), bit for bit the separate append kernel.
-    int8_t *const j_aq = J->app_q;
-    float *const j_as = J->app_s;
-    const long long j_aqs = J->app_q_stride, j_ass = J->app_s_stride;
-    const int j_apos = j_aq ? J->app_pos[act] : -1;
-    const bool j_app = j_aq && j_apos >= 0 && j_apos < J->app_cap;
-    const CQ_GLOBAL float *j_acos = gptr(J->app_cos), *j_asin = gptr(J->app_sin);
+    int8_t *const j_aq = JOB(jr, int8_t *, app_q);
+    float *const j_as = JOB(jr, float *, app_s);
+    const long long j_aqs = JOB(jr, long long, app_q_stride), j_ass = JOB(jr, long long, app_s_stride);
+    const int j_apos = j_aq ? JOB(jr, const int32_t *, app_pos)[act] : -1;
+    const bool j_app = j_aq && j_apos >= 0 && j_apos < JOB(jr, int, app_cap);
+    const CQ_GLOBAL float *j_acos = gptr(JOB(jr, const float *, app_cos)), *j_asin = gptr(JOB(jr, const float *, app_sin));
     auto append_block = [&](int bb, int ln, float v) {
         const int r0 = (blk0 + bb) * 64 - j_row0;  // view row of the head's first value
         if (j_acos) {
@@ -521,7 +559,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
         }
         if (S > 1) {
             __syncthreads();
-            for (int t = tid; t < bc * 64; t += blockDim.x) {
+            for (int t = tid; t < bc * 64; t += 64 * W) {
                 const int bb = t >> 6, ln = t & 63;
                 float y = g0 == 0 ? 0.0f : yacc[t];
                 for (int gi = 0; gi < gch; ++gi) y = y + term[(static_cast<size_t>(gi) * tc + bb) * 64 + ln];
@@ -537,22 +575,25 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JobDesc *J, i
 
 template <int BITS, int GB, bool DEV>
 __global__ __launch_bounds__(256, (lut_waves_per_simd<BITS, GB>())) void lut_kernel(LutLaunch a) {
+    const int lane = threadIdx.x & 63;
     if constexpr (DEV) {  // a batch plan: one unit per workgroup
         const WorkUnit u = a.dunits[blockIdx.x];
-        lut_unit<BITS, GB>(a, a.djobs + u.job, u.blk, u.nb, u.act);
-    } else {
-        int j = 0;
-#pragma unroll
-        for (int k = 1; k < kKernargJobs; ++k)
-            if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.wg0[k]) j = k;
-        const JobDesc *J = &a.jobs[j];
-        const int b0 = (static_cast<int>(blockIdx.x) - a.wg0[j]) * a.bpw;
-        lut_unit<BITS, GB>(a, J, b0, min(a.bpw, J->nblk - b0), blockIdx.y);
+        lut_unit<BITS, GB>(a, JobPtr{a.djobs + u.job}, u.blk, u.nb, u.act, blockDim.x >> 6);
+    } else {  // job blockIdx.z: its address needs no load first
+        const JobRegs jr = job_regs(&a.jobs[blockIdx.z], lane);
+        const int bpw = a.bpw, gc = a.gc, tb = a.tb, bpw_max = a.bpw_max;
+        // the job and the launch's fields arrive in one round
+        asm volatile("" ::"v"(jr.d), "s"(bpw), "s"(gc), "s"(tb), "s"(bpw_max));
+        const int b0 = static_cast<int>(blockIdx.x) * bpw, nblk = JOB(jr, int, nblk);
+        if (b0 >= nblk) return;  // a shorter job's surplus workgroups, before any barrier
+        // kLutWaves wavefronts (blockDim.x would be one more kernel-argument load)
+        lut_unit<BITS, GB>(a, jr, b0, min(bpw, nblk - b0), blockIdx.y, kLutWaves);
     }
 }
 
 template <int BITS, int GB>
 hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, hipStream_t s) {
+    if (a.dunits == nullptr && waves != kLutWaves) return hipErrorInvalidValue;  // that path assumes kLutWaves
     const bool dev = a.dunits != nullptr;
     const void *fn = dev ? reinterpret_cast<const void *>(&lut_kernel<BITS, GB, true>)
                          : reinterpret_cast<const void *>(&lut_kernel<BITS, GB, false>);
@@ -565,7 +606,7 @@ hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, h
     if (dev)
         hipLaunchKernelGGL((lut_kernel<BITS, GB, true>), dim3(gx), dim3(64 * waves), lds, s, a);
     else
-        hipLaunchKernelGGL((lut_kernel<BITS, GB, false>), dim3(gx, gy), dim3(64 * waves), lds, s, a);
+        hipLaunchKernelGGL((lut_kernel<BITS, GB, false>), dim3(gx, gy, a.njobs), dim3(64 * waves), lds, s, a);
     return hipGetLastError();
 }
 
