@@ -308,6 +308,20 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
         while (a.gc * 2 <= groups_max && 2 * a.gc * 2 * s0.group_bytes * 16 * static_cast<int>(sizeof(short)) <= 32 * 1024)
             a.gc *= 2;
     a.bpw_max = a.bpw;
+    // Latency-bound launches of one-block units (batch-1 decode) take the
+    // wide form: a wavefront per group of the chunk (up to 16), or two per
+    // group when the chunk has fewer than 8, so the lookups of one unit
+    // spread over more SIMDs.
+    a.waves = kLutWaves;
+    a.vsplit = 1;
+    if (units * rows * 4 <= device_info().cus && a.bpw == 1 && (s0.group_bytes == 32 || s0.group_bytes == 64)) {
+        if (a.gc >= 8) {
+            a.waves = std::min(16, a.gc);
+        } else if (a.gc >= 2) {
+            a.waves = 2 * a.gc;
+            a.vsplit = 2;
+        }
+    }
     const size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, a.gc, a.tb, a.bpw);
     for (int r0 = 0; r0 < rows; r0 += 65535) {
         LutLaunch b = a;
@@ -322,7 +336,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
                 b.jobs[k].app_pos += r0;
             }
         }
-        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, kLutWaves, wg, nr, lds, stream), "lut launch");
+        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, a.waves, wg, nr, lds, stream), "lut launch");
     }
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;

@@ -116,6 +116,8 @@ struct LutLaunch {
     int tb;                      // blocks of the lut kernel's term buffer (>= W / 2)
     int gc;                      // groups per LDS chunk
     int bpw_max;                 // LDS sizing: most blocks of any workgroup
+    int waves;                   // kernel-argument path: wavefronts per workgroup (> kLutWaves: the wide form)
+    int vsplit;                  // wide form: wavefronts per group (1 or 2)
 };
 
 size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw);

@@ -318,10 +318,15 @@ struct JobPtr {
 
 // One work unit: blocks [b0, b0 + bc) of job jr (counted from its blk0) for
 // activation act.
-template <int BITS, int GB, class JS>
+// V = 2 (wide launches of one-block units): two wavefronts share each group
+// of the block, one half of its index units each; their exact int32 sums
+// meet in LDS before the float term.
+template <int BITS, int GB, class JS, int V = 1>
 __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b0, int bc, int act, int W) {
     using Gm = LutGeo<BITS, GB>;
     constexpr int U = Gm::U, UPG = Gm::UPG, NT = Gm::NT;
+    static_assert(UPG % V == 0, "a group's units split evenly");
+    constexpr int UPGV = UPG / V;  // index units per item of one wavefront
     constexpr int DG = lut_loads_ahead<BITS, GB>();  // groups of index loads in flight per wavefront
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -456,12 +461,18 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     // block (groups gs, gs + S, ...), their terms meet in LDS and one pass
     // folds them in group order.
     int S = 1;
-    while (S * 2 * bc <= W) S *= 2;
+    if constexpr (V == 1) {
+        while (S * 2 * bc <= W) S *= 2;
+    } else {
+        S = W / V;  // one block: wavefront w takes half w % V of groups w / V, w / V + S, ...
+    }
+    const int vp = V == 1 ? 0 : w % V;  // this wavefront's half of each group's units
 
     for (int g0 = 0; g0 < groups; g0 += gc) {
         const int gch = min(gc, groups - g0);
         const bool last = g0 + gch >= groups;
-        const int bbs = w / S, gs = w - (w / S) * S;
+        const int wv = w / V;  // V = 1: w
+        const int bbs = wv / S, gs = wv - (wv / S) * S;
         int Q;
         if (S == 1)
             Q = w < bc ? ((bc - w + W - 1) / W) * gch : 0;
@@ -484,21 +495,22 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
             }
         };
         const Pos first = S == 1 ? Pos{w, 0} : Pos{bbs, gs};
-        uint32_t buf[DG][UPG][4];
+        uint32_t buf[DG][UPGV][4];
         uint32_t nv[DG];
         // Loads past the wavefront's last item read one 16-byte line of the
         // activation row instead (kept in L2 by the tables' reads of it): the
         // stream issues the same loads every turn, so each of its waits is a
         // fixed count, and no index byte is fetched twice.
         const CQ_GLOBAL uint8_t *spare = (const CQ_GLOBAL uint8_t *)(reinterpret_cast<uintptr_t>(x) & ~uintptr_t(15));
-        auto load_group = [&](const Pos &p, bool real, uint32_t (&bf)[UPG][4], uint32_t &nrm) {
+        auto load_group = [&](const Pos &p, bool real, uint32_t (&bf)[UPGV][4], uint32_t &nrm) {
             const CQ_GLOBAL uint8_t *ip =
-                real ? idx + (static_cast<size_t>(blk0 + p.bb) * units + static_cast<size_t>(g0 + p.gi) * UPG) * 64 * U +
+                real ? idx + (static_cast<size_t>(blk0 + p.bb) * units + static_cast<size_t>(g0 + p.gi) * UPG +
+                              static_cast<size_t>(vp) * UPGV) * 64 * U +
                            static_cast<size_t>(lane) * U
                      : spare;
             const size_t ustride = real ? static_cast<size_t>(64) * U : 0;
 #pragma unroll
-            for (int u = 0; u < UPG; ++u) load_unit<U>(ip + u * ustride, bf[u]);
+            for (int u = 0; u < UPGV; ++u) load_unit<U>(ip + u * ustride, bf[u]);
             const CQ_GLOBAL uint16_t *np =
                 real ? j_norm + (static_cast<size_t>(blk0 + p.bb) * groups + g0 + p.gi) * 64 + lane
                      : (const CQ_GLOBAL uint16_t *)spare;
@@ -507,7 +519,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
         // The first items are in flight while the tables are built.
         Pos lp = first;
         int lq = 0;  // items loaded
-        auto refill = [&](uint32_t (&bf)[UPG][4], uint32_t &nrm) {
+        auto refill = [&](uint32_t (&bf)[UPGV][4], uint32_t &nrm) {
             load_group(lp, lq < Q, bf, nrm);
             if (lq < Q) next(lp);
             ++lq;
@@ -536,9 +548,18 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
                     const uint32_t tg = lds_addr(tab + static_cast<size_t>(gi) * NT * 16);
                     int s = 0;
 #pragma unroll
-                    for (int u = 0; u < UPG; ++u) s += lookup_unit<U>(buf[d][u], tg + u * 2 * U * 16 * 2);
+                    for (int u = 0; u < UPGV; ++u)
+                        s += lookup_unit<U>(buf[d][u], tg + (vp * UPGV + u) * 2 * U * 16 * 2);
                     const float n = __half2float(__ushort_as_half(static_cast<unsigned short>(nv[d])));
                     const float coef = n * steps[gi];
+                    if constexpr (V > 1) {  // [gi][half][lane] int32 sums, then [gi][lane] coefficients
+                        int *termi = reinterpret_cast<int *>(term);
+                        termi[(gi * V + vp) * 64 + lane] = s;
+                        if (vp == 0) term[gc * V * 64 + gi * 64 + lane] = coef;
+                        next(cp);
+                        refill(buf[d], nv[d]);
+                        continue;
+                    }
                     const float t = static_cast<float>(s) * coef;
                     if (S == 1) {
                         if (gi == 0) acc = g0 == 0 ? 0.0f : yacc[bb * 64 + lane];
@@ -557,7 +578,24 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
                 refill(buf[d], nv[d]);
             }
         }
-        if (S > 1) {
+        if (V > 1) {  // one block: the halves' sums added (exact), then the unfused fold in group order
+            __syncthreads();
+            if (tid < 64) {
+                const int *termi = reinterpret_cast<const int *>(term);
+                float y = g0 == 0 ? 0.0f : yacc[tid];
+                for (int gi = 0; gi < gch; ++gi) {
+                    int sum = 0;
+#pragma unroll
+                    for (int h = 0; h < V; ++h) sum += termi[(gi * V + h) * 64 + tid];
+                    const float t = static_cast<float>(sum) * term[gc * V * 64 + gi * 64 + tid];
+                    y = y + t;
+                }
+                if (last)
+                    write_out(0, tid, y);
+                else
+                    yacc[tid] = y;
+            }
+        } else if (S > 1) {
             __syncthreads();
             for (int t = tid; t < bc * 64; t += 64 * W) {
                 const int bb = t >> 6, ln = t & 63;
@@ -591,8 +629,42 @@ __global__ __launch_bounds__(256, (lut_waves_per_simd<BITS, GB>())) void lut_ker
     }
 }
 
+// Latency-bound launches of one-block units (the decode step at batch 1):
+// a.waves wavefronts per workgroup, one per group (V = 1), or two per group
+// each on half its index units (V = 2), so that each wavefront's chain of
+// table lookups is shorter.
+template <int BITS, int GB, int V>
+__global__ __launch_bounds__(1024) void lut_kernel_wide(LutLaunch a) {
+    const int lane = threadIdx.x & 63;
+    const JobRegs jr = job_regs(&a.jobs[blockIdx.z], lane);
+    const int bpw = a.bpw, gc = a.gc, tb = a.tb, bpw_max = a.bpw_max, waves = a.waves;
+    asm volatile("" ::"v"(jr.d), "s"(bpw), "s"(gc), "s"(tb), "s"(bpw_max), "s"(waves));
+    const int b0 = static_cast<int>(blockIdx.x) * bpw, nblk = JOB(jr, int, nblk);
+    if (b0 >= nblk) return;
+    lut_unit<BITS, GB, JobRegs, V>(a, jr, b0, min(bpw, nblk - b0), blockIdx.y, waves);
+}
+
+template <int BITS, int GB, int V>
+hipError_t launch_wide(const LutLaunch &a, int gx, int gy, size_t lds, hipStream_t s) {
+    static bool attr = false;  // idempotent attribute write; a race is benign
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_kernel_wide<BITS, GB, V>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((lut_kernel_wide<BITS, GB, V>), dim3(gx, gy, a.njobs), dim3(64 * a.waves), lds, s, a);
+    return hipGetLastError();
+}
+
 template <int BITS, int GB>
 hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, hipStream_t s) {
+    if constexpr (GB == 32 || GB == 64) {
+        if (a.dunits == nullptr && a.waves > kLutWaves) {
+            if (a.waves != waves || a.waves > 16 || a.bpw != 1) return hipErrorInvalidValue;
+            return a.vsplit == 2 ? launch_wide<BITS, GB, 2>(a, gx, gy, lds, s) : launch_wide<BITS, GB, 1>(a, gx, gy, lds, s);
+        }
+    }
     if (a.dunits == nullptr && waves != kLutWaves) return hipErrorInvalidValue;  // that path assumes kLutWaves
     const bool dev = a.dunits != nullptr;
     const void *fn = dev ? reinterpret_cast<const void *>(&lut_kernel<BITS, GB, true>)

@@ -55,6 +55,25 @@ def test_lut_gemv_sweep_bit_exact(shape, bits):
         assert same_bits(got, want), first_diff(got, want)
 
 
+@pytest.mark.parametrize("out,inp,bits", [(300, 4096, 4), (200, 4096, 2), (130, 384, 4), (130, 256, 2),
+                                          (512, 2048, 4)])
+def test_batch1_wide_units(out, inp, bits):
+    """Few activations of a small matrix take the lut kernel's wide form (a
+    wavefront per group, or two per group on half its units each, up to 16
+    per workgroup); wide rows also run several chunks of groups. Bit for
+    bit the oracle, also for views that cut blocks."""
+    print(f"wide lut units {out}x{inp} CQ{bits}", flush=True)
+    g = synth.rng(2000 + out + inp + bits)
+    p = synth.random_packed(g, out, inp, 128, bits, sigma=0.05)
+    m, o = cq.New(p), orc.OMatrix.new(p)
+    for rows in (1, 2):
+        x = synth.activations(g, rows, inp)
+        got, want = gemm(m, x, rows), o.gemm(x, rows, orc.LUT)
+        assert same_bits(got, want), (rows, first_diff(got, want))
+        got = gemm(m.Rows(5, 69), x, rows)
+        assert same_bits(got, o.rows(5, 69).gemm(x, rows, orc.LUT)), rows
+
+
 @pytest.mark.parametrize("shape", TEST_SHAPES)
 @pytest.mark.parametrize("bits", [2, 4])
 def test_small_shapes_all_kernels_bit_exact(shape, bits):
