@@ -1112,6 +1112,45 @@ int nd_add_dev(float *x, const float *y, long long n, void *stream) {
     return CQ_OK;
 }
 
+int nd_hadamard_mlp_dev(float *out, const float *x, int rows, int dim, int na, int nb, int rank,
+                        const float *const *vecs, const float *const *factors, const float *cond_v,
+                        const float *cond_u, const int32_t *p1, const int32_t *p2, void *stream) {
+    if (rows < 0 || !hadamard_shape_ok(na, nb, dim, rank))
+        return fail(CQ_ERR_MISUSE, "needle: HadamardMLP of %d rows, width %d in %d x %d blocks, rank %d", rows, dim, na,
+                    nb, rank);
+    if (rows == 0) return CQ_OK;
+    if (!out || !x || !vecs || !factors || !cond_v || !cond_u || !p1 || !p2)
+        return fail(CQ_ERR_MISUSE, "needle: HadamardMLP with a missing array");
+    for (int k = 0; k < 5; ++k)
+        if (!vecs[k]) return fail(CQ_ERR_MISUSE, "needle: HadamardMLP without vector %d", k);
+    for (int k = 0; k < 6; ++k)
+        if (!factors[k]) return fail(CQ_ERR_MISUSE, "needle: HadamardMLP without factor %d", k);
+    HadaArgs h;
+    h.out = out;
+    h.x = x;
+    h.dim = dim;
+    h.na = na;
+    h.nb = nb;
+    h.rank = rank;
+    h.d1 = vecs[0];
+    h.d2 = vecs[1];
+    h.b2 = vecs[2];
+    h.d3 = vecs[3];
+    h.d4 = vecs[4];
+    h.w1a = factors[0];
+    h.w1b = factors[1];
+    h.w2a = factors[2];
+    h.w2b = factors[3];
+    h.w3a = factors[4];
+    h.w3b = factors[5];
+    h.cond_v = cond_v;
+    h.cond_u = cond_u;
+    h.p1 = p1;
+    h.p2 = p2;
+    HIP_TRY(launch_hadamard_mlp(h, rows, static_cast<hipStream_t>(stream)), "HadamardMLP launch");
+    return CQ_OK;
+}
+
 int nd_sigmoid_gate_dev(float *out, float *gate, long long n, void *stream) {
     if (n < 0) return fail(CQ_ERR_MISUSE, "needle: gate of %lld values", n);
     HIP_TRY(launch_sigmoid_gate(out, gate, n, static_cast<hipStream_t>(stream)), "gate launch");

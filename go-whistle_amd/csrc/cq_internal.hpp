@@ -178,6 +178,21 @@ struct AttendArgs {
 };
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream);
 
+// HadamardMLP, Whistle's Monarch FFN (hadamard_kernels.hip): rows of dim
+// values in x and out, n = na * nb >= dim, factors row-major (na x na,
+// nb x nb), cond_v dim x rank, cond_u rank x n, permutations p1, p2 of n.
+struct HadaArgs {
+    float *out;
+    const float *x;
+    int dim, na, nb, rank;
+    const float *d1, *d2, *b2, *d3, *d4;
+    const float *w1a, *w1b, *w2a, *w2b, *w3a, *w3b;
+    const float *cond_v, *cond_u;
+    const int32_t *p1, *p2;
+};
+hipError_t launch_hadamard_mlp(const HadaArgs &h, int rows, hipStream_t s);
+bool hadamard_shape_ok(int na, int nb, int dim, int rank);
+
 // decode-step float blocks (step_kernels.hip)
 hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int rows, int dim, hipStream_t s);
 hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,

@@ -1,0 +1,140 @@
+// gfx950 HadamardMLP: Whistle's Monarch FFN (internal/needle/hadamard.go:
+// 12-24, 172-310), one workgroup per row, one thread per element of the
+// n = na * nb mix, float32 throughout as the reference computes it:
+//
+//   cond = 1 + softmax(x @ cond_v) @ cond_u
+//   z1   = kron(d1 * x; w1a, w1b)[p1]
+//   z2   = kron(silu(d2 * cond * z1 + b2); w2a, w2b)[p2]
+//   out  = d4 * kron(d3 * z2; w3a, w3b)
+//
+// kron(z; a, b) = a^T Z b with Z = z as na x nb (kronApply, hadamard.go:
+// 296-310), as two small products through LDS: Y = Z b (each thread one
+// element, a dot of nb), then a^T Y (a dot of na), gathered through the
+// stage's permutation. x is zero-padded from the model width dim to n and
+// the output cut back to dim. The reference's GEMMs (algo-tensor, absent)
+// sum in an order of their own, so the result is held to the reference
+// test's bar: within 1e-5 of the float64 form (hadamard_test.go:152-191).
+#include "cq_internal.hpp"
+#include "cq_device.hpp"
+
+namespace cqhip {
+namespace {
+
+constexpr int kHadaMaxN = 1024;
+constexpr int kHadaMaxRank = 32;
+
+// out[c] = (a^T Z b)[c] for c = tid < n, Z in zs; ys is scratch of n.
+__device__ __forceinline__ float kron_elem(const float *zs, float *ys, const float *a, const float *b, int na,
+                                           int nb, int tid, int n) {
+    if (tid < n) {
+        const int i = tid / nb, l = tid - i * nb;  // Y[i][l] = sum_j Z[i][j] b[j][l]
+        float y = 0.0f;
+        for (int j = 0; j < nb; ++j) {
+            const float p = zs[i * nb + j] * b[j * nb + l];
+            y = y + p;
+        }
+        ys[tid] = y;
+    }
+    __syncthreads();
+    float o = 0.0f;
+    if (tid < n) {
+        const int k = tid / nb, l = tid - k * nb;  // out[k][l] = sum_i a[i][k] Y[i][l]
+        for (int i = 0; i < na; ++i) {
+            const float p = a[i * na + k] * ys[i * nb + l];
+            o = o + p;
+        }
+    }
+    __syncthreads();
+    return o;
+}
+
+__global__ __launch_bounds__(kHadaMaxN) void hadamard_mlp_kernel(HadaArgs h) {
+    __shared__ float zs[kHadaMaxN], ys[kHadaMaxN], ks[kHadaMaxN];
+    __shared__ float part[kHadaMaxN / 64][kHadaMaxRank];
+    __shared__ float prob[kHadaMaxRank];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int n = h.na * h.nb, dim = h.dim, rank = h.rank;
+    const float *x = h.x + static_cast<long long>(blockIdx.x) * dim;
+    float *out = h.out + static_cast<long long>(blockIdx.x) * dim;
+
+    // The conditioning logits x @ cond_v (linear, hadamard.go:176-177): per
+    // wavefront partial sums of its 64 inputs, reduced across lanes, then
+    // across wavefronts.
+    const float xv = tid < dim ? x[tid] : 0.0f;
+    for (int r = 0; r < rank; ++r) {
+        float v = tid < dim ? xv * h.cond_v[static_cast<long long>(tid) * rank + r] : 0.0f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off);
+        if (lane == 0) part[wave][r] = v;
+    }
+    __syncthreads();
+    if (tid == 0) {  // softmax over the rank logits (in LDS: no private array)
+        float m = -INFINITY;
+        for (int r = 0; r < rank; ++r) {
+            float s = 0.0f;
+            for (int w = 0; w < nw; ++w) s = s + part[w][r];
+            prob[r] = s;
+            m = fmaxf(m, s);
+        }
+        float sum = 0.0f;
+        for (int r = 0; r < rank; ++r) {
+            prob[r] = expf(prob[r] - m);
+            sum = sum + prob[r];
+        }
+        for (int r = 0; r < rank; ++r) prob[r] = prob[r] / sum;
+    }
+    __syncthreads();
+    float cond = 1.0f;  // 1 + softmax @ cond_u
+    if (tid < n) {
+        float c = 0.0f;
+        for (int r = 0; r < rank; ++r) {
+            const float p = prob[r] * h.cond_u[static_cast<long long>(r) * n + tid];
+            c = c + p;
+        }
+        cond = c + 1.0f;
+    }
+
+    // z1 = kron(d1 * x; w1)[p1]
+    if (tid < n) zs[tid] = tid < dim ? h.d1[tid] * xv : 0.0f;
+    __syncthreads();
+    float k = kron_elem(zs, ys, h.w1a, h.w1b, h.na, h.nb, tid, n);
+    if (tid < n) ks[tid] = k;
+    __syncthreads();
+    // z2 = kron(silu(d2 * cond * z1 + b2); w2)[p2], sigma as jax.nn.sigmoid
+    if (tid < n) {
+        const int q = h.p1[tid];
+        const float z1 = ks[static_cast<unsigned>(q) < static_cast<unsigned>(n) ? q : 0];  // a permutation of n
+        const float t1 = h.d2[tid] * cond;
+        const float a = t1 * z1 + h.b2[tid];
+        zs[tid] = a * gate_sigmoid(a);
+    }
+    __syncthreads();
+    k = kron_elem(zs, ys, h.w2a, h.w2b, h.na, h.nb, tid, n);
+    if (tid < n) ks[tid] = k;
+    __syncthreads();
+    // out = d4 * kron(d3 * z2; w3)
+    if (tid < n) {
+        const int q = h.p2[tid];
+        zs[tid] = h.d3[tid] * ks[static_cast<unsigned>(q) < static_cast<unsigned>(n) ? q : 0];
+    }
+    __syncthreads();
+    k = kron_elem(zs, ys, h.w3a, h.w3b, h.na, h.nb, tid, n);
+    if (tid < dim) out[tid] = h.d4[tid] * k;
+}
+
+}  // namespace
+
+hipError_t launch_hadamard_mlp(const HadaArgs &h, int rows, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    const int n = h.na * h.nb;
+    const int threads = (n + 63) / 64 * 64;
+    hipLaunchKernelGGL(hadamard_mlp_kernel, dim3(static_cast<unsigned>(rows)), dim3(threads), 0, s, h);
+    return hipGetLastError();
+}
+
+bool hadamard_shape_ok(int na, int nb, int dim, int rank) {
+    const long long n = static_cast<long long>(na) * nb;
+    return na > 0 && nb > 0 && n <= kHadaMaxN && dim > 0 && dim <= n && rank > 0 && rank <= kHadaMaxRank;
+}
+
+}  // namespace cqhip

@@ -90,6 +90,37 @@ def sigmoid_gate_dev(out, gate, n):
     check(lib().nd_sigmoid_gate_dev(c_void_p(out.data_ptr()), c_void_p(gate.data_ptr()), n, _stream()))
 
 
+class HadamardMLP:
+    """HadamardMLP (internal/needle/hadamard.go:12-24, 172-310), Whistle's
+    Monarch FFN, with its weights on the device: w holds d1, d2, b2, d3, d4,
+    w1a..w3b (square factors), cond_v (dim x rank), cond_u (rank x n) and the
+    permutations p1, p2 (hada_p1/p2). forward_dev(out, x, rows) runs
+    nd_hadamard_mlp_dev on device tensors of rows x dim."""
+
+    def __init__(self, w, device="cuda"):
+        import torch
+
+        f32 = lambda a: torch.as_tensor(np.ascontiguousarray(a, np.float32), device=device)
+        self.na, self.nb = int(np.shape(w["w1a"])[0]), int(np.shape(w["w1b"])[0])
+        self.dim, self.rank = int(np.shape(w["cond_v"])[0]), int(np.shape(w["cond_v"])[1])
+        self._vecs = [f32(w[k]) for k in ("d1", "d2", "b2", "d3", "d4")]
+        self._facs = [f32(w[f"w{s}{h}"]) for s in (1, 2, 3) for h in ("a", "b")]
+        self._cv, self._cu = f32(w["cond_v"]), f32(w["cond_u"])
+        self._p = [torch.as_tensor(np.ascontiguousarray(w[k], np.int32), device=device) for k in ("p1", "p2")]
+        n = self.na * self.nb
+        for k in ("p1", "p2"):
+            if sorted(np.asarray(w[k]).tolist()) != list(range(n)):
+                raise CQPanic(f"needle: {k} is not a permutation of {n}")
+
+    def forward_dev(self, out, x, rows):
+        vp = (c_void_p * 5)(*[t.data_ptr() for t in self._vecs])
+        fp_ = (c_void_p * 6)(*[t.data_ptr() for t in self._facs])
+        check(lib().nd_hadamard_mlp_dev(c_void_p(out.data_ptr()), c_void_p(x.data_ptr()), rows, self.dim, self.na,
+                                        self.nb, self.rank, vp, fp_, c_void_p(self._cv.data_ptr()),
+                                        c_void_p(self._cu.data_ptr()), c_void_p(self._p[0].data_ptr()),
+                                        c_void_p(self._p[1].data_ptr()), _stream()))
+
+
 class Linear:
     """needle.Linear over a packed matrix (internal/needle/linear.go:11-145),
     on device tensors: x rows × In -> dst rows × Out. With WithInt8Input the

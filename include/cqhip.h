@@ -250,6 +250,20 @@ int nd_silu_dev(float *x, long long n, void *stream);
 int nd_fake_quant_dev(float *dst, const float *x, long long rows, int cols, int width, void *stream);
 /* x += y elementwise (the residual adds). */
 int nd_add_dev(float *x, const float *y, long long n, void *stream);
+/* HadamardMLP.Forward (internal/needle/hadamard.go:172-294), Whistle's
+ * Monarch FFN, on rows of dim values: cond = 1 + softmax(x cond_v) cond_u;
+ * z1 = kron(d1 x; w1a, w1b)[p1]; z2 = kron(silu(d2 cond z1 + b2); w2a,
+ * w2b)[p2]; out = d4 kron(d3 z2; w3a, w3b), kron(z; a, b) = a^T Z b with Z
+ * the na x nb matrix of z (kronApply, hadamard.go:296-310); x zero-padded
+ * to n = na * nb >= dim, out cut back to dim (LoadHadamardMLP's padding,
+ * hadamard.go:19-24). vecs = {d1, d2, b2, d3, d4} (n each), factors =
+ * {w1a, w1b, w2a, w2b, w3a, w3b} row-major, cond_v dim x rank, cond_u
+ * rank x n, p1 and p2 permutations of n (hada_p1/p2). n <= 1024, rank <= 32.
+ * Float32, within 1e-5 of the float64 form (hadamard_test.go:152-191); the
+ * reference's GEMMs sum in their library's own order. */
+int nd_hadamard_mlp_dev(float *out, const float *x, int rows, int dim, int na, int nb, int rank,
+                        const float *const *vecs, const float *const *factors, const float *cond_v,
+                        const float *cond_u, const int32_t *p1, const int32_t *p2, void *stream);
 /* The attention's output gate (internal/needle/attention.go:245-249):
  * gate[i] = sigmoid(gate[i]), out[i] *= gate[i], sigmoid being jax.nn.sigmoid
  * in float32 as the reference writes it, float32(1 / (1 + exp(-float64(x))))
