@@ -1151,6 +1151,55 @@ int nd_hadamard_mlp_dev(float *out, const float *x, int rows, int dim, int na, i
     return CQ_OK;
 }
 
+int nd_rms_unit_dev(float *dst, const float *x, int rows, int dim, void *stream) {
+    if (rows < 0 || dim <= 0) return fail(CQ_ERR_MISUSE, "needle: RMSUnit of %d rows of %d", rows, dim);
+    HIP_TRY(launch_rms_unit(dst, x, rows, dim, static_cast<hipStream_t>(stream)), "RMSUnit launch");
+    return CQ_OK;
+}
+
+int nd_mhc_heads_dev(float *h_pre, float *h_post, float *h_res, float *u, const float *pre_logits,
+                     const float *post_logits, const float *res_logits, const float *stream_rows, int rows, int lanes,
+                     int dim, const float *affine, void *stream) {
+    if (rows < 0 || !mhc_shape_ok(lanes, dim))
+        return fail(CQ_ERR_MISUSE, "needle: mHC heads of %d rows, %d lanes of %d", rows, lanes, dim);
+    if (rows == 0) return CQ_OK;
+    MhcArgs m;
+    std::memset(&m, 0, sizeof m);
+    m.h_pre = h_pre;
+    m.h_post = h_post;
+    m.h_res = h_res;
+    m.u = u;
+    m.pre_logits = pre_logits;
+    m.post_logits = post_logits;
+    m.res_logits = res_logits;
+    m.stream = stream_rows;
+    m.affine = affine;
+    m.lanes = lanes;
+    m.dim = dim;
+    HIP_TRY(launch_mhc_heads(m, rows, static_cast<hipStream_t>(stream)), "mHC heads launch");
+    return CQ_OK;
+}
+
+int nd_mhc_mix_dev(float *out, const float *stream_rows, const float *h_res, const float *h_post,
+                   const float *block_out, const float *u, int rows, int lanes, int dim, void *stream) {
+    if (rows < 0 || !mhc_shape_ok(lanes, dim))
+        return fail(CQ_ERR_MISUSE, "needle: mHC mix of %d rows, %d lanes of %d", rows, lanes, dim);
+    if (rows == 0) return CQ_OK;
+    if (out == stream_rows) return fail(CQ_ERR_MISUSE, "needle: mHC mix in place");
+    MhcArgs m;
+    std::memset(&m, 0, sizeof m);
+    m.out = out;
+    m.stream = stream_rows;
+    m.h_res = const_cast<float *>(h_res);
+    m.h_post = const_cast<float *>(h_post);
+    m.block_out = block_out;
+    m.u = const_cast<float *>(u);
+    m.lanes = lanes;
+    m.dim = dim;
+    HIP_TRY(launch_mhc_mix(m, rows, static_cast<hipStream_t>(stream)), "mHC mix launch");
+    return CQ_OK;
+}
+
 int nd_sigmoid_gate_dev(float *out, float *gate, long long n, void *stream) {
     if (n < 0) return fail(CQ_ERR_MISUSE, "needle: gate of %lld values", n);
     HIP_TRY(launch_sigmoid_gate(out, gate, n, static_cast<hipStream_t>(stream)), "gate launch");

@@ -193,6 +193,19 @@ struct HadaArgs {
 hipError_t launch_hadamard_mlp(const HadaArgs &h, int rows, hipStream_t s);
 bool hadamard_shape_ok(int na, int nb, int dim, int rank);
 
+// Manifold hyper-connections around a block (mhc_kernels.hip): streams of
+// rows x lanes x dim, heads rows x lanes (h_res rows x lanes x lanes),
+// u / block_out rows x dim.
+struct MhcArgs {
+    float *h_pre, *h_post, *h_res, *u, *out;
+    const float *pre_logits, *post_logits, *res_logits, *stream, *block_out, *affine;
+    int lanes, dim;
+};
+bool mhc_shape_ok(int lanes, int dim);
+hipError_t launch_rms_unit(float *dst, const float *x, int rows, int dim, hipStream_t s);
+hipError_t launch_mhc_heads(const MhcArgs &m, int rows, hipStream_t s);
+hipError_t launch_mhc_mix(const MhcArgs &m, int rows, hipStream_t s);
+
 // decode-step float blocks (step_kernels.hip)
 hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int rows, int dim, hipStream_t s);
 hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,

@@ -90,6 +90,26 @@ def sigmoid_gate_dev(out, gate, n):
     check(lib().nd_sigmoid_gate_dev(c_void_p(out.data_ptr()), c_void_p(gate.data_ptr()), n, _stream()))
 
 
+def rms_unit_dev(dst, x, rows, dim):
+    """RMSUnit (norm.go:68-81) on device rows."""
+    check(lib().nd_rms_unit_dev(c_void_p(dst.data_ptr()), c_void_p(x.data_ptr()), rows, dim, _stream()))
+
+
+def mhc_heads_dev(h_pre, h_post, h_res, u, pre_logits, post_logits, res_logits, stream, rows, lanes, dim,
+                  affine=None):
+    """MHC.forward's heads and block input from the φ logits (mhc.go:204-263)."""
+    p = lambda t: c_void_p(t.data_ptr()) if t is not None else None
+    check(lib().nd_mhc_heads_dev(p(h_pre), p(h_post), p(h_res), p(u), p(pre_logits), p(post_logits), p(res_logits),
+                                 p(stream), rows, lanes, dim, p(affine), _stream()))
+
+
+def mhc_mix_dev(out, stream, h_res, h_post, block_out, u, rows, lanes, dim):
+    """MHC.forward's output stream (mhc.go:229-299)."""
+    p = lambda t: c_void_p(t.data_ptr())
+    check(lib().nd_mhc_mix_dev(p(out), p(stream), p(h_res), p(h_post), p(block_out), p(u), rows, lanes, dim,
+                               _stream()))
+
+
 class HadamardMLP:
     """HadamardMLP (internal/needle/hadamard.go:12-24, 172-310), Whistle's
     Monarch FFN, with its weights on the device: w holds d1, d2, b2, d3, d4,

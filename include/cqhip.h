@@ -264,6 +264,26 @@ int nd_add_dev(float *x, const float *y, long long n, void *stream);
 int nd_hadamard_mlp_dev(float *out, const float *x, int rows, int dim, int na, int nb, int rank,
                         const float *const *vecs, const float *const *factors, const float *cond_v,
                         const float *cond_u, const int32_t *p1, const int32_t *p2, void *stream);
+/* RMSUnit (internal/needle/norm.go:68-81): each row of dim times
+ * float32(1 / sqrt(float64(meanSquare + 1e-6))), meanSquare in float64 as
+ * ZCRMSNorm's; mHC's nx of the lane stream (rows of lanes * dim). */
+int nd_rms_unit_dev(float *dst, const float *x, int rows, int dim, void *stream);
+/* MHC.forward's heads and block input (internal/needle/mhc.go:204-219,
+ * 246-263) from the φ products' logits (rows x lanes, rows x lanes x
+ * lanes): with affine non-null (device floats {a_pre, a_post, a_res,
+ * b_pre[lanes], pre_off[lanes], b_post[lanes], post_off[lanes],
+ * b_res[lanes^2]}) the logits are first a * logit + b (+ off) as MHC.logits
+ * rounds them; h_pre = sigmoid, h_post = 2 sigmoid, h_res = sinkhorn of 20
+ * iterations (mhc.go:301-417), u[i] = sum_k h_pre[k] stream[i, k] in k
+ * order (stream rows x lanes x dim, u rows x dim). lanes <= 8. */
+int nd_mhc_heads_dev(float *h_pre, float *h_post, float *h_res, float *u, const float *pre_logits,
+                     const float *post_logits, const float *res_logits, const float *stream_rows, int rows, int lanes,
+                     int dim, const float *affine, void *stream);
+/* MHC.forward's output (internal/needle/mhc.go:229-234, 266-299): y =
+ * block_out - u, out[i, a] = sum_b h_res[i, a, b] stream[i, b] (b in order)
+ * + h_post[i, a] y. out must not be the stream. */
+int nd_mhc_mix_dev(float *out, const float *stream_rows, const float *h_res, const float *h_post,
+                   const float *block_out, const float *u, int rows, int lanes, int dim, void *stream);
 /* The attention's output gate (internal/needle/attention.go:245-249):
  * gate[i] = sigmoid(gate[i]), out[i] *= gate[i], sigmoid being jax.nn.sigmoid
  * in float32 as the reference writes it, float32(1 / (1 + exp(-float64(x))))

@@ -77,6 +77,10 @@ def lib():
             "orc_exp64": (ctypes.c_double, [ctypes.c_double]),
             "orc_gate_sigmoid": (c_float, [c_float]),
             "orc_sigmoid_gate": (None, [POINTER(c_float), POINTER(c_float), ctypes.c_long]),
+            "orc_rms_unit": (None, [POINTER(c_float), POINTER(c_float), c_int, c_int]),
+            "orc_sinkhorn": (None, [POINTER(c_float), c_int, c_int]),
+            "orc_mhc_heads": (None, [POINTER(c_float)] * 8 + [c_int, c_int, c_int, c_void_p]),
+            "orc_mhc_mix": (None, [POINTER(c_float)] * 6 + [c_int, c_int, c_int]),
             "orc_attend_int8_spans": (c_int, [POINTER(c_float), POINTER(c_float), c_int, c_int, POINTER(c_int8),
                                               POINTER(c_float), c_int, c_int, POINTER(c_int8), POINTER(c_float), c_int,
                                               c_int, c_int, POINTER(c_int32), c_float, c_int, c_int, POINTER(c_float)]),
@@ -353,3 +357,35 @@ def sigmoid_gate(out, gate):
     assert out.size == gate.size
     lib().orc_sigmoid_gate(fp(out), fp(gate), out.size)
     return out, gate
+
+
+def rms_unit(x, rows, dim):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(rows * dim, np.float32)
+    lib().orc_rms_unit(fp(out), fp(x), rows, dim)
+    return out
+
+
+def sinkhorn(k, n, iters=20):
+    k = np.array(k, dtype=np.float32)
+    lib().orc_sinkhorn(fp(k), n, iters)
+    return k
+
+
+def mhc_heads(pre_l, post_l, res_l, stream, rows, n, dim, affine=None):
+    """(h_pre, h_post, h_res, u) of MHC.forward from the φ logits."""
+    c = lambda a: np.ascontiguousarray(a, np.float32)
+    pre_l, post_l, res_l, stream = c(pre_l), c(post_l), c(res_l), c(stream)
+    hp, hq = np.zeros(rows * n, np.float32), np.zeros(rows * n, np.float32)
+    hr, u = np.zeros(rows * n * n, np.float32), np.zeros(rows * dim, np.float32)
+    aff = c(affine) if affine is not None else None
+    lib().orc_mhc_heads(fp(hp), fp(hq), fp(hr), fp(u), fp(pre_l), fp(post_l), fp(res_l), fp(stream), rows, n, dim,
+                        aff.ctypes.data if aff is not None else None)
+    return hp, hq, hr, u
+
+
+def mhc_mix(stream, h_res, h_post, block_out, u, rows, n, dim):
+    c = lambda a: np.ascontiguousarray(a, np.float32)
+    out = np.zeros(rows * n * dim, np.float32)
+    lib().orc_mhc_mix(fp(out), fp(c(stream)), fp(c(h_res)), fp(c(h_post)), fp(c(block_out)), fp(c(u)), rows, n, dim)
+    return out

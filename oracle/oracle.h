@@ -146,6 +146,12 @@ void orc_silu(float *x, long n);
 double orc_exp64(double x);                             /* fdlibm e_exp.c; Go's portable math.Exp */
 float orc_gate_sigmoid(float x);                        /* load.go:120-123, cross.go:322-325 */
 void orc_sigmoid_gate(float *out, float *gate, long n); /* attention.go:245-249 */
+void orc_rms_unit(float *dst, const float *x, int rows, int dim);                  /* norm.go:68-81 */
+void orc_sinkhorn(float *k, int n, int iters);                                      /* mhc.go:301-417 */
+void orc_mhc_heads(float *h_pre, float *h_post, float *h_res, float *u, const float *pre_l, const float *post_l,
+                   const float *res_l, const float *stream, int rows, int n, int dim, const float *affine);
+void orc_mhc_mix(float *out, const float *stream, const float *h_res, const float *h_post, const float *block_out,
+                 const float *u, int rows, int n, int dim);                          /* mhc.go:229-299 */
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,10 @@
  *   internal/decoder/greedy.go:181-191     argmax
  *   internal/needle/attention.go:245-249   Attention.output's gate
  *   internal/needle/load.go:120-123        sigmoid = float32(1/(1 + exp(-float64(x))))
+ *   internal/needle/norm.go:68-81          RMSUnit
+ *   internal/needle/mhc.go:182-300         MHC.forward's heads, lane sum and mix
+ *   internal/needle/mhc.go:301-417         sinkhorn (exp domain in float64; log
+ *                                          domain in float32 past its range)
  *
  * Pinned by tests/test_oracle_step.py: ZCRMSNorm against float64 and a
  * closed form (a constant row); RoPE against the float64 rotation and the
@@ -131,5 +135,139 @@ void orc_sigmoid_gate(float *out, float *gate, long n) {
     for (long i = 0; i < n; i++) {
         gate[i] = orc_gate_sigmoid(gate[i]);
         out[i] *= gate[i];
+    }
+}
+
+static float mean_square(const float *row, int dim) {
+    /* meanSquare (norm.go:91-109): four float64 partial sums, float32 result */
+    double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+    int i = 0;
+    for (; i + 3 < dim; i += 4) {
+        s0 += (double)row[i] * (double)row[i];
+        s1 += (double)row[i + 1] * (double)row[i + 1];
+        s2 += (double)row[i + 2] * (double)row[i + 2];
+        s3 += (double)row[i + 3] * (double)row[i + 3];
+    }
+    for (; i < dim; i++) s0 += (double)row[i] * (double)row[i];
+    return (float)((s0 + s1 + s2 + s3) / (double)dim);
+}
+
+void orc_rms_unit(float *dst, const float *x, int rows, int dim) {
+    /* RMSUnit (norm.go:68-81): v * float32(1 / sqrt(float64(ms + eps))) */
+    for (int r = 0; r < rows; r++) {
+        const float *row = x + (size_t)r * dim;
+        float e = mean_square(row, dim) + 1e-6f;
+        float inv = (float)(1.0 / sqrt((double)e));
+        for (int c = 0; c < dim; c++) dst[(size_t)r * dim + c] = row[c] * inv;
+    }
+}
+
+static float log_sum_exp(const float *k, int off, int stride, int n) {
+    /* logSumExp (mhc.go:401-417) */
+    float m = -INFINITY;
+    for (int i = 0; i < n; i++) m = fmaxf(m, k[off + i * stride]);
+    if (isinf(m)) m = 0.0f;
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s += (float)orc_exp64((double)(k[off + i * stride] - m));
+    return m + (float)log((double)s);
+}
+
+void orc_sinkhorn(float *k, int n, int iters) {
+    /* sinkhorn (mhc.go:301-399): the float64 exp domain while the logits'
+     * spread allows it, else the float32 log domain */
+    float lo = k[0], hi = k[0];
+    for (int i = 1; i < n * n; i++) {
+        lo = fminf(lo, k[i]);
+        hi = fmaxf(hi, k[i]);
+    }
+    double spread = (double)hi - (double)lo;
+    if (!(isinf(spread) || isnan(spread) || spread + 2.0 * iters * log((double)n) > 700.0)) {
+        double e[64];
+        for (int i = 0; i < n * n; i++) e[i] = orc_exp64((double)k[i] - (double)hi);
+        for (int it = 0; it < iters; it++) {
+            for (int r = 0; r < n; r++) {
+                double s = 0;
+                for (int c = 0; c < n; c++) s += e[r * n + c];
+                for (int c = 0; c < n; c++) e[r * n + c] /= s;
+            }
+            for (int c = 0; c < n; c++) {
+                double s = 0;
+                for (int r = 0; r < n; r++) s += e[r * n + c];
+                for (int r = 0; r < n; r++) e[r * n + c] /= s;
+            }
+        }
+        for (int i = 0; i < n * n; i++) k[i] = (float)e[i];
+        return;
+    }
+    for (int it = 0; it < iters; it++) {
+        for (int r = 0; r < n; r++) {
+            float l = log_sum_exp(k, r * n, 1, n);
+            for (int c = 0; c < n; c++) k[r * n + c] -= l;
+        }
+        for (int c = 0; c < n; c++) {
+            float l = log_sum_exp(k, c, n, n);
+            for (int r = 0; r < n; r++) k[r * n + c] -= l;
+        }
+    }
+    for (int i = 0; i < n * n; i++) k[i] = (float)orc_exp64((double)k[i]);
+}
+
+void orc_mhc_heads(float *h_pre, float *h_post, float *h_res, float *u, const float *pre_l, const float *post_l,
+                   const float *res_l, const float *stream, int rows, int n, int dim, const float *affine) {
+    /* MHC.logits' affine maps (mhc.go:246-263; affine = {a_pre, a_post,
+     * a_res, b_pre[n], pre_off[n], b_post[n], post_off[n], b_res[n*n]} or
+     * NULL for none), then forward's heads and lane sum (mhc.go:204-219):
+     * h_pre = sigmoid, u = sum_k h_pre[k] stream[k] (in k order), h_post =
+     * 2 sigmoid, h_res = sinkhorn, 20 iterations */
+    for (int i = 0; i < rows; i++) {
+        for (int k = 0; k < n; k++) {
+            float p = pre_l[i * n + k], q = post_l[i * n + k];
+            if (affine) {
+                float ap = affine[0] * p;
+                p = ap + affine[3 + k] + affine[3 + n + k];
+                float aq = affine[1] * q;
+                q = aq + affine[3 + 2 * n + k] + affine[3 + 3 * n + k];
+            }
+            h_pre[i * n + k] = orc_gate_sigmoid(p);
+            h_post[i * n + k] = 2.0f * orc_gate_sigmoid(q);
+        }
+        float *ui = u + (size_t)i * dim;
+        for (int c = 0; c < dim; c++) ui[c] = 0.0f;
+        for (int k = 0; k < n; k++) {
+            const float *sk = stream + ((size_t)i * n + k) * dim;
+            for (int c = 0; c < dim; c++) ui[c] += h_pre[i * n + k] * sk[c];
+        }
+        float *hr = h_res + (size_t)i * n * n;
+        for (int k = 0; k < n * n; k++) {
+            float v = res_l[(size_t)i * n * n + k];
+            if (affine) {
+                float av = affine[2] * v;
+                v = av + affine[3 + 4 * n + k];
+            }
+            hr[k] = v;
+        }
+        orc_sinkhorn(hr, n, 20);
+    }
+}
+
+void orc_mhc_mix(float *out, const float *stream, const float *h_res, const float *h_post, const float *block_out,
+                 const float *u, int rows, int n, int dim) {
+    /* y = block(u) - u, then mix (mhc.go:229-234, 266-299): out[a] = sum_b
+     * h_res[a, b] stream[b] (in b order) + h_post[a] y */
+    for (int i = 0; i < rows; i++) {
+        for (int a = 0; a < n; a++) {
+            float *o = out + ((size_t)i * n + a) * dim;
+            for (int c = 0; c < dim; c++) o[c] = 0.0f;
+            for (int b = 0; b < n; b++) {
+                const float h = h_res[((size_t)i * n + a) * n + b];
+                const float *sb = stream + ((size_t)i * n + b) * dim;
+                for (int c = 0; c < dim; c++) o[c] += h * sb[c];
+            }
+            const float hp = h_post[i * n + a];
+            for (int c = 0; c < dim; c++) {
+                float y = block_out[(size_t)i * dim + c] - u[(size_t)i * dim + c];
+                o[c] += hp * y;
+            }
+        }
     }
 }
