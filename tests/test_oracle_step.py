@@ -138,3 +138,22 @@ def test_sigmoid_gate_updates_both():
     o, gg = orc.sigmoid_gate(out, gate)
     assert np.array_equal(gg, orc.gate_sigmoid(gate))
     assert np.array_equal(o, (out * gg).astype(np.float32))
+
+
+def test_norms_match_upstream_fixture():
+    """ZCRMSNorm's divisor and RMSUnit against go-whistle's golden fixture
+    (testdata/needle/zcrmsnorm.safetensors, upstream at float32; extracted
+    into tests/golden/zcrmsnorm_fixture.npz): within 4e-7 relative, the
+    reference's own figure for this fixture (its README lists 3.9e-7). The
+    mean square here sums in float64, upstream in float32."""
+    import os
+
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "zcrmsnorm_fixture.npz"))
+    x = f["x"].reshape(-1, 512)
+    rows = x.shape[0]
+    ru = orc.rms_unit(x, rows, 512).reshape(rows, 512)
+    want = f["rms_unit"].reshape(rows, 512)
+    assert np.max(np.abs(ru - want)) <= 4e-7 * np.max(np.abs(want))
+    y = orc.zc_rmsnorm(x.ravel(), np.ones(512, np.float32), 512).reshape(rows, 512)  # gain 1: x / rms
+    ref = x / f["rms"].reshape(rows, 1)
+    assert np.max(np.abs(y - ref)) <= 4e-7 * np.max(np.abs(ref))
