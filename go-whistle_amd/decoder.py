@@ -27,6 +27,7 @@ does it (cross.go:181-204, without q/k norms or cross RoPE):
 
   per layer: K, V = GEMMs(Wck, Wcv; enc) over the frames  needle.ApplyShared
              int8 K, V = QuantizeRows per head             int8.go:116-141
+             (stored head-major: [head][frame][64] per stream)
 
 on the device (the batched products take the MFMA form); that build is
 not part of the decode step.
@@ -167,7 +168,12 @@ class Decoder:
         self.tok = z(B, dt=i32)
         self.pos = z(B, dt=i32)
         self.spans_self = z(B, 4, dt=i32)
-        self.spans_cross = z(B, 4, dt=i32)
+        hk = c.dim // c.head_dim
+        # The cross memory is head-major, [stream][head][frame][code]: every
+        # (stream, head) a contiguous block, read as batch * heads one-head
+        # streams (measured 104 -> 95 us per batch-256 call against the
+        # key-major rows Int8Rows uses for the self cache).
+        self.spans_cross = z(B * hk, 4, dt=i32)
         self.spans_cross[:, 3] = c.frames
         self.x, self.h = z(B, c.dim), z(B, c.dim)
         self.q, self.k, self.v, self.g = z(B, c.dim), z(B, c.dim), z(B, c.dim), z(B, c.dim)
@@ -179,10 +185,10 @@ class Decoder:
         self.self_ks = [z(B, c.max_pos, hk) for _ in range(c.layers)]
         self.self_v = [z(B, c.max_pos, c.dim, dt=i8) for _ in range(c.layers)]
         self.self_vs = [z(B, c.max_pos, hk) for _ in range(c.layers)]
-        self.cross_k = [z(B, c.frames, c.dim, dt=i8) for _ in range(c.layers)]
-        self.cross_ks = [z(B, c.frames, hk) for _ in range(c.layers)]
-        self.cross_v = [z(B, c.frames, c.dim, dt=i8) for _ in range(c.layers)]
-        self.cross_vs = [z(B, c.frames, hk) for _ in range(c.layers)]
+        self.cross_k = [z(B, hk, c.frames, c.head_dim, dt=i8) for _ in range(c.layers)]
+        self.cross_ks = [z(B, hk, c.frames) for _ in range(c.layers)]
+        self.cross_v = [z(B, hk, c.frames, c.head_dim, dt=i8) for _ in range(c.layers)]
+        self.cross_vs = [z(B, hk, c.frames) for _ in range(c.layers)]
 
     def set_memory(self, seed, generator="numpy"):
         """Builds each stream's int8 cross memory from its encoder states
@@ -206,10 +212,12 @@ class Decoder:
             for layer in range(c.layers):
                 m = self.mats[layer]
                 cq.gemms_dev([m["wck"], m["wcv"]], [tmp_k, tmp_v], enc, c.frames)
-                needle.quantize_rows_dev(self.cross_k[layer][b], self.cross_ks[layer][b], tmp_k, c.frames, c.dim,
-                                         c.head_dim)
-                needle.quantize_rows_dev(self.cross_v[layer][b], self.cross_vs[layer][b], tmp_v, c.frames, c.dim,
-                                         c.head_dim)
+                hk = c.dim // c.head_dim
+                for tmp, dq, ds in ((tmp_k, self.cross_k[layer][b], self.cross_ks[layer][b]),
+                                    (tmp_v, self.cross_v[layer][b], self.cross_vs[layer][b])):
+                    # head-major rows of one head each: QuantizeRow per 64-wide chunk, as on the key-major rows
+                    hm = tmp.view(c.frames, hk, c.head_dim).transpose(0, 1).contiguous()
+                    needle.quantize_rows_dev(dq, ds, hm, hk * c.frames, c.head_dim, c.head_dim)
         torch.cuda.synchronize()
 
     def encoder_states_device(self, seed, stream):
@@ -231,9 +239,13 @@ class Decoder:
     def _attend(self, layer, cross, s, rope=None):
         c, B = self.cfg, self.batch
         hk = c.dim // c.head_dim
-        if cross:
-            kq, ks, vq, vs, spans, n = (self.cross_k[layer], self.cross_ks[layer], self.cross_v[layer],
-                                        self.cross_vs[layer], self.spans_cross, c.frames)
+        if cross:  # head-major memory: batch * heads streams of one head
+            n, d = c.frames, c.head_dim
+            args = [_ptr(self.att), 0, _ptr(self.q), 0, 1, 1, _ptr(self.cross_k[layer]), _ptr(self.cross_ks[layer]), d,
+                    d, _ptr(self.cross_v[layer]), _ptr(self.cross_vs[layer]), d, d, n * d, n, _ptr(self.spans_cross),
+                    n, float(np.float32(math.sqrt(c.head_dim))), 1, B * hk]
+            check(lib().kv_attend_int8_dev(*args, s))
+            return
         else:
             kq, ks, vq, vs, spans, n = (self.self_k[layer], self.self_ks[layer], self.self_v[layer],
                                         self.self_vs[layer], self.spans_self, c.max_pos)
@@ -341,8 +353,8 @@ class Decoder:
         dev = self.tok.device
         par = torch.as_tensor(np.asarray(parents, np.int32), device=dev)
         self_len = self.pos.index_select(0, par.long()).to(torch.int32)
-        cross_len = torch.full((B,), c.frames, dtype=torch.int32, device=dev)
         hk = c.dim // c.head_dim
+        cross_len = torch.full((B,), hk * c.frames, dtype=torch.int32, device=dev)  # head-major: hk * frames rows of one head
         if getattr(self, "_fork_tmp", None) is None:
             rows = max(c.max_pos, c.frames)
             self._fork_tmp = (torch.empty(B * rows * c.dim, dtype=torch.int8, device=dev),
@@ -350,11 +362,11 @@ class Decoder:
         tq, ts = self._fork_tmp
         s = cq._stream()
         for l in range(c.layers):
-            for q, sc, cap, ln in ((self.self_k[l], self.self_ks[l], c.max_pos, self_len),
-                                   (self.self_v[l], self.self_vs[l], c.max_pos, self_len),
-                                   (self.cross_k[l], self.cross_ks[l], c.frames, cross_len),
-                                   (self.cross_v[l], self.cross_vs[l], c.frames, cross_len)):
-                check(lib().kv_reorder_dev(_ptr(q), _ptr(sc), _ptr(tq), _ptr(ts), _ptr(par), _ptr(ln), B, cap, c.dim,
+            for q, sc, cap, cols, ln in ((self.self_k[l], self.self_ks[l], c.max_pos, c.dim, self_len),
+                                         (self.self_v[l], self.self_vs[l], c.max_pos, c.dim, self_len),
+                                         (self.cross_k[l], self.cross_ks[l], hk * c.frames, c.head_dim, cross_len),
+                                         (self.cross_v[l], self.cross_vs[l], hk * c.frames, c.head_dim, cross_len)):
+                check(lib().kv_reorder_dev(_ptr(q), _ptr(sc), _ptr(tq), _ptr(ts), _ptr(par), _ptr(ln), B, cap, cols,
                                            c.head_dim, s))
         self.tok.copy_(self.tok.index_select(0, par.long()))
         self.pos.copy_(self.pos.index_select(0, par.long()))
