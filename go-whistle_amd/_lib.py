@@ -64,8 +64,13 @@ SIGNATURES = {
                                     POINTER(c_void_p), POINTER(c_void_p), c_longlong, c_longlong, c_void_p, c_int,
                                     POINTER(c_void_p), POINTER(c_void_p), c_void_p]),
     "nd_zcrmsnorm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
-    "nd_rope_dev": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "nd_rope_dev": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p]),
     "nd_argmax_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "nd_argmax_advance_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p]),
+    "kv_attend_int8_shared_dev": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_int, c_int, c_void_p,
+                                          c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_longlong,
+                                          c_longlong, c_void_p, c_int, c_float, c_int, c_int, c_void_p, c_int,
+                                          c_void_p]),
     "nd_silu_dev": (c_int, [c_void_p, c_longlong, c_void_p]),
     "nd_fake_quant_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_int, c_int, c_void_p]),
     "kv_reorder_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

@@ -650,8 +650,19 @@ int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *
     if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
     if (rows < 0) return fail(CQ_ERR_MISUSE, "cq: GEMM of %d rows", rows);
     if (rows == 0 || m->out == 0) return CQ_OK;  // kernel.go:105-107
+    if (!dst || !x) return fail(CQ_ERR_MISUSE, "cq: GEMM of %d rows with a nil operand", rows);
     cq_matrix *mm = const_cast<cq_matrix *>(m);
     return run_product(&mm, 1, &dst, x, rows, static_cast<hipStream_t>(stream));
+}
+
+// Nil operands of a device product: a nil Go slice reaches the C ABI as a
+// null pointer, which must not reach a kernel.
+static int nil_operands(int n, float *const *dsts, const float *x, int rows) {
+    if (rows == 0 || n == 0) return CQ_OK;
+    if (!x) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d rows with a nil input", rows);
+    for (int k = 0; k < n; ++k)
+        if (!dsts[k]) return fail(CQ_ERR_MISUSE, "cq: GEMMs with a nil output %d", k);
+    return CQ_OK;
 }
 
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream) {
@@ -660,6 +671,7 @@ int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x
     for (int k = 0; k < n; ++k)
         if (!ms[k] || ms[k]->st->in != ms[0]->st->in)
             return fail(CQ_ERR_MISUSE, "cq: GEMMs over matrices of different input widths");
+    if (int e = nil_operands(n, dsts, x, rows)) return e;
     if (rows == 0 || n == 0) return CQ_OK;
     return gemms_dev(n, ms, dsts, x, rows, static_cast<hipStream_t>(stream));
 }
@@ -677,6 +689,7 @@ int cq_gemms_fused_dev(int n, cq_matrix *const *ms, float *const *dsts, const fl
         if (!uses_lut(ms[k]))
             return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel, not %s", cq_kernel_name(ms[k]));
     }
+    if (int e = nil_operands(n, dsts, x, rows)) return e;
     if (rows == 0 || n == 0) return CQ_OK;
     Fuse f;
     f.ngain = norm_gain;
@@ -698,6 +711,7 @@ int cq_gemms_gated_dev(int n, cq_matrix *const *ms, float *const *dsts, const fl
         if (!uses_lut(ms[k]))
             return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel, not %s", cq_kernel_name(ms[k]));
     }
+    if (int e = nil_operands(n, dsts, x, rows)) return e;
     if (rows == 0 || n == 0) return CQ_OK;
     Fuse f;
     f.xgate = gate;
@@ -729,6 +743,7 @@ int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const f
         if (cos_t && cos_t[k] && !(sin_t && sin_t[k])) return fail(CQ_ERR_MISUSE, "cq: RoPE cosines without sines");
     }
     if (any && !pos) return fail(CQ_ERR_MISUSE, "cq: append without positions");
+    if (int e = nil_operands(n, dsts, x, rows)) return e;
     if (rows == 0 || n == 0) return CQ_OK;
     Fuse f;
     f.ngain = norm_gain;
@@ -1031,9 +1046,12 @@ static int attend_impl(float *out, long long out_stride, const float *q, long lo
                        const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
                        int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
                        float scale, int quant_q, int batch, const float *rope_cos, const float *rope_sin,
-                       const int32_t *qpos, void *stream) {
+                       const int32_t *qpos, const int32_t *kv_index, int kv_streams, void *stream) {
     if (rope_cos && (!rope_sin || !qpos || qk % 2 != 0))
         return fail(CQ_ERR_MISUSE, "needle: RoPE of query heads of %d", qk);
+    if (kv_index && kv_streams < 0) return fail(CQ_ERR_MISUSE, "needle: %d shared caches", kv_streams);
+    if (static_cast<long long>(t) * heads * batch > 0 && (!out || !q || !kq || !ks || !vq || !vs || !spans))
+        return fail(CQ_ERR_MISUSE, "needle: int8 attention with a nil operand");
     if (qk <= 0 || vd <= 0 || k_cols % qk != 0)
         return fail(CQ_ERR_MISUSE, "needle: int8 keys of %d in chunks of %d", k_cols, qk);
     const int kv_heads = k_cols / qk;
@@ -1054,7 +1072,7 @@ static int attend_impl(float *out, long long out_stride, const float *q, long lo
     const int resident = wgs <= 2LL * device_info().cus ? 1 : 0;
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
                  kv_stride, s_stride, spans, nk_max, vchunk, resident, scale, quant_q, batch,
-                 rope_cos, rope_sin, qpos};
+                 rope_cos, rope_sin, qpos, kv_index, kv_streams};
     HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");
     return CQ_OK;
 }
@@ -1064,7 +1082,19 @@ int kv_attend_int8_dev(float *out, long long out_stride, const float *q, long lo
                        int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
                        float scale, int quant_q, int batch, void *stream) {
     return attend_impl(out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, kv_stride,
-                       s_stride, spans, nk_max, scale, quant_q, batch, nullptr, nullptr, nullptr, stream);
+                       s_stride, spans, nk_max, scale, quant_q, batch, nullptr, nullptr, nullptr, nullptr, 0, stream);
+}
+
+int kv_attend_int8_shared_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                              const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                              int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans,
+                              int nk_max, float scale, int quant_q, int batch, const int32_t *kv_index, int kv_streams,
+                              void *stream) {
+    if (!kv_index && static_cast<long long>(t) * heads * batch > 0)
+        return fail(CQ_ERR_MISUSE, "needle: shared caches without an index");
+    return attend_impl(out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, kv_stride,
+                       s_stride, spans, nk_max, scale, quant_q, batch, nullptr, nullptr, nullptr, kv_index, kv_streams,
+                       stream);
 }
 
 int kv_attend_int8_rope_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
@@ -1074,7 +1104,7 @@ int kv_attend_int8_rope_dev(float *out, long long out_stride, const float *q, lo
                             const int32_t *qpos, void *stream) {
     if (!cos_t) return fail(CQ_ERR_MISUSE, "needle: RoPE tables missing");
     return attend_impl(out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, kv_stride,
-                       s_stride, spans, nk_max, scale, quant_q, batch, cos_t, sin_t, qpos, stream);
+                       s_stride, spans, nk_max, scale, quant_q, batch, cos_t, sin_t, qpos, nullptr, 0, stream);
 }
 
 // ---- decode-step float blocks -------------------------------------------------
@@ -1085,18 +1115,31 @@ int nd_zcrmsnorm_dev(float *dst, const float *x, const float *gain, int rows, in
     return CQ_OK;
 }
 
-int nd_rope_dev(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
+int nd_rope_dev(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t, int positions,
                 const int32_t *pos, int rows_per_pos, void *stream) {
-    if (rows < 0 || heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || rows_per_pos <= 0)
+    if (rows < 0 || heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || rows_per_pos <= 0 || positions < 0)
         return fail(CQ_ERR_MISUSE, "needle: RoPE of %d rows, %d heads of %d", rows, heads, head_dim);
-    HIP_TRY(launch_rope(x, rows, heads, head_dim, cos_t, sin_t, pos, rows_per_pos, static_cast<hipStream_t>(stream)),
+    if (rows > 0 && (!x || !cos_t || !sin_t || !pos)) return fail(CQ_ERR_MISUSE, "needle: RoPE with a nil operand");
+    HIP_TRY(launch_rope(x, rows, heads, head_dim, cos_t, sin_t, positions, pos, rows_per_pos,
+                        static_cast<hipStream_t>(stream)),
             "rope launch");
     return CQ_OK;
 }
 
 int nd_argmax_dev(int32_t *out, const float *v, int rows, int n, void *stream) {
     if (rows < 0 || n <= 0) return fail(CQ_ERR_MISUSE, "decoder: argmax of %d rows of %d", rows, n);
-    HIP_TRY(launch_argmax(out, v, rows, n, static_cast<hipStream_t>(stream)), "argmax launch");
+    if (rows > 0 && (!out || !v)) return fail(CQ_ERR_MISUSE, "decoder: argmax with a nil operand");
+    HIP_TRY(launch_argmax(out, v, rows, n, nullptr, nullptr, 0, static_cast<hipStream_t>(stream)), "argmax launch");
+    return CQ_OK;
+}
+
+int nd_argmax_advance_dev(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
+                          int span_stride, void *stream) {
+    if (rows < 0 || n <= 0) return fail(CQ_ERR_MISUSE, "decoder: argmax of %d rows of %d", rows, n);
+    if (rows > 0 && (!out || !v || !pos || !span_hi))
+        return fail(CQ_ERR_MISUSE, "decoder: argmax with a nil operand");
+    HIP_TRY(launch_argmax(out, v, rows, n, pos, span_hi, span_stride, static_cast<hipStream_t>(stream)),
+            "argmax launch");
     return CQ_OK;
 }
 
@@ -1214,6 +1257,8 @@ static int append_impl(int8_t *q, float *s, const float *x, int batch, int cols,
     if (batch < 0 || cap < 0) return fail(CQ_ERR_MISUSE, "needle: append of %d streams", batch);
     if (width > 256) return fail(CQ_ERR_UNSUPPORTED, "needle: append in chunks of %d (at most 256)", width);
     if (cos_t && (!sin_t || width % 2 != 0)) return fail(CQ_ERR_MISUSE, "needle: RoPE of heads of %d", width);
+    if (batch > 0 && cols > 0 && (!q || !s || !x || !pos))
+        return fail(CQ_ERR_MISUSE, "needle: append with a nil operand");
     HIP_TRY(launch_append(q, s, x, batch, cols, width, q_stride, s_stride, pos, cap, cos_t, sin_t,
                           static_cast<hipStream_t>(stream)),
             "append launch");

@@ -43,6 +43,23 @@ __device__ __forceinline__ float xor_lane(float v, int h) {
     }
 }
 
+// Go's built-in max of two float32 values, which every max-reduction of the
+// reference uses (QuantizeRow's bound, softmaxInPlace's max, the lut tables'
+// bound): NaN when either operand is NaN, and -0 below +0. That is IEEE
+// 754-2019 maximum, one v_maximum3_f32 on gfx950; fmaxf would drop a NaN.
+__device__ __forceinline__ float go_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// Go's built-in min (and slices.Min's rule): NaN when either is NaN.
+__device__ __forceinline__ float go_min(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+
+// QuantizeRow's code of r = RNE(x / s) (internal/needle/int8.go:50-53):
+// int8(min(max(r, -128), 127)) with Go's NaN-propagating min and max, and
+// the conversion of a NaN to int8 gives 0 on amd64 (the float64 to integer
+// conversion returns the integer indefinite 0x80000000, whose low byte is 0)
+// as on arm64 (FCVTZS of a NaN is 0). A +-Inf r clamps to 127 / -128.
+__device__ __forceinline__ int go_int8_code(float r) {
+    return r != r ? 0 : static_cast<int>(fminf(fmaxf(r, -128.0f), 127.0f));
+}
+
 // Workgroup barrier for LDS only: this wavefront's LDS operations complete
 // (lgkmcnt 0), then s_barrier. Unlike __syncthreads it does not wait for
 // the wavefront's global loads, so loads issued ahead stay in flight across

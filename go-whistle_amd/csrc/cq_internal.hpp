@@ -175,8 +175,22 @@ struct AttendArgs {
     // qpos[b * t + i] of the tables, pairs (j, j + qk/2).
     const float *rope_cos, *rope_sin;
     const int32_t *qpos;
+    // Shared caches (null: stream b reads cache b): stream b reads the keys
+    // and values of cache kv_index[b], one of kv_streams caches kv_stride /
+    // s_stride apart; an index outside [0, kv_streams) leaves its output
+    // untouched.
+    const int32_t *kv_index;
+    int kv_streams;
 };
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream);
+
+// The cache stream a workgroup of stream b reads (kv_index, or b itself),
+// or -1 when the index is outside the caches.
+__device__ __forceinline__ long long attend_cache_of(const AttendArgs &a, int b) {
+    if (!a.kv_index) return b;
+    const int c = a.kv_index[b];
+    return (c >= 0 && c < a.kv_streams) ? c : -1;
+}
 
 // HadamardMLP, Whistle's Monarch FFN (hadamard_kernels.hip): rows of dim
 // values in x and out, n = na * nb >= dim, factors row-major (na x na,
@@ -209,8 +223,9 @@ hipError_t launch_mhc_mix(const MhcArgs &m, int rows, hipStream_t s);
 // decode-step float blocks (step_kernels.hip)
 hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int rows, int dim, hipStream_t s);
 hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
-                       const int32_t *pos, int rows_per_pos, hipStream_t s);
-hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, hipStream_t s);
+                       int positions, const int32_t *pos, int rows_per_pos, hipStream_t s);
+hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
+                         int span_stride, hipStream_t s);
 hipError_t launch_silu(float *x, long long n, hipStream_t s);
 hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s);
 hipError_t launch_sigmoid_gate(float *out, float *gate, long long n, hipStream_t s);

@@ -26,6 +26,7 @@
 // meet in LDS and the lane that owns the row folds them into y in group
 // order.
 #include "cq_internal.hpp"
+#include "cq_device.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -145,15 +146,15 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProdArgs a) {
                 const float *xg = xh + gi * G;
                 float mx = 0.0f;
                 if constexpr (BITS == 4) {
-                    for (int k = lane; k < G; k += 64) mx = fmaxf(mx, fabsf(xg[k]));
+                    for (int k = lane; k < G; k += 64) mx = go_max(mx, fabsf(xg[k]));
                 } else {
                     for (int k = lane; k < G / 2; k += 64) {
                         const float s2 = fabsf(xg[2 * k]) + fabsf(xg[2 * k + 1]);
-                        mx = fmaxf(mx, s2);
+                        mx = go_max(mx, s2);
                     }
                 }
 #pragma unroll
-                for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                for (int off = 32; off > 0; off >>= 1) mx = go_max(mx, __shfl_xor(mx, off));
                 if (lane == 0) {
                     const float m = a.cb_max * mx;
                     st_inv[gi] = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;

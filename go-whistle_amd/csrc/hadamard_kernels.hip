@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kHadaMaxN) void hadamard_mlp_kernel(HadaArgs h) {
             float s = 0.0f;
             for (int w = 0; w < nw; ++w) s = s + part[w][r];
             prob[r] = s;
-            m = fmaxf(m, s);
+            m = go_max(m, s);
         }
         float sum = 0.0f;
         for (int r = 0; r < rank; ++r) {

@@ -39,16 +39,12 @@ __global__ __launch_bounds__(256) void quantize_kernel(int8_t *q, float *s, cons
     if (c >= chunks) return;
     const float *xc = x + c * width;
     float m = 0.0f;
-    for (int i = lane; i < width; i += 64) m = fmaxf(m, fabsf(xc[i]));
+    for (int i = lane; i < width; i += 64) m = go_max(m, fabsf(xc[i]));
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+    for (int off = 32; off > 0; off >>= 1) m = go_max(m, __shfl_xor(m, off));
+    const float sc = m > 0.0f ? m / 127.0f : 1.0f;  // a NaN bound fails m > 0: scale 1
     int8_t *qc = q + c * width;
-    for (int i = lane; i < width; i += 64) {
-        float r = rintf(xc[i] / sc);
-        r = fminf(fmaxf(r, -128.0f), 127.0f);
-        qc[i] = static_cast<int8_t>(static_cast<int>(r));
-    }
+    for (int i = lane; i < width; i += 64) qc[i] = static_cast<int8_t>(go_int8_code(rintf(xc[i] / sc)));
     if (lane == 0) s[c] = sc;
 }
 
@@ -62,16 +58,13 @@ __global__ __launch_bounds__(256) void fake_quant_kernel(float *dst, const float
     if (c >= chunks) return;
     const float *xc = x + c * width;
     float m = 0.0f;
-    for (int i = lane; i < width; i += 64) m = fmaxf(m, fabsf(xc[i]));
+    for (int i = lane; i < width; i += 64) m = go_max(m, fabsf(xc[i]));
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    for (int off = 32; off > 0; off >>= 1) m = go_max(m, __shfl_xor(m, off));
     const float sc = m > 0.0f ? m / 127.0f : 1.0f;
     float *dc = dst + c * width;
-    for (int i = lane; i < width; i += 64) {
-        float r = rintf(xc[i] / sc);
-        r = fminf(fmaxf(r, -128.0f), 127.0f);
-        dc[i] = static_cast<float>(static_cast<int>(r)) * sc;  // float32(q): a code of 0 is +0, never -0
-    }
+    for (int i = lane; i < width; i += 64)
+        dc[i] = static_cast<float>(go_int8_code(rintf(xc[i] / sc))) * sc;  // float32(q): a code of 0 is +0, never -0
 }
 
 // Stream b of dst gets rows [0, len[b]) of stream idx[b] of src (idx null:
@@ -118,11 +111,11 @@ __device__ __forceinline__ float query_value(const AttendArgs &a, const float *q
 __device__ __forceinline__ float block_max(float v, float *red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    for (int off = 32; off > 0; off >>= 1) v = go_max(v, __shfl_xor(v, off));
     if (lane == 0) red[wave] = v;
     __syncthreads();
     float r = red[0];
-    for (int w = 1; w < kAttThreads / 64; ++w) r = fmaxf(r, red[w]);
+    for (int w = 1; w < kAttThreads / 64; ++w) r = go_max(r, red[w]);
     __syncthreads();
     return r;
 }
@@ -143,7 +136,9 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
     const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
     const int n = len0 + len1;
-    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
+    const long long kb = attend_cache_of(a, b);  // the cache this stream reads
+    if (kb < 0 || lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max)
+        return;  // spans off the cache, or no cache
 
     float *s = reinterpret_cast<float *>(smem);  // n logits, then weights
     int8_t *vbuf = reinterpret_cast<int8_t *>(s + ((a.nk_max + 3) & ~3));  // value codes: one or two chunks
@@ -153,10 +148,10 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     __shared__ float sq_sh, sum_sh;
 
     const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
-    const int8_t *kq = a.kq + b * a.kv_stride;
-    const float *ks = a.ks + b * a.s_stride;
-    const int8_t *vq = a.vq + b * a.kv_stride;
-    const float *vs = a.vs + b * a.s_stride;
+    const int8_t *kq = a.kq + kb * a.kv_stride;
+    const float *ks = a.ks + kb * a.s_stride;
+    const int8_t *vq = a.vq + kb * a.kv_stride;
+    const float *vs = a.vs + kb * a.s_stride;
     auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
 
     // The query head (after RoPE when asked), then QuantizeRow of it
@@ -166,14 +161,10 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     __syncthreads();
     if (a.quant_q) {
         float m = 0.0f;
-        for (int c = tid; c < a.qk; c += kAttThreads) m = fmaxf(m, fabsf(qg[c]));
+        for (int c = tid; c < a.qk; c += kAttThreads) m = go_max(m, fabsf(qg[c]));
         m = block_max(m, red);
         const float sc = m > 0.0f ? m / 127.0f : 1.0f;
-        for (int c = tid; c < a.qk; c += kAttThreads) {
-            float r = rintf(qg[c] / sc);
-            r = fminf(fmaxf(r, -128.0f), 127.0f);
-            q8[c] = static_cast<int8_t>(static_cast<int>(r));
-        }
+        for (int c = tid; c < a.qk; c += kAttThreads) q8[c] = static_cast<int8_t>(go_int8_code(rintf(qg[c] / sc)));
         if (tid == 0) sq_sh = sc;
         __syncthreads();
     }
@@ -275,7 +266,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
 
     // 2. softmaxInPlace with amd64's expSubSum.
     float m = -INFINITY;
-    for (int j = tid; j < n; j += kAttThreads) m = fmaxf(m, s[j]);
+    for (int j = tid; j < n; j += kAttThreads) m = go_max(m, s[j]);
     m = block_max(m, red);
     const int n8 = n & ~7;
     const bool kernel_path = n8 > 0;
@@ -459,7 +450,9 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
     const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
     const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
     const int n = len0 + len1;
-    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
+    const long long kb = attend_cache_of(a, b);  // the cache this stream reads
+    if (kb < 0 || lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max)
+        return;  // spans off the cache, or no cache
     float *outp = a.out + b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * VD;
     if (n == 0) {
         if (tid < VD) outp[tid] = 0.0f;
@@ -477,10 +470,10 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
     __shared__ float sq_sh, sum_sh;
 
     const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
-    const int8_t *kq = a.kq + b * a.kv_stride;
-    const float *ks = a.ks + b * a.s_stride;
-    const int8_t *vq = a.vq + b * a.kv_stride;
-    const float *vs = a.vs + b * a.s_stride;
+    const int8_t *kq = a.kq + kb * a.kv_stride;
+    const float *ks = a.ks + kb * a.s_stride;
+    const int8_t *vq = a.vq + kb * a.kv_stride;
+    const float *vs = a.vs + kb * a.s_stride;
     auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
 
     const int nch = (n + G::kJC - 1) / G::kJC;
@@ -557,9 +550,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
         const float m = block_max(tid < a.qk ? fabsf(qv) : 0.0f, red);
         const float sc = m > 0.0f ? m / 127.0f : 1.0f;
         if (tid < a.qk) {
-            float rq = rintf(qv / sc);
-            rq = fminf(fmaxf(rq, -128.0f), 127.0f);
-            q8[tid] = static_cast<int8_t>(static_cast<int>(rq));
+            q8[tid] = static_cast<int8_t>(go_int8_code(rintf(qv / sc)));
         }
         if (tid == 0) sq_sh = sc;
     }
@@ -598,7 +589,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
     // the exponentials from a copy transposed to [lane][index] in the
     // product buffers (free until step 3) when it fits.
     float m = -INFINITY;
-    for (int j = tid; j < n; j += kAttThreads) m = fmaxf(m, s[j]);
+    for (int j = tid; j < n; j += kAttThreads) m = go_max(m, s[j]);
     m = block_max(m, red);
     const int n8 = n & ~7;
     const bool kernel_path = n8 > 0;
@@ -735,7 +726,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
 template <int NW>
 __device__ __forceinline__ float block_max_nw(float v, float *red) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    for (int off = 32; off > 0; off >>= 1) v = go_max(v, __shfl_xor(v, off));
     if constexpr (NW == 1) {
         return __shfl(v, 0);
     } else {
@@ -744,7 +735,7 @@ __device__ __forceinline__ float block_max_nw(float v, float *red) {
         __syncthreads();
         float r = red[0];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) r = fmaxf(r, red[w]);
+        for (int w = 1; w < NW; ++w) r = go_max(r, red[w]);
         __syncthreads();
         return r;
     }
@@ -801,7 +792,9 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
     const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
     const int n = len0 + len1;
-    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
+    const long long kb = attend_cache_of(a, b);  // the cache this stream reads
+    if (kb < 0 || lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max)
+        return;  // spans off the cache, or no cache
     float *outp = a.out + b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * kChainVd;
     if (n == 0) {
         if (tid < kChainVd) outp[tid] = 0.0f;
@@ -819,10 +812,10 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     __shared__ float sq_sh, sum_sh;
 
     const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * a.qk;
-    const int8_t *kq = a.kq + b * a.kv_stride;
-    const float *ks = a.ks + b * a.s_stride;
-    const int8_t *vq = a.vq + b * a.kv_stride;
-    const float *vs = a.vs + b * a.s_stride;
+    const int8_t *kq = a.kq + kb * a.kv_stride;
+    const float *ks = a.ks + kb * a.s_stride;
+    const int8_t *vq = a.vq + kb * a.kv_stride;
+    const float *vs = a.vs + kb * a.s_stride;
     auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
     const int nch = (n + JC - 1) / JC;
 
@@ -890,9 +883,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
         const float m = block_max_nw<NW>(tid < a.qk ? fabsf(qv) : 0.0f, red);
         const float sc = m > 0.0f ? m / 127.0f : 1.0f;
         if (tid < a.qk) {
-            float rq = rintf(qv / sc);
-            rq = fminf(fmaxf(rq, -128.0f), 127.0f);
-            q8[tid] = static_cast<int8_t>(static_cast<int>(rq));
+            q8[tid] = static_cast<int8_t>(go_int8_code(rintf(qv / sc)));
         }
         if (tid == 0) sq_sh = sc;
     }
@@ -927,7 +918,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     // 2. softmaxInPlace with amd64's expSubSum; the eight lane sums read a
     // copy transposed to [lane][index].
     float m0 = -INFINITY;
-    for (int j = tid; j < n; j += NT) m0 = fmaxf(m0, s[j]);
+    for (int j = tid; j < n; j += NT) m0 = go_max(m0, s[j]);
     const float m = block_max_nw<NW>(m0, red);
     const int n8 = n & ~7;
     const bool kernel_path = n8 > 0;
@@ -1096,7 +1087,9 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
     const int32_t *sp = a.spans + (static_cast<long long>(b) * a.t + i) * 4;
     const int lo0 = sp[0], len0 = sp[1] - sp[0], lo1 = sp[2], len1 = sp[3] - sp[2];
     const int n = len0 + len1;
-    if (lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max) return;  // spans off the cache
+    const long long kb = attend_cache_of(a, b);  // the cache this stream reads
+    if (kb < 0 || lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max)
+        return;  // spans off the cache, or no cache
     float *outp = a.out + b * a.out_stride + (static_cast<long long>(i) * a.heads + h) * ROW;
     if (n == 0) {
         outp[lane] = 0.0f;
@@ -1109,10 +1102,10 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
     __shared__ float red[8];
 
     const float *qi = a.q + b * a.q_stride + (static_cast<long long>(i) * a.heads + h) * ROW;
-    const int8_t *kq = a.kq + b * a.kv_stride;
-    const float *ks = a.ks + b * a.s_stride;
-    const int8_t *vq = a.vq + b * a.kv_stride;
-    const float *vs = a.vs + b * a.s_stride;
+    const int8_t *kq = a.kq + kb * a.kv_stride;
+    const float *ks = a.ks + kb * a.s_stride;
+    const int8_t *vq = a.vq + kb * a.kv_stride;
+    const float *vs = a.vs + kb * a.s_stride;
     auto key_of = [&](int j) { return j < len0 ? lo0 + j : lo1 + (j - len0); };
     const int nch = (n + JC - 1) / JC, total = 2 * nch;  // key chunks, then value chunks
 
@@ -1161,11 +1154,9 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
     if (a.quant_q) {
         float m = fabsf(qv);
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        for (int off = 32; off > 0; off >>= 1) m = go_max(m, __shfl_xor(m, off));
         const float sc = m > 0.0f ? m / 127.0f : 1.0f;
-        float rq = rintf(qv / sc);
-        rq = fminf(fmaxf(rq, -128.0f), 127.0f);
-        const int code = static_cast<int>(rq) & 255;
+        const int code = go_int8_code(rintf(qv / sc)) & 255;
         // gather this lane's 32 query codes (lanes 32*half ..) into 8 words
         int words[8];
 #pragma unroll
@@ -1228,9 +1219,9 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
 
     // 2. softmaxInPlace with amd64's expSubSum.
     float m = -INFINITY;
-    for (int j = lane; j < n; j += 64) m = fmaxf(m, s[j]);
+    for (int j = lane; j < n; j += 64) m = go_max(m, s[j]);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    for (int off = 32; off > 0; off >>= 1) m = go_max(m, __shfl_xor(m, off));
     const int n8 = n & ~7;
     const bool kernel_path = n8 > 0;
     for (int j = lane; j < n8; j += 64) s[j] = exp_lane(s[j] - m);

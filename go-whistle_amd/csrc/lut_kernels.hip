@@ -216,15 +216,18 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         if constexpr (BITS == 4) {
-            mx = fmaxf(mx, fabsf(v[e]));
+            mx = go_max(mx, fabsf(v[e]));
         } else {
             const float p = xor_lane<1>(v[e]);
             const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
-            mx = fmaxf(mx, s2);
+            mx = go_max(mx, s2);
         }
     }
+    // Go's max keeps a NaN (lut.go:241-243, 266-268): a group holding one
+    // has M = NaN, inv = 0 and step NaN, so every row's y is NaN, as the
+    // generic Go and the arm64 kernel (FMAX) give.
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, xor_lane(mx, off));
+    for (int off = 32; off > 0; off >>= 1) mx = go_max(mx, xor_lane(mx, off));
     const float m = cb_max * mx;
     const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
     if (lane == 0) *step = m * lut_step;
@@ -432,12 +435,10 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
         }
         float m = fabsf(v);
 #pragma unroll
-        for (int h = 32; h > 0; h >>= 1) m = fmaxf(m, xor_lane(m, h));
+        for (int h = 32; h > 0; h >>= 1) m = go_max(m, xor_lane(m, h));
         const float sc = m > 0.0f ? m / 127.0f : 1.0f;
-        float c = rintf(v / sc);
-        c = fminf(fmaxf(c, -128.0f), 127.0f);
         CQ_GLOBAL int8_t *qp = gptr_w(j_aq) + static_cast<long long>(act) * j_aqs + static_cast<long long>(j_apos) * j_out;
-        qp[r0 + ln] = static_cast<int8_t>(static_cast<int>(c));
+        qp[r0 + ln] = static_cast<int8_t>(go_int8_code(rintf(v / sc)));
         if (ln == 0)
             gptr_w(j_as)[static_cast<long long>(act) * j_ass + static_cast<long long>(j_apos) * (j_out >> 6) + (r0 >> 6)] = sc;
     };

@@ -264,18 +264,18 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     if constexpr (BITS == 4) {
-                        mx[k] = fmaxf(mx[k], fabsf(v[k][e]));
+                        mx[k] = go_max(mx[k], fabsf(v[k][e]));
                     } else {
                         const float p = xor_lane<1>(v[k][e]);
                         const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
-                        mx[k] = fmaxf(mx[k], s2);
+                        mx[k] = go_max(mx[k], s2);
                     }
                 }
             }
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-                for (int k = 0; k < PW; ++k) mx[k] = fmaxf(mx[k], xor_lane(mx[k], off));
+                for (int k = 0; k < PW; ++k) mx[k] = go_max(mx[k], xor_lane(mx[k], off));
 #pragma unroll
             for (int k = 0; k < PW; ++k) {
                 const int tt = w + k * kMfmaWaves;

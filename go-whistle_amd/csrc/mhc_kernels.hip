@@ -32,7 +32,7 @@ __global__ __launch_bounds__(64) void rms_unit_kernel(float *dst, const float *x
 // logSumExp (mhc.go:401-417) over k[off], k[off + stride], ...
 __device__ float log_sum_exp(const float *k, int off, int stride, int n) {
     float m = -INFINITY;
-    for (int i = 0; i < n; ++i) m = fmaxf(m, k[off + i * stride]);
+    for (int i = 0; i < n; ++i) m = go_max(m, k[off + i * stride]);
     if (isinf(m)) m = 0.0f;
     float s = 0.0f;
     for (int i = 0; i < n; ++i) s = s + static_cast<float>(exp_f64(static_cast<double>(k[off + i * stride] - m)));
@@ -43,8 +43,8 @@ __device__ float log_sum_exp(const float *k, int off, int stride, int n) {
 __device__ void sinkhorn_one(float *k, double *e, int n, int iters) {
     float lo = k[0], hi = k[0];
     for (int i = 1; i < n * n; ++i) {
-        lo = fminf(lo, k[i]);
-        hi = fmaxf(hi, k[i]);
+        lo = go_min(lo, k[i]);  // slices.Min / slices.Max keep a NaN
+        hi = go_max(hi, k[i]);
     }
     const double spread = static_cast<double>(hi) - static_cast<double>(lo);
     if (!(isinf(spread) || isnan(spread) || spread + 2.0 * iters * log(static_cast<double>(n)) > 700.0)) {

@@ -73,10 +73,12 @@ __global__ __launch_bounds__(64) void zc_rmsnorm_kernel(float *dst, const float 
 }
 
 __global__ __launch_bounds__(256) void rope_kernel(float *x, int heads, int head_dim, const float *cos_t,
-                                                   const float *sin_t, const int32_t *pos, int rows_per_pos) {
+                                                   const float *sin_t, int positions, const int32_t *pos,
+                                                   int rows_per_pos) {
     const int r = blockIdx.x;
     const int half = head_dim / 2;
     const int p = pos[r / rows_per_pos];
+    if (p < 0 || p >= positions) return;  // a position past the tables: the row is left as it is
     const float *cs = cos_t + static_cast<long long>(p) * half, *sn = sin_t + static_cast<long long>(p) * half;
     float *row = x + static_cast<long long>(r) * heads * head_dim;
     for (int e = threadIdx.x; e < heads * half; e += blockDim.x) {
@@ -106,7 +108,12 @@ __device__ __forceinline__ ArgmaxCand argmax_pick(ArgmaxCand a, ArgmaxCand b) {
     return a;
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *v, int n) {
+// With pos: the decode step's position advance rides on the argmax, pos[r]
+// += 1 and the row's self-attention key bound span_hi[r * span_stride] =
+// the new position + 1 (the keys the next step's query sees after its
+// append), so a step needs no separate launches for them.
+__global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *v, int n, int32_t *pos,
+                                                     int32_t *span_hi, int span_stride) {
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *row = v + static_cast<long long>(r) * n;
     ArgmaxCand c{0.0f, INT_MAX};
@@ -155,6 +162,11 @@ __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *
         for (int w = 1; w < 4; ++w) c = argmax_pick(c, ArgmaxCand{sv[w], si[w]});
         const bool nan0 = n > 0 && row[0] != row[0];
         out[r] = (n == 0 || nan0 || c.i == INT_MAX) ? 0 : c.i;
+        if (pos) {
+            const int p = pos[r] + 1;
+            pos[r] = p;
+            span_hi[static_cast<long long>(r) * span_stride] = p + 1;
+        }
     }
 }
 
@@ -218,19 +230,15 @@ __global__ __launch_bounds__(256) void append_kernel(int8_t *q, float *s, const 
     float m = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-        if (lane + 64 * k < width) m = fmaxf(m, fabsf(v[k]));
+        if (lane + 64 * k < width) m = go_max(m, fabsf(v[k]));
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    for (int off = 32; off > 0; off >>= 1) m = go_max(m, __shfl_xor(m, off));
     const float sc = m > 0.0f ? m / 127.0f : 1.0f;
     int8_t *qc = q + b * q_stride + static_cast<long long>(p) * cols + static_cast<long long>(c) * width;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int i = lane + 64 * k;
-        if (i < width) {
-            float r = rintf(v[k] / sc);
-            r = fminf(fmaxf(r, -128.0f), 127.0f);
-            qc[i] = static_cast<int8_t>(static_cast<int>(r));
-        }
+        if (i < width) qc[i] = static_cast<int8_t>(go_int8_code(rintf(v[k] / sc)));
     }
     if (lane == 0) s[b * s_stride + static_cast<long long>(p) * chunks + c] = sc;
 }
@@ -246,15 +254,17 @@ hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int 
 }
 
 hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
-                       const int32_t *pos, int rows_per_pos, hipStream_t s) {
+                       int positions, const int32_t *pos, int rows_per_pos, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rope_kernel, dim3(rows), dim3(256), 0, s, x, heads, head_dim, cos_t, sin_t, pos, rows_per_pos);
+    hipLaunchKernelGGL(rope_kernel, dim3(rows), dim3(256), 0, s, x, heads, head_dim, cos_t, sin_t, positions, pos,
+                       rows_per_pos);
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, hipStream_t s) {
+hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
+                         int span_stride, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, out, v, n);
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, out, v, n, pos, span_hi, span_stride);
     return hipGetLastError();
 }
 

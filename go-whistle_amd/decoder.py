@@ -168,13 +168,20 @@ class Decoder:
         self.tok = z(B, dt=i32)
         self.pos = z(B, dt=i32)
         self.spans_self = z(B, 4, dt=i32)
+        self.spans_self[:, 3] = 1  # keys 0..pos after the first step's append
+        self.steps = 0  # tokens decoded since reset (every stream is at this position)
         hk = c.dim // c.head_dim
         # The cross memory is head-major, [stream][head][frame][code]: every
         # (stream, head) a contiguous block, read as batch * heads one-head
-        # streams (measured 104 -> 95 us per batch-256 call against the
-        # key-major rows Int8Rows uses for the self cache).
+        # streams (faster than the key-major rows Int8Rows uses for the self
+        # cache; profiles/attend_ring_kernel_decode_b256_pmc.txt).
         self.spans_cross = z(B * hk, 4, dt=i32)
         self.spans_cross[:, 3] = c.frames
+        # After a fork, stream b reads the cross memory built for stream
+        # mem_of[b] (State.Fork shares it, decoder.go:223-240): the
+        # attention takes the (stream, head) -> memory-block index.
+        self.mem_of = np.arange(B)
+        self.mem_index = None
         self.x, self.h = z(B, c.dim), z(B, c.dim)
         self.q, self.k, self.v, self.g = z(B, c.dim), z(B, c.dim), z(B, c.dim), z(B, c.dim)
         self.att, self.o = z(B, c.dim), z(B, c.dim)
@@ -218,6 +225,8 @@ class Decoder:
                     # head-major rows of one head each: QuantizeRow per 64-wide chunk, as on the key-major rows
                     hm = tmp.view(c.frames, hk, c.head_dim).transpose(0, 1).contiguous()
                     needle.quantize_rows_dev(dq, ds, hm, hk * c.frames, c.head_dim, c.head_dim)
+        self.mem_of = np.arange(self.batch)
+        self.mem_index = None
         torch.cuda.synchronize()
 
     def encoder_states_device(self, seed, stream):
@@ -235,6 +244,23 @@ class Decoder:
 
         self.tok.copy_(torch.as_tensor(np.asarray(tokens, np.int32), device=self.tok.device))
         self.pos.zero_()
+        self._sync_spans()
+        self.steps = 0
+
+    def _sync_spans(self):
+        """The self-attention key bound of the next step, pos + 1 (the step
+        itself keeps it, in its argmax launch)."""
+        import torch
+
+        torch.add(self.pos, 1, out=self.spans_self[:, 3])
+
+    def _reserve(self, n):
+        """Checks that n more steps fit the caches and RoPE tables: the
+        reference's cache slicing and table lookup panic past them."""
+        from ._lib import CQPanic
+
+        if n < 0 or self.steps + n > self.cfg.max_pos:
+            raise CQPanic(f"decoder: {n} more tokens after {self.steps} exceed max_pos {self.cfg.max_pos}")
 
     def _attend(self, layer, cross, s, rope=None):
         c, B = self.cfg, self.batch
@@ -244,7 +270,10 @@ class Decoder:
             args = [_ptr(self.att), 0, _ptr(self.q), 0, 1, 1, _ptr(self.cross_k[layer]), _ptr(self.cross_ks[layer]), d,
                     d, _ptr(self.cross_v[layer]), _ptr(self.cross_vs[layer]), d, d, n * d, n, _ptr(self.spans_cross),
                     n, float(np.float32(math.sqrt(c.head_dim))), 1, B * hk]
-            check(lib().kv_attend_int8_dev(*args, s))
+            if self.mem_index is None:
+                check(lib().kv_attend_int8_dev(*args, s))
+            else:  # forked streams share their parents' memories
+                check(lib().kv_attend_int8_shared_dev(*args, _ptr(self.mem_index), B * hk, s))
             return
         else:
             kq, ks, vq, vs, spans, n = (self.self_k[layer], self.self_ks[layer], self.self_v[layer],
@@ -259,18 +288,25 @@ class Decoder:
 
     def step(self):
         """One greedy token for every stream: reads tok and pos, writes the
-        next token to tok and advances pos."""
+        next token to tok and advances pos (and the key bound pos + 1)."""
+        self._reserve(1)
         if self.fused:
-            return self._step_fused()
-        return self._step_plain()
+            self._step_fused()
+        else:
+            self._step_plain()
+        self.steps += 1
+
+    def _advance(self, s):
+        """argmax of the logits into tok, pos += 1 and the next step's key
+        bound, in one launch."""
+        c = self.cfg
+        check(lib().nd_argmax_advance_dev(_ptr(self.tok), _ptr(self.logits), self.batch, c.vocab, _ptr(self.pos),
+                                          _ptr(self.spans_self[:, 3]), 4, s))
 
     def _step_fused(self):
-        import torch
-
-        c, B, L = self.cfg, self.batch, lib()
+        c, B = self.cfg, self.batch
         s = cq._stream()
         D, hk = c.dim, c.dim // c.head_dim
-        torch.add(self.pos, 1, out=self.spans_self[:, 3])  # keys 0..pos after this step's append
         self.emb.row_gather_dev(self.x, self.tok, float(self.model.scale))
         rope = (self.cos, self.sin)
         for l in range(c.layers):
@@ -296,24 +332,20 @@ class Decoder:
             cq.gemms_fused_dev([m["w1"]], [self.u], self.x, B, norm_gain=self.gains[3 * l + 2], act=1)
             cq.gemms_fused_dev([m["w2"]], [self.x], self.u, B, resid=self.x)
         cq.gemms_fused_dev([self.emb], [self.logits], self.x, B, norm_gain=self.gains[3 * c.layers])
-        check(L.nd_argmax_dev(_ptr(self.tok), _ptr(self.logits), B, c.vocab, s))
-        self.pos.add_(1)
+        self._advance(s)
 
     def _step_plain(self):
-        import torch
-
         c, B, L = self.cfg, self.batch, lib()
         s = cq._stream()
         D, hk = c.dim, c.dim // c.head_dim
-        torch.add(self.pos, 1, out=self.spans_self[:, 3])  # keys 0..pos after this step's append
         self.emb.row_gather_dev(self.x, self.tok, float(self.model.scale))
         for l in range(c.layers):
             m = self.mats[l]
             check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * l]), B, D, s))
             cq.gemms_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.h, B)
             for t in (self.q, self.k):
-                check(L.nd_rope_dev(_ptr(t), B, c.heads, c.head_dim, _ptr(self.cos), _ptr(self.sin), _ptr(self.pos),
-                                    1, s))
+                check(L.nd_rope_dev(_ptr(t), B, c.heads, c.head_dim, _ptr(self.cos), _ptr(self.sin), c.max_pos,
+                                    _ptr(self.pos), 1, s))
             for src, cq_, cs_ in ((self.k, self.self_k[l], self.self_ks[l]), (self.v, self.self_v[l], self.self_vs[l])):
                 check(L.kv_append_dev(_ptr(cq_), _ptr(cs_), _ptr(src), B, D, c.head_dim, c.max_pos * D,
                                       c.max_pos * hk, _ptr(self.pos), c.max_pos, s))
@@ -334,15 +366,18 @@ class Decoder:
             check(L.nd_add_dev(_ptr(self.x), _ptr(self.o), B * D, s))
         check(L.nd_zcrmsnorm_dev(_ptr(self.h), _ptr(self.x), _ptr(self.gains[3 * c.layers]), B, D, s))
         self.emb.gemm_dev(self.logits, self.h, B)
-        check(L.nd_argmax_dev(_ptr(self.tok), _ptr(self.logits), B, c.vocab, s))
-        self.pos.add_(1)
+        self._advance(s)
 
     def fork(self, parents):
-        """KVCache.Fork for every stream at once (cache.go:62-67), as a beam
-        search reorders its hypotheses: stream b continues from stream
-        parents[b]'s state (its token, position, self-attention rows so far
-        and cross memory), after which every stream extends on its own. The
-        rows are copied (kv_reorder_dev), not shared until written."""
+        """KVCache.Fork / State.Fork for every stream at once (cache.go:
+        62-67, decoder.go:223-240), as a beam search reorders its
+        hypotheses: stream b continues from stream parents[b]'s state (its
+        token, position, self-attention rows so far and cross memory), after
+        which every stream extends on its own. The cross memory is shared,
+        never copied: stream b reads its parent's through the attention's
+        memory index. The self rows so far are copied (kv_reorder_dev), not
+        shared until written, so a fork's cost grows with the decoded
+        positions only, not with the frames."""
         import torch
 
         from ._lib import CQPanic
@@ -351,31 +386,34 @@ class Decoder:
         if len(parents) != B or any(not 0 <= int(p) < B for p in parents):
             raise CQPanic(f"decoder: fork of {B} streams from parents {list(parents)}")
         dev = self.tok.device
-        par = torch.as_tensor(np.asarray(parents, np.int32), device=dev)
+        parents = np.asarray(parents, np.int64)
+        par = torch.as_tensor(parents.astype(np.int32), device=dev)
         self_len = self.pos.index_select(0, par.long()).to(torch.int32)
         hk = c.dim // c.head_dim
-        cross_len = torch.full((B,), hk * c.frames, dtype=torch.int32, device=dev)  # head-major: hk * frames rows of one head
         if getattr(self, "_fork_tmp", None) is None:
-            rows = max(c.max_pos, c.frames)
-            self._fork_tmp = (torch.empty(B * rows * c.dim, dtype=torch.int8, device=dev),
-                              torch.empty(B * rows * hk, dtype=torch.float32, device=dev))
+            self._fork_tmp = (torch.empty(B * c.max_pos * c.dim, dtype=torch.int8, device=dev),
+                              torch.empty(B * c.max_pos * hk, dtype=torch.float32, device=dev))
         tq, ts = self._fork_tmp
         s = cq._stream()
         for l in range(c.layers):
-            for q, sc, cap, cols, ln in ((self.self_k[l], self.self_ks[l], c.max_pos, c.dim, self_len),
-                                         (self.self_v[l], self.self_vs[l], c.max_pos, c.dim, self_len),
-                                         (self.cross_k[l], self.cross_ks[l], hk * c.frames, c.head_dim, cross_len),
-                                         (self.cross_v[l], self.cross_vs[l], hk * c.frames, c.head_dim, cross_len)):
-                check(lib().kv_reorder_dev(_ptr(q), _ptr(sc), _ptr(tq), _ptr(ts), _ptr(par), _ptr(ln), B, cap, cols,
-                                           c.head_dim, s))
+            for q, sc in ((self.self_k[l], self.self_ks[l]), (self.self_v[l], self.self_vs[l])):
+                check(lib().kv_reorder_dev(_ptr(q), _ptr(sc), _ptr(tq), _ptr(ts), _ptr(par), _ptr(self_len), B,
+                                           c.max_pos, c.dim, c.head_dim, s))
+        self.mem_of = self.mem_of[parents]
+        blocks = (self.mem_of[:, None] * hk + np.arange(hk)[None, :]).astype(np.int32).reshape(-1)
+        self.mem_index = torch.as_tensor(blocks, device=dev)
         self.tok.copy_(self.tok.index_select(0, par.long()))
         self.pos.copy_(self.pos.index_select(0, par.long()))
+        self._sync_spans()
 
     def resume(self, n, graph=True):
         """Greedy-decodes n more tokens from the current state; [batch, n]."""
         import torch
 
+        self._reserve(n)
         out = torch.zeros(self.batch, n, dtype=torch.int32, device=self.tok.device)
+        if n == 0:
+            return out
         if not graph:
             for i in range(n):
                 self.step()
@@ -385,35 +423,33 @@ class Decoder:
         for i in range(n):
             g.replay()
             out[:, i] = self.tok
+        self.steps += n
         return out
 
     def decode(self, first_tokens, n, graph=True):
-        """Greedy-decodes n tokens after first_tokens; returns [batch, n]."""
-        import torch
+        """Greedy-decodes n tokens after first_tokens; returns [batch, n].
+        n past max_pos raises CQPanic before anything runs."""
+        from ._lib import CQPanic
 
+        if not 0 <= n <= self.cfg.max_pos:
+            raise CQPanic(f"decoder: {n} tokens exceed max_pos {self.cfg.max_pos}")
         self.reset(first_tokens)
-        out = torch.zeros(self.batch, n, dtype=torch.int32, device=self.tok.device)
-        if not graph:
-            for i in range(n):
-                self.step()
-                out[:, i] = self.tok
-            return out
-        g = self.capture()
-        for i in range(n):
-            g.replay()
-            out[:, i] = self.tok
-        return out
+        return self.resume(n, graph)
 
     def capture(self):
-        """A HIP graph of one step (the state it reads is on the device)."""
+        """A HIP graph of one step (the state it reads is on the device).
+        Replaying it does not advance the host's step count: resume() does."""
         import torch
 
-        pos0, tok0 = self.pos.clone(), self.tok.clone()
+        pos0, tok0, steps0 = self.pos.clone(), self.tok.clone(), self.steps
         self.step()  # kernel attributes are set outside the capture
         torch.cuda.synchronize()
         self.pos.copy_(pos0)
         self.tok.copy_(tok0)
+        self._sync_spans()
+        self.steps = steps0
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.step()
+        self.steps = steps0
         return g  # capturing runs nothing: the state is as before

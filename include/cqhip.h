@@ -209,6 +209,17 @@ int kv_attend_int8_rope_dev(float *out, long long out_stride, const float *q, lo
                             int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans,
                             int nk_max, float scale, int quant_q, int batch, const float *cos_t, const float *sin_t,
                             const int32_t *qpos, void *stream);
+/* kv_attend_int8_dev over caches that streams share: stream b reads the
+ * keys and values of cache kv_index[b] (a device int32 array of `batch`),
+ * one of kv_streams caches kv_stride codes / s_stride scales apart; an
+ * index outside [0, kv_streams) leaves stream b's output untouched. The
+ * beams of one utterance after State.Fork (internal/decoder/decoder.go:
+ * 223-240) share its cross-attention memory, which is never copied. */
+int kv_attend_int8_shared_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                              const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                              int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans,
+                              int nk_max, float scale, int quant_q, int batch, const int32_t *kv_index, int kv_streams,
+                              void *stream);
 
 /* Int8Rows.Append (int8.go:125-141) on a device KV cache for `batch`
  * streams: stream b's row x + b*cols is quantised per chunk of width
@@ -233,12 +244,22 @@ int kv_append_rope_dev(int8_t *q, float *s, const float *x, int batch, int cols,
 int nd_zcrmsnorm_dev(float *dst, const float *x, const float *gain, int rows, int dim, void *stream);
 /* Rope.apply (internal/needle/rope.go:69-81) in place on rows of heads
  * vectors of head_dim: row r uses position pos[r / rows_per_pos] of the
- * (positions x head_dim/2) cos/sin tables (NewRope, rope.go:17-44). */
-int nd_rope_dev(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
+ * (positions x head_dim/2) cos/sin tables (NewRope, rope.go:17-44). A row
+ * whose position is outside [0, positions) is left unchanged (the
+ * reference's table slice would panic there). */
+int nd_rope_dev(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t, int positions,
                 const int32_t *pos, int rows_per_pos, void *stream);
 /* argmax (internal/decoder/greedy.go:181-191) of each row of n: the first
  * index of the largest value. */
 int nd_argmax_dev(int32_t *out, const float *v, int rows, int n, void *stream);
+/* nd_argmax_dev that also advances each stream's decode position, the end
+ * of Decoder.Extend's step (internal/decoder/decoder.go:252-302, greedy.go:
+ * 31-69): pos[r] += 1, and span_hi[r * span_stride] = pos[r] + 1, the key
+ * bound of the next step's self-attention after its append. No reference
+ * counterpart as one call: the device decode step's bookkeeping without
+ * launches of its own. */
+int nd_argmax_advance_dev(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
+                          int span_stride, void *stream);
 /* x = x * sigmoid(x), sigmoid from the amd64 exponent kernel's arithmetic
  * (exp_amd64.s:84-112) on non-positive arguments. No reference
  * counterpart: the synthetic decoder's FFN activation. */

@@ -17,6 +17,9 @@
  *                                     lutLookupGeneric
  * The amd64 assembly (lut_amd64.s) equals these Go routines bit for bit
  * (internal/cq/asm_test.go:11-17), so the Go code is the one definition.
+ * On a NaN input the two differ (VMAXPS keeps or drops a NaN by its lane
+ * and chunk; Go's max and arm64's FMAX keep it): the Go code is followed,
+ * so a group holding a NaN or an Inf gives NaN rows.
  *
  * How each part is pinned without running the reference (tests/):
  *   f16 widen     exhaustive against numpy float16 -> float32
@@ -294,7 +297,7 @@ static float lut_inv(float m) { return m > 0 ? (float)LUT_Q / m : 0; } /* lut.go
 
 static void lut_put(uint8_t *t, int c, float e) {
     /* lut.go:229-233: round half to even, two byte planes */
-    int32_t v = (int32_t)rint((double)e);
+    int32_t v = go_int32_of(rint((double)e)); /* a NaN entry: the integer indefinite */
     t[c] = (uint8_t)(v & 127);
     t[16 + c] = (uint8_t)((v >> 7) + LUT_BIAS);
 }

@@ -53,9 +53,11 @@ float orc_quantize_row(int8_t *q, const float *x, int n) {
     for (int i = 0; i < n; i++) {
         float d = x[i] / s;
         double r = rint((double)d);
+        /* min(max(r, -128), 127) with Go's NaN-propagating max and min: a
+         * NaN stays NaN, and int8 of it is 0 */
         if (r < -128) r = -128;
         if (r > 127) r = 127;
-        q[i] = (int8_t)r;
+        q[i] = go_int8_of(r);
     }
     return s;
 }

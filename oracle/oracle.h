@@ -25,6 +25,16 @@
 extern "C" {
 #endif
 
+/* Go's conversion of a float64 to int32 on amd64 (CVTTSD2SL): truncation,
+ * and the integer indefinite 0x80000000 for a NaN or a value out of range
+ * (C leaves that case undefined). int8(r) is its low byte: 0 for a NaN,
+ * as arm64's FCVTZS gives too. */
+static inline int32_t go_int32_of(double r) {
+    if (r != r || r >= 2147483648.0 || r < -2147483648.0) return INT32_MIN;
+    return (int32_t)r;
+}
+static inline int8_t go_int8_of(double r) { return (int8_t)(uint8_t)((uint32_t)go_int32_of(r) & 0xFFu); }
+
 /* ---- internal/cact: the packed CQ form ---------------------------------- */
 
 /* cact.Packed (internal/cact/packed.go:18-29): Out rows of RowBytes index

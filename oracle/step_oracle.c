@@ -162,10 +162,23 @@ void orc_rms_unit(float *dst, const float *x, int rows, int dim) {
     }
 }
 
+/* Go's built-in max and min for float32, and slices.Max / slices.Min: NaN
+ * when any operand is NaN. */
+static float gomax(float a, float b) {
+    if (a != a || b != b) return NAN;
+    if (a == 0 && b == 0) return signbit(a) ? b : a;
+    return a > b ? a : b;
+}
+static float gomin(float a, float b) {
+    if (a != a || b != b) return NAN;
+    if (a == 0 && b == 0) return signbit(a) ? a : b;
+    return a < b ? a : b;
+}
+
 static float log_sum_exp(const float *k, int off, int stride, int n) {
     /* logSumExp (mhc.go:401-417) */
     float m = -INFINITY;
-    for (int i = 0; i < n; i++) m = fmaxf(m, k[off + i * stride]);
+    for (int i = 0; i < n; i++) m = gomax(m, k[off + i * stride]);
     if (isinf(m)) m = 0.0f;
     float s = 0.0f;
     for (int i = 0; i < n; i++) s += (float)orc_exp64((double)(k[off + i * stride] - m));
@@ -177,8 +190,8 @@ void orc_sinkhorn(float *k, int n, int iters) {
      * spread allows it, else the float32 log domain */
     float lo = k[0], hi = k[0];
     for (int i = 1; i < n * n; i++) {
-        lo = fminf(lo, k[i]);
-        hi = fmaxf(hi, k[i]);
+        lo = gomin(lo, k[i]);
+        hi = gomax(hi, k[i]);
     }
     double spread = (double)hi - (double)lo;
     if (!(isinf(spread) || isnan(spread) || spread + 2.0 * iters * log((double)n) > 700.0)) {

@@ -52,7 +52,7 @@ def test_step_blocks_bit_exact():
     cos, sin = dec.rope_tables(64, 300, 1e5)
     pos = np.array([0, 1, 5, 63, 100, 200, 299], np.int32)
     rd, cd, sd, pd = _t(x.copy()), _t(cos), _t(sin), _t(pos)  # held: a freed temporary's block is reused
-    check(lib().nd_rope_dev(_p(rd), rows, 8, 64, _p(cd), _p(sd), _p(pd), 1, _s()))
+    check(lib().nd_rope_dev(_p(rd), rows, 8, 64, _p(cd), _p(sd), 300, _p(pd), 1, _s()))
     v = g.standard_normal((5, 16384)).astype(np.float32)
     v[1, 3], v[1, 16000] = 40, 40
     v[2] = 1.5
@@ -125,6 +125,8 @@ def test_argmax_edges(n):
 
 @pytest.mark.parametrize("graph", [True, False])
 def test_fork_continues_as_parent(graph):
+    import torch
+
     # KVCache.Fork (cache.go:62-67) for a beam reorder: after 8 tokens, stream
     # b takes stream parents[b]'s state and must go on exactly as that stream
     # does without the fork (its self rows, cross memory, token, position)
@@ -138,10 +140,18 @@ def test_fork_continues_as_parent(graph):
     d.set_memory(9)
     head = d.decode(first, 8, graph=graph).cpu().numpy()
     assert np.array_equal(head, full[:, :8])
+    cross = [t.clone() for t in d.cross_k + d.cross_vs]
     d.fork(parents)
+    # the memories are shared through the index, not copied (State.Fork,
+    # decoder.go:223-240): the arrays are as they were
+    assert all(torch.equal(a, b) for a, b in zip(cross, d.cross_k + d.cross_vs))
+    assert list(d.mem_of) == parents
     tail = d.resume(8, graph=graph).cpu().numpy()
     for b, p in enumerate(parents):
         assert list(tail[b]) == list(full[p, 8:]), (b, p)
+    # a second fork composes: stream b now reads the memory of parents[p2[b]]
+    d.fork([1, 1, 3, 0])
+    assert list(d.mem_of) == [parents[1], parents[1], parents[3], parents[0]]
     with pytest.raises(Exception):
         d.fork([0, 1, 2])
 
@@ -201,6 +211,28 @@ def test_full_decoder_batch1_200_tokens():
 
 
 def test_full_decoder_batch256_streams():
+    # config 5 at batch 256: the whole 200-token run, five streams checked
+    # (each against its own C restatement), among them the last
     cfg = dec.DecoderConfig()
-    print("full decoder, batch 256, 40 tokens", flush=True)
-    _run(cfg, 9, 256, list(range(256)), 40, [0, 131, 255], generator="device")
+    print("full decoder, batch 256, 200 tokens", flush=True)
+    _run(cfg, 9, 256, list(range(256)), 200, [0, 77, 131, 200, 255], generator="device")
+
+
+def test_argmax_advances_positions():
+    # nd_argmax_advance_dev: the argmax of nd_argmax_dev, pos += 1 and the
+    # key bound pos + 1 in the spans' fourth column, nothing else touched
+    import torch
+
+    g = synth.rng(3)
+    rows, n = 6, 16384
+    v = g.standard_normal((rows, n)).astype(np.float32)
+    pos = np.array([0, 5, 9, 200, 1, 7], np.int32)
+    spans = g.integers(0, 9, size=(rows, 4)).astype(np.int32)
+    am, vd, pd, sd = torch.zeros(rows, dtype=torch.int32, device="cuda"), _t(v), _t(pos), _t(spans)
+    check(lib().nd_argmax_advance_dev(_p(am), _p(vd), rows, n, _p(pd), _p(sd[:, 3]), 4, _s()))
+    torch.cuda.synchronize()
+    assert list(am.cpu().numpy()) == list(orc.argmax(v, rows, n))
+    assert list(pd.cpu().numpy()) == list(pos + 1)
+    want = spans.copy()
+    want[:, 3] = pos + 2
+    assert np.array_equal(sd.cpu().numpy(), want)

@@ -123,7 +123,7 @@ def test_append_with_rope():
     s1 = torch.zeros(B, cap, heads, device="cuda")
     q2, s2 = q1.clone(), s1.clone()
     xr = x.clone()
-    check(lib().nd_rope_dev(_p(xr), B, heads, hd, _p(cos), _p(sin), _p(pos), 1, _s()))
+    check(lib().nd_rope_dev(_p(xr), B, heads, hd, _p(cos), _p(sin), cos.shape[0], _p(pos), 1, _s()))
     needle.append_dev(q1, s1, xr, B, D, hd, cap * D, cap * heads, pos, cap)
     needle.append_dev(q2, s2, x, B, D, hd, cap * D, cap * heads, pos, cap, rope=(cos, sin))
     torch.cuda.synchronize()
@@ -225,7 +225,7 @@ def test_attention_with_query_rope(batch, n, vd):
     kw = dict(batch=batch, q_stride=heads * qk, kv_stride=stride, s_stride=n * heads, out_stride=heads * vd)
     args = (1, heads, kq, ks, heads * qk, qk, vq, vs, heads * vd, vd, spans, n, np.float32(math.sqrt(qk)), True)
     qr = q.clone()
-    check(lib().nd_rope_dev(_p(qr), batch, heads, qk, _p(cos), _p(sin), _p(qpos), 1, _s()))
+    check(lib().nd_rope_dev(_p(qr), batch, heads, qk, _p(cos), _p(sin), cos.shape[0], _p(qpos), 1, _s()))
     want = torch.zeros(batch * heads * vd, device="cuda")
     got = torch.zeros_like(want)
     needle.attend_int8_dev(want, qr, *args, **kw)

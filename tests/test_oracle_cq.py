@@ -414,3 +414,25 @@ def test_lut2_table_entry_is_unfused():
     orc.lib().orc_lut_tables2(orc.u8p(tab), orc.fp(xh), 8, orc.fp(cb), cb_max)
     c, v = hit
     assert 128 * (int(tab[16 + c]) - 64) + int(tab[c]) == v
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("special", ["nan", "inf"])
+def test_lut_nan_or_inf_input_gives_nan_rows(bits, special):
+    # lutTables{2,4}Generic (lut.go:239-282) reduce the group bound with Go's
+    # max, which keeps a NaN: a group holding one has M = NaN, lutInv gives 0
+    # (NaN > 0 fails) and the step is NaN, so every row's y is NaN. +Inf
+    # spreads through the rotation to every value of its group: M = Inf,
+    # lutInv 8191/Inf = 0, each entry Inf * 0 = NaN (an integer of 0 after
+    # lutPut), the step Inf and y = 0 * Inf = NaN. (The amd64 kernel's
+    # VMAXPS keeps or drops a NaN depending on its lane and chunk, an
+    # artefact; arm64's FMAX keeps it, as the generic Go does.)
+    g = synth.rng(bits)
+    p = synth.random_packed(g, 70, 384, 128, bits, sigma=0.05)
+    m = orc.OMatrix.new(p)
+    x = g.standard_normal(384).astype(np.float32)
+    x[200] = np.float32(special)
+    y = m.gemm(x, 1, orc.LUT)
+    assert np.isnan(y).all()
+    x[200] = 1.0
+    assert np.isfinite(m.gemm(x, 1, orc.LUT)).all()

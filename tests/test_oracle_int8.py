@@ -22,6 +22,47 @@ def test_quantize_row_hand_vectors():
     assert s == 1 and list(q) == [0, 0, 0, 0]
 
 
+NAN, INF = np.float32("nan"), np.float32("inf")
+
+
+@pytest.mark.parametrize("row,scale,codes", [
+    # Go's max keeps a NaN (int8.go:40-42): the bound is NaN, m > 0 fails,
+    # s = 1; codes are RNE(x) clamped by Go's NaN-propagating min/max, and
+    # int8 of a NaN is 0 (amd64's integer indefinite 0x80000000, low byte 0)
+    ([1, NAN, -2, 3.6, 200, -1000], 1, [1, 0, -2, 4, 127, -128]),
+    ([NAN, INF, -INF, 0.4, 2.5], 1, [0, 127, -128, 0, 2]),
+    # an infinite bound: s = Inf, x / Inf is +-0 for finite x and NaN for
+    # +-Inf, so every code is 0
+    ([INF, 1, -1, 1e30], INF, [0, 0, 0, 0]),
+    ([-INF, 5], INF, [0, 0]),
+    ([NAN], 1, [0]),
+])
+def test_quantize_row_nan_and_inf(row, scale, codes):
+    q, s = orc.quantize_row(np.array(row, np.float32))
+    assert (s == scale) and list(q) == codes
+
+
+def test_fake_quant_nan_and_inf():
+    # float32(q) * s: a NaN row comes back as its clamped codes (scale 1), an
+    # infinite row as 0 * Inf = NaN everywhere
+    got = orc.fake_quant(np.array([NAN, 2.5, -300, 1, INF, 0.5], np.float32), 6, 3)
+    assert list(got[:3]) == [0, 2, -128]
+    assert np.isnan(got[3:]).all()
+
+
+def test_softmax_nan_and_inf():
+    # softmaxInPlace (load.go:128-138): Go's max keeps a NaN, so one NaN logit
+    # makes every weight NaN; a +Inf logit gives Inf - Inf = NaN at its key
+    # and a NaN sum; -Inf logits beside finite ones weigh 0
+    for variant in (0, 1):
+        s = orc.softmax(np.array([0, -1, NAN, 2, 0.5, 1, 1, 1, 3], np.float32), variant)
+        assert np.isnan(s).all()
+        s = orc.softmax(np.array([0, INF, 2, 0.5, 1, 1, 1, 3, 4], np.float32), variant)
+        assert np.isnan(s).all()
+        s = orc.softmax(np.array([0, -INF, 0, -INF, 0, 0, 0, 0, 0], np.float32), variant)
+        assert s[1] == 0 and s[3] == 0 and np.all(s[[0, 2, 4, 5, 6, 7, 8]] == np.float32(1 / 7))
+
+
 @pytest.mark.parametrize("n", [1, 7, 48, 64, 2048])
 @pytest.mark.parametrize("scale", [1e-6, 1, 1e4])
 def test_quantize_row_invariants(n, scale):
