@@ -75,6 +75,8 @@ SIGNATURES = {
     "nd_fake_quant_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_int, c_int, c_void_p]),
     "kv_reorder_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                c_void_p]),
+    "kv_reorder_noalloc_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                       c_void_p]),
     "nd_add_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_void_p]),
     "nd_sigmoid_gate_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_void_p]),
     "nd_rms_unit_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),

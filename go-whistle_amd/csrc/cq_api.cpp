@@ -1012,6 +1012,70 @@ int kv_reorder_dev(int8_t *q, float *s, int8_t *tmp_q, float *tmp_s, const int32
     return CQ_OK;
 }
 
+// ---- the allocation-free reorder ------------------------------------------
+//
+// kv_reorder_noalloc_dev keeps kv_reorder_dev's temporaries in `scratch`, a
+// file-scope device array of kScratchBytes that every GPU the library runs
+// on holds until the process ends. Host code never uses the array's name as
+// an address (on the host it is only a stand-in for the symbol): the device
+// address comes from hipGetSymbolAddress, once per device, with that device
+// current, and is kept per device. Every call on one GPU shares that GPU's
+// array, so calls that overlap on one GPU (different streams, or threads
+// without ordering) race; the reorder needs nothing in it cleared.
+}  // extern "C"
+
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_ptr[kMaxDevices];  // per device: the array's device address
+
+int scratch_of_current_device(unsigned char **out) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev), "current device");
+    if (dev < 0 || dev >= kMaxDevices) return fail(CQ_ERR_DEVICE, "needle: device %d has no scratch slot", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "scratch address");
+        g_scratch_ptr[dev] = static_cast<unsigned char *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return CQ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int kv_reorder_noalloc_dev(int8_t *q, float *s, const int32_t *parent, const int32_t *len, int streams, int cap,
+                           int cols, int width, void *stream) {
+    if (width <= 0 || cols % width != 0)
+        return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);
+    if (streams < 0 || cap < 0) return fail(CQ_ERR_MISUSE, "needle: %d streams of %d rows", streams, cap);
+    if (streams == 0 || cap == 0) return CQ_OK;
+    if (!q || !s || !parent || !len) return fail(CQ_ERR_MISUSE, "needle: reorder needs caches, parents and lengths");
+    const int sb = (cols / width) * static_cast<int>(sizeof(float));
+    const size_t rows = static_cast<size_t>(streams) * static_cast<size_t>(cap);
+    const size_t qbytes = align256(rows * static_cast<size_t>(cols)), need = qbytes + rows * static_cast<size_t>(sb);
+    if (need > kScratchBytes)
+        return fail(CQ_ERR_MISUSE,
+                    "needle: a reorder of %d streams of %d rows of %d codes needs %zu bytes of temporaries; the "
+                    "allocation-free form holds %zu (use kv_reorder_dev with temporaries of your own)",
+                    streams, cap, cols, need, kScratchBytes);
+    unsigned char *base = nullptr;
+    if (int e = scratch_of_current_device(&base)) return e;
+    int8_t *tmp_q = reinterpret_cast<int8_t *>(base);
+    float *tmp_s = reinterpret_cast<float *>(base + qbytes);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    HIP_TRY(launch_gather_rows(tmp_q, q, parent, len, streams, cap, cols, st), "reorder gather");
+    HIP_TRY(launch_gather_rows(tmp_s, s, parent, len, streams, cap, sb, st), "reorder gather");
+    HIP_TRY(launch_gather_rows(q, tmp_q, nullptr, len, streams, cap, cols, st), "reorder copy back");
+    HIP_TRY(launch_gather_rows(s, tmp_s, nullptr, len, streams, cap, sb, st), "reorder copy back");
+    return CQ_OK;
+}
+
 int nd_fake_quant_dev(float *dst, const float *x, long long rows, int cols, int width, void *stream) {
     if (width <= 0 || cols % width != 0)
         return fail(CQ_ERR_MISUSE, "needle: int8 rows of %d in chunks of %d", cols, width);

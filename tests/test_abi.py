@@ -90,3 +90,14 @@ def test_no_device_fails_loudly():
 def test_quantize_rows_misuse_through_the_abi():
     with pytest.raises(gw.CQPanic):
         gw.needle.QuantizeRows(np.zeros(96, np.float32), 96, 40)
+
+
+def test_noalloc_reorder_refuses_oversize_before_the_device():
+    # kv_reorder_noalloc_dev checks its temporaries against its 64 MiB array
+    # before any device call: 256 streams x 512 rows x 512 codes exceed it
+    from ctypes import c_void_p
+
+    p = c_void_p(256)  # never dereferenced: the size check comes first
+    with pytest.raises(gw.CQPanic) as e:
+        _lib.check(_lib.lib().kv_reorder_noalloc_dev(p, p, p, p, 256, 512, 512, 64, None))
+    assert "67108864" in str(e.value)
