@@ -160,9 +160,12 @@ def batched_gemm_leg(gw, torch, reps=5):
                 us = e0.elapsed_time(e1) * 1e3 / reps
                 path = m.gemm_path(M)
                 rec = {"path": path, "us": round(us, 2), "dense_TFLOPs": round(2.0 * M * o * i / us / 1e6, 2)}
-                if path == "lut-mfma":
+                if path in ("lut-mfma", "lut-mfma-split"):
+                    # one 32x32x32 int8 product per 32 weight rows, 32 activations and table position
+                    # (the 512-row form pads activations to its 64-wide tiles, the split form to 32)
                     positions = (i // GROUP) * (2 * GROUP * bits // 8)
-                    mfmas = -(-o // 64) * -(-M // 64) * positions * 4
+                    tile = 64 if path == "lut-mfma" else 32
+                    mfmas = -(-o // 64) * 2 * (-(-M // tile) * tile // 32) * positions
                     ops = mfmas * 2 * 32 * 32 * 32
                     rec["mfma_TOPs"] = round(ops / us / 1e6, 1)
                     rec["mfma_util"] = round(ops / (us * 1e-6) / INT8_PEAK_OPS, 4)

@@ -403,6 +403,112 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
     return CQ_OK;
 }
 
+// ---- the MFMA form split over groups ----
+//
+// Its workspace holds the groups' float terms between the two launches.
+// Each host thread has its own per device, grown when a product needs more
+// and never freed or moved while the process runs (a captured graph keeps
+// the address it recorded), so products queued from different threads do
+// not share one; products queued from one thread on several streams at once
+// would.
+struct SplitWorkspace {
+    void *buf = nullptr;
+    size_t size = 0;
+};
+thread_local SplitWorkspace t_split[64];
+
+int split_workspace(size_t bytes, float **out) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev), "current device");
+    if (dev < 0 || dev >= 64) return fail(CQ_ERR_DEVICE, "cq: device %d has no workspace slot", dev);
+    SplitWorkspace &w = t_split[dev];
+    if (w.size < bytes) {
+        void *p = nullptr;
+        const size_t want = std::max(bytes, 2 * w.size);
+        HIP_TRY(hipMalloc(&p, want), "hipMalloc split workspace");
+        w.buf = p;  // the smaller one stays allocated: a graph may still use it
+        w.size = want;
+    }
+    *out = static_cast<float *>(w.buf);
+    return CQ_OK;
+}
+
+constexpr int kSplitMinRows = 320;  // activations from which the split form pays
+
+// The split form pays where the 512-row MFMA form leaves CUs idle and the
+// lut kernel repeats every table lookup per activation: some hundreds of
+// activations or more (measured on MI355X: 375 and 1500 encoder frames of
+// 512x2048 CQ4 52 -> 40 us and 142 -> 86 us, 2048x512 CQ4 at 375 46 -> 40
+// us). At the decode step's 256 activations its workgroups (one wavefront
+// per SIMD, tables and one-hot operands built per 32 activations) lose to
+// the lut kernel (a 512x512 CQ4 product 12 -> 28 us), and so do 2-bit
+// products of four groups (2048x512 CQ2 at 375: 27 -> 30 us). Its grid
+// (256-row tiles x 32-activation tiles x groups) must also reach a quarter
+// of the CUs.
+bool split_pays(cq_matrix *const *ms, int n, int rows) {
+    if (rows < kSplitMinRows || n > kKernargJobs) return false;
+    const CqStore &s0 = *ms[0]->st;
+    if (!mfma_geometry_supported(s0.width, s0.group)) return false;
+    if (s0.width == 2 && s0.groups <= 4) return false;
+    const int rpw = mfma_split_rows_per_workgroup() / kBlockRows;
+    long long wgs = 0;
+    for (int k = 0; k < n; ++k) {
+        if (!uses_lut(ms[k])) return false;
+        const int nblk = (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
+        wgs += (nblk + rpw - 1) / rpw;
+    }
+    const int ta = mfma_split_activations();
+    wgs *= static_cast<long long>((rows + ta - 1) / ta) * s0.groups;
+    return 4 * wgs >= device_info().cus;
+}
+
+int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
+              const Fuse *fz = nullptr) {
+    const CqStore &s0 = *ms[0]->st;
+    const int ta = mfma_split_activations();
+    const int rpw = mfma_split_rows_per_workgroup() / kBlockRows;
+    const int max_rows = 65535 * ta;
+    for (int r0 = 0; r0 < rows; r0 += max_rows) {
+        const int nr = std::min(max_rows, rows - r0);
+        LutLaunch a;
+        std::memset(&a, 0, sizeof a);
+        int wg = 0, fold = 0;
+        size_t terms = 0;
+        for (int k = 0; k < n; ++k) {
+            if (ms[k]->out == 0) continue;
+            JobDesc &j = a.jobs[a.njobs];
+            fill_job(j, ms[k], x + static_cast<long long>(r0) * s0.in, dsts[k] + static_cast<long long>(r0) * ms[k]->out,
+                     nr);
+            apply_fuse(j, fz, k);
+            if (j.resid) j.resid += static_cast<long long>(r0) * j.resid_stride;
+            if (j.xgate) j.xgate += static_cast<long long>(r0) * j.x_stride;
+            if (j.app_q) {
+                j.app_q += static_cast<long long>(r0) * j.app_q_stride;
+                j.app_s += static_cast<long long>(r0) * j.app_s_stride;
+                j.app_pos += r0;
+            }
+            a.wg0[a.njobs] = wg;
+            a.fold0[a.njobs] = fold;
+            wg += (j.nblk + rpw - 1) / rpw;
+            fold += j.nblk;
+            terms += static_cast<size_t>(j.groups) * nr * j.nblk * kBlockRows;
+            ++a.njobs;
+        }
+        if (a.njobs == 0 || nr == 0) return CQ_OK;
+        float *ws = nullptr;
+        if (int e = split_workspace(terms * sizeof(float), &ws)) return e;
+        size_t off = 0;
+        for (int k = 0; k < a.njobs; ++k) {
+            a.term[k] = ws + off;
+            off += static_cast<size_t>(a.jobs[k].groups) * nr * a.jobs[k].nblk * kBlockRows;
+        }
+        HIP_TRY(launch_lut_mfma_split(a, s0.width, wg, (nr + ta - 1) / ta, s0.groups, fold, nr, stream),
+                "lut mfma split launch");
+    }
+    for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
+    return CQ_OK;
+}
+
 // Launches the product of up to kMaxMatrices views sharing their tables.
 int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
                 const Fuse *fz = nullptr) {
@@ -411,6 +517,7 @@ int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x,
     if (mode == kModeLut && n <= kKernargJobs && mfma_geometry_supported(s0.width, s0.group) &&
         mfma_pays(ms, n, rows))
         return run_mfma(ms, n, dsts, x, rows, stream, fz);
+    if (mode == kModeLut && split_pays(ms, n, rows)) return run_split(ms, n, dsts, x, rows, stream, fz);
     if (mode == kModeLut && lut_fits(s0) && n <= kKernargJobs) return run_lut(ms, n, dsts, x, rows, stream, fz);
     if (fz && fz->any())
         return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel (this is %s, group bytes %d)",
@@ -643,6 +750,7 @@ const char *cq_gemm_path(const cq_matrix *m, int rows) {
     if (!m || !uses_lut(m)) return "nibble4";
     cq_matrix *mm = const_cast<cq_matrix *>(m);
     if (mfma_geometry_supported(m->st->width, m->st->group) && mfma_pays(&mm, 1, rows)) return "lut-mfma";
+    if (split_pays(&mm, 1, rows)) return "lut-mfma-split";
     return "lut";
 }
 
@@ -757,6 +865,8 @@ int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const f
         f.app_pos = pos;
         f.app_cap = cap;
     }
+    // the split MFMA form appends in its fold (whole 64-row blocks, checked above)
+    if (split_pays(ms, n, rows)) return run_split(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
     return run_lut(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
 }
 

@@ -403,7 +403,312 @@ hipError_t launch_mfma_t(const LutLaunch &a, int wg, int act_tiles, hipStream_t 
     return hipGetLastError();
 }
 
+// ---- The split form: one group per workgroup, then a fold in group order ----
+//
+// For products whose 512-row workgroups would leave most CUs idle (the
+// decode step's 512- and 2048-row matrices at a few hundred activations, the
+// encoder's 375 frames): a workgroup of 4 wavefronts owns 256 weight rows (a
+// 64-row block per wavefront), 32 activations and ONE group g. It rotates
+// the group, builds its tables and runs its MFMAs as lut_mfma_kernel does,
+// then writes the group's float terms float32(S) * (norm * step) (the lut
+// kernel's term, rounded the same way) to the workspace, [g][activation]
+// [row]. mfma_fold_kernel then adds an output's terms in group order from 0
+// (lut.go:297-310) and applies the fused epilogue: bit for bit the lut
+// kernel's result.
+constexpr int kSplitWaves = 4;
+constexpr int kSplitThreads = 64 * kSplitWaves;
+constexpr int kSplitTa = 32;  // activations per workgroup: one 32-wide MFMA tile
+
+template <int BITS>
+__global__ __launch_bounds__(kSplitThreads) void lut_mfma_split_kernel(LutLaunch a) {
+    using M = MfmaGeo<BITS>;
+    constexpr int G = M::G, AP = M::AP, CK = M::CK, TA = kSplitTa;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float *av = reinterpret_cast<float *>(smem);                    // [TA][AP] scaled rotated group
+    float *stp = av + TA * AP;                                       // [TA] steps of the group
+    int8_t *tab = reinterpret_cast<int8_t *>(stp + TA);              // [2][CK][2][TA][16] table planes
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
+
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kKernargJobs; ++k)
+        if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.wg0[k]) jb = k;
+    const JobDesc &J = a.jobs[jb];
+    const int blk = (static_cast<int>(blockIdx.x) - a.wg0[jb]) * kSplitWaves + w;  // this wavefront's block
+    const bool rows_here = blk < J.nblk;
+    const int gblk = J.blk0 + blk;
+    const int t0 = blockIdx.y * TA;
+    const int g = blockIdx.z;
+    const int groups = J.groups;
+
+    // Fused ZCRMSNorm of the activation rows (norm.go:53-109): the
+    // workgroup's activations' divisors over their whole rows.
+    __shared__ double zpart[4 * TA];
+    __shared__ float zrms[TA];
+    if (J.ngain) {
+        for (int e = tid; e < 4 * TA; e += kSplitThreads) {
+            const int t = t0 + e / 4;
+            zpart[e] = t < J.rows ? zc_partial(J.x + static_cast<long long>(t) * J.x_stride, J.in, e % 4) : 0.0;
+        }
+        __syncthreads();
+        for (int e = tid; e < TA; e += kSplitThreads)
+            zrms[e] = zc_rms(zpart[4 * e], zpart[4 * e + 1], zpart[4 * e + 2], zpart[4 * e + 3], J.in);
+        __syncthreads();
+    }
+
+    // The group's index bytes of the wavefront's rows: UPG 16-byte units,
+    // issued before the rotation so that they land under it.
+    uint32_t idx[M::UPG][2][4];
+#pragma unroll
+    for (int u = 0; u < M::UPG; ++u)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            if (rows_here) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(
+                    J.idx + ((static_cast<size_t>(gblk) * J.units + g * M::UPG + u) * 64 + rt * 32 + l32) * 16);
+                idx[u][rt][0] = v.x; idx[u][rt][1] = v.y; idx[u][rt][2] = v.z; idx[u][rt][3] = v.w;
+            } else {
+                idx[u][rt][0] = idx[u][rt][1] = idx[u][rt][2] = idx[u][rt][3] = 0u;
+            }
+        }
+    float nrm[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+        nrm[rt] = rows_here ? __half2float(__ushort_as_half(
+                                  J.norm[(static_cast<size_t>(gblk) * groups + g) * 64 + rt * 32 + l32]))
+                            : 0.0f;
+
+    // 1. Rotation and bound of group g of each activation (lut.go:158-178),
+    // TA / 4 activations per wavefront, their butterflies interleaved.
+    constexpr int PW = TA / kSplitWaves;
+    {
+        float v[PW][2];
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int tt = w + k * kSplitWaves, t = t0 + tt;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int col = g * G + e * 64 + lane;
+                float xv = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
+                if (J.xgate && t < J.rows && col < J.in)  // Attention.output's gate (attention.go:245-249)
+                    xv = xv * gate_sigmoid(J.xgate[static_cast<long long>(t) * J.x_stride + col]);
+                if (J.ngain && t < J.rows && col < J.in) {
+                    const float gx = J.ngain[col] * xv;
+                    xv = gx / zrms[tt];
+                }
+                v[k][e] = xv;
+            }
+        }
+#pragma unroll
+        for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
+#pragma unroll
+            for (int k = 0; k < PW; ++k)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float p = xor_lane(v[k][e], h);
+                    v[k][e] = (lane & h) ? p - v[k][e] : v[k][e] + p;
+                }
+        }
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {  // stage h = 64 within the lane
+            const float p = v[k][0], q = v[k][1];
+            v[k][0] = p + q;
+            v[k][1] = p - q;
+        }
+        float mx[PW];
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            mx[k] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                if constexpr (BITS == 4) {
+                    mx[k] = go_max(mx[k], fabsf(v[k][e]));
+                } else {
+                    const float p = xor_lane<1>(v[k][e]);
+                    const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                    mx[k] = go_max(mx[k], s2);
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int k = 0; k < PW; ++k) mx[k] = go_max(mx[k], xor_lane(mx[k], off));
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int tt = w + k * kSplitWaves;
+            const float m = J.cb_max * mx[k];
+            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[k][e] * inv;
+            if (lane == 0) stp[tt] = m * J.lut_step;
+        }
+    }
+
+    // 2. The group's tables, CK positions a chunk, two planes each (as
+    // lut_mfma_kernel's build, TA activations).
+    auto build = [&](int c, int buf) {
+        for (int e = tid; e < TA * CK; e += kSplitThreads) {
+            const int t = e % TA, jc = e / TA;
+            const int j = c * CK + jc;
+            uint32_t b[16];
+            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
+                const float x = av[t * AP + j];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const float f = J.cb[q] * x;
+                    b[q] = rne_bits(f);
+                }
+            } else {  // lutTables2Generic (lut.go:239-258): code q = hi << 2 | lo
+                const float x0 = av[t * AP + 2 * j], x1 = av[t * AP + 2 * j + 1];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const float l = J.cb[q & 3] * x0, h = J.cb[q >> 2] * x1;
+                    const float s = l + h;
+                    b[q] = rne_bits(s);
+                }
+            }
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) planes4(b[4 * q], b[4 * q + 1], b[4 * q + 2], b[4 * q + 3], lo[q], hi[q]);
+            int8_t *dst = tab + ((static_cast<size_t>(buf) * CK + jc) * 2 * TA + t) * 16;
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4 *>(dst + TA * 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        }
+    };
+    lds_barrier();
+    build(0, 0);
+    i32x16 acc[2] = {i32x16{}, i32x16{}};
+    lds_barrier();
+
+    // 3. Per chunk: the next chunk's tables built while this one's MFMAs run.
+    const unsigned long long val = half ? 64ull : 1ull;
+    constexpr int CW = M::CW;
+#pragma unroll
+    for (int u = 0; u < M::UPG; ++u) {
+#pragma unroll
+        for (int q = 0; q < 4 / CW; ++q) {
+            const int c = (4 / CW) * u + q;
+            if (c + 1 < M::NCH) build(c + 1, (c + 1) & 1);
+            if (rows_here) {
+                // lane half 0 reads a position's l plane, half 1 its h plane
+                const int8_t *tb = tab + (static_cast<size_t>(c & 1) * CK * 2 + half) * TA * 16;
+                i32x4 A[2];
+                A[0] = *reinterpret_cast<const i32x4 *>(tb + l32 * 16);
+#pragma unroll
+                for (int jc = 0; jc < CK; ++jc) {
+                    if (jc + 1 < CK)
+                        A[(jc + 1) & 1] =
+                            *reinterpret_cast<const i32x4 *>(tb + (static_cast<size_t>(jc + 1) * 2 * TA + l32) * 16);
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) {
+                        // position jc: word jc / 8 of the chunk, byte (jc % 8) / 2, nibble jc % 2
+                        const uint32_t n = (idx[u][rt][q * CW + jc / 8] >> (4 * (jc % 8))) & 15u;
+                        acc[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[jc & 1], one_hot(n, val), acc[rt], 0, 0, 0);
+                    }
+                }
+            }
+            lds_barrier();
+        }
+    }
+
+    // 4. The group's terms float32(S) * (norm * step) (lut.go:297-310), to
+    // the workspace: [g][activation][64 * nblk rows] of this job.
+    if (rows_here) {
+        const long long rs = static_cast<long long>(J.nblk) * 64;
+        float *tg = a.term[jb] + static_cast<long long>(g) * J.rows * rs;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int tt = (i >> 2) * 8 + half * 4 + (i & 3), t = t0 + tt;
+            if (t >= J.rows) continue;
+            const float step = stp[tt];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const float coef = nrm[rt] * step;
+                tg[static_cast<long long>(t) * rs + blk * 64 + rt * 32 + l32] = static_cast<float>(acc[rt][i]) * coef;
+            }
+        }
+    }
+}
+
+// The fold of the split form: one wavefront per (activation, 64-row block),
+// lane = row: y = 0, then y = y + term[g] for g in order (lut.go:297-310),
+// then the lut kernel's epilogue: the int8 append of the block as a head
+// (Int8Rows.Append, int8.go:36-55, after RoPE at the stream's position,
+// rope.go:69-81), and y, with the residual add or SiLU, for the view's rows.
+__global__ __launch_bounds__(256) void mfma_fold_kernel(LutLaunch a) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kKernargJobs; ++k)
+        if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.fold0[k]) jb = k;
+    const JobDesc &J = a.jobs[jb];
+    const int blk = static_cast<int>(blockIdx.x) - a.fold0[jb];
+    const int t = blockIdx.y * 4 + w;
+    if (blk >= J.nblk || t >= J.rows) return;
+    const long long rs = static_cast<long long>(J.nblk) * 64;
+    const float *tp = a.term[jb] + static_cast<long long>(t) * rs + blk * 64 + lane;
+    float y = 0.0f;
+    for (int g = 0; g < J.groups; ++g) y = y + tp[static_cast<long long>(g) * J.rows * rs];
+
+    const int row = (J.blk0 + blk) * 64;  // root row of lane 0
+    if (J.app_q) {
+        const int p = J.app_pos[t];
+        if (p >= 0 && p < J.app_cap) {
+            float v = y;
+            if (J.app_cos) {
+                const float o = xor_lane<32>(v);
+                const int jj = lane & 31;
+                const float x1 = lane < 32 ? v : o, x2 = lane < 32 ? o : v;
+                float o1, o2;
+                rope_pair(x1, x2, J.app_cos[p * 32 + jj], J.app_sin[p * 32 + jj], o1, o2);
+                v = lane < 32 ? o1 : o2;
+            }
+            float m = fabsf(v);
+#pragma unroll
+            for (int h = 32; h > 0; h >>= 1) m = go_max(m, xor_lane(m, h));
+            const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+            const int r0 = row - J.row0;  // view row of the head's first value
+            int8_t *qp = J.app_q + static_cast<long long>(t) * J.app_q_stride + static_cast<long long>(p) * J.out;
+            qp[r0 + lane] = static_cast<int8_t>(go_int8_code(rintf(v / sc)));
+            if (lane == 0)
+                J.app_s[static_cast<long long>(t) * J.app_s_stride + static_cast<long long>(p) * (J.out >> 6) +
+                        (r0 >> 6)] = sc;
+        }
+    }
+    const int r = row + lane;
+    if (r >= J.row0 && r < J.row0 + J.out) {
+        float out = y;
+        if (J.resid)
+            out = J.resid[static_cast<long long>(t) * J.resid_stride + (r - J.row0)] + out;
+        else if (J.act == 1)
+            out = silu_value(out);
+        J.y[static_cast<long long>(t) * J.y_stride + (r - J.row0)] = out;
+    }
+}
+
+template <int BITS>
+hipError_t launch_split_t(const LutLaunch &a, int wg, int act_tiles, int groups, hipStream_t s) {
+    const size_t lds = mfma_lds_bytes<BITS, kSplitTa>();
+    hipLaunchKernelGGL((lut_mfma_split_kernel<BITS>), dim3(wg, act_tiles, groups), dim3(kSplitThreads), lds, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+int mfma_split_rows_per_workgroup() { return 64 * kSplitWaves; }
+int mfma_split_activations() { return kSplitTa; }
+
+hipError_t launch_lut_mfma_split(const LutLaunch &a, int bits, int wg, int act_tiles, int groups, int fold_blocks,
+                                 int rows, hipStream_t s) {
+    if (wg <= 0 || act_tiles <= 0 || groups <= 0 || fold_blocks <= 0 || rows <= 0) return hipSuccess;
+    hipError_t e = bits == 4 ? launch_split_t<4>(a, wg, act_tiles, groups, s)
+                   : bits == 2 ? launch_split_t<2>(a, wg, act_tiles, groups, s)
+                               : hipErrorInvalidValue;
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(mfma_fold_kernel, dim3(fold_blocks, (rows + 3) / 4), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
 
 bool mfma_geometry_supported(int bits, int group) { return group == 128 && (bits == 2 || bits == 4); }
 
