@@ -749,16 +749,21 @@ __device__ __forceinline__ void block_sync() {
 }
 
 constexpr int kChainVd = 64;  // value codes per head of the chain kernel: one per lane of wavefront 0
+constexpr int kProdKeys = 48;    // keys per step of the resident chain's product pipeline
+constexpr int kProdStride = 52;  // floats per output row of a product buffer (48 keys, padded)
+constexpr int kProdFloats = kChainVd * kProdStride;  // one product buffer, [output][key]
 
 // AttendInt8Spans for one (stream, query row, head) per workgroup of NW
 // wavefronts, value heads of 64 codes, key heads of at most 64 codes,
 // 16-byte aligned rows. Same arithmetic as attend_kernel. Lane d of
-// wavefront 0 carries output d's in-order chain (axpysI8) and forms each
-// product itself: per key one LDS byte read, a sign-extending convert, the
-// rounded multiply by the key's weight (read four at a time) and the add.
-// Value rows stream from HBM straight into LDS (global_load_lds, 16-byte
-// pieces, rows [key][64 codes]): with RES every row of the stream, issued by
-// all wavefronts under the logits' tail and the softmax; otherwise a ring of
+// wavefront 0 carries output d's in-order chain (axpysI8). Value rows stream
+// from HBM straight into LDS (global_load_lds, 16-byte pieces, rows
+// [key][64 codes]). With RES (NW = 4) every row of the stream is loaded,
+// issued by all wavefronts under the logits' tail and the softmax, and the
+// three other wavefronts form the products fl(w_j * code_jd) a step of 48
+// keys ahead of the adds, so the chain costs one add per key. Otherwise
+// wavefront 0 forms each product itself (a sign-extending convert of the
+// key's code, the rounded multiply by the key's weight, the add) over a ring of
 // rs chunks of JC keys that wavefront 0 refills behind the chain. The
 // logits and the softmax are spread over the NW wavefronts.
 template <int NW, int JC, bool RES>
@@ -834,7 +839,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     const int qp = a.rope_cos ? a.qpos[static_cast<long long>(b) * a.t + i] : 0;
     const float qv = tid < a.qk ? query_value(a, qi, qp, tid) : 0.0f;
     int4 kw[KPT][kStreamQk / 16];
-    float skr[KPT];
+    float skr[KPT], svr[KPT];  // key scales; value scales (kept when one round covers every key)
     auto kload = [&](int g, int j) {
         const int key = key_of(j);
         const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
@@ -842,6 +847,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
         for (int p = 0; p < kStreamQk / 16; ++p)
             if (p < kpieces) kw[g][p] = *reinterpret_cast<const int4 *>(krow + 16 * p);
         skr[g] = ks[static_cast<long long>(key) * kv_heads + kv];
+        svr[g] = vs[static_cast<long long>(key) * kv_heads + kv];
     };
     auto logit = [&](int g) -> float {
         if (a.quant_q) {
@@ -968,18 +974,110 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     }
     block_sync<NW>();
     const float sum = sum_sh;
-    for (int j = tid; j < n; j += NT) {
-        const float p = s[j] / sum;
-        s[j] = p * vs[static_cast<long long>(key_of(j)) * kv_heads + kv];
+    if (n <= KPT * NT) {  // the value scales came with the keys
+#pragma unroll
+        for (int g = 0; g < KPT; ++g) {
+            const int j = tid + g * NT;
+            if (j < n) {
+                const float p = s[j] / sum;
+                s[j] = p * svr[g];
+            }
+        }
+    } else {
+        for (int j = tid; j < n; j += NT) {
+            const float p = s[j] / sum;
+            s[j] = p * vs[static_cast<long long>(key_of(j)) * kv_heads + kv];
+        }
     }
-    if constexpr (RES) wait_vm_const<0>();  // this wavefront's value rows have landed
-    __syncthreads();                         // weights and (RES) every value row in LDS
+    if constexpr (RES) {
+        static_assert(NW == 4, "the resident chain runs one adding and three multiplying wavefronts");
+        wait_vm_const<0>();  // this wavefront's value rows have landed
+        __syncthreads();     // weights and every value row in LDS
+        // 3. axpysI8 (int8kernel.go:360-368), pipelined over steps of 48
+        // keys: wavefronts 1-3 form the step's products fl(w_j * code_jd)
+        // into a product buffer [output d][key], while lane d of wavefront 0
+        // adds the previous step's row d in key order, so the in-order
+        // chain costs one add per key. Two buffers alternate; a barrier
+        // ends each step. Key j's codes sit at ring + 64 j.
+        float *prod = reinterpret_cast<float *>(ring + rs * (JC * kChainVd));
+        const int steps = (n + kProdKeys - 1) / kProdKeys;
+        // A multiplying lane's task: codes 4m..4m+3 of keys 4jq..4jq+3 of
+        // the step (16 lanes of one write cover 16 distinct bank quads).
+        const int m = (lane & 3) + 4 * (lane >> 4), jq = 4 * (wave - 1) + ((lane >> 2) & 3);
+        auto produce = [&](int t) {
+            const int j = t * kProdKeys + 4 * jq;
+            if (j >= n) return;
+            const uint32_t *row = reinterpret_cast<const uint32_t *>(ring + static_cast<long long>(j) * kChainVd) + m;
+            const uint32_t c0 = row[0], c1 = row[16], c2 = row[32], c3 = row[48];
+            const float4 wv = *reinterpret_cast<const float4 *>(s + j);
+            float *dst = prod + (t & 1) * kProdFloats + 4 * m * kProdStride + 4 * jq;
+            auto code = [](uint32_t cw, int k) { return static_cast<float>(static_cast<int8_t>(cw >> (8 * k))); };
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float4 pv;
+                pv.x = wv.x * code(c0, e);
+                pv.y = wv.y * code(c1, e);
+                pv.z = wv.z * code(c2, e);
+                pv.w = wv.w * code(c3, e);
+                *reinterpret_cast<float4 *>(dst + e * kProdStride) = pv;
+            }
+        };
+        if (wave != 0) produce(0);
+        __syncthreads();
+        float acc = 0.0f;
+        // Step t: wavefront 0 reads step t's row into ld, then adds step
+        // t-1's (all 48 keys: only the last step is partial) from ad under
+        // the reads' latency; two register sets alternate.
+        auto step = [&](int t, float4 (&ld)[kProdKeys / 4], const float4 (&ad)[kProdKeys / 4]) {
+            if (wave == 0) {
+                const float4 *src = reinterpret_cast<const float4 *>(prod + (t & 1) * kProdFloats + lane * kProdStride);
+#pragma unroll
+                for (int q = 0; q < kProdKeys / 4; ++q) ld[q] = src[q];
+                if (t > 0) {
+#pragma unroll
+                    for (int q = 0; q < kProdKeys / 4; ++q) {
+                        acc = acc + ad[q].x;
+                        acc = acc + ad[q].y;
+                        acc = acc + ad[q].z;
+                        acc = acc + ad[q].w;
+                    }
+                }
+            } else if (t + 1 < steps) {
+                produce(t + 1);
+            }
+            __syncthreads();
+        };
+        float4 ra[kProdKeys / 4], rb[kProdKeys / 4];
+        for (int t = 0; t < steps; t += 2) {
+            step(t, ra, rb);
+            if (t + 1 < steps) step(t + 1, rb, ra);
+        }
+        if (wave != 0) return;
+        const int cnt = n - (steps - 1) * kProdKeys;  // keys of the last step, 1..48
+        auto tail = [&](const float4 (&ad)[kProdKeys / 4]) {
+#pragma unroll
+            for (int q = 0; q < kProdKeys / 4; ++q) {
+                if (4 * q < cnt) acc = acc + ad[q].x;
+                if (4 * q + 1 < cnt) acc = acc + ad[q].y;
+                if (4 * q + 2 < cnt) acc = acc + ad[q].z;
+                if (4 * q + 3 < cnt) acc = acc + ad[q].w;
+            }
+        };
+        if ((steps - 1) & 1)
+            tail(rb);
+        else
+            tail(ra);
+        outp[lane] = acc;
+        return;
+    }
+    __syncthreads();  // weights in LDS
     if (wave != 0) return;
 
-    // 3. axpysI8 (int8kernel.go:360-368): lane d adds fl(w_j * code_jd) in key order.
+    // 3. axpysI8 (int8kernel.go:360-368): lane d adds fl(w_j * code_jd) in
+    // key order, forming each product itself.
     float acc = 0.0f;
     for (int c = 0; c < nch; ++c) {
-        if constexpr (!RES) wait_vm(LPC * (min(c + rs, nch) - 1 - c));  // chunk c has landed
+        wait_vm(LPC * (min(c + rs, nch) - 1 - c));  // chunk c has landed
         const int j0 = c * JC, cnt = min(JC, n - j0);
         const int8_t *slot = ring + (c % rs) * (JC * kChainVd) + lane;
         const float *wj = s + j0;
@@ -1024,11 +1122,9 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
             const float pr = wj[jj] * static_cast<float>(slot[jj * kChainVd]);
             acc = acc + pr;
         }
-        if constexpr (!RES) {
-            if (c + rs < nch) {
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this chunk's slot reads are done
-                for (int u = 0; u < LPC; ++u) dma(c + rs, u);
-            }
+        if (c + rs < nch) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this chunk's slot reads are done
+            for (int u = 0; u < LPC; ++u) dma(c + rs, u);
         }
     }
     if (lane < kChainVd) outp[lane] = acc;
@@ -1417,6 +1513,9 @@ size_t chain_lds(const AttendArgs &a, int jc, int rs) {
     return 4 * nk_pad + 4 * 8 * r8 + static_cast<size_t>(rs) * jc * kChainVd;
 }
 
+// The resident form also holds the two product buffers behind the rows.
+size_t chain_res_lds(const AttendArgs &a, int rs) { return chain_lds(a, 64, rs) + 2 * sizeof(float) * kProdFloats; }
+
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
     if (a.t <= 0 || a.heads <= 0 || a.batch <= 0) return hipSuccess;
     const bool aligned = (a.kv_stride & 15) == 0 && (reinterpret_cast<uintptr_t>(a.kq) & 15) == 0 &&
@@ -1426,7 +1525,7 @@ hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
     if (stream_ok && a.vd == kChainVd) {
         if (a.resident) {
             const int rs = std::max(1, (a.nk_max + 63) / 64);
-            const size_t lds = chain_lds(a, 64, rs);
+            const size_t lds = chain_res_lds(a, rs);
             if (lds <= 150 * 1024) return launch_attend_chain<4, 64, true>(a, rs, lds, stream);
         }
         if (a.qk == kChainVd) {
