@@ -166,18 +166,41 @@ __device__ __forceinline__ uint32_t rne_pair(float a, float b) {
     return __builtin_amdgcn_perm(eb, ea, 0x05040100u);  // ea.lo16 | eb.lo16 << 16
 }
 
+// This lane's raw inputs of group g: the activation values (zero past In,
+// lut.go:163-165) and, where given, the norm gains and the gate values.
+template <int BITS, int GB>
+__device__ __forceinline__ void group_inputs(const CQ_GLOBAL float *x, int in, int g, const CQ_GLOBAL float *ngain,
+                                             const CQ_GLOBAL float *xg, float (&xv)[LutGeo<BITS, GB>::E],
+                                             float (&gv)[LutGeo<BITS, GB>::E], float (&hv)[LutGeo<BITS, GB>::E],
+                                             int lane) {
+    using Gm = LutGeo<BITS, GB>;
+    constexpr int G = Gm::G, E = Gm::E;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = G >= 64 ? e * 64 + lane : lane;
+        const int col = g * G + i;
+        const bool ok = i < G && col < in;
+        xv[e] = ok ? x[col] : 0.0f;
+        gv[e] = ngain && ok ? ngain[col] : 0.0f;
+        hv[e] = xg && ok ? xg[col] : 0.0f;
+    }
+}
+
 // Rotation, bound, tables and step of group g of the activation row x
-// (lut.go:158-178, 235-282) by one wavefront: the plain FWHT of the group
-// in registers (a group of G values is G/64 registers per lane; butterflies
-// below 64 exchange lanes with shuffles, the others stay in a lane), M
-// reduced across the wavefront, the NT tables of 16 int16 to tg and the
-// step to *step (lane 0). With ngain the row is ZCRMSNorm'ed first (divisor
-// rms); with xg each value is first gated, x * sigmoid(xg) (Attention.output,
+// (lut.go:158-178, 235-282) by one wavefront, from the lane's raw inputs
+// (group_inputs): the plain FWHT of the group in registers (a group of G
+// values is G/64 registers per lane; butterflies below 64 exchange lanes
+// with shuffles, the others stay in a lane), M reduced across the
+// wavefront, the NT tables of 16 int16 to tg and the step to *step (lane
+// 0). With ngain the row is ZCRMSNorm'ed first (divisor rms); with xg each
+// value is first gated, x * sigmoid(xg) (Attention.output,
 // internal/needle/attention.go:245-249).
 template <int BITS, int GB>
-__device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, int g, const float (&cbv)[16],
-                                             float cb_max, float lut_step, const CQ_GLOBAL float *ngain, float rms,
-                                             const CQ_GLOBAL float *xg, short *tg, float *step, int lane) {
+__device__ __forceinline__ void group_tables(const float (&xin)[LutGeo<BITS, GB>::E],
+                                             const float (&gin)[LutGeo<BITS, GB>::E],
+                                             const float (&hin)[LutGeo<BITS, GB>::E], int in, int g,
+                                             const float (&cbv)[16], float cb_max, float lut_step, bool ngain,
+                                             float rms, bool xg, short *tg, float *step, int lane) {
     using Gm = LutGeo<BITS, GB>;
     constexpr int G = Gm::G, E = Gm::E;
     float v[E];
@@ -185,12 +208,12 @@ __device__ __forceinline__ void group_tables(const CQ_GLOBAL float *x, int in, i
     for (int e = 0; e < E; ++e) {
         const int i = G >= 64 ? e * 64 + lane : lane;
         const int col = g * G + i;
-        float xv = (i < G && col < in) ? x[col] : 0.0f;  // zero-padded past In (lut.go:163-165)
+        float xv = xin[e];
         if (ngain && i < G && col < in) {
-            const float gx = ngain[col] * xv;
+            const float gx = gin[e] * xv;
             xv = gx / rms;
         }
-        if (xg && i < G && col < in) xv = xv * gate_sigmoid(xg[col]);
+        if (xg && i < G && col < in) xv = xv * gate_sigmoid(hin[e]);
         v[e] = xv;
     }
 #pragma unroll
@@ -324,7 +347,7 @@ struct JobPtr {
 // V = 2 (wide launches of one-block units): two wavefronts share each group
 // of the block, one half of its index units each; their exact int32 sums
 // meet in LDS before the float term.
-template <int BITS, int GB, class JS, int V = 1>
+template <int BITS, int GB, class JS, int V = 1, bool PRE = false>
 __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b0, int bc, int act, int W) {
     using Gm = LutGeo<BITS, GB>;
     constexpr int U = Gm::U, UPG = Gm::UPG, NT = Gm::NT;
@@ -368,9 +391,11 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     // through LDS in pieces (one coalesced read each), lanes 0-3 of
     // wavefront 0 keep the four float64 partial sums in the reference's
     // order (lane k: elements i = k mod 4 below In & ~3, lane 0 then the
-    // tail), and the divisor is shared through LDS.
+    // tail), and the divisor is shared through LDS. With PRE (the
+    // latency-bound launches) it runs after the first chunk's index loads
+    // are issued, with them in flight.
     float rms = 1.0f;
-    if (j_ngain) {
+    auto row_norm = [&]() {
         float *xs = reinterpret_cast<float *>(smem);
         const int cap = static_cast<int>(misc - xs) & ~63;
         const int dim = j_in, full = dim & ~3;
@@ -411,6 +436,22 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
         }
         __syncthreads();
         rms = misc[0];
+    };
+
+    if (!PRE && j_ngain) row_norm();
+
+    // With PRE, this wavefront's first group's raw inputs and, for the
+    // fold's first wavefront, its row's residual are loaded up front, so
+    // that no global read waits behind the norm or the lookups (more
+    // registers: the launches of many units go without).
+    using GmI = LutGeo<BITS, GB>;
+    float pxv[GmI::E], pgv[GmI::E], phv[GmI::E];
+    float rpre = 0.0f;
+    if constexpr (PRE) {
+        if (w < min(a.gc, groups)) group_inputs<BITS, GB>(x, j_in, w, j_ngain, xg, pxv, pgv, phv, lane);
+        const int r = blk0 * 64 + tid;
+        if (j_resid && tid < 64 && r >= j_row0 && r < j_row0 + j_out)
+            rpre = j_resid[static_cast<long long>(act) * j_rstride + (r - j_row0)];
     }
 
     // The fused int8 append of a finished block: the whole wavefront holds
@@ -449,7 +490,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
         if (r >= j_row0 && r < j_row0 + j_out) {
             float out = v;
             if (j_resid)
-                out = j_resid[static_cast<long long>(act) * j_rstride + (r - j_row0)] + out;
+                out = (PRE && bb == 0 && ln == tid ? rpre : j_resid[static_cast<long long>(act) * j_rstride + (r - j_row0)]) + out;
             else if (j_act == 1)
                 out = silu_value(out);
             j_y[static_cast<long long>(act) * j_ystride + (r - j_row0)] = out;
@@ -530,10 +571,24 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
             for (int d = 0; d < DG; ++d) refill(buf[d], nv[d]);
         }
 
+        if (PRE && g0 == 0 && j_ngain) row_norm();
+
         // 1. Rotation, bound and tables of the chunk's groups w, w+W, ...
-        for (int gi = w; gi < gch; gi += W)
-            group_tables<BITS, GB>(x, j_in, g0 + gi, cbv, j_cbmax, j_step, j_ngain, rms, xg,
-                                   tab + static_cast<size_t>(gi) * NT * 16, &steps[gi], lane);
+        for (int gi = w; gi < gch; gi += W) {
+            float xv[GmI::E], gv[GmI::E], hv[GmI::E];
+            if (PRE && g0 == 0 && gi == w) {
+#pragma unroll
+                for (int e = 0; e < GmI::E; ++e) {
+                    xv[e] = pxv[e];
+                    gv[e] = pgv[e];
+                    hv[e] = phv[e];
+                }
+            } else {
+                group_inputs<BITS, GB>(x, j_in, g0 + gi, j_ngain, xg, xv, gv, hv, lane);
+            }
+            group_tables<BITS, GB>(xv, gv, hv, j_in, g0 + gi, cbv, j_cbmax, j_step, j_ngain != nullptr, rms,
+                                   xg != nullptr, tab + static_cast<size_t>(gi) * NT * 16, &steps[gi], lane);
+        }
         __syncthreads();
 
         // 2. The wavefront's items in order, DG groups of loads ahead: the
@@ -642,7 +697,7 @@ __global__ __launch_bounds__(1024) void lut_kernel_wide(LutLaunch a) {
     asm volatile("" ::"v"(jr.d), "s"(bpw), "s"(gc), "s"(tb), "s"(bpw_max), "s"(waves));
     const int b0 = static_cast<int>(blockIdx.x) * bpw, nblk = JOB(jr, int, nblk);
     if (b0 >= nblk) return;
-    lut_unit<BITS, GB, JobRegs, V>(a, jr, b0, min(bpw, nblk - b0), blockIdx.y, waves);
+    lut_unit<BITS, GB, JobRegs, V, true>(a, jr, b0, min(bpw, nblk - b0), blockIdx.y, waves);
 }
 
 template <int BITS, int GB, int V>
