@@ -441,18 +441,59 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     if (!PRE && j_ngain) row_norm();
 
     // With PRE, this wavefront's first group's raw inputs and, for the
-    // fold's first wavefront, its row's residual are loaded up front, so
-    // that no global read waits behind the norm or the lookups (more
-    // registers: the launches of many units go without).
+    // fold's first wavefront, its row's residual are loaded together with
+    // the first index loads, so that no global read waits behind the norm or
+    // the lookups (more registers: the launches of many units go without).
     using GmI = LutGeo<BITS, GB>;
     float pxv[GmI::E], pgv[GmI::E], phv[GmI::E];
     float rpre = 0.0f;
-    if constexpr (PRE) {
+    auto preload = [&]() {
         if (w < min(a.gc, groups)) group_inputs<BITS, GB>(x, j_in, w, j_ngain, xg, pxv, pgv, phv, lane);
         const int r = blk0 * 64 + tid;
         if (j_resid && tid < 64 && r >= j_row0 && r < j_row0 + j_out)
             rpre = j_resid[static_cast<long long>(act) * j_rstride + (r - j_row0)];
-    }
+    };
+
+    // The same norm from the row as the wavefronts hold it (with PRE, one
+    // chunk of at most W groups, In a multiple of 4): each lane's squares
+    // d * d go to LDS as [k][i / 4] for k = i mod 4, so that lanes 0-3 only
+    // add, in the reference's order, with no second read of the row.
+    auto row_norm_held = [&]() {
+        constexpr int Gh = LutGeo<BITS, GB>::G, Eh = LutGeo<BITS, GB>::E;
+        const int qn = j_in >> 2, qs = qn + 2;  // row length, padded stride (16-byte rows)
+        double *sq = reinterpret_cast<double *>(smem);
+        if (w < groups) {
+#pragma unroll
+            for (int e = 0; e < Eh; ++e) {
+                const int i = Gh >= 64 ? e * 64 + lane : lane;
+                const int col = w * Gh + i;
+                if (i < Gh && col < j_in) {
+                    const double d = pxv[e];
+                    sq[(col & 3) * qs + (col >> 2)] = d * d;
+                }
+            }
+        }
+        __syncthreads();
+        double part = 0.0;
+        if (tid < 4) {
+            const double *row = sq + tid * qs;
+            int m = 0;
+            for (; m + 16 <= qn; m += 16) {
+                double v[16];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) v[k] = row[m + k];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) part = part + v[k];
+            }
+            for (; m < qn; ++m) part = part + row[m];
+        }
+        if (w == 0) {
+            const double p0 = __shfl(part, 0), p1 = __shfl(part, 1), p2 = __shfl(part, 2), p3 = __shfl(part, 3);
+            if (lane == 0) misc[0] = zc_rms(p0, p1, p2, p3, j_in);
+        }
+        __syncthreads();
+        rms = misc[0];
+    };
 
     // The fused int8 append of a finished block: the whole wavefront holds
     // its 64 values (lane = row), one head of the cache row. Int8Rows.Append
@@ -461,17 +502,31 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     int8_t *const j_aq = JOB(jr, int8_t *, app_q);
     float *const j_as = JOB(jr, float *, app_s);
     const long long j_aqs = JOB(jr, long long, app_q_stride), j_ass = JOB(jr, long long, app_s_stride);
-    const int j_apos = j_aq ? JOB(jr, const int32_t *, app_pos)[act] : -1;
-    const bool j_app = j_aq && j_apos >= 0 && j_apos < JOB(jr, int, app_cap);
+    // The row's cache position, a global load whose value is first needed
+    // at the write: with PRE it is issued with the first index loads. An
+    // opaque per-lane zero in its address keeps the value in a vector
+    // register, where the compiler would otherwise move it to a scalar one
+    // at once and wait for every load issued so far.
+    int j_apos = -1;
+    auto load_apos = [&]() {
+        int vz;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(vz));
+        if (j_aq) j_apos = *gptr(JOB(jr, const int32_t *, app_pos) + act + vz);
+    };
+    if (!PRE) load_apos();
+    const int j_acap = JOB(jr, int, app_cap);
     const CQ_GLOBAL float *j_acos = gptr(JOB(jr, const float *, app_cos)), *j_asin = gptr(JOB(jr, const float *, app_sin));
-    auto append_block = [&](int bb, int ln, float v) {
+    float pcos = 0.0f, psin = 0.0f;  // with PRE: wavefront 0's RoPE pair at that position, loaded early
+    auto append_block = [&](int bb, int ln, float v, int j_apos) {
         const int r0 = (blk0 + bb) * 64 - j_row0;  // view row of the head's first value
         if (j_acos) {
             const float o = xor_lane<32>(v);
             const int jj = ln & 31;
             const float a = ln < 32 ? v : o, b = ln < 32 ? o : v;
+            const float cs = PRE && ln == tid ? pcos : j_acos[j_apos * 32 + jj];
+            const float sn = PRE && ln == tid ? psin : j_asin[j_apos * 32 + jj];
             float o1, o2;
-            rope_pair(a, b, j_acos[j_apos * 32 + jj], j_asin[j_apos * 32 + jj], o1, o2);
+            rope_pair(a, b, cs, sn, o1, o2);
             v = ln < 32 ? o1 : o2;
         }
         float m = fabsf(v);
@@ -485,7 +540,11 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     };
 
     auto write_out = [&](int bb, int ln, float v) {
-        if (j_app) append_block(bb, ln, v);
+        if (j_aq) {
+            int ap = j_apos;
+            asm volatile("" : "+v"(ap));  // the position's wait stays here
+            if (ap >= 0 && ap < j_acap) append_block(bb, ln, v, ap);
+        }
         const int r = (blk0 + bb) * 64 + ln;
         if (r >= j_row0 && r < j_row0 + j_out) {
             float out = v;
@@ -510,7 +569,11 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     }
     const int vp = V == 1 ? 0 : w % V;  // this wavefront's half of each group's units
 
-    for (int g0 = 0; g0 < groups; g0 += gc) {
+    // One chunk of groups from g0. With PRE and a single chunk it runs
+    // outside any loop: in a loop the compiler's wait analysis carries
+    // loads across the back edge and waits for the first index loads before
+    // the preloads go out.
+    auto chunk = [&](int g0) {
         const int gch = min(gc, groups - g0);
         const bool last = g0 + gch >= groups;
         const int wv = w / V;  // V = 1: w
@@ -553,10 +616,15 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
             const size_t ustride = real ? static_cast<size_t>(64) * U : 0;
 #pragma unroll
             for (int u = 0; u < UPGV; ++u) load_unit<U>(ip + u * ustride, bf[u]);
-            const CQ_GLOBAL uint16_t *np =
-                real ? j_norm + (static_cast<size_t>(blk0 + p.bb) * groups + g0 + p.gi) * 64 + lane
-                     : (const CQ_GLOBAL uint16_t *)spare;
-            nrm = *np;
+            // The row norm as the aligned 32-bit word holding it (this
+            // lane's half: lane & 1), the norm table's own first word on a
+            // spare turn: a merge of 32-bit loads needs no extension where
+            // the branches meet, so nothing waits for the load here.
+            const CQ_GLOBAL uint32_t *np32 =
+                real ? reinterpret_cast<const CQ_GLOBAL uint32_t *>(
+                           j_norm + (static_cast<size_t>(blk0 + p.bb) * groups + g0 + p.gi) * 64) + (lane >> 1)
+                     : reinterpret_cast<const CQ_GLOBAL uint32_t *>(j_norm);
+            nrm = *np32;
         };
         // The first items are in flight while the tables are built.
         Pos lp = first;
@@ -571,7 +639,25 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
             for (int d = 0; d < DG; ++d) refill(buf[d], nv[d]);
         }
 
-        if (PRE && g0 == 0 && j_ngain) row_norm();
+        if (PRE && g0 == 0) {
+            preload();
+            load_apos();
+        }
+        if (PRE && g0 == 0 && j_ngain) {
+            if (gch == groups && groups <= W && (j_in & 3) == 0 &&
+                2 * (j_in + 8) <= (static_cast<int>(misc - reinterpret_cast<float *>(smem)) & ~63))
+                row_norm_held();
+            else
+                row_norm();
+        }
+        if (PRE && g0 == 0 && j_acos && tid < 64 && j_aq) {
+            int ap = j_apos;
+            asm volatile("" : "+v"(ap));  // the position's wait stays here, behind the norm
+            if (ap >= 0 && ap < j_acap) {
+                pcos = j_acos[ap * 32 + (lane & 31)];
+                psin = j_asin[ap * 32 + (lane & 31)];
+            }
+        }
 
         // 1. Rotation, bound and tables of the chunk's groups w, w+W, ...
         for (int gi = w; gi < gch; gi += W) {
@@ -606,7 +692,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
 #pragma unroll
                     for (int u = 0; u < UPGV; ++u)
                         s += lookup_unit<U>(buf[d][u], tg + (vp * UPGV + u) * 2 * U * 16 * 2);
-                    const float n = __half2float(__ushort_as_half(static_cast<unsigned short>(nv[d])));
+                    const float n = __half2float(__ushort_as_half(static_cast<unsigned short>(nv[d] >> (16 * (lane & 1)))));
                     const float coef = n * steps[gi];
                     if constexpr (V > 1) {  // [gi][half][lane] int32 sums, then [gi][lane] coefficients
                         int *termi = reinterpret_cast<int *>(term);
@@ -664,7 +750,11 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
             }
         }
         if (!last) __syncthreads();  // tables, steps and terms are rewritten by the next chunk
-    }
+    };
+    if (PRE && gc >= groups)
+        chunk(0);
+    else
+        for (int g0 = 0; g0 < groups; g0 += gc) chunk(g0);
 }
 
 template <int BITS, int GB, bool DEV>
