@@ -16,7 +16,15 @@ step time, in GB/s. The roofline object is the step's dominant launch, the
 steps). detail holds per-shape
 rates and the rate of one launch per GEMV (a captured graph of 8 * copies
 launches). The cpu_baseline is the C restatement of the reference's lut
-kernel (oracle/), one thread, on a bounded sample of the same sweep.
+kernel (oracle/) on the host cores, on a bounded sample of the same sweep.
+
+Further legs, each with its own cpu_baseline (the oracle, bounded samples;
+batch-256 legs run streams concurrently, one per host process, as the
+reference runs one goroutine per hypothesis): batched_gemm (the encoder's
+M x 512 / M x 2048 products, M = 375, 1500, 12000), ref_shapes (the
+reference's BenchmarkGEMM shapes with its published M5 Pro times),
+attention (int8 KV attention at batch 1 and 256, self and cross) and
+decode (the synthetic decoder's 200-token greedy decode at batch 1 and 256).
 """
 
 import argparse
@@ -174,6 +182,137 @@ def batched_gemm_leg(gw, torch, reps=5):
     return out
 
 
+def batched_gemm_cpu(seconds):
+    """The batched GEMM leg's shapes on the oracle's lut GEMM, split over
+    the host cores as gemmLUT splits a GEMM (lut.go:88-124)."""
+    from oracle import cpu_legs
+
+    threads = cpu_threads()
+    shapes = [(bits, o, i, M) for bits in (4, 2) for (o, i) in ((2048, 512), (512, 2048)) for M in (375, 1500, 12000)]
+    res = cpu_legs.gemm_baseline(shapes, threads, seconds)
+    return {"unit": "rows/s", "cores": threads, "kind": "port", "host": cpu_host(), "configs": res,
+            "sample": f"oracle lut GEMM (AVX2 where the host has it) over at most 375 activations of each shape, "
+                      f"repeated for about {seconds:.1f} s, split over {threads} threads; time is linear in rows"}
+
+
+# The reference's own benchmark shapes (internal/cq/bench_test.go:23-39)
+# and its published M5 Pro single-core lut times (docs/FINDINGS.md:2675-2686).
+REF_SHAPES = [("k_proj", 96, 512, 2, 1, 1.15), ("q_proj", 384, 512, 2, 1, 2.91), ("out_proj", 512, 512, 2, 1, 3.68),
+              ("pw1", 1024, 512, 2, 1, 6.84), ("stem.out", 512, 1280, 2, 1, 9.18), ("phi_res", 128, 2048, 4, 1, 8.89),
+              ("head", 8199, 512, 4, 1, 97.2), ("q_proj", 384, 512, 2, 5, 14.5), ("head", 8199, 512, 4, 5, 487.0),
+              ("q_proj", 384, 512, 2, 375, 1090.0)]
+
+
+def ref_shapes_leg(gw, torch, with_cpu, cpu_seconds):
+    """BenchmarkGEMM's shapes and batches through cq_gemm_dev: microseconds
+    per call (a captured graph of 20 calls on the same inputs, so the small
+    matrices stay cache-resident, as the reference's repeated b.Loop calls
+    do), next to the reference's published M5 Pro times and the oracle on
+    one host thread (its -cpu 1)."""
+    out = {}
+    for name, o, i, bits, rows, m5 in REF_SHAPES:
+        g = gw.synth.rng(o * 7919 + i)
+        m = gw.cq.New(gw.synth.random_packed(g, o, i, GROUP, bits, sigma=0.05))
+        x = torch.from_numpy(gw.synth.activations(g, rows, i)).cuda()
+        y = torch.empty(rows, o, device="cuda")
+        m.gemm_dev(y, x, rows)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(20):
+                m.gemm_dev(y, x, rows)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 100
+        out[f"{name}_{o}x{i}_cq{bits}_rows{rows}"] = {"us": round(us, 2), "path": m.gemm_path(rows),
+                                                       "m5pro_lut_1core_us": m5,
+                                                       "weight_GBps": round(weight_bytes(o, i, bits) / us / 1e3, 1)}
+        del graph, m, x, y
+    res = {"shapes": out}
+    if with_cpu:
+        from oracle import cpu_legs
+
+        cpu = cpu_legs.shapes_baseline([(n, o, i, b, r) for n, o, i, b, r, _ in REF_SHAPES], cpu_seconds)
+        for k, v in cpu.items():
+            out[k]["cpu_1t_us"] = v
+        res["cpu_baseline"] = {"unit": "us per call", "cores": 1, "kind": "port", "host": cpu_host(),
+                               "sample": f"oracle lut GEMM on one thread (AVX2 where the host has it), each "
+                                         f"shape repeated for about {cpu_seconds:.2f} s"}
+    return res
+
+
+ATTN_CASES = [("self", 64), ("self", 200), ("self", 448), ("cross", 1500)]
+
+
+def attention_leg(gw, torch, with_cpu, cpu_seconds):
+    """Int8 KV attention (AttendInt8Spans) of one query row per stream, 8
+    heads x 64, at batch 1 and 256: self over n keys of an n-key cache and
+    cross over 1500 frames, K/V ~N(0,1) quantised per row on the device
+    (QuantizeRows), Q ~N(0,1), int8 query. Microseconds per call (a captured
+    graph of 20 calls), stream-steps/s and the K/V bytes read (codes and
+    scales) per second against 8 TB/s."""
+    from go_whistle_amd import needle
+
+    H, D = 8, 64
+    C = H * D
+    out = {}
+    for batch in (1, 256):
+        for kind, n in ATTN_CASES:
+            gen = torch.Generator(device="cuda")
+            gen.manual_seed(11 + n)
+            kq = torch.empty(batch * n, C, dtype=torch.int8, device="cuda")
+            vq = torch.empty_like(kq)
+            ks = torch.empty(batch * n, H, device="cuda")
+            vs = torch.empty_like(ks)
+            for dq, ds in ((kq, ks), (vq, vs)):
+                f32 = torch.randn(batch * n, C, generator=gen, device="cuda")
+                needle.quantize_rows_dev(dq, ds, f32, batch * n, C, D)
+                del f32
+            q = torch.randn(batch, C, generator=gen, device="cuda")
+            o = torch.zeros(batch, C, device="cuda")
+            span = [0, n, 0, 0] if kind == "self" else [0, 0, 0, n]
+            spans = torch.tensor([span] * batch, dtype=torch.int32, device="cuda")
+
+            def call():
+                needle.attend_int8_dev(o, q, 1, H, kq, ks, C, D, vq, vs, C, D, spans, n, math.sqrt(D), True,
+                                       batch=batch, kv_stride=n * C, s_stride=n * H)
+
+            call()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(20):
+                    call()
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / 100
+            kv = batch * n * (2 * C + 2 * 4 * H)
+            out[f"b{batch}_{kind}{n}"] = {"us": round(us, 2), "stream_steps_per_s": round(batch / us * 1e6, 1),
+                                          "kv_GBps": round(kv / us / 1e3, 1),
+                                          "hbm_frac": round(kv / us / 1e3 / HBM_PEAK_GBS, 4)}
+            del graph, kq, vq, ks, vs, q, o, spans
+        torch.cuda.empty_cache()
+    res = {"cases": out}
+    if with_cpu:
+        from oracle import cpu_legs
+
+        res["cpu_baseline"] = cpu_legs.attention_baseline(ATTN_CASES, cpu_seconds, cpu_threads())
+        res["cpu_baseline"]["host"] = cpu_host()
+    return res
+
+
 def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
     """Greedy decode of the synthetic 8-layer decoder (d 512, 8 heads, FFN
     2048, vocab 16384, 1500-frame int8 cross memory per stream), 200 tokens
@@ -210,26 +349,11 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
     if with_cpu:
         if ROOT not in sys.path:
             sys.path.insert(0, ROOT)
-        from oracle import decoder_ref
+        from oracle import cpu_legs
 
-        from oracle import binding as orc
-
-        ref = decoder_ref.RefDecoder(model)
-        avx2, threads = orc.have_avx2(), cpu_threads()
-        orc.set_cpu(avx2, threads)
-        ref.memory(dec.encoder_states(7, cfg, 0))  # untimed: the memory is built once per clip
-        n, t0 = 0, time.perf_counter()
-        while True:
-            n += len(ref.decode(1, 10))
-            el = time.perf_counter() - t0
-            if el >= cpu_seconds:
-                break
-        orc.set_cpu(False, 1)
-        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-                               "host": cpu_host(),
-                               "sample": f"{n} greedy tokens at batch 1 (runs of 10 from position 0), oracle "
-                                         f"decoder, lut products and int8 attention {'AVX2' if avx2 else 'generic'}, products split over "
-                                         f"{threads} threads as the reference splits them, {el:.1f} s"}
+        base = cpu_legs.decode_baseline(tokens, cpu_threads(), cpu_threads())
+        res["cpu_baseline"] = dict(base["batch1"], host=cpu_host())
+        res["cpu_baseline_batch256"] = dict(base["batch256"], host=cpu_host())
     return res
 
 
@@ -246,6 +370,9 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM leg")
     ap.add_argument("--gemm-only", action="store_true", help="run only the batched GEMM leg (prints its JSON)")
     ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (prints its JSON)")
+    ap.add_argument("--no-attention", action="store_true", help="skip the int8 attention leg")
+    ap.add_argument("--no-ref-shapes", action="store_true", help="skip the reference's benchmark shapes")
+    ap.add_argument("--attention-only", action="store_true", help="run only the attention leg (prints its JSON)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the step's 4-bit launch and a 512 MiB device copy (for rocprofv3 counters)")
     args = ap.parse_args()
@@ -260,7 +387,13 @@ def main():
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
     if args.gemm_only:
-        print(json.dumps({"batched_gemm": batched_gemm_leg(gw, torch)}))
+        leg = batched_gemm_leg(gw, torch)
+        if not args.no_cpu:
+            leg["cpu_baseline"] = batched_gemm_cpu(0.5)
+        print(json.dumps({"batched_gemm": leg}))
+        return
+    if args.attention_only:
+        print(json.dumps({"attention": attention_leg(gw, torch, not args.no_cpu, 1.0)}))
         return
     if args.decode_only:
         print(json.dumps({"decode": decode_leg(gw, torch, args.decode_tokens, args.cpu_seconds, not args.no_cpu)}))
@@ -379,6 +512,12 @@ def main():
         line["cpu_baseline"] = cpu_baseline(gw, packs, args.cpu_seconds)
     if not args.no_gemm:
         line["batched_gemm"] = batched_gemm_leg(gw, torch)
+        if not args.no_cpu:
+            line["batched_gemm"]["cpu_baseline"] = batched_gemm_cpu(0.5)
+    if not args.no_ref_shapes:
+        line["ref_shapes"] = ref_shapes_leg(gw, torch, not args.no_cpu, 0.25)
+    if not args.no_attention:
+        line["attention"] = attention_leg(gw, torch, not args.no_cpu, 1.0)
     if not args.no_decode:
         del plans, mats
         torch.cuda.empty_cache()
