@@ -23,8 +23,9 @@ batch-256 legs run streams concurrently, one per host process, as the
 reference runs one goroutine per hypothesis): batched_gemm (the encoder's
 M x 512 / M x 2048 products, M = 375, 1500, 12000), ref_shapes (the
 reference's BenchmarkGEMM shapes with its published M5 Pro times),
-attention (int8 KV attention at batch 1 and 256, self and cross) and
-decode (the synthetic decoder's 200-token greedy decode at batch 1 and 256).
+attention (int8 KV attention at batch 1 and 256, self and cross), aux
+(HadamardMLP and the mHC block at 1/375/1500 rows) and decode (the
+synthetic decoder's 200-token greedy decode at batch 1 and 256).
 """
 
 import argparse
@@ -247,6 +248,93 @@ def ref_shapes_leg(gw, torch, with_cpu, cpu_seconds):
     return res
 
 
+def aux_leg(gw, torch, with_cpu, cpu_seconds):
+    """The device forms of two float blocks next to the CQ linears, timed
+    at Whistle's shapes (a captured graph of 20 calls): HadamardMLP.Forward
+    (internal/needle/hadamard.go:172-294; 16 x 32 Monarch blocks, rank 8,
+    width 512) and an mHC layer's heads, Sinkhorn and lane mix
+    (internal/needle/mhc.go:182-299; 4 lanes of 512), at 1, 375 and 1500
+    rows. The cpu_baseline is the oracle on one host thread: the C mHC
+    routines and the float64 numpy restatement of HadamardMLP."""
+    import numpy as np
+
+    from go_whistle_amd import needle
+
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from oracle import binding as orc
+    from oracle import hadamard_ref as hr
+
+    def graph_us(call):
+        call()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(20):
+                call()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / 100
+
+    def cpu_us(call):
+        call()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            call()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= cpu_seconds:
+                return el / n * 1e6
+
+    g = np.random.default_rng(17)
+    w = hr.random_weights(g, 16, 32, 8, 512)
+    h = needle.HadamardMLP(w)
+    n, dim = 4, 512
+    out = {}
+    for rows in (1, 375, 1500):
+        x = (g.standard_normal((rows, 512)) * 1.5).astype(np.float32)
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty(rows, 512, device="cuda")
+        rec = {"us": round(graph_us(lambda: h.forward_dev(yd, xd, rows)), 2)}
+        if with_cpu:
+            rec["cpu_1t_us"] = round(cpu_us(lambda: hr.forward(w, x, rows)), 1)
+        out[f"hadamard_mlp_rows{rows}"] = rec
+
+        pre, post = g.standard_normal((rows, n)).astype(np.float32), g.standard_normal((rows, n)).astype(np.float32)
+        res = g.standard_normal((rows, n * n)).astype(np.float32)
+        stream = g.standard_normal((rows, n, dim)).astype(np.float32)
+        block_out = g.standard_normal((rows, dim)).astype(np.float32)
+        t = [torch.from_numpy(a.reshape(-1)).cuda() for a in (pre, post, res, stream, block_out)]
+        hp, hq = torch.zeros(rows * n, device="cuda"), torch.zeros(rows * n, device="cuda")
+        hres, u = torch.zeros(rows * n * n, device="cuda"), torch.zeros(rows * dim, device="cuda")
+        mixed = torch.zeros(rows * n * dim, device="cuda")
+
+        def mhc():
+            needle.mhc_heads_dev(hp, hq, hres, u, t[0], t[1], t[2], t[3], rows, n, dim, None)
+            needle.mhc_mix_dev(mixed, t[3], hres, hq, t[4], u, rows, n, dim)
+
+        rec = {"us": round(graph_us(mhc), 2)}
+        if with_cpu:
+            def mhc_cpu():
+                _, ohq, ohr, ou = orc.mhc_heads(pre, post, res, stream, rows, n, dim)
+                orc.mhc_mix(stream, ohr, ohq, block_out, ou, rows, n, dim)
+
+            rec["cpu_1t_us"] = round(cpu_us(mhc_cpu), 1)
+        out[f"mhc_heads_mix_rows{rows}"] = rec
+    res = {"cases": out}
+    if with_cpu:
+        res["cpu_baseline"] = {"unit": "us per call", "cores": 1, "kind": "port", "host": cpu_host(),
+                               "sample": "oracle on one thread: C mHC heads/Sinkhorn/mix; HadamardMLP as the "
+                                         f"float64 numpy restatement; each case repeated for about {cpu_seconds} s"}
+    return res
+
+
 ATTN_CASES = [("self", 64), ("self", 200), ("self", 448), ("cross", 1500)]
 
 
@@ -371,6 +459,8 @@ def main():
     ap.add_argument("--gemm-only", action="store_true", help="run only the batched GEMM leg (prints its JSON)")
     ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (prints its JSON)")
     ap.add_argument("--no-attention", action="store_true", help="skip the int8 attention leg")
+    ap.add_argument("--no-aux", action="store_true", help="skip the HadamardMLP / mHC leg")
+    ap.add_argument("--aux-only", action="store_true", help="run only the HadamardMLP / mHC leg")
     ap.add_argument("--no-ref-shapes", action="store_true", help="skip the reference's benchmark shapes")
     ap.add_argument("--attention-only", action="store_true", help="run only the attention leg (prints its JSON)")
     ap.add_argument("--roofline-only", action="store_true",
@@ -391,6 +481,9 @@ def main():
         if not args.no_cpu:
             leg["cpu_baseline"] = batched_gemm_cpu(0.5)
         print(json.dumps({"batched_gemm": leg}))
+        return
+    if args.aux_only:
+        print(json.dumps({"aux": aux_leg(gw, torch, not args.no_cpu, 0.3)}))
         return
     if args.attention_only:
         print(json.dumps({"attention": attention_leg(gw, torch, not args.no_cpu, 1.0)}))
@@ -518,6 +611,8 @@ def main():
         line["ref_shapes"] = ref_shapes_leg(gw, torch, not args.no_cpu, 0.25)
     if not args.no_attention:
         line["attention"] = attention_leg(gw, torch, not args.no_cpu, 1.0)
+    if not args.no_aux:
+        line["aux"] = aux_leg(gw, torch, not args.no_cpu, 0.3)
     if not args.no_decode:
         del plans, mats
         torch.cuda.empty_cache()

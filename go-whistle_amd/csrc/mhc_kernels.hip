@@ -29,57 +29,55 @@ __global__ __launch_bounds__(64) void rms_unit_kernel(float *dst, const float *x
     for (int c = lane; c < dim; c += 64) out[c] = row[c] * inv;
 }
 
-// logSumExp (mhc.go:401-417) over k[off], k[off + stride], ...
-__device__ float log_sum_exp(const float *k, int off, int stride, int n) {
-    float m = -INFINITY;
-    for (int i = 0; i < n; ++i) m = go_max(m, k[off + i * stride]);
-    if (isinf(m)) m = 0.0f;
-    float s = 0.0f;
-    for (int i = 0; i < n; ++i) s = s + static_cast<float>(exp_f64(static_cast<double>(k[off + i * stride] - m)));
-    return m + static_cast<float>(log(static_cast<double>(s)));
-}
-
-// sinkhorn (mhc.go:301-399) of one n x n matrix in k (LDS), one thread.
-__device__ void sinkhorn_one(float *k, double *e, int n, int iters) {
-    float lo = k[0], hi = k[0];
-    for (int i = 1; i < n * n; ++i) {
-        lo = go_min(lo, k[i]);  // slices.Min / slices.Max keep a NaN
-        hi = go_max(hi, k[i]);
+// sinkhorn (mhc.go:301-399) of one n x n matrix in k (LDS) by one
+// wavefront: lane t < n*n holds entry t = r*n + c. Rows (then columns) are
+// independent within a pass, so each lane forms its row's (column's) sum in
+// the reference's order from its neighbours' values and divides its own
+// entry: the serial routine's operations, n*n of them at a time.
+__device__ void sinkhorn_wave(float *k, int n, int iters, int lane) {
+    const int nn = n * n;
+    const bool act = lane < nn;
+    const int r = act ? lane / n : 0, c = act ? lane - r * n : 0;
+    float kv = act ? k[lane] : k[0];  // idle lanes repeat entry 0: neutral for min and max
+    // slices.Min / slices.Max keep a NaN; min and max are exact in any order
+    float lo = kv, hi = kv;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        lo = go_min(lo, __shfl_xor(lo, off));
+        hi = go_max(hi, __shfl_xor(hi, off));
     }
     const double spread = static_cast<double>(hi) - static_cast<double>(lo);
     if (!(isinf(spread) || isnan(spread) || spread + 2.0 * iters * log(static_cast<double>(n)) > 700.0)) {
-        for (int i = 0; i < n * n; ++i) e[i] = exp_f64(static_cast<double>(k[i]) - static_cast<double>(hi));
+        double e = exp_f64(static_cast<double>(kv) - static_cast<double>(hi));
         for (int it = 0; it < iters; ++it) {
-            for (int r = 0; r < n; ++r) {
-                double s = 0.0;
-                for (int c = 0; c < n; ++c) s = s + e[r * n + c];
-                for (int c = 0; c < n; ++c) e[r * n + c] = e[r * n + c] / s;
-            }
-            for (int c = 0; c < n; ++c) {
-                double s = 0.0;
-                for (int r = 0; r < n; ++r) s = s + e[r * n + c];
-                for (int r = 0; r < n; ++r) e[r * n + c] = e[r * n + c] / s;
-            }
+            double s = 0.0;
+            for (int j = 0; j < n; ++j) s = s + __shfl(e, r * n + j);
+            e = e / s;
+            s = 0.0;
+            for (int j = 0; j < n; ++j) s = s + __shfl(e, j * n + c);
+            e = e / s;
         }
-        for (int i = 0; i < n * n; ++i) k[i] = static_cast<float>(e[i]);
+        if (act) k[lane] = static_cast<float>(e);
         return;
     }
+    // logSumExp (mhc.go:401-417) of the lane's row (then column), in order
+    auto lse = [&](int base, int stride) {
+        float m = -INFINITY;
+        for (int j = 0; j < n; ++j) m = go_max(m, __shfl(kv, base + j * stride));
+        if (isinf(m)) m = 0.0f;
+        float s = 0.0f;
+        for (int j = 0; j < n; ++j) s = s + static_cast<float>(exp_f64(static_cast<double>(__shfl(kv, base + j * stride) - m)));
+        return m + static_cast<float>(log(static_cast<double>(s)));
+    };
     for (int it = 0; it < iters; ++it) {
-        for (int r = 0; r < n; ++r) {
-            const float l = log_sum_exp(k, r * n, 1, n);
-            for (int c = 0; c < n; ++c) k[r * n + c] = k[r * n + c] - l;
-        }
-        for (int c = 0; c < n; ++c) {
-            const float l = log_sum_exp(k, c, n, n);
-            for (int r = 0; r < n; ++r) k[r * n + c] = k[r * n + c] - l;
-        }
+        kv = kv - lse(r * n, 1);
+        kv = kv - lse(c, n);
     }
-    for (int i = 0; i < n * n; ++i) k[i] = static_cast<float>(exp_f64(static_cast<double>(k[i])));
+    if (act) k[lane] = static_cast<float>(exp_f64(static_cast<double>(kv)));
 }
 
 __global__ __launch_bounds__(256) void mhc_heads_kernel(MhcArgs m) {
     __shared__ float hp[kMhcMaxLanes], kr[kMhcMaxLanes * kMhcMaxLanes];
-    __shared__ double ew[kMhcMaxLanes * kMhcMaxLanes];
     const int i = blockIdx.x, tid = threadIdx.x, n = m.lanes, dim = m.dim;
     const float *A = m.affine;  // {a_pre, a_post, a_res, b_pre[n], pre_off[n], b_post[n], post_off[n], b_res[n*n]}
     if (tid < n) {
@@ -104,7 +102,7 @@ __global__ __launch_bounds__(256) void mhc_heads_kernel(MhcArgs m) {
         kr[tid] = v;
     }
     __syncthreads();
-    if (tid == 0) sinkhorn_one(kr, ew, n, 20);
+    if (tid < 64) sinkhorn_wave(kr, n, 20, tid);
     const float *st = m.stream + static_cast<long long>(i) * n * dim;
     for (int c = tid; c < dim; c += blockDim.x) {  // u = sum_k h_pre[k] stream[k], k in order
         float u = 0.0f;
