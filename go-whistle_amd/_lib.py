@@ -67,6 +67,8 @@ SIGNATURES = {
     "nd_rope_dev": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p]),
     "nd_argmax_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "nd_argmax_advance_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p]),
+    "nd_argmax_advance_eos_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p,
+                                          c_int, c_void_p]),
     "kv_attend_int8_shared_dev": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_int, c_int, c_void_p,
                                           c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_longlong,
                                           c_longlong, c_void_p, c_int, c_float, c_int, c_int, c_void_p, c_int,

@@ -1303,7 +1303,8 @@ int nd_rope_dev(float *x, int rows, int heads, int head_dim, const float *cos_t,
 int nd_argmax_dev(int32_t *out, const float *v, int rows, int n, void *stream) {
     if (rows < 0 || n <= 0) return fail(CQ_ERR_MISUSE, "decoder: argmax of %d rows of %d", rows, n);
     if (rows > 0 && (!out || !v)) return fail(CQ_ERR_MISUSE, "decoder: argmax with a nil operand");
-    HIP_TRY(launch_argmax(out, v, rows, n, nullptr, nullptr, 0, static_cast<hipStream_t>(stream)), "argmax launch");
+    HIP_TRY(launch_argmax(out, v, rows, n, nullptr, nullptr, 0, nullptr, 0, static_cast<hipStream_t>(stream)),
+            "argmax launch");
     return CQ_OK;
 }
 
@@ -1312,7 +1313,18 @@ int nd_argmax_advance_dev(int32_t *out, const float *v, int rows, int n, int32_t
     if (rows < 0 || n <= 0) return fail(CQ_ERR_MISUSE, "decoder: argmax of %d rows of %d", rows, n);
     if (rows > 0 && (!out || !v || !pos || !span_hi))
         return fail(CQ_ERR_MISUSE, "decoder: argmax with a nil operand");
-    HIP_TRY(launch_argmax(out, v, rows, n, pos, span_hi, span_stride, static_cast<hipStream_t>(stream)),
+    HIP_TRY(launch_argmax(out, v, rows, n, pos, span_hi, span_stride, nullptr, 0, static_cast<hipStream_t>(stream)),
+            "argmax launch");
+    return CQ_OK;
+}
+
+int nd_argmax_advance_eos_dev(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
+                              int span_stride, int32_t *done, int eos, void *stream) {
+    if (rows < 0 || n <= 0) return fail(CQ_ERR_MISUSE, "decoder: argmax of %d rows of %d", rows, n);
+    if (rows > 0 && (!out || !v || !pos || !span_hi || !done))
+        return fail(CQ_ERR_MISUSE, "decoder: argmax with a nil operand");
+    if (eos < 0 || eos >= n) return fail(CQ_ERR_MISUSE, "decoder: stop token %d outside a vocabulary of %d", eos, n);
+    HIP_TRY(launch_argmax(out, v, rows, n, pos, span_hi, span_stride, done, eos, static_cast<hipStream_t>(stream)),
             "argmax launch");
     return CQ_OK;
 }

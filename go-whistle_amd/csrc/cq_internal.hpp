@@ -239,7 +239,7 @@ hipError_t launch_zc_rmsnorm(float *dst, const float *x, const float *gain, int 
 hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float *cos_t, const float *sin_t,
                        int positions, const int32_t *pos, int rows_per_pos, hipStream_t s);
 hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
-                         int span_stride, hipStream_t s);
+                         int span_stride, int32_t *done, int eos, hipStream_t s);
 hipError_t launch_silu(float *x, long long n, hipStream_t s);
 hipError_t launch_add(float *x, const float *y, long long n, hipStream_t s);
 hipError_t launch_sigmoid_gate(float *out, float *gate, long long n, hipStream_t s);

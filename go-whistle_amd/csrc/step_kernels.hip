@@ -113,8 +113,11 @@ __device__ __forceinline__ ArgmaxCand argmax_pick(ArgmaxCand a, ArgmaxCand b) {
 // the new position + 1 (the keys the next step's query sees after its
 // append), so a step needs no separate launches for them.
 __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *v, int n, int32_t *pos,
-                                                     int32_t *span_hi, int span_stride) {
+                                                     int32_t *span_hi, int span_stride, int32_t *done, int eos) {
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // A stream that has stopped keeps its token (the stop token) and its
+    // position: the steps it still runs in the batch change nothing it reports.
+    if (done && done[r]) return;
     const float *row = v + static_cast<long long>(r) * n;
     ArgmaxCand c{0.0f, INT_MAX};
     auto take = [&](float x, int i) {
@@ -161,12 +164,14 @@ __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *
     if (tid == 0) {
         for (int w = 1; w < 4; ++w) c = argmax_pick(c, ArgmaxCand{sv[w], si[w]});
         const bool nan0 = n > 0 && row[0] != row[0];
-        out[r] = (n == 0 || nan0 || c.i == INT_MAX) ? 0 : c.i;
+        const int tok = (n == 0 || nan0 || c.i == INT_MAX) ? 0 : c.i;
+        out[r] = tok;
         if (pos) {
             const int p = pos[r] + 1;
             pos[r] = p;
             span_hi[static_cast<long long>(r) * span_stride] = p + 1;
         }
+        if (done && tok == eos) done[r] = 1;  // greedy.go:55-59: the stream stops at EOS
     }
 }
 
@@ -262,9 +267,9 @@ hipError_t launch_rope(float *x, int rows, int heads, int head_dim, const float 
 }
 
 hipError_t launch_argmax(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
-                         int span_stride, hipStream_t s) {
+                         int span_stride, int32_t *done, int eos, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, out, v, n, pos, span_hi, span_stride);
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, out, v, n, pos, span_hi, span_stride, done, eos);
     return hipGetLastError();
 }
 

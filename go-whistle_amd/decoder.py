@@ -167,9 +167,13 @@ class Decoder:
         self.sin = torch.from_numpy(model.rope_sin).to(device)
         self.tok = z(B, dt=i32)
         self.pos = z(B, dt=i32)
+        # Greedy's stop (greedy.go:50-66): with a stop token set, done[b]
+        # becomes 1 at stream b's EOS and its token and position stay put.
+        self.done = z(B, dt=i32)
+        self.eos = None
         self.spans_self = z(B, 4, dt=i32)
         self.spans_self[:, 3] = 1  # keys 0..pos after the first step's append
-        self.steps = 0  # tokens decoded since reset (every stream is at this position)
+        self.steps = 0  # steps run since reset (a stream that stopped at EOS is behind it)
         hk = c.dim // c.head_dim
         # The cross memory is head-major, [stream][head][frame][code]: every
         # (stream, head) a contiguous block, read as batch * heads one-head
@@ -244,6 +248,7 @@ class Decoder:
 
         self.tok.copy_(torch.as_tensor(np.asarray(tokens, np.int32), device=self.tok.device))
         self.pos.zero_()
+        self.done.zero_()
         self._sync_spans()
         self.steps = 0
 
@@ -300,8 +305,13 @@ class Decoder:
         """argmax of the logits into tok, pos += 1 and the next step's key
         bound, in one launch."""
         c = self.cfg
-        check(lib().nd_argmax_advance_dev(_ptr(self.tok), _ptr(self.logits), self.batch, c.vocab, _ptr(self.pos),
-                                          _ptr(self.spans_self[:, 3]), 4, s))
+        if self.eos is None:
+            check(lib().nd_argmax_advance_dev(_ptr(self.tok), _ptr(self.logits), self.batch, c.vocab, _ptr(self.pos),
+                                              _ptr(self.spans_self[:, 3]), 4, s))
+        else:
+            check(lib().nd_argmax_advance_eos_dev(_ptr(self.tok), _ptr(self.logits), self.batch, c.vocab,
+                                                  _ptr(self.pos), _ptr(self.spans_self[:, 3]), 4, _ptr(self.done),
+                                                  int(self.eos), s))
 
     def _step_fused(self):
         c, B = self.cfg, self.batch
@@ -404,48 +414,73 @@ class Decoder:
         self.mem_index = torch.as_tensor(blocks, device=dev)
         self.tok.copy_(self.tok.index_select(0, par.long()))
         self.pos.copy_(self.pos.index_select(0, par.long()))
+        self.done.copy_(self.done.index_select(0, par.long()))
         self._sync_spans()
 
-    def resume(self, n, graph=True):
-        """Greedy-decodes n more tokens from the current state; [batch, n]."""
+    def resume(self, n, graph=True, eos=None, check_every=16):
+        """Greedy-decodes n more tokens from the current state; [batch, n].
+
+        With eos (a token id), each stream stops at its own EOS, as
+        GreedyMemory stops (greedy.go:50-66): the row holds the stream's
+        tokens, then -1 from its EOS on (the reference's Result.Tokens
+        leaves EOS out); stopped[b] is True for a stream that stopped at
+        EOS, False for one that reached n tokens (MaxTokens). Every
+        check_every steps the host looks at the streams' done flags and
+        ends early once all have stopped."""
         import torch
 
+        from ._lib import CQPanic
+
         self._reserve(n)
+        if eos is not None and not 0 <= int(eos) < self.cfg.vocab:
+            raise CQPanic(f"decoder: stop token {eos} outside a vocabulary of {self.cfg.vocab}")
+        self.eos = None if eos is None else int(eos)
         out = torch.zeros(self.batch, n, dtype=torch.int32, device=self.tok.device)
-        if n == 0:
-            return out
-        if not graph:
-            for i in range(n):
-                self.step()
-                out[:, i] = self.tok
-            return out
-        g = self.capture()
-        for i in range(n):
-            g.replay()
-            out[:, i] = self.tok
-        self.steps += n
+        try:
+            done = 0
+            g = self.capture() if graph and n > 0 else None
+            while done < n:
+                if g is None:
+                    self.step()
+                else:
+                    g.replay()
+                    self.steps += 1
+                out[:, done] = self.tok
+                done += 1
+                if self.eos is not None and done % check_every == 0 and done < n and bool(self.done.all()):
+                    out[:, done:] = self.eos
+                    break
+        finally:
+            eos, self.eos = self.eos, None
+        if eos is not None:
+            hit = out == eos
+            after = torch.cumsum(hit.to(torch.int32), dim=1) > 0
+            out[after] = -1
+            self.stopped = hit.any(dim=1).cpu().numpy()
         return out
 
-    def decode(self, first_tokens, n, graph=True):
-        """Greedy-decodes n tokens after first_tokens; returns [batch, n].
+    def decode(self, first_tokens, n, graph=True, eos=None):
+        """Greedy-decodes n tokens after first_tokens; returns [batch, n]
+        (with eos: each stream up to its EOS, then -1, as resume says).
         n past max_pos raises CQPanic before anything runs."""
         from ._lib import CQPanic
 
         if not 0 <= n <= self.cfg.max_pos:
             raise CQPanic(f"decoder: {n} tokens exceed max_pos {self.cfg.max_pos}")
         self.reset(first_tokens)
-        return self.resume(n, graph)
+        return self.resume(n, graph, eos)
 
     def capture(self):
         """A HIP graph of one step (the state it reads is on the device).
         Replaying it does not advance the host's step count: resume() does."""
         import torch
 
-        pos0, tok0, steps0 = self.pos.clone(), self.tok.clone(), self.steps
+        pos0, tok0, done0, steps0 = self.pos.clone(), self.tok.clone(), self.done.clone(), self.steps
         self.step()  # kernel attributes are set outside the capture
         torch.cuda.synchronize()
         self.pos.copy_(pos0)
         self.tok.copy_(tok0)
+        self.done.copy_(done0)
         self._sync_spans()
         self.steps = steps0
         g = torch.cuda.CUDAGraph()

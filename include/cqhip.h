@@ -271,6 +271,13 @@ int nd_argmax_dev(int32_t *out, const float *v, int rows, int n, void *stream);
  * launches of its own. */
 int nd_argmax_advance_dev(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
                           int span_stride, void *stream);
+/* nd_argmax_advance_dev with greedy decoding's stop (internal/decoder/
+ * greedy.go:50-66): a stream whose done[r] is nonzero is left as it is (its
+ * token, position and key bound); otherwise, after the argmax and the
+ * advance, done[r] = 1 when the token is eos. Streams of one batch stop one
+ * by one, each after its own EOS, as GreedyMemory stops each hypothesis. */
+int nd_argmax_advance_eos_dev(int32_t *out, const float *v, int rows, int n, int32_t *pos, int32_t *span_hi,
+                              int span_stride, int32_t *done, int eos, void *stream);
 /* x = x * sigmoid(x), sigmoid from the amd64 exponent kernel's arithmetic
  * (exp_amd64.s:84-112) on non-positive arguments. No reference
  * counterpart: the synthetic decoder's FFN activation. */

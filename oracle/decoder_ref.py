@@ -36,8 +36,12 @@ class RefDecoder:
             vq, vs = orc.quantize_rows(v, c.dim, c.head_dim)
             self.mem.append((kq, ks, vq, vs))
 
-    def decode(self, first, n, want_logits=False):
+    def decode(self, first, n, want_logits=False, eos=None):
+        """Greedy tokens after first, at most n (MaxTokens); with eos, the
+        loop stops at EOS, which it leaves out, and self.stopped says so
+        (GreedyMemory, greedy.go:50-66)."""
         c, m = self.cfg, self.model
+        self.stopped = False
         hk = c.dim // c.head_dim
         scale = np.float32(math.sqrt(c.head_dim))
         caches = [[np.zeros(c.max_pos * c.dim, np.int8), np.zeros(c.max_pos * hk, np.float32),
@@ -76,6 +80,9 @@ class RefDecoder:
             h = orc.zc_rmsnorm(x, m.gains[3 * c.layers], c.dim)
             logits = self.emb.gemm(h, 1)
             tok = int(orc.argmax(logits, 1, c.vocab)[0])
+            if eos is not None and tok == eos:
+                self.stopped = True
+                break
             out.append(tok)
             if want_logits:
                 logits_all.append(logits)

@@ -101,3 +101,14 @@ def test_noalloc_reorder_refuses_oversize_before_the_device():
     with pytest.raises(gw.CQPanic) as e:
         _lib.check(_lib.lib().kv_reorder_noalloc_dev(p, p, p, p, 256, 512, 512, 64, None))
     assert "67108864" in str(e.value)
+
+
+@pytest.mark.parametrize("eos,done", [(-1, True), (16384, True), (5, False)])
+def test_argmax_eos_misuse_before_the_device(eos, done):
+    # nd_argmax_advance_eos_dev rejects a stop token outside the vocabulary
+    # and a nil done mask before any device call
+    from ctypes import c_void_p
+
+    p = c_void_p(256)  # never dereferenced: the checks come first
+    with pytest.raises(gw.CQPanic):
+        _lib.check(_lib.lib().nd_argmax_advance_eos_dev(p, p, 4, 16384, p, p, 4, p if done else None, eos, None))

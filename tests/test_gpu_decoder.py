@@ -203,6 +203,52 @@ def test_small_decoder_batch_bit_exact():
     assert len(set(toks[0].tolist())) > 1
 
 
+def _eos_case(n_batch, first, n, eos_from, check_every=16, shared=False):
+    """Decodes without a stop token, picks EOS as a token stream eos_from[0]
+    emits at step eos_from[1], decodes again with it: each stream must give
+    its oracle's GreedyMemory tokens, stopping at its own first EOS. shared:
+    every stream reads stream 0's cross memory (a fork from stream 0)."""
+    cfg = dec.DecoderConfig(vocab=4096, layers=2, frames=100, max_pos=64)
+    model = dec.make_model(5, cfg)
+    d = dec.Decoder(model, n_batch)
+    d.set_memory(5)
+    if shared:
+        d.fork([0] * n_batch)
+    plain = d.decode(first, n).cpu().numpy()
+    eos = int(plain[eos_from[0], eos_from[1]])
+    d.reset(first)
+    got = d.resume(n, eos=eos, check_every=check_every).cpu().numpy()
+    pos = d.pos.cpu().numpy()
+    ref = decoder_ref.RefDecoder(model)
+    enc = {}
+    for b in range(n_batch):
+        m = 0 if shared else b
+        ref.memory(enc.setdefault(m, dec.encoder_states(5, cfg, m)))
+        want = ref.decode(first[b], n, eos=eos)
+        row = list(got[b])
+        k = row.index(-1) if -1 in row else n
+        assert row[:k] == want and all(t == -1 for t in row[k:]), (b, row, want)
+        assert bool(d.stopped[b]) == ref.stopped, b
+        # a stopped stream's position froze after the step that gave EOS
+        assert pos[b] == (len(want) + 1 if ref.stopped else n), (b, pos[b])
+        # tokens before the stop are the plain run's
+        assert list(plain[b][:k]) == want, b
+    return d, eos
+
+
+def test_eos_stops_each_stream():
+    d, eos = _eos_case(4, [1, 2, 3, 4], 40, (1, 12))
+    assert d.stopped[1]
+
+
+def test_eos_ends_the_batch_once_every_stream_stopped():
+    # two streams with the same first token and memory decode alike: both
+    # stop at the same step, and the host ends the run at its next check
+    d, eos = _eos_case(2, [7, 7], 40, (0, 2), check_every=4, shared=True)
+    assert all(d.stopped)
+    assert d.steps <= 8
+
+
 def test_full_decoder_batch1_200_tokens():
     cfg = dec.DecoderConfig()
     print("full decoder, batch 1, 200 tokens", flush=True)
