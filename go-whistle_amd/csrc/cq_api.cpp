@@ -467,7 +467,7 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
     const CqStore &s0 = *ms[0]->st;
     const int ta = mfma_split_activations();
     const int rpw = mfma_split_rows_per_workgroup() / kBlockRows;
-    const int max_rows = 65535 * ta;
+    const int max_rows = 65535 * 4;  // the fold's grid y: activations in fours
     for (int r0 = 0; r0 < rows; r0 += max_rows) {
         const int nr = std::min(max_rows, rows - r0);
         LutLaunch a;
@@ -495,6 +495,8 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
             ++a.njobs;
         }
         if (a.njobs == 0 || nr == 0) return CQ_OK;
+        a.split_at = (nr + ta - 1) / ta;
+        a.split_tiles = wg * a.split_at;
         float *ws = nullptr;
         if (int e = split_workspace(terms * sizeof(float), &ws)) return e;
         size_t off = 0;
@@ -502,8 +504,7 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
             a.term[k] = ws + off;
             off += static_cast<size_t>(a.jobs[k].groups) * nr * a.jobs[k].nblk * kBlockRows;
         }
-        HIP_TRY(launch_lut_mfma_split(a, s0.width, wg, (nr + ta - 1) / ta, s0.groups, fold, nr, stream),
-                "lut mfma split launch");
+        HIP_TRY(launch_lut_mfma_split(a, s0.width, fold, stream), "lut mfma split launch");
     }
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;

@@ -119,9 +119,12 @@ struct LutLaunch {
     int waves;                   // kernel-argument path: wavefronts per workgroup (> kLutWaves: the wide form)
     int vsplit;                  // wide form: wavefronts per group (1 or 2)
     // The MFMA form split over groups: job k's float terms [group][activation]
-    // [64 * nblk rows] in the workspace, and its first block in the fold's grid.
+    // [64 * nblk rows] in the workspace; the tiles (256-row groups over the
+    // jobs, wg0, times split_at activation tiles) and one counter per tile,
+    // zero between launches.
     float *term[kKernargJobs];
-    int fold0[kKernargJobs];
+    int fold0[kKernargJobs];  // the job's first block in the fold's grid
+    int split_tiles, split_at;
 };
 
 size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw);
@@ -138,15 +141,14 @@ bool mfma_geometry_supported(int bits, int group);
 int mfma_rows_per_workgroup();
 hipError_t launch_lut_mfma(const LutLaunch &a, int bits, int ta, int wg, int act_tiles, hipStream_t s);
 // The MFMA form split over groups (mfma_kernels.hip), for products whose
-// 512-row workgroups would leave most CUs idle: grid x covers the jobs'
-// 256-row tiles (wg0), y the 32-activation tiles, z the groups; each
-// workgroup writes its group's float terms to a.term. Then the fold, grid x
-// over the jobs' 64-row blocks (fold0), y over the activations in fours,
-// adds them in group order and applies the epilogue. Both on stream s.
+// 512-row workgroups would leave most CUs idle: a workgroup per (tile,
+// group), a tile being 256 rows (wg0 counts the jobs' row groups) by 32
+// activations; each writes its group's float terms to a.term. Then the
+// fold, grid x over the jobs' 64-row blocks (fold0), y over the activations
+// in fours, adds them in group order and applies the epilogue. On stream s.
 int mfma_split_rows_per_workgroup();
 int mfma_split_activations();
-hipError_t launch_lut_mfma_split(const LutLaunch &a, int bits, int wg, int act_tiles, int groups, int fold_blocks,
-                                 int rows, hipStream_t s);
+hipError_t launch_lut_mfma_split(const LutLaunch &a, int bits, int fold_blocks, hipStream_t s);
 
 struct RowArgs {
     const uint8_t *idx;

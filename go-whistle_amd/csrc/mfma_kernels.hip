@@ -406,251 +406,49 @@ hipError_t launch_mfma_t(const LutLaunch &a, int wg, int act_tiles, hipStream_t 
 // ---- The split form: one group per workgroup, then a fold in group order ----
 //
 // For products whose 512-row workgroups would leave most CUs idle (the
-// decode step's 512- and 2048-row matrices at a few hundred activations, the
-// encoder's 375 frames): a workgroup of 4 wavefronts owns 256 weight rows (a
-// 64-row block per wavefront), 32 activations and ONE group g. It rotates
-// the group, builds its tables and runs its MFMAs as lut_mfma_kernel does,
-// then writes the group's float terms float32(S) * (norm * step) (the lut
-// kernel's term, rounded the same way) to the workspace, [g][activation]
-// [row]. mfma_fold_kernel then adds an output's terms in group order from 0
+// decode step's products at a few hundred activations, the encoder's 375
+// frames): a workgroup of 4 wavefronts owns 256 weight rows (a 64-row block
+// per wavefront), 32 activations and ONE group g. It rotates the group,
+// builds the group's tables in LDS and runs the MFMAs, then writes the
+// group's float terms float32(S) * (norm * step) (the lut kernel's term,
+// rounded the same way) to the workspace, [g][activation][row].
+// mfma_fold_kernel then adds an output's terms in group order from 0
 // (lut.go:297-310) and applies the fused epilogue: bit for bit the lut
 // kernel's result.
+//
+// Operands of v_mfma_i32_32x32x32_i8 (lane 32h + c holds K = 16h .. 16h + 15
+// of row or column c): one K step is a position pair (2p, 2p + 1), lane half
+// h carrying position 2p + h. B (columns = weight rows) is the one-hot of
+// the row's code at that position, 1 at byte code; A (rows = activations)
+// is one plane of the position's 16 entries (l = v & 63 or h = v >> 6). Two
+// MFMAs per pair and row tile, one per plane, into two accumulators, so one
+// one-hot serves both planes and S = S_l + 64 * S_h exactly.
+//
+// Grid: one dimension, 8-aligned tiles (256 rows x 32 activations) times
+// groups, the groups of a tile 8 workgroups apart.
 constexpr int kSplitWaves = 4;
 constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kSplitTa = 32;  // activations per workgroup: one 32-wide MFMA tile
 
-template <int BITS>
-__global__ __launch_bounds__(kSplitThreads) void lut_mfma_split_kernel(LutLaunch a) {
-    using M = MfmaGeo<BITS>;
-    constexpr int G = M::G, AP = M::AP, CK = M::CK, TA = kSplitTa;
-    extern __shared__ __align__(16) unsigned char smem[];
-    float *av = reinterpret_cast<float *>(smem);                    // [TA][AP] scaled rotated group
-    float *stp = av + TA * AP;                                       // [TA] steps of the group
-    int8_t *tab = reinterpret_cast<int8_t *>(stp + TA);              // [2][CK][2][TA][16] table planes
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
-
-    int jb = 0;
-#pragma unroll
-    for (int k = 1; k < kKernargJobs; ++k)
-        if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.wg0[k]) jb = k;
-    const JobDesc &J = a.jobs[jb];
-    const int blk = (static_cast<int>(blockIdx.x) - a.wg0[jb]) * kSplitWaves + w;  // this wavefront's block
-    const bool rows_here = blk < J.nblk;
-    const int gblk = J.blk0 + blk;
-    const int t0 = blockIdx.y * TA;
-    const int g = blockIdx.z;
-    const int groups = J.groups;
-
-    // Fused ZCRMSNorm of the activation rows (norm.go:53-109): the
-    // workgroup's activations' divisors over their whole rows.
-    __shared__ double zpart[4 * TA];
-    __shared__ float zrms[TA];
-    if (J.ngain) {
-        for (int e = tid; e < 4 * TA; e += kSplitThreads) {
-            const int t = t0 + e / 4;
-            zpart[e] = t < J.rows ? zc_partial(J.x + static_cast<long long>(t) * J.x_stride, J.in, e % 4) : 0.0;
-        }
-        __syncthreads();
-        for (int e = tid; e < TA; e += kSplitThreads)
-            zrms[e] = zc_rms(zpart[4 * e], zpart[4 * e + 1], zpart[4 * e + 2], zpart[4 * e + 3], J.in);
-        __syncthreads();
-    }
-
-    // The group's index bytes of the wavefront's rows: UPG 16-byte units,
-    // issued before the rotation so that they land under it.
-    uint32_t idx[M::UPG][2][4];
-#pragma unroll
-    for (int u = 0; u < M::UPG; ++u)
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            if (rows_here) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(
-                    J.idx + ((static_cast<size_t>(gblk) * J.units + g * M::UPG + u) * 64 + rt * 32 + l32) * 16);
-                idx[u][rt][0] = v.x; idx[u][rt][1] = v.y; idx[u][rt][2] = v.z; idx[u][rt][3] = v.w;
-            } else {
-                idx[u][rt][0] = idx[u][rt][1] = idx[u][rt][2] = idx[u][rt][3] = 0u;
-            }
-        }
-    float nrm[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-        nrm[rt] = rows_here ? __half2float(__ushort_as_half(
-                                  J.norm[(static_cast<size_t>(gblk) * groups + g) * 64 + rt * 32 + l32]))
-                            : 0.0f;
-
-    // 1. Rotation and bound of group g of each activation (lut.go:158-178),
-    // TA / 4 activations per wavefront, their butterflies interleaved.
-    constexpr int PW = TA / kSplitWaves;
-    {
-        float v[PW][2];
-#pragma unroll
-        for (int k = 0; k < PW; ++k) {
-            const int tt = w + k * kSplitWaves, t = t0 + tt;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int col = g * G + e * 64 + lane;
-                float xv = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
-                if (J.xgate && t < J.rows && col < J.in)  // Attention.output's gate (attention.go:245-249)
-                    xv = xv * gate_sigmoid(J.xgate[static_cast<long long>(t) * J.x_stride + col]);
-                if (J.ngain && t < J.rows && col < J.in) {
-                    const float gx = J.ngain[col] * xv;
-                    xv = gx / zrms[tt];
-                }
-                v[k][e] = xv;
-            }
-        }
-#pragma unroll
-        for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
-#pragma unroll
-            for (int k = 0; k < PW; ++k)
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const float p = xor_lane(v[k][e], h);
-                    v[k][e] = (lane & h) ? p - v[k][e] : v[k][e] + p;
-                }
-        }
-#pragma unroll
-        for (int k = 0; k < PW; ++k) {  // stage h = 64 within the lane
-            const float p = v[k][0], q = v[k][1];
-            v[k][0] = p + q;
-            v[k][1] = p - q;
-        }
-        float mx[PW];
-#pragma unroll
-        for (int k = 0; k < PW; ++k) {
-            mx[k] = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                if constexpr (BITS == 4) {
-                    mx[k] = go_max(mx[k], fabsf(v[k][e]));
-                } else {
-                    const float p = xor_lane<1>(v[k][e]);
-                    const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
-                    mx[k] = go_max(mx[k], s2);
-                }
-            }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-            for (int k = 0; k < PW; ++k) mx[k] = go_max(mx[k], xor_lane(mx[k], off));
-#pragma unroll
-        for (int k = 0; k < PW; ++k) {
-            const int tt = w + k * kSplitWaves;
-            const float m = J.cb_max * mx[k];
-            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
-#pragma unroll
-            for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[k][e] * inv;
-            if (lane == 0) stp[tt] = m * J.lut_step;
-        }
-    }
-
-    // 2. The group's tables, CK positions a chunk, two planes each (as
-    // lut_mfma_kernel's build, TA activations).
-    auto build = [&](int c, int buf) {
-        for (int e = tid; e < TA * CK; e += kSplitThreads) {
-            const int t = e % TA, jc = e / TA;
-            const int j = c * CK + jc;
-            uint32_t b[16];
-            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
-                const float x = av[t * AP + j];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const float f = J.cb[q] * x;
-                    b[q] = rne_bits(f);
-                }
-            } else {  // lutTables2Generic (lut.go:239-258): code q = hi << 2 | lo
-                const float x0 = av[t * AP + 2 * j], x1 = av[t * AP + 2 * j + 1];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const float l = J.cb[q & 3] * x0, h = J.cb[q >> 2] * x1;
-                    const float s = l + h;
-                    b[q] = rne_bits(s);
-                }
-            }
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) planes4(b[4 * q], b[4 * q + 1], b[4 * q + 2], b[4 * q + 3], lo[q], hi[q]);
-            int8_t *dst = tab + ((static_cast<size_t>(buf) * CK + jc) * 2 * TA + t) * 16;
-            *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4 *>(dst + TA * 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        }
-    };
-    lds_barrier();
-    build(0, 0);
-    i32x16 acc[2] = {i32x16{}, i32x16{}};
-    lds_barrier();
-
-    // 3. Per chunk: the next chunk's tables built while this one's MFMAs run.
-    const unsigned long long val = half ? 64ull : 1ull;
-    constexpr int CW = M::CW;
-#pragma unroll
-    for (int u = 0; u < M::UPG; ++u) {
-#pragma unroll
-        for (int q = 0; q < 4 / CW; ++q) {
-            const int c = (4 / CW) * u + q;
-            if (c + 1 < M::NCH) build(c + 1, (c + 1) & 1);
-            if (rows_here) {
-                // lane half 0 reads a position's l plane, half 1 its h plane
-                const int8_t *tb = tab + (static_cast<size_t>(c & 1) * CK * 2 + half) * TA * 16;
-                i32x4 A[2];
-                A[0] = *reinterpret_cast<const i32x4 *>(tb + l32 * 16);
-#pragma unroll
-                for (int jc = 0; jc < CK; ++jc) {
-                    if (jc + 1 < CK)
-                        A[(jc + 1) & 1] =
-                            *reinterpret_cast<const i32x4 *>(tb + (static_cast<size_t>(jc + 1) * 2 * TA + l32) * 16);
-#pragma unroll
-                    for (int rt = 0; rt < 2; ++rt) {
-                        // position jc: word jc / 8 of the chunk, byte (jc % 8) / 2, nibble jc % 2
-                        const uint32_t n = (idx[u][rt][q * CW + jc / 8] >> (4 * (jc % 8))) & 15u;
-                        acc[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[jc & 1], one_hot(n, val), acc[rt], 0, 0, 0);
-                    }
-                }
-            }
-            lds_barrier();
-        }
-    }
-
-    // 4. The group's terms float32(S) * (norm * step) (lut.go:297-310), to
-    // the workspace: [g][activation][64 * nblk rows] of this job.
-    if (rows_here) {
-        const long long rs = static_cast<long long>(J.nblk) * 64;
-        float *tg = a.term[jb] + static_cast<long long>(g) * J.rows * rs;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int tt = (i >> 2) * 8 + half * 4 + (i & 3), t = t0 + tt;
-            if (t >= J.rows) continue;
-            const float step = stp[tt];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const float coef = nrm[rt] * step;
-                tg[static_cast<long long>(t) * rs + blk * 64 + rt * 32 + l32] = static_cast<float>(acc[rt][i]) * coef;
-            }
-        }
-    }
+// 16-byte one-hot: 1 at byte c (c < 16), as two 64-bit shifts.
+__device__ __forceinline__ i32x4 one_hot1(uint32_t c) {
+    const uint32_t sh = (c & 7u) << 3;
+    const uint32_t up = c >> 3;  // 1: the byte is in the upper eight
+    const unsigned long long lo = static_cast<unsigned long long>(up ^ 1u) << sh;
+    const unsigned long long hi = static_cast<unsigned long long>(up) << sh;
+    i32x4 r;
+    r.x = static_cast<int>(lo);
+    r.y = static_cast<int>(lo >> 32);
+    r.z = static_cast<int>(hi);
+    r.w = static_cast<int>(hi >> 32);
+    return r;
 }
 
-// The fold of the split form: one wavefront per (activation, 64-row block),
-// lane = row: y = 0, then y = y + term[g] for g in order (lut.go:297-310),
-// then the lut kernel's epilogue: the int8 append of the block as a head
-// (Int8Rows.Append, int8.go:36-55, after RoPE at the stream's position,
-// rope.go:69-81), and y, with the residual add or SiLU, for the view's rows.
-__global__ __launch_bounds__(256) void mfma_fold_kernel(LutLaunch a) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int jb = 0;
-#pragma unroll
-    for (int k = 1; k < kKernargJobs; ++k)
-        if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.fold0[k]) jb = k;
-    const JobDesc &J = a.jobs[jb];
-    const int blk = static_cast<int>(blockIdx.x) - a.fold0[jb];
-    const int t = blockIdx.y * 4 + w;
-    if (blk >= J.nblk || t >= J.rows) return;
-    const long long rs = static_cast<long long>(J.nblk) * 64;
-    const float *tp = a.term[jb] + static_cast<long long>(t) * rs + blk * 64 + lane;
-    float y = 0.0f;
-    for (int g = 0; g < J.groups; ++g) y = y + tp[static_cast<long long>(g) * J.rows * rs];
-
+// The lut kernel's epilogue for one activation t and one 64-row block (lane
+// = row): the int8 append of the block as a head (Int8Rows.Append,
+// int8.go:36-55, after RoPE at the stream's position, rope.go:69-81), and
+// y, with the residual add or SiLU, for the view's rows.
+__device__ __forceinline__ void fold_epilogue(const JobDesc &J, int t, int blk, int lane, float y) {
     const int row = (J.blk0 + blk) * 64;  // root row of lane 0
     if (J.app_q) {
         const int p = J.app_pos[t];
@@ -688,9 +486,346 @@ __global__ __launch_bounds__(256) void mfma_fold_kernel(LutLaunch a) {
 }
 
 template <int BITS>
-hipError_t launch_split_t(const LutLaunch &a, int wg, int act_tiles, int groups, hipStream_t s) {
+__global__ __launch_bounds__(kSplitThreads) void lut_mfma_split_kernel(LutLaunch a) {
+    using M = MfmaGeo<BITS>;
+    constexpr int G = M::G, AP = M::AP, CK = M::CK, TA = kSplitTa;
+    constexpr int CPP = CK / 2;          // position pairs per chunk
+    constexpr int PLANE = 2 * TA * 16;   // one plane of a pair: 2 positions x TA activations x 16 codes
+    constexpr int PAIR = 2 * PLANE;      // both planes
+    constexpr int BUF = CPP * PAIR;      // a chunk's tables
+    extern __shared__ __align__(16) unsigned char smem[];
+    float *av = reinterpret_cast<float *>(smem);                    // [TA][AP] scaled rotated group
+    float *stp = av + TA * AP;                                       // [TA] steps of the group
+    int8_t *tab = reinterpret_cast<int8_t *>(stp + TA);              // [2][CPP][plane][half][TA][16]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
+
+    const int groups = a.jobs[0].groups;  // one geometry per launch
+    const int L = blockIdx.x;
+    const int rest = L >> 3;
+    const int g = rest % groups;
+    const int tile = (rest / groups) * 8 + (L & 7);
+    if (tile >= a.split_tiles) return;
+    const int rg = tile / a.split_at;  // row group over the jobs' 256-row groups
+    const int t0 = (tile % a.split_at) * TA;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kKernargJobs; ++k)
+        if (k < a.njobs && rg >= a.wg0[k]) jb = k;
+    const JobDesc &J = a.jobs[jb];
+    const int blk = (rg - a.wg0[jb]) * kSplitWaves + w;  // this wavefront's block
+    const bool rows_here = blk < J.nblk;
+    const int gblk = J.blk0 + blk;
+    const int rows = J.rows, in = J.in, units = J.units;
+    const long long xs = J.x_stride;
+    const float *X = J.x, *XG = J.xgate, *NG = J.ngain;
+    const uint8_t *IDX = J.idx;
+    const uint16_t *NRM = J.norm;
+
+    // Every first load at once, without branches (rows past the view and
+    // activations past the rows read a clamped address and go unused): the
+    // group's index bytes of the wavefront's rows (UPG 16-byte units), their
+    // norms, and the wavefront's activations' values of the group (TA / 4
+    // activations, two per lane).
+    const size_t bk = static_cast<size_t>(J.blk0 + min(blk, J.nblk - 1));
+    uint32_t idx[M::UPG][2][4];
+#pragma unroll
+    for (int u = 0; u < M::UPG; ++u)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(
+                IDX + ((bk * units + g * M::UPG + u) * 64 + rt * 32 + l32) * 16);
+            idx[u][rt][0] = v.x; idx[u][rt][1] = v.y; idx[u][rt][2] = v.z; idx[u][rt][3] = v.w;
+        }
+    unsigned short nrm16[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) nrm16[rt] = NRM[(bk * groups + g) * 64 + rt * 32 + l32];
+    constexpr int PW = TA / kSplitWaves;
+    float v[PW][2], gv[PW][2];
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const long long rowoff = static_cast<long long>(min(t0 + w + k * kSplitWaves, rows - 1)) * xs;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int col = min(g * G + e * 64 + lane, in - 1);
+            v[k][e] = X[rowoff + col];
+            gv[k][e] = XG ? XG[rowoff + col] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < PW; ++k)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            if (!(t0 + w + k * kSplitWaves < rows && g * G + e * 64 + lane < in)) v[k][e] = 0.0f;
+
+    // Fused ZCRMSNorm of the activation rows (norm.go:53-109): the tile's
+    // activations' divisors over their whole rows, the reference's four
+    // float64 partial sums (i mod 4, each in order), the rows staged through
+    // LDS 256 columns at a time.
+    __shared__ double zpart[4 * TA];
+    __shared__ float zrms[TA];
+    if (NG) {
+        float *stage = reinterpret_cast<float *>(tab);  // [TA][256]
+        const int full = in & ~3;
+        const int ct = tid >> 2, ck = tid & 3;         // chain thread (tid < 4 * TA): activation, partial
+        double s = 0.0;
+        for (int p0 = 0; p0 < full; p0 += 256) {
+            float st[TA * 256 / kSplitThreads];
+#pragma unroll
+            for (int r = 0; r < TA * 256 / kSplitThreads; ++r) {
+                const int e = tid + r * kSplitThreads;
+                const int tt = e >> 8, col = p0 + (e & 255);
+                st[r] = X[static_cast<long long>(min(t0 + tt, rows - 1)) * xs + min(col, full - 1)];
+            }
+#pragma unroll
+            for (int r = 0; r < TA * 256 / kSplitThreads; ++r) {
+                const int e = tid + r * kSplitThreads;
+                if (!(t0 + (e >> 8) < rows && p0 + (e & 255) < full)) st[r] = 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < TA * 256 / kSplitThreads; ++r) stage[tid + r * kSplitThreads] = st[r];
+            __syncthreads();
+            if (tid < 4 * TA) {
+                const int n = min(256, full - p0);
+                for (int i = ck; i < n; i += 4) {
+                    const double d = stage[ct * 256 + i];
+                    s = s + d * d;
+                }
+            }
+            __syncthreads();
+        }
+        if (tid < 4 * TA) {
+            if (ck == 0 && t0 + ct < rows)
+                for (int c = full; c < in; ++c) {
+                    const double d = X[static_cast<long long>(t0 + ct) * xs + c];
+                    s = s + d * d;
+                }
+            zpart[tid] = s;
+        }
+        __syncthreads();
+        if (tid < TA) zrms[tid] = zc_rms(zpart[4 * tid], zpart[4 * tid + 1], zpart[4 * tid + 2], zpart[4 * tid + 3], in);
+        __syncthreads();
+    }
+
+    // 1. Rotation and bound of group g of each activation (lut.go:158-178),
+    // the wavefront's TA / 4 activations together, their butterflies
+    // interleaved; first Attention.output's gate (attention.go:245-249) and
+    // the norm.
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const int tt = w + k * kSplitWaves, t = t0 + tt;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int col = g * G + e * 64 + lane;
+            if (t < rows && col < in) {
+                if (XG) v[k][e] = v[k][e] * gate_sigmoid(gv[k][e]);
+                if (NG) {
+                    const float gx = NG[col] * v[k][e];
+                    v[k][e] = gx / zrms[tt];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
+#pragma unroll
+        for (int k = 0; k < PW; ++k)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float p = xor_lane(v[k][e], h);
+                v[k][e] = (lane & h) ? p - v[k][e] : v[k][e] + p;
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {  // stage h = 64 within the lane
+        const float p = v[k][0], q = v[k][1];
+        v[k][0] = p + q;
+        v[k][1] = p - q;
+    }
+    {
+        float mx[PW];
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            mx[k] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                if constexpr (BITS == 4) {
+                    mx[k] = go_max(mx[k], fabsf(v[k][e]));
+                } else {
+                    const float p = xor_lane<1>(v[k][e]);
+                    const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                    mx[k] = go_max(mx[k], s2);
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int k = 0; k < PW; ++k) mx[k] = go_max(mx[k], xor_lane(mx[k], off));
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int tt = w + k * kSplitWaves;
+            const float m = J.cb_max * mx[k];
+            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[k][e] * inv;
+            if (lane == 0) stp[tt] = m * J.lut_step;
+        }
+    }
+
+    // 2. Table items: this thread's are activation tid % TA at positions
+    // jc0 and jc0 + 8 of every chunk, both planes to [buf][jc / 2][plane]
+    // [jc % 2][activation] (as lut_mfma_kernel's build). An item is built a
+    // quarter (four entries) at a time, so that the building spreads over
+    // the previous chunk's MFMAs.
+    float cbv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cbv[q] = J.cb[q];
+    const int tA = tid & (TA - 1), jc0 = tid / TA;
+    float ix[2][2];           // [item][input]: the item's rotated value(s)
+    uint32_t blo[4], bhi[4];  // the item under construction
+    auto item_inputs = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int j = c * CK + jc0 + 8 * k;
+            if constexpr (BITS == 4) {
+                ix[k][0] = av[tA * AP + j];
+            } else {
+                ix[k][0] = av[tA * AP + 2 * j];
+                ix[k][1] = av[tA * AP + 2 * j + 1];
+            }
+        }
+    };
+    auto item_quarter = [&](int c, int s) {  // quarter s & 3 of item s >> 2 of chunk c
+        const int k = s >> 2, qd = s & 3;
+        uint32_t b[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int code = 4 * qd + q;
+            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
+                b[q] = rne_bits(cbv[code] * ix[k][0]);
+            } else {  // lutTables2Generic (lut.go:239-258): code = hi << 2 | lo
+                const float l = cbv[code & 3] * ix[k][0], h = cbv[code >> 2] * ix[k][1];
+                const float sm = l + h;
+                b[q] = rne_bits(sm);
+            }
+        }
+        planes4(b[0], b[1], b[2], b[3], blo[qd], bhi[qd]);
+        if (qd == 3) {
+            const int jc = jc0 + 8 * k;
+            int8_t *dst = tab + ((c & 1) * CPP + (jc >> 1)) * PAIR + ((jc & 1) * TA + tA) * 16;
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(blo[0], blo[1], blo[2], blo[3]);
+            *reinterpret_cast<uint4 *>(dst + PLANE) = make_uint4(bhi[0], bhi[1], bhi[2], bhi[3]);
+        }
+    };
+    lds_barrier();
+    item_inputs(0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) item_quarter(0, s);
+    lds_barrier();
+
+    // 3. Per chunk of CK positions: its MFMAs, and between them the next
+    // chunk's items, a quarter per position pair.
+    i32x16 accl[2] = {i32x16{}, i32x16{}}, acch[2] = {i32x16{}, i32x16{}};
+    const uint32_t hs = 4u * static_cast<uint32_t>(half);  // a lane half takes the odd nibbles
+#pragma unroll
+    for (int c = 0; c < M::NCH; ++c) {
+        const bool more = c + 1 < M::NCH;
+        if (more) item_inputs(c + 1);
+        uint32_t wv[2][2];  // [row tile][word]: 4 position pairs a word, this half's nibbles at 8k
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) wv[rt][q] = idx[c >> 1][rt][(c & 1) * 2 + q] >> hs;
+        const int8_t *tb = tab + (c & 1) * BUF + (half * TA + l32) * 16;
+        // A of pair pp in slot pp % 3 (read two pairs ahead), B of pair pp in
+        // slot pp % 2 (built one pair ahead)
+        i32x4 Al[3], Ah[3], B[2][2];
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+            Al[pp] = *reinterpret_cast<const i32x4 *>(tb + pp * PAIR);
+            Ah[pp] = *reinterpret_cast<const i32x4 *>(tb + pp * PAIR + PLANE);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) B[0][rt] = one_hot1(wv[rt][0] & 15u);
+#pragma unroll
+        for (int pp = 0; pp < CPP; ++pp) {
+            const int sa = pp % 3, sb = pp & 1;
+            if (pp + 2 < CPP) {
+                const int8_t *nb = tb + (pp + 2) * PAIR;
+                Al[(pp + 2) % 3] = *reinterpret_cast<const i32x4 *>(nb);
+                Ah[(pp + 2) % 3] = *reinterpret_cast<const i32x4 *>(nb + PLANE);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // the reads go out here, two pairs before their use
+            if (pp + 1 < CPP) {
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    B[sb ^ 1][rt] = one_hot1((wv[rt][(pp + 1) >> 2] >> (8 * ((pp + 1) & 3))) & 15u);
+            }
+            if (more) item_quarter(c + 1, pp);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+                accl[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al[sa], B[sb][rt], accl[rt], 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+                acch[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah[sa], B[sb][rt], acch[rt], 0, 0, 0);
+            // one MFMA and a share of the VALU work, four times
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        lds_barrier();  // the next chunk's tables are whole; this chunk's buffer is free again
+    }
+
+    // 4. The group's terms float32(S) * (norm * step) (lut.go:297-310), to
+    // the workspace: [g][activation][64 * nblk rows] of this job.
+    const long long rs = static_cast<long long>(J.nblk) * 64;
+    if (rows_here) {
+        float *tg = a.term[jb] + static_cast<long long>(g) * rows * rs;
+        float nrm[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) nrm[rt] = __half2float(__ushort_as_half(nrm16[rt]));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int tt = (i >> 2) * 8 + half * 4 + (i & 3), t = t0 + tt;
+            if (t >= rows) continue;
+            const float step = stp[tt];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int sum = accl[rt][i] + 64 * acch[rt][i];
+                const float coef = nrm[rt] * step;
+                tg[static_cast<long long>(t) * rs + blk * 64 + rt * 32 + l32] = static_cast<float>(sum) * coef;
+            }
+        }
+    }
+}
+
+// The fold of the split form: one wavefront per (activation, 64-row block),
+// lane = row: y = 0, then y = y + term[g] for g in order (lut.go:297-310),
+// then the lut kernel's epilogue.
+__global__ __launch_bounds__(256) void mfma_fold_kernel(LutLaunch a) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kKernargJobs; ++k)
+        if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.fold0[k]) jb = k;
+    const JobDesc &J = a.jobs[jb];
+    const int blk = static_cast<int>(blockIdx.x) - a.fold0[jb];
+    const int t = blockIdx.y * 4 + w;
+    if (blk >= J.nblk || t >= J.rows) return;
+    const long long rs = static_cast<long long>(J.nblk) * 64;
+    const float *tp = a.term[jb] + static_cast<long long>(t) * rs + blk * 64 + lane;
+    float y = 0.0f;
+    for (int g = 0; g < J.groups; ++g) y = y + tp[static_cast<long long>(g) * J.rows * rs];
+    fold_epilogue(J, t, blk, lane, y);
+}
+
+template <int BITS>
+hipError_t launch_split_t(const LutLaunch &a, int grid, hipStream_t s) {
     const size_t lds = mfma_lds_bytes<BITS, kSplitTa>();
-    hipLaunchKernelGGL((lut_mfma_split_kernel<BITS>), dim3(wg, act_tiles, groups), dim3(kSplitThreads), lds, s, a);
+    hipLaunchKernelGGL((lut_mfma_split_kernel<BITS>), dim3(grid), dim3(kSplitThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -699,14 +834,13 @@ hipError_t launch_split_t(const LutLaunch &a, int wg, int act_tiles, int groups,
 int mfma_split_rows_per_workgroup() { return 64 * kSplitWaves; }
 int mfma_split_activations() { return kSplitTa; }
 
-hipError_t launch_lut_mfma_split(const LutLaunch &a, int bits, int wg, int act_tiles, int groups, int fold_blocks,
-                                 int rows, hipStream_t s) {
-    if (wg <= 0 || act_tiles <= 0 || groups <= 0 || fold_blocks <= 0 || rows <= 0) return hipSuccess;
-    hipError_t e = bits == 4 ? launch_split_t<4>(a, wg, act_tiles, groups, s)
-                   : bits == 2 ? launch_split_t<2>(a, wg, act_tiles, groups, s)
-                               : hipErrorInvalidValue;
+hipError_t launch_lut_mfma_split(const LutLaunch &a, int bits, int fold_blocks, hipStream_t s) {
+    if (a.split_tiles <= 0 || a.njobs <= 0) return hipSuccess;
+    const int grid = (a.split_tiles + 7) / 8 * 8 * a.jobs[0].groups;
+    hipError_t e = bits == 4 ? launch_split_t<4>(a, grid, s) : bits == 2 ? launch_split_t<2>(a, grid, s)
+                                                                          : hipErrorInvalidValue;
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(mfma_fold_kernel, dim3(fold_blocks, (rows + 3) / 4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(mfma_fold_kernel, dim3(fold_blocks, (a.jobs[0].rows + 3) / 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
