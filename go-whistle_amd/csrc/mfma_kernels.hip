@@ -43,6 +43,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <type_traits>
+
 namespace cqhip {
 namespace {
 
@@ -84,11 +86,31 @@ __device__ __forceinline__ void planes4(uint32_t e0, uint32_t e1, uint32_t e2, u
     hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, r23), __builtin_bit_cast(uint32_t, r01), 0x06040200u);
 }
 
-// 16-byte one-hot of a nibble n holding `val` (1 or 64) at byte n.
-__device__ __forceinline__ i32x4 one_hot(uint32_t n, unsigned long long val) {
-    const unsigned long long one = val << ((n & 7u) << 3);
-    const bool low = n < 8u;
-    const unsigned long long lo = low ? one : 0ull, hi = low ? 0ull : one;
+// m & byte B of t, in one VALU op (an SDWA byte select).
+template <int B>
+__device__ __forceinline__ uint32_t and_byte(uint32_t m, uint32_t t) {
+    uint32_t r;
+    if constexpr (B == 0)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(r) : "v"(m), "v"(t));
+    else if constexpr (B == 1)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(r) : "v"(m), "v"(t));
+    else if constexpr (B == 2)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(r) : "v"(m), "v"(t));
+    else
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(r) : "v"(m), "v"(t));
+    return r;
+}
+
+// 16-byte one-hot: 1 at byte c (c < 16), as two 64-bit shifts.
+__device__ __forceinline__ i32x4 one_hot1(uint32_t c) {
+    const uint32_t sh = (c & 7u) << 3;
+    const uint32_t up = c >> 3;  // 1: the byte is in the upper eight
+    const unsigned long long lo = static_cast<unsigned long long>(up ^ 1u) << sh;
+    const unsigned long long hi = static_cast<unsigned long long>(up) << sh;
     i32x4 r;
     r.x = static_cast<int>(lo);
     r.y = static_cast<int>(lo >> 32);
@@ -100,13 +122,27 @@ __device__ __forceinline__ i32x4 one_hot(uint32_t n, unsigned long long val) {
 template <int BITS, int TA>
 __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
     using M = MfmaGeo<BITS>;
-    constexpr int G = M::G, AP = M::AP, CK = M::CK;
+    constexpr int G = M::G, AP = M::AP, CK = M::CK, NCH = M::NCH;
     constexpr int AT = TA / 32;  // activation tiles per wavefront
+    constexpr int NI = TA * CK / kMfmaThreads;  // table items per thread and chunk: 2 or 1
+    constexpr int CPP = CK / 2;                 // position pairs per chunk
+    constexpr int PLANE = 2 * TA * 16, PAIR = 2 * PLANE, BUF = CPP * PAIR;
+    constexpr int PW = TA / kMfmaWaves;         // activations a wavefront rotates per group
+    constexpr int APS = TA == 64 ? 2 : 1;       // activations of a rotation slice
+    constexpr int NS = PW / APS;                // slices per group
+    constexpr int NA = NCH - 1;                 // chunks of a group that rotate the next one
+    constexpr int MAXS = NS > NA ? NS - NA + 1 : 1;  // most slices in one chunk
     extern __shared__ __align__(16) unsigned char smem[];
-    float *av = reinterpret_cast<float *>(smem);                    // [TA][AP] scaled rotated groups
-    float *stp = av + TA * AP;                                       // [TA] steps of the group
-    int8_t *tab = reinterpret_cast<int8_t *>(stp + TA);              // [2][CK][2][TA][16] table planes
+    float *av = reinterpret_cast<float *>(smem);          // [2][TA][AP] scaled rotated groups (by group parity)
+    float *stp = av + 2 * TA * AP;                         // [2][TA] their steps
+    int8_t *tab = reinterpret_cast<int8_t *>(stp + 2 * TA);  // [2][CPP][plane][half][TA][16] table planes
+    int8_t *ohot = tab + 2 * BUF;                              // [16][16]: entry c is the one-hot of code c
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
+    if (tid < 16) {
+        const uint32_t one = 1u << (8 * (tid & 3)), d = tid >> 2;
+        *reinterpret_cast<uint4 *>(ohot + tid * 16) =
+            make_uint4(d == 0 ? one : 0u, d == 1 ? one : 0u, d == 2 ? one : 0u, d == 3 ? one : 0u);
+    }
 
     int jb = 0;
 #pragma unroll
@@ -116,248 +152,340 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
     const int blk = (static_cast<int>(blockIdx.x) - a.wg0[jb]) * kMfmaWaves + w;  // this wavefront's block
     const bool rows_here = blk < J.nblk;
     const int gblk = J.blk0 + blk;
+    const size_t bk = static_cast<size_t>(J.blk0 + min(blk, J.nblk - 1));  // clamped: loads need no branch
     const int t0 = blockIdx.y * TA;
-    const int groups = J.groups;
+    const int groups = J.groups, rows = J.rows, in = J.in, units = J.units;
+    const long long xs = J.x_stride;
+    const float *X = J.x, *XG = J.xgate, *NG = J.ngain;
 
     // Fused ZCRMSNorm of the activation rows (norm.go:53-109): divisors of
     // the workgroup's activations, four float64 partial sums each.
     __shared__ double zpart[4 * TA];
     __shared__ float zrms[TA];
-    if (J.ngain) {
+    if (NG) {
         for (int e = tid; e < 4 * TA; e += kMfmaThreads) {
             const int t = t0 + e / 4;
-            zpart[e] = t < J.rows ? zc_partial(J.x + static_cast<long long>(t) * J.x_stride, J.in, e % 4) : 0.0;
+            zpart[e] = t < rows ? zc_partial(X + static_cast<long long>(t) * xs, in, e % 4) : 0.0;
         }
         __syncthreads();
         for (int e = tid; e < TA; e += kMfmaThreads)
-            zrms[e] = zc_rms(zpart[4 * e], zpart[4 * e + 1], zpart[4 * e + 2], zpart[4 * e + 3], J.in);
+            zrms[e] = zc_rms(zpart[4 * e], zpart[4 * e + 1], zpart[4 * e + 2], zpart[4 * e + 3], in);
         __syncthreads();
     }
+
+    // The wavefront's rows' index bytes, one 16-byte unit (2 chunks of 16
+    // positions per 4-bit unit, 4 per 2-bit unit) a load, read one unit
+    // ahead in a sequence that runs on across groups; the rows' norms of a
+    // group, read one group ahead.
+    auto load_unit = [&](int un, uint32_t (&d)[2][4]) {  // unit un of the row's units (group un / UPG)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(J.idx + ((bk * units + un) * 64 + rt * 32 + l32) * 16);
+            d[rt][0] = v.x; d[rt][1] = v.y; d[rt][2] = v.z; d[rt][3] = v.w;
+        }
+    };
+    auto load_norm = [&](int g, unsigned short (&d)[2]) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) d[rt] = J.norm[(bk * groups + g) * 64 + rt * 32 + l32];
+    };
+    // Values of group g of the wavefront's activations k0 .. k0 + n - 1 (of
+    // its PW; two per lane each), with Attention.output's gate
+    // (attention.go:245-249).
+    auto load_x = [&](int g, int k0, auto n_c, float (&d)[decltype(n_c)::value][2]) {
+        constexpr int NA = decltype(n_c)::value;
+#pragma unroll
+        for (int k = 0; k < NA; ++k) {
+            const int t = t0 + w + (k0 + k) * kMfmaWaves;
+            const long long ro = static_cast<long long>(min(t, rows - 1)) * xs;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int col = min(g * G + e * 64 + lane, in - 1);
+                float xv = X[ro + col];
+                if (XG) xv = xv * gate_sigmoid(XG[ro + col]);
+                d[k][e] = (t < rows && g * G + e * 64 + lane < in) ? xv : 0.0f;
+            }
+        }
+    };
+    // Rotation and bound of group g of activations [k0, k0 + n) of the
+    // wavefront's (lut.go:158-178): the norm, the plain FWHT in the
+    // reference's stage order, lutInv; to av / stp of the group's parity.
+    auto rotate = [&](int g, int k0, auto n_c, const float (&xv)[decltype(n_c)::value][2]) {
+        constexpr int NA = decltype(n_c)::value;
+        float v[NA][2];
+#pragma unroll
+        for (int k = 0; k < NA; ++k) {
+            const int tt = w + (k0 + k) * kMfmaWaves, t = t0 + tt;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int col = g * G + e * 64 + lane;
+                v[k][e] = xv[k][e];
+                if (NG && t < rows && col < in) {
+                    const float gx = NG[col] * v[k][e];
+                    v[k][e] = gx / zrms[tt];
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
+#pragma unroll
+            for (int k = 0; k < NA; ++k)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float p = xor_lane(v[k][e], h);
+                    v[k][e] = (lane & h) ? p - v[k][e] : v[k][e] + p;
+                }
+        }
+#pragma unroll
+        for (int k = 0; k < NA; ++k) {  // stage h = 64 within the lane
+            const float p = v[k][0], q = v[k][1];
+            v[k][0] = p + q;
+            v[k][1] = p - q;
+        }
+        float mx[NA];
+#pragma unroll
+        for (int k = 0; k < NA; ++k) {
+            mx[k] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                if constexpr (BITS == 4) {
+                    mx[k] = go_max(mx[k], fabsf(v[k][e]));
+                } else {
+                    const float p = xor_lane<1>(v[k][e]);
+                    const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                    mx[k] = go_max(mx[k], s2);
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int k = 0; k < NA; ++k) mx[k] = go_max(mx[k], xor_lane(mx[k], off));
+        float *avg = av + (g & 1) * TA * AP;
+#pragma unroll
+        for (int k = 0; k < NA; ++k) {
+            const int tt = w + (k0 + k) * kMfmaWaves;
+            const float m = J.cb_max * mx[k];
+            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) avg[tt * AP + e * 64 + lane] = v[k][e] * inv;
+            if (lane == 0) stp[(g & 1) * TA + tt] = m * J.lut_step;
+        }
+    };
+
+    // Table items: this thread's are activation tid % TA at positions
+    // jc0 + k * (kMfmaThreads / TA) of every chunk (NI per thread), both
+    // planes to [buf][jc / 2][plane][jc % 2][activation], built a quarter
+    // (four entries) at a time between the previous chunk's MFMAs.
+    float cbv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cbv[q] = J.cb[q];
+    const int tA = tid % TA, jc0 = tid / TA;
+    float ix[NI][2];
+    uint32_t blo[4], bhi[4];
+    auto item_inputs = [&](int g, int c) {
+        const float *avg = av + (g & 1) * TA * AP;
+#pragma unroll
+        for (int k = 0; k < NI; ++k) {
+            const int j = c * CK + jc0 + k * (kMfmaThreads / TA);
+            if constexpr (BITS == 4) {
+                ix[k][0] = avg[tA * AP + j];
+            } else {
+                ix[k][0] = avg[tA * AP + 2 * j];
+                ix[k][1] = avg[tA * AP + 2 * j + 1];
+            }
+        }
+    };
+    auto item_quarter = [&](int buf, int s) {  // quarter s & 3 of item s >> 2, into table buffer buf
+        const int k = s >> 2, qd = s & 3;
+        uint32_t b[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int code = 4 * qd + q;
+            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
+                b[q] = rne_bits(cbv[code] * ix[k][0]);
+            } else {  // lutTables2Generic (lut.go:239-258): code = hi << 2 | lo
+                const float l = cbv[code & 3] * ix[k][0], h = cbv[code >> 2] * ix[k][1];
+                const float sm = l + h;
+                b[q] = rne_bits(sm);
+            }
+        }
+        planes4(b[0], b[1], b[2], b[3], blo[qd], bhi[qd]);
+        if (qd == 3) {
+            const int jc = jc0 + k * (kMfmaThreads / TA);
+            int8_t *dst = tab + (buf * CPP + (jc >> 1)) * PAIR + ((jc & 1) * TA + tA) * 16;
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(blo[0], blo[1], blo[2], blo[3]);
+            *reinterpret_cast<uint4 *>(dst + PLANE) = make_uint4(bhi[0], bhi[1], bhi[2], bhi[3]);
+        }
+    };
+
+    // Prologue: group 0 rotated, its first chunk's tables built; group 1's
+    // values, the first index unit and the norms on their way.
+    uint32_t cur[2][4], nxt[2][4];
+    unsigned short nrm16[2], nrm16n[2];
+    load_unit(0, nxt);
+    load_norm(0, nrm16);
+    {
+        float x0[PW][2];
+        load_x(0, 0, std::integral_constant<int, PW>{}, x0);
+        rotate(0, 0, std::integral_constant<int, PW>{}, x0);
+    }
+    if (groups > 1) load_norm(1, nrm16n);
+    lds_barrier();
+    item_inputs(0, 0);
+#pragma unroll
+    for (int s4 = 0; s4 < 4 * NI; ++s4) item_quarter(0, s4);
+    lds_barrier();
 
     i32x16 acc[AT][2];     // [activation tile][row tile]
     float yv[AT][2][16];   // [activation tile][row tile][element]
 #pragma unroll
     for (int at = 0; at < AT; ++at)
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < 2; ++rt) {
+            acc[at][rt] = i32x16{};
 #pragma unroll
             for (int i = 0; i < 16; ++i) yv[at][rt][i] = 0.0f;
-
-    auto build = [&](int c, int buf) {
-        for (int e = tid; e < TA * CK; e += kMfmaThreads) {
-            const int t = e % TA, jc = e / TA;
-            const int j = c * CK + jc;
-            uint32_t b[16];
-            if constexpr (BITS == 4) {  // lutTables4Generic (lut.go:263-282)
-                const float x = av[t * AP + j];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const float f = J.cb[q] * x;
-                    b[q] = rne_bits(f);
-                }
-            } else {  // lutTables2Generic (lut.go:239-258): code q = hi << 2 | lo
-                const float x0 = av[t * AP + 2 * j], x1 = av[t * AP + 2 * j + 1];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const float l = J.cb[q & 3] * x0, h = J.cb[q >> 2] * x1;
-                    const float s = l + h;
-                    b[q] = rne_bits(s);
-                }
-            }
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) planes4(b[4 * q], b[4 * q + 1], b[4 * q + 2], b[4 * q + 3], lo[q], hi[q]);
-            int8_t *dst = tab + ((static_cast<size_t>(buf) * CK + jc) * 2 * TA + t) * 16;
-            *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4 *>(dst + TA * 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         }
-    };
 
-    // The wavefront's rows' index bytes of group g, unit u (lut layout:
-    // 16-byte units of a 64-row block side by side); word q of a unit holds
-    // the index bytes of chunk 4u + q.
-    auto load_unit = [&](int g, int u, uint32_t (&d)[2][4]) {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            if (rows_here) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(
-                    J.idx + ((static_cast<size_t>(gblk) * J.units + g * M::UPG + u) * 64 + rt * 32 + l32) * 16);
-                d[rt][0] = v.x; d[rt][1] = v.y; d[rt][2] = v.z; d[rt][3] = v.w;
-            } else {
-                d[rt][0] = d[rt][1] = d[rt][2] = d[rt][3] = 0u;
-            }
-        }
-    };
-
-    // A wavefront's activations' values of group g (TA / 8 of them, two per
-    // lane each): group 0 loaded here, group g + 1 while group g streams.
-    constexpr int PW = TA / kMfmaWaves;  // activations per wavefront
-    float xg[PW][2];
-    auto load_x = [&](int g) {
-#pragma unroll
-        for (int k = 0; k < PW; ++k) {
-            const int t = t0 + w + k * kMfmaWaves;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int col = g * G + e * 64 + lane;
-                float xv = (t < J.rows && col < J.in) ? J.x[static_cast<long long>(t) * J.x_stride + col] : 0.0f;
-                if (J.xgate && t < J.rows && col < J.in)  // Attention.output's gate (attention.go:245-249)
-                    xv = xv * gate_sigmoid(J.xgate[static_cast<long long>(t) * J.x_stride + col]);
-                xg[k][e] = xv;
-            }
-        }
-    };
-    load_x(0);
-    for (int g = 0; g < groups; ++g) {
-        uint32_t cur[2][4], nxt[2][4];
-        load_unit(g, 0, nxt);
-        float nrm[2];
+    // Chunks of CK positions, one sequence over all groups. Chunk q's
+    // MFMAs, with chunk q + 1's items built between them and, in the first
+    // NR chunks of group g, group g + 1 rotated APS activations a chunk. One
+    // K step is a position pair (lane half h: position 2p + h); per pair and
+    // row tile one one-hot B (1 at the code's byte) for the l plane and
+    // B << 6 (64) for the h plane, into one accumulator. After a group's
+    // last chunk its sums are folded into y, groups in order (lut.go:
+    // 297-310).
+    constexpr int CW = M::CW;      // index words per row and chunk
+    constexpr int CPU = 4 / CW;    // chunks per unit
+    const uint32_t hs = 4u * static_cast<uint32_t>(half);  // a lane half takes the odd nibbles
+    const int nq = groups * NCH;
+    for (int qq = 0; qq < nq; qq += CPU) {
+        const int g = qq / NCH;
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
-            nrm[rt] = rows_here ? __half2float(__ushort_as_half(
-                                      J.norm[(static_cast<size_t>(gblk) * groups + g) * 64 + rt * 32 + l32]))
-                                : 0.0f;
-
-        // 1. Rotation and bound of the group of each activation (lut.go:158-178):
-        // a wavefront's TA / 8 activations together, their butterflies
-        // interleaved.
-        {
-            float v[PW][2];
 #pragma unroll
-            for (int k = 0; k < PW; ++k)
+            for (int e = 0; e < 4; ++e) cur[rt][e] = nxt[rt][e];
+        if (qq + CPU < nq) load_unit(qq / CPU + 1, nxt);  // units run on across groups: unit u is chunks CPU*u..
 #pragma unroll
-                for (int e = 0; e < 2; ++e) v[k][e] = xg[k][e];
-            if (J.ngain) {
+        for (int q = 0; q < CPU; ++q) {
+            const int c = qq % NCH + q;  // chunk within group g
+            // The slices of group g + 1 this chunk rotates after its MFMAs:
+            // slice c, and in chunk NA - 1 also the slices past NA - 1. Their
+            // values are read now, under the MFMAs.
+            const bool rot = g + 1 < groups && c < (NS < NA ? NS : NA);
+            float xr[MAXS][APS][2];
+            if (rot) {
 #pragma unroll
-                for (int k = 0; k < PW; ++k) {
-                    const int tt = w + k * kMfmaWaves, t = t0 + tt;
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        const int col = g * G + e * 64 + lane;
-                        if (t < J.rows && col < J.in) {
-                            const float gx = J.ngain[col] * v[k][e];
-                            v[k][e] = gx / zrms[tt];
-                        }
-                    }
+                for (int m = 0; m < MAXS; ++m) {
+                    const int sl = m == 0 ? c : NA - 1 + m;
+                    if (m == 0 || (c == NA - 1 && sl < NS))
+                        load_x(g + 1, sl * APS, std::integral_constant<int, APS>{}, xr[m]);
                 }
             }
-#pragma unroll
-            for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
-#pragma unroll
-                for (int k = 0; k < PW; ++k)
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        const float p = xor_lane(v[k][e], h);
-                        v[k][e] = (lane & h) ? p - v[k][e] : v[k][e] + p;
-                    }
-            }
-#pragma unroll
-            for (int k = 0; k < PW; ++k) {  // stage h = 64 within the lane
-                const float p = v[k][0], q = v[k][1];
-                v[k][0] = p + q;
-                v[k][1] = p - q;
-            }
-            float mx[PW];
-#pragma unroll
-            for (int k = 0; k < PW; ++k) {
-                mx[k] = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    if constexpr (BITS == 4) {
-                        mx[k] = go_max(mx[k], fabsf(v[k][e]));
-                    } else {
-                        const float p = xor_lane<1>(v[k][e]);
-                        const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
-                        mx[k] = go_max(mx[k], s2);
-                    }
-                }
-            }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-                for (int k = 0; k < PW; ++k) mx[k] = go_max(mx[k], xor_lane(mx[k], off));
-#pragma unroll
-            for (int k = 0; k < PW; ++k) {
-                const int tt = w + k * kMfmaWaves;
-                const float m = J.cb_max * mx[k];
-                const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
-#pragma unroll
-                for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[k][e] * inv;
-                if (lane == 0) stp[tt] = m * J.lut_step;
-            }
-        }
-        lds_barrier();
-        build(0, 0);
-#pragma unroll
-        for (int at = 0; at < AT; ++at)
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) acc[at][rt] = i32x16{};
-        lds_barrier();
-
-        if (g + 1 < groups) load_x(g + 1);
-
-        // 2./3. Chunks of CK positions (CW index words per row): the next
-        // chunk's tables are built while this chunk's MFMAs run.
-        const unsigned long long val = half ? 64ull : 1ull;
-        constexpr int CW = M::CW;
-        for (int u = 0; u < M::UPG; ++u) {
+            item_inputs((qq + q + 1) / NCH, (qq + q + 1) % NCH);
+            // this half's nibble of pair k in the high nibble of byte k: an
+            // entry's offset in the one-hot table is one SDWA and
+            uint32_t wv[2][CW];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) cur[rt][q] = nxt[rt][q];
-            if (u + 1 < M::UPG) load_unit(g, u + 1, nxt);
+                for (int e = 0; e < CW; ++e) wv[rt][e] = (cur[rt][q * CW + e] >> hs) << 4;
+            auto onehot_of = [&](int rt, int pp) -> i32x4 {
+                const uint32_t w4 = wv[rt][pp >> 2];
+                uint32_t off;
+                switch (pp & 3) {
+                    case 0: off = and_byte<0>(0xf0u, w4); break;
+                    case 1: off = and_byte<1>(0xf0u, w4); break;
+                    case 2: off = and_byte<2>(0xf0u, w4); break;
+                    default: off = and_byte<3>(0xf0u, w4); break;
+                }
+                return *reinterpret_cast<const i32x4 *>(ohot + off);
+            };
+            const int buf = (qq + q) & 1;
+            const int8_t *tb = tab + buf * BUF + (half * TA + l32) * 16;
+            i32x4 Al[2][AT], Ah[2][AT], Bl[2][2];
 #pragma unroll
-            for (int q = 0; q < 4 / CW; ++q) {
-                const int c = (4 / CW) * u + q;
-                if (c + 1 < M::NCH) build(c + 1, (c + 1) & 1);
+            for (int at = 0; at < AT; ++at) {
+                Al[0][at] = *reinterpret_cast<const i32x4 *>(tb + at * 512);
+                Ah[0][at] = *reinterpret_cast<const i32x4 *>(tb + PLANE + at * 512);
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) Bl[0][rt] = onehot_of(rt, 0);
+#pragma unroll
+            for (int pp = 0; pp < CPP; ++pp) {
+                const int sl = pp & 1;
+                if (pp + 1 < CPP) {
+                    const int8_t *nb = tb + (pp + 1) * PAIR;
+#pragma unroll
+                    for (int at = 0; at < AT; ++at) {
+                        Al[sl ^ 1][at] = *reinterpret_cast<const i32x4 *>(nb + at * 512);
+                        Ah[sl ^ 1][at] = *reinterpret_cast<const i32x4 *>(nb + PLANE + at * 512);
+                    }
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) Bl[sl ^ 1][rt] = onehot_of(rt, pp + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // the next pair's reads go out here
+                // (past the last chunk the items land in the spare buffer and
+                // go unread; a wavefront past the view's rows multiplies its
+                // clamped rows and stores nothing)
+                if (pp < 4 * NI) item_quarter(buf ^ 1, pp);
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const i32x4 bh = Bl[sl][rt] << 6;  // 64 at the code's byte: the h plane's weight
+#pragma unroll
+                    for (int at = 0; at < AT; ++at) {
+                        acc[at][rt] =
+                            __builtin_amdgcn_mfma_i32_32x32x32_i8(Al[sl][at], Bl[sl][rt], acc[at][rt], 0, 0, 0);
+                        acc[at][rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah[sl][at], bh, acc[at][rt], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < 4 * AT; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+
+            if (rot) {
+#pragma unroll
+                for (int m = 0; m < MAXS; ++m) {
+                    const int sl = m == 0 ? c : NA - 1 + m;
+                    if (m == 0 || (c == NA - 1 && sl < NS))
+                        rotate(g + 1, sl * APS, std::integral_constant<int, APS>{}, xr[m]);
+                }
+            }
+            lds_barrier();
+            if (c == NCH - 1) {
+                // fold group g into y (lut.go:297-310); the next group's norms become current
                 if (rows_here) {
-                    // lane half 0 reads a position's l plane, half 1 its h plane
-                    const int8_t *tb = tab + (static_cast<size_t>(c & 1) * CK * 2 + half) * TA * 16;
-                    i32x4 A[2][AT];  // [position parity][activation tile]
+                    const float *sg = stp + (g & 1) * TA;
+                    float nrm[2];
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) nrm[rt] = __half2float(__ushort_as_half(nrm16[rt]));
 #pragma unroll
                     for (int at = 0; at < AT; ++at)
-                        A[0][at] = *reinterpret_cast<const i32x4 *>(tb + (at * 32 + l32) * 16);
 #pragma unroll
-                    for (int jc = 0; jc < CK; ++jc) {
-                        if (jc + 1 < CK) {
+                        for (int i = 0; i < 16; ++i) {
+                            const float step = sg[at * 32 + (i >> 2) * 8 + half * 4 + (i & 3)];
 #pragma unroll
-                            for (int at = 0; at < AT; ++at)
-                                A[(jc + 1) & 1][at] = *reinterpret_cast<const i32x4 *>(
-                                    tb + (static_cast<size_t>(jc + 1) * 2 * TA + at * 32 + l32) * 16);
+                            for (int rt = 0; rt < 2; ++rt) {
+                                const int sum = acc[at][rt][i];
+                                const float coef = nrm[rt] * step;
+                                const float prod = static_cast<float>(sum) * coef;
+                                yv[at][rt][i] = yv[at][rt][i] + prod;
+                            }
                         }
-#pragma unroll
-                        for (int rt = 0; rt < 2; ++rt) {
-                            // position jc: word jc / 8 of the chunk, byte (jc % 8) / 2, nibble jc % 2
-                            const uint32_t n = (cur[rt][q * CW + jc / 8] >> (4 * (jc % 8))) & 15u;
-                            const i32x4 B = one_hot(n, val);
-#pragma unroll
-                            for (int at = 0; at < AT; ++at)
-                                acc[at][rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[jc & 1][at], B, acc[at][rt], 0, 0, 0);
-                        }
-                    }
                 }
-                lds_barrier();
+#pragma unroll
+                for (int at = 0; at < AT; ++at)
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) acc[at][rt] = i32x16{};
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) nrm16[rt] = nrm16n[rt];
+                if (g + 2 < groups) load_norm(g + 2, nrm16n);
             }
         }
-
-        // 4. Fold group g into y, in group order (lut.go:297-310).
-        if (rows_here) {
-#pragma unroll
-            for (int at = 0; at < AT; ++at)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int tt = at * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-                    const float step = stp[tt];
-#pragma unroll
-                    for (int rt = 0; rt < 2; ++rt) {
-                        const int s = acc[at][rt][i];
-                        const float coef = nrm[rt] * step;
-                        const float prod = static_cast<float>(s) * coef;
-                        yv[at][rt][i] = yv[at][rt][i] + prod;
-                    }
-                }
-        }
-        lds_barrier();  // av and stp are rewritten by the next group
     }
 
     if (rows_here) {
@@ -366,7 +494,7 @@ __global__ __launch_bounds__(kMfmaThreads) void lut_mfma_kernel(LutLaunch a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int t = t0 + at * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-                if (t >= J.rows) continue;
+                if (t >= rows) continue;
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
                     const int r = gblk * 64 + rt * 32 + l32;
@@ -389,10 +517,18 @@ size_t mfma_lds_bytes() {
     return sizeof(float) * (TA * M::AP + TA) + static_cast<size_t>(2) * M::CK * 2 * TA * 16;
 }
 
+// The MFMA form holds two groups' rotated values and steps (the next one is
+// rotated while the current one streams).
+template <int BITS, int TA>
+size_t mfma_lds_bytes2() {
+    using M = MfmaGeo<BITS>;
+    return sizeof(float) * 2 * (TA * M::AP + TA) + static_cast<size_t>(2) * M::CK * 2 * TA * 16 + 16 * 16;
+}
+
 template <int BITS, int TA>
 hipError_t launch_mfma_t(const LutLaunch &a, int wg, int act_tiles, hipStream_t s) {
     static bool attr = false;  // idempotent attribute write; a race is benign
-    const size_t lds = mfma_lds_bytes<BITS, TA>();
+    const size_t lds = mfma_lds_bytes2<BITS, TA>();
     if (!attr) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_mfma_kernel<BITS, TA>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -430,19 +566,6 @@ constexpr int kSplitWaves = 4;
 constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kSplitTa = 32;  // activations per workgroup: one 32-wide MFMA tile
 
-// 16-byte one-hot: 1 at byte c (c < 16), as two 64-bit shifts.
-__device__ __forceinline__ i32x4 one_hot1(uint32_t c) {
-    const uint32_t sh = (c & 7u) << 3;
-    const uint32_t up = c >> 3;  // 1: the byte is in the upper eight
-    const unsigned long long lo = static_cast<unsigned long long>(up ^ 1u) << sh;
-    const unsigned long long hi = static_cast<unsigned long long>(up) << sh;
-    i32x4 r;
-    r.x = static_cast<int>(lo);
-    r.y = static_cast<int>(lo >> 32);
-    r.z = static_cast<int>(hi);
-    r.w = static_cast<int>(hi >> 32);
-    return r;
-}
 
 // The lut kernel's epilogue for one activation t and one 64-row block (lane
 // = row): the int8 append of the block as a head (Int8Rows.Append,
@@ -514,7 +637,6 @@ __global__ __launch_bounds__(kSplitThreads) void lut_mfma_split_kernel(LutLaunch
     const JobDesc &J = a.jobs[jb];
     const int blk = (rg - a.wg0[jb]) * kSplitWaves + w;  // this wavefront's block
     const bool rows_here = blk < J.nblk;
-    const int gblk = J.blk0 + blk;
     const int rows = J.rows, in = J.in, units = J.units;
     const long long xs = J.x_stride;
     const float *X = J.x, *XG = J.xgate, *NG = J.ngain;
