@@ -448,8 +448,11 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    # The GPU's clocks settle over the first ~10 ms of sustained load (the
+    # sweep's launches run ~15% slower before that), so the default warm-up
+    # is ~50 ms of steps.
+    ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--copies", type=int, default=0, help="device copies of the sweep (0: > 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
