@@ -524,6 +524,10 @@ def main():
     if args.roofline_only:
         src = torch.empty(128 * 2 ** 20, dtype=torch.float32, device=dev).uniform_()
         dst = torch.empty_like(src)
+        # ~50 ms of copies first, so that the clocks have settled before the
+        # first lut launch (a profiler's average then covers steady launches)
+        for _ in range(250):
+            dst.copy_(src)
         for _ in range(args.steps):
             plans[4].run()
             plans[2].run()
