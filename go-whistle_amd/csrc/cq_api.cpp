@@ -490,7 +490,7 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
             a.wg0[a.njobs] = wg;
             a.fold0[a.njobs] = fold;
             wg += (j.nblk + rpw - 1) / rpw;
-            fold += j.nblk;
+            fold += (j.nblk + 3) / 4;  // the fold's workgroups cover 256 rows
             terms += static_cast<size_t>(j.groups) * nr * j.nblk * kBlockRows;
             ++a.njobs;
         }

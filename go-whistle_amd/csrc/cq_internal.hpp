@@ -123,7 +123,7 @@ struct LutLaunch {
     // jobs, wg0, times split_at activation tiles) and one counter per tile,
     // zero between launches.
     float *term[kKernargJobs];
-    int fold0[kKernargJobs];  // the job's first block in the fold's grid
+    int fold0[kKernargJobs];  // the job's first 256-row group in the fold's grid
     int split_tiles, split_at;
 };
 
@@ -144,7 +144,7 @@ hipError_t launch_lut_mfma(const LutLaunch &a, int bits, int ta, int wg, int act
 // 512-row workgroups would leave most CUs idle: a workgroup per (tile,
 // group), a tile being 256 rows (wg0 counts the jobs' row groups) by 32
 // activations; each writes its group's float terms to a.term. Then the
-// fold, grid x over the jobs' 64-row blocks (fold0), y over the activations
+// fold, grid x over the jobs' 256-row groups (fold0), y over the activations
 // in fours, adds them in group order and applies the epilogue. On stream s.
 int mfma_split_rows_per_workgroup();
 int mfma_split_activations();

@@ -924,9 +924,13 @@ __global__ __launch_bounds__(kSplitThreads) void lut_mfma_split_kernel(LutLaunch
     }
 }
 
-// The fold of the split form: one wavefront per (activation, 64-row block),
-// lane = row: y = 0, then y = y + term[g] for g in order (lut.go:297-310),
-// then the lut kernel's epilogue.
+// The fold of the split form: a wavefront per (activation, 256 rows), four
+// rows per lane (16 lanes a 64-row block), the terms read as 16-byte
+// vectors: y = 0, then y = y + term[g] for g in order (lut.go:297-310),
+// then the lut kernel's epilogue: the int8 append of each block as a head
+// (Int8Rows.Append, int8.go:36-55, after RoPE at the stream's position,
+// rope.go:69-81; row i < 32 pairs with i + 32, lane q with lane q + 8), and
+// y, with the residual add or SiLU, for the view's rows.
 __global__ __launch_bounds__(256) void mfma_fold_kernel(LutLaunch a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int jb = 0;
@@ -934,14 +938,62 @@ __global__ __launch_bounds__(256) void mfma_fold_kernel(LutLaunch a) {
     for (int k = 1; k < kKernargJobs; ++k)
         if (k < a.njobs && static_cast<int>(blockIdx.x) >= a.fold0[k]) jb = k;
     const JobDesc &J = a.jobs[jb];
-    const int blk = static_cast<int>(blockIdx.x) - a.fold0[jb];
+    const int q = lane & 15;
+    const int blk = (static_cast<int>(blockIdx.x) - a.fold0[jb]) * 4 + (lane >> 4);
     const int t = blockIdx.y * 4 + w;
-    if (blk >= J.nblk || t >= J.rows) return;
-    const long long rs = static_cast<long long>(J.nblk) * 64;
-    const float *tp = a.term[jb] + static_cast<long long>(t) * rs + blk * 64 + lane;
-    float y = 0.0f;
-    for (int g = 0; g < J.groups; ++g) y = y + tp[static_cast<long long>(g) * J.rows * rs];
-    fold_epilogue(J, t, blk, lane, y);
+    if (blk >= J.nblk || t >= J.rows) return;  // whole 16-lane blocks leave together
+    const long long rs = static_cast<long long>(J.nblk) * 64, gs = static_cast<long long>(J.rows) * rs;
+    const float *tp = a.term[jb] + static_cast<long long>(t) * rs + blk * 64 + 4 * q;
+    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g = 0; g < J.groups; ++g) {
+        const float4 v = *reinterpret_cast<const float4 *>(tp + g * gs);
+        y[0] = y[0] + v.x;
+        y[1] = y[1] + v.y;
+        y[2] = y[2] + v.z;
+        y[3] = y[3] + v.w;
+    }
+
+    const int row = (J.blk0 + blk) * 64;  // root row of the block's first value
+    if (J.app_q) {
+        const int p = J.app_pos[t];
+        if (p >= 0 && p < J.app_cap) {
+            float v[4] = {y[0], y[1], y[2], y[3]};
+            if (J.app_cos) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float o = xor_lane<8>(v[e]);
+                    const int jj = (4 * q + e) & 31;
+                    const float x1 = q < 8 ? v[e] : o, x2 = q < 8 ? o : v[e];
+                    float o1, o2;
+                    rope_pair(x1, x2, J.app_cos[p * 32 + jj], J.app_sin[p * 32 + jj], o1, o2);
+                    v[e] = q < 8 ? o1 : o2;
+                }
+            }
+            float m = go_max(go_max(fabsf(v[0]), fabsf(v[1])), go_max(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+            for (int h = 8; h > 0; h >>= 1) m = go_max(m, xor_lane(m, h));
+            const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+            const int r0 = row - J.row0;  // view row of the head's first value
+            int8_t *qp = J.app_q + static_cast<long long>(t) * J.app_q_stride + static_cast<long long>(p) * J.out + r0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qp[4 * q + e] = static_cast<int8_t>(go_int8_code(rintf(v[e] / sc)));
+            if (q == 0)
+                J.app_s[static_cast<long long>(t) * J.app_s_stride + static_cast<long long>(p) * (J.out >> 6) +
+                        (r0 >> 6)] = sc;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int r = row + 4 * q + e;
+        if (r >= J.row0 && r < J.row0 + J.out) {
+            float out = y[e];
+            if (J.resid)
+                out = J.resid[static_cast<long long>(t) * J.resid_stride + (r - J.row0)] + out;
+            else if (J.act == 1)
+                out = silu_value(out);
+            J.y[static_cast<long long>(t) * J.y_stride + (r - J.row0)] = out;
+        }
+    }
 }
 
 template <int BITS>
