@@ -467,7 +467,8 @@ def main():
     ap.add_argument("--no-ref-shapes", action="store_true", help="skip the reference's benchmark shapes")
     ap.add_argument("--attention-only", action="store_true", help="run only the attention leg (prints its JSON)")
     ap.add_argument("--roofline-only", action="store_true",
-                    help="run only the step's 4-bit launch and a 512 MiB device copy (for rocprofv3 counters)")
+                    help="run only the roofline leg's launches (4 of 4 bits, 1 of 2 bits, per step) after 50 ms of "
+                         "512 MiB device copies, then 4 more copies (for rocprofv3 traces and counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported"}))
@@ -528,12 +529,14 @@ def main():
         # first lut launch (a profiler's average then covers steady launches)
         for _ in range(250):
             dst.copy_(src)
-        for _ in range(args.steps):
-            plans[4].run()
+        for _ in range(args.steps):  # the launches the roofline leg times: 4 of 4 bits, then one of 2
+            for _ in range(ROOF_REPS):
+                plans[4].run()
             plans[2].run()
+        for _ in range(4):
             dst.copy_(src)  # calibration: 512 MiB read, 512 MiB written
         torch.cuda.synchronize()
-        print(json.dumps({"roofline_only": True, "launches": args.steps, "copy_bytes": src.numel() * 4,
+        print(json.dumps({"roofline_only": True, "launches_4bit": args.steps * ROOF_REPS, "copy_bytes": src.numel() * 4,
                           "algorithmic_bytes_4bit_launch": sum(algorithmic_bytes(packs[k].Out, packs[k].In, 4)
                                                                for c, k in by_bits[4])}))
         return
