@@ -330,6 +330,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
             b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
             b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
             if (b.jobs[k].resid) b.jobs[k].resid += static_cast<long long>(r0) * b.jobs[k].resid_stride;
+            if (b.jobs[k].xgate) b.jobs[k].xgate += static_cast<long long>(r0) * b.jobs[k].x_stride;
             if (b.jobs[k].app_q) {
                 b.jobs[k].app_q += static_cast<long long>(r0) * b.jobs[k].app_q_stride;
                 b.jobs[k].app_s += static_cast<long long>(r0) * b.jobs[k].app_s_stride;
@@ -395,6 +396,7 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
             b.jobs[k].x += static_cast<long long>(r0) * b.jobs[k].x_stride;
             b.jobs[k].y += static_cast<long long>(r0) * b.jobs[k].y_stride;
             if (b.jobs[k].resid) b.jobs[k].resid += static_cast<long long>(r0) * b.jobs[k].resid_stride;
+            if (b.jobs[k].xgate) b.jobs[k].xgate += static_cast<long long>(r0) * b.jobs[k].x_stride;
             b.jobs[k].rows = nr;
         }
         HIP_TRY(launch_lut_mfma(b, s0.width, ta, wg, (nr + ta - 1) / ta, stream), "lut mfma launch");
@@ -510,11 +512,87 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
     return CQ_OK;
 }
 
+// ---- the table form ----
+//
+// Between the lut kernel's few activations and the split form's several
+// hundred: a pre-pass builds each activation's tables once and the MFMAs of
+// every 64-row block stream them. A workgroup reads its 32 activations'
+// tables whole (16 KiB per activation and 512 inputs), so the form pays
+// where there are enough row blocks to spread that over the CUs. Measured
+// on MI355X at 256 activations (pre-pass + product against the lut kernel):
+// the four 512x512 CQ4 q/k/v/gate products with the norm 18.6 against 28.2
+// us, 2048x512 CQ2 with the norm and SiLU 16.2 against 18.8 us, the
+// 16384x512 head 64.4 us against the 512-row MFMA form's 69.5 us; it loses
+// at 1024 rows or fewer (a 512x512 CQ4 product 14.9 against 9.6 us,
+// 2x512x512 with the norm 17.9 against 17.0 us) and at 16 groups. The views
+// must share their tables (one pre-pass serves them all). The tables live
+// in the split form's workspace.
+constexpr int kTabMinRows = 64;
+constexpr int kTabMinBlocks = 32;  // 64-row blocks over the views: 2048 rows
+constexpr int kTabMaxGroups = 8;
+
+bool tab_pays(cq_matrix *const *ms, int n, int rows) {
+    if (rows < kTabMinRows || rows >= kSplitMinRows || n > kKernargJobs) return false;
+    const CqStore &s0 = *ms[0]->st;
+    if (!mfma_geometry_supported(s0.width, s0.group) || s0.groups > std::min(kTabMaxGroups, tab_max_groups()))
+        return false;
+    long long blocks = 0;
+    for (int k = 0; k < n; ++k) {
+        if (!uses_lut(ms[k]) || !shares_tables(s0, *ms[k]->st)) return false;
+        blocks += (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
+    }
+    return blocks >= kTabMinBlocks;
+}
+
+int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
+            const Fuse *fz = nullptr) {
+    const CqStore &s0 = *ms[0]->st;
+    LutLaunch a;
+    std::memset(&a, 0, sizeof a);
+    int blocks = 0;
+    for (int k = 0; k < n; ++k) {
+        if (ms[k]->out == 0) continue;
+        JobDesc &j = a.jobs[a.njobs];
+        fill_job(j, ms[k], x, dsts[k], rows);
+        apply_fuse(j, fz, k);
+        a.wg0[a.njobs] = blocks;
+        blocks += j.nblk;
+        ++a.njobs;
+    }
+    if (a.njobs == 0 || rows == 0) return CQ_OK;
+    const int tiles = (rows + 31) / 32;
+    TabArgs t;
+    std::memset(&t, 0, sizeof t);
+    t.x = x;
+    t.x_stride = s0.in;
+    t.xgate = a.jobs[0].xgate;
+    t.ngain = a.jobs[0].ngain;
+    t.rows = rows;
+    t.in = s0.in;
+    t.groups = s0.groups;
+    t.tiles = tiles;
+    for (int c = 0; c < 16; ++c) t.cb[c] = a.jobs[0].cb[c];
+    t.cb_max = s0.cb_max;
+    t.lut_step = s0.lut_step;
+    const size_t tb = tab_table_bytes(s0.width, s0.groups, tiles), sb = tab_step_bytes(s0.groups, tiles);
+    float *ws = nullptr;
+    if (int e = split_workspace(tb + sb, &ws)) return e;
+    t.tab = reinterpret_cast<int8_t *>(ws);
+    t.stp = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + tb);
+    a.tab = t.tab;
+    a.tstp = t.stp;
+    a.tab_at = tiles;
+    HIP_TRY(launch_lut_tab(t, a, s0.width, blocks, stream), "lut table-form launch");
+    for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
+    return CQ_OK;
+}
+
 // Launches the product of up to kMaxMatrices views sharing their tables.
 int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
                 const Fuse *fz = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     const int mode = uses_lut(ms[0]) ? kModeLut : kModeExact;
+    if (mode == kModeLut && tab_pays(ms, n, rows)) return run_tab(ms, n, dsts, x, rows, stream, fz);
     if (mode == kModeLut && n <= kKernargJobs && mfma_geometry_supported(s0.width, s0.group) &&
         mfma_pays(ms, n, rows))
         return run_mfma(ms, n, dsts, x, rows, stream, fz);
@@ -750,6 +828,7 @@ int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, v
 const char *cq_gemm_path(const cq_matrix *m, int rows) {
     if (!m || !uses_lut(m)) return "nibble4";
     cq_matrix *mm = const_cast<cq_matrix *>(m);
+    if (tab_pays(&mm, 1, rows)) return "lut-mfma-tab";
     if (mfma_geometry_supported(m->st->width, m->st->group) && mfma_pays(&mm, 1, rows)) return "lut-mfma";
     if (split_pays(&mm, 1, rows)) return "lut-mfma-split";
     return "lut";
@@ -866,7 +945,9 @@ int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const f
         f.app_pos = pos;
         f.app_cap = cap;
     }
-    // the split MFMA form appends in its fold (whole 64-row blocks, checked above)
+    // the table and split MFMA forms append in their folds (whole 64-row
+    // blocks, checked above)
+    if (tab_pays(ms, n, rows)) return run_tab(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
     if (split_pays(ms, n, rows)) return run_split(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
     return run_lut(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
 }

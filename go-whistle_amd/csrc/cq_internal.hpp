@@ -125,7 +125,38 @@ struct LutLaunch {
     float *term[kKernargJobs];
     int fold0[kKernargJobs];  // the job's first 256-row group in the fold's grid
     int split_tiles, split_at;
+    // The table form: the activations' table planes and steps as
+    // lut_tables_kernel wrote them, for tab_at tiles of 32 activations.
+    const int8_t *tab;
+    const float *tstp;
+    int tab_at;
 };
+
+// The table pre-pass of the table form (mfma_kernels.hip): per activation
+// and group, the prologue (gate, ZCRMSNorm), the rotation, the bound and the
+// int8 planes of the 16-entry tables, written for tiles of 32 activations
+// [tile][group][position pair][plane][half][32][16 codes] (a wavefront's
+// MFMA A operand of one plane and pair is 1 KiB contiguous), and the
+// groups' steps [tile][group][32]. Activations past rows get zero tables.
+struct TabArgs {
+    const float *x;
+    long long x_stride;
+    const float *xgate;  // product of x * sigmoid(xgate) (null: none)
+    const float *ngain;  // ZCRMSNorm gain (null: none)
+    int rows, in, groups, tiles;
+    float cb[16];
+    float cb_max, lut_step;
+    int8_t *tab;
+    float *stp;
+};
+// Bytes of the tables and of the steps for `tiles` tiles of 32 activations.
+size_t tab_table_bytes(int bits, int groups, int tiles);
+size_t tab_step_bytes(int groups, int tiles);
+// Groups the product kernel's LDS holds terms for.
+int tab_max_groups();
+// The pre-pass, then the product: grid over the jobs' 64-row blocks (wg0)
+// times a.tab_at activation tiles. On stream s.
+hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s);
 
 size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw);
 // grid_y = activations on the kernel-argument path, 1 on the device path.

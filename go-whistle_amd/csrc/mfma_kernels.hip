@@ -567,44 +567,84 @@ constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kSplitTa = 32;  // activations per workgroup: one 32-wide MFMA tile
 
 
-// The lut kernel's epilogue for one activation t and one 64-row block (lane
-// = row): the int8 append of the block as a head (Int8Rows.Append,
-// int8.go:36-55, after RoPE at the stream's position, rope.go:69-81), and
-// y, with the residual add or SiLU, for the view's rows.
-__device__ __forceinline__ void fold_epilogue(const JobDesc &J, int t, int blk, int lane, float y) {
+// A job's epilogue fields, read from the kernel arguments once (each use of
+// a JobDesc field indexed by a run-time job is a scalar load and a wait).
+struct Epilogue {
+    int8_t *app_q;
+    float *app_s;
+    long long app_q_stride, app_s_stride;
+    const int32_t *app_pos;
+    const float *app_cos, *app_sin;
+    int app_cap;
+    const float *resid;
+    long long resid_stride;
+    float *y;
+    long long y_stride;
+    int act, row0, out, blk0;
+    __device__ explicit Epilogue(const JobDesc &J)
+        : app_q(J.app_q), app_s(J.app_s), app_q_stride(J.app_q_stride), app_s_stride(J.app_s_stride),
+          app_pos(J.app_pos), app_cos(J.app_cos), app_sin(J.app_sin), app_cap(J.app_cap), resid(J.resid),
+          resid_stride(J.resid_stride), y(J.y), y_stride(J.y_stride), act(J.act), row0(J.row0), out(J.out),
+          blk0(J.blk0) {}
+};
+
+// The lut kernel's epilogue for activations t0 .. t0 + nt - 1 of one 64-row
+// block (lane = row), FA of them computed together so that their lane
+// reductions and divides overlap: the int8 append of the block as a head
+// (Int8Rows.Append, int8.go:36-55, after RoPE at the stream's position,
+// rope.go:69-81), and y, with the residual add or SiLU, for the view's rows.
+// The memory operands come preloaded: p the streams' positions (app_q), c
+// and s the RoPE rows' cosine and sine of the lane's pair (app_cos), rv the
+// residuals (resid).
+template <int FA>
+__device__ __forceinline__ void fold_epilogue(const Epilogue &J, int t0, int nt, int blk, int lane, const float *y,
+                                              const int *p, const float *c, const float *s, const float *rv) {
     const int row = (J.blk0 + blk) * 64;  // root row of lane 0
     if (J.app_q) {
-        const int p = J.app_pos[t];
-        if (p >= 0 && p < J.app_cap) {
-            float v = y;
-            if (J.app_cos) {
-                const float o = xor_lane<32>(v);
-                const int jj = lane & 31;
-                const float x1 = lane < 32 ? v : o, x2 = lane < 32 ? o : v;
-                float o1, o2;
-                rope_pair(x1, x2, J.app_cos[p * 32 + jj], J.app_sin[p * 32 + jj], o1, o2);
-                v = lane < 32 ? o1 : o2;
-            }
-            float m = fabsf(v);
+        float v[FA], m[FA];
 #pragma unroll
-            for (int h = 32; h > 0; h >>= 1) m = go_max(m, xor_lane(m, h));
-            const float sc = m > 0.0f ? m / 127.0f : 1.0f;
-            const int r0 = row - J.row0;  // view row of the head's first value
-            int8_t *qp = J.app_q + static_cast<long long>(t) * J.app_q_stride + static_cast<long long>(p) * J.out;
-            qp[r0 + lane] = static_cast<int8_t>(go_int8_code(rintf(v / sc)));
-            if (lane == 0)
-                J.app_s[static_cast<long long>(t) * J.app_s_stride + static_cast<long long>(p) * (J.out >> 6) +
-                        (r0 >> 6)] = sc;
+        for (int k = 0; k < FA; ++k) {
+            v[k] = y[k];
+            if (J.app_cos) {
+                const float o = xor_lane<32>(v[k]);
+                const float x1 = lane < 32 ? v[k] : o, x2 = lane < 32 ? o : v[k];
+                float o1, o2;
+                rope_pair(x1, x2, c[k], s[k], o1, o2);
+                v[k] = lane < 32 ? o1 : o2;
+            }
+            m[k] = fabsf(v[k]);
+        }
+#pragma unroll
+        for (int h = 32; h > 0; h >>= 1)
+#pragma unroll
+            for (int k = 0; k < FA; ++k) m[k] = go_max(m[k], xor_lane(m[k], h));
+        const int r0 = row - J.row0;  // view row of the head's first value
+#pragma unroll
+        for (int k = 0; k < FA; ++k) {
+            const float sc = m[k] > 0.0f ? m[k] / 127.0f : 1.0f;
+            const int8_t code = static_cast<int8_t>(go_int8_code(rintf(v[k] / sc)));
+            const int t = t0 + k;
+            if (k < nt && p[k] >= 0 && p[k] < J.app_cap) {
+                J.app_q[static_cast<long long>(t) * J.app_q_stride + static_cast<long long>(p[k]) * J.out + r0 + lane] =
+                    code;
+                if (lane == 0)
+                    J.app_s[static_cast<long long>(t) * J.app_s_stride + static_cast<long long>(p[k]) * (J.out >> 6) +
+                            (r0 >> 6)] = sc;
+            }
         }
     }
     const int r = row + lane;
     if (r >= J.row0 && r < J.row0 + J.out) {
-        float out = y;
-        if (J.resid)
-            out = J.resid[static_cast<long long>(t) * J.resid_stride + (r - J.row0)] + out;
-        else if (J.act == 1)
-            out = silu_value(out);
-        J.y[static_cast<long long>(t) * J.y_stride + (r - J.row0)] = out;
+#pragma unroll
+        for (int k = 0; k < FA; ++k) {
+            if (k >= nt) break;
+            float out = y[k];
+            if (J.resid)
+                out = rv[k] + out;
+            else if (J.act == 1)
+                out = silu_value(out);
+            J.y[static_cast<long long>(t0 + k) * J.y_stride + (r - J.row0)] = out;
+        }
     }
 }
 
@@ -1003,6 +1043,421 @@ hipError_t launch_split_t(const LutLaunch &a, int grid, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---- The table form: tables built once per activation, MFMAs over them ----
+//
+// At some hundred activations (the decode step's batch) the MFMA forms
+// rebuild an activation tile's tables in every row tile's workgroup, and the
+// lut kernel looks every entry up once per activation. The table form
+// builds each activation's tables once: lut_tables_kernel rotates and
+// bounds each (activation, group) and writes the int8 planes of its 16-entry
+// tables, in the A-operand order of v_mfma_i32_32x32x32_i8, and the group's
+// step; lut_mfma_tab_kernel streams them into the MFMAs of every row tile,
+// 64 rows x 32 activations a workgroup, its four wavefronts taking the
+// groups in turn. The arithmetic is the split form's, so the result is bit
+// for bit the lut kernel's.
+constexpr int kTabActs = 8;       // activations per workgroup of the pre-pass
+constexpr int kTabWaves = 4;      // wavefronts per workgroup of the product
+constexpr int kTabDepth = 4;      // position pairs of A operands in flight per wavefront
+constexpr int kTabMaxGroups = 16;  // groups whose terms the product's LDS holds
+
+// The pre-pass: a workgroup per 8 activations and one group g. Wavefront w
+// rotates activations w and w + 4 (two values per lane), then every thread
+// builds items (an activation's 16 entries at one position, both planes):
+// threads 8j .. 8j + 7 take position j (and j + 32, ...) of the 8
+// activations, so each plane write of 8 threads is 128 contiguous bytes.
+template <int BITS>
+__global__ __launch_bounds__(256) void lut_tables_kernel(TabArgs a) {
+    using M = MfmaGeo<BITS>;
+    constexpr int G = M::G, AP = M::AP, NJ = M::NJ, NP = NJ / 2, TT = kTabActs, PW = TT / 4;
+    __shared__ float av[TT * AP];      // scaled rotated groups
+    __shared__ double stage[TT * 512];  // the norm's squares, 512 columns at a time
+    __shared__ double zpart[4 * TT];
+    __shared__ float zrms[TT];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = blockIdx.y, t0 = blockIdx.x * TT;
+    const int rows = a.rows, in = a.in;
+    const long long xs = a.x_stride;
+    const float *X = a.x, *XG = a.xgate, *NG = a.ngain;
+
+    // first loads without branches: rows past the activations and columns
+    // past the row read clamped addresses and go unused; with no gate the
+    // gate loads read x
+    const float *GP = XG ? XG : X;
+    float v[PW][2], gv[PW][2];
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const long long rowoff = static_cast<long long>(min(t0 + w + 4 * k, rows - 1)) * xs;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int col = min(g * G + e * 64 + lane, in - 1);
+            v[k][e] = X[rowoff + col];
+            gv[k][e] = GP[rowoff + col];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < PW; ++k)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            if (!(t0 + w + 4 * k < rows && g * G + e * 64 + lane < in)) v[k][e] = 0.0f;
+
+    // ZCRMSNorm divisors of the 8 activations over their whole rows
+    // (norm.go:53-109): four float64 partial sums over i mod 4, each in
+    // order. A round of 512 columns: every thread squares its columns
+    // (float64 of a float squared is exact) into LDS by partial, then a
+    // thread per (activation, partial) adds its 128 squares in order.
+    if (NG) {
+        const int full = in & ~3;
+        const int ct = tid >> 2, ck = tid & 3;  // chain thread (tid < 4 * TT): activation, partial
+        double s = 0.0;
+        for (int p0 = 0; p0 < full; p0 += 512) {
+            float st[2][TT];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < TT; ++r)
+                    st[h][r] = X[static_cast<long long>(min(t0 + r, rows - 1)) * xs + min(p0 + h * 256 + tid, full - 1)];
+            // column p0 + 256h + tid is value 64h + tid / 4 of partial tid mod 4: [r][partial][128]
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < TT; ++r) {
+                    const double d = st[h][r];
+                    stage[r * 512 + (tid & 3) * 128 + h * 64 + (tid >> 2)] = d * d;
+                }
+            __syncthreads();
+            if (tid < 4 * TT) {
+                const int n4 = min(512, full - p0) >> 2;  // the partial's values this round, in order
+                const double2 *sp = reinterpret_cast<const double2 *>(stage + ct * 512 + ck * 128);
+                if (n4 == 128) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        double2 dd[16];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) dd[i] = sp[q * 16 + i];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            s = s + dd[i].x;
+                            s = s + dd[i].y;
+                        }
+                    }
+                } else {
+                    for (int i = 0; i < n4; ++i) s = s + stage[ct * 512 + ck * 128 + i];
+                }
+            }
+            __syncthreads();
+        }
+        if (tid < 4 * TT) {
+            if (ck == 0 && t0 + ct < rows)
+                for (int c = full; c < in; ++c) {
+                    const double d = X[static_cast<long long>(t0 + ct) * xs + c];
+                    s = s + d * d;
+                }
+            zpart[tid] = s;
+        }
+        __syncthreads();
+        if (tid < TT) zrms[tid] = zc_rms(zpart[4 * tid], zpart[4 * tid + 1], zpart[4 * tid + 2], zpart[4 * tid + 3], in);
+        __syncthreads();
+    }
+
+    // Gate, norm, rotation and bound (lut.go:158-178, 219-225), as the
+    // split form.
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const int tt = w + 4 * k, t = t0 + tt;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int col = g * G + e * 64 + lane;
+            if (t < rows && col < in) {
+                if (XG) v[k][e] = v[k][e] * gate_sigmoid(gv[k][e]);
+                if (NG) {
+                    const float gx = NG[col] * v[k][e];
+                    v[k][e] = gx / zrms[tt];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {  // stages h = 1 .. 32 across lanes (kernel.go:384-393)
+#pragma unroll
+        for (int k = 0; k < PW; ++k)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float p = xor_lane(v[k][e], h);
+                v[k][e] = (lane & h) ? p - v[k][e] : v[k][e] + p;
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {  // stage h = 64 within the lane
+        const float p = v[k][0], q = v[k][1];
+        v[k][0] = p + q;
+        v[k][1] = p - q;
+    }
+    {
+        float mx[PW];
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            mx[k] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                if constexpr (BITS == 4) {
+                    mx[k] = go_max(mx[k], fabsf(v[k][e]));
+                } else {
+                    const float p = xor_lane<1>(v[k][e]);
+                    const float s2 = fabsf(v[k][e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                    mx[k] = go_max(mx[k], s2);
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int k = 0; k < PW; ++k) mx[k] = go_max(mx[k], xor_lane(mx[k], off));
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int tt = w + 4 * k, t = t0 + tt;
+            const float m = a.cb_max * mx[k];
+            const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) av[tt * AP + e * 64 + lane] = v[k][e] * inv;
+            if (lane == 0) a.stp[(static_cast<size_t>(t >> 5) * a.groups + g) * 32 + (t & 31)] = m * a.lut_step;
+        }
+    }
+    __syncthreads();
+
+    // Items (lutTables4Generic / lutTables2Generic, lut.go:239-282).
+    float cbv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cbv[q] = a.cb[q];
+    const int tt = tid % TT, jb = tid / TT, t = t0 + tt;
+    int8_t *base = a.tab + (static_cast<size_t>(t >> 5) * a.groups + g) * NP * 2048 + (t & 31) * 16;
+#pragma unroll
+    for (int k = 0; k < NJ / 32; ++k) {
+        const int j = jb + 32 * k;
+        float x0, x1 = 0.0f;
+        if constexpr (BITS == 4) {
+            x0 = av[tt * AP + j];
+        } else {
+            x0 = av[tt * AP + 2 * j];
+            x1 = av[tt * AP + 2 * j + 1];
+        }
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            uint32_t b[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int code = 4 * qd + q;
+                if constexpr (BITS == 4) {
+                    b[q] = rne_bits(cbv[code] * x0);
+                } else {  // code = hi << 2 | lo
+                    const float l = cbv[code & 3] * x0, h = cbv[code >> 2] * x1;
+                    const float sm = l + h;
+                    b[q] = rne_bits(sm);
+                }
+            }
+            planes4(b[0], b[1], b[2], b[3], lo[qd], hi[qd]);
+        }
+        int8_t *dst = base + (j >> 1) * 2048 + (j & 1) * 512;  // [pair][plane][half][32][16]
+        *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<uint4 *>(dst + 1024) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    }
+}
+
+// The product: a workgroup per (64-row block, 32-activation tile), the
+// tiles of one block on consecutive workgroups so that a tile's workgroups
+// share an XCD's L2 (dispatch goes round the XCDs) when there are 8 tiles.
+// Wavefront w takes groups w, w + 4, ...: per position pair it reads the
+// pair's two A planes (1 KiB each, kTabDepth pairs ahead), builds the
+// one-hots of its two 32-row tiles and runs 4 MFMAs; at the group's end its
+// terms float32(S) * (norm * step) go to LDS [group][activation][row]. Then
+// wavefront w folds activations 8w .. 8w + 7 (lane = row) in group order
+// from 0 (lut.go:297-310) and runs the lut kernel's epilogue.
+template <int BITS>
+__global__ __launch_bounds__(64 * kTabWaves) void lut_mfma_tab_kernel(LutLaunch a) {
+    using M = MfmaGeo<BITS>;
+    constexpr int NP = M::NJ / 2, D = kTabDepth, TP = 64;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float *terms = reinterpret_cast<float *>(smem);  // [groups][32][TP]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
+    const int nat = a.tab_at;
+    const int L = blockIdx.x;
+    const int at = L % nat, rb = L / nat;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kKernargJobs; ++k)
+        if (k < a.njobs && rb >= a.wg0[k]) jb = k;
+    const JobDesc &J = a.jobs[jb];
+    const int blk = rb - a.wg0[jb];
+    if (blk >= J.nblk) return;  // the whole workgroup
+    const int groups = J.groups, units = J.units;
+    int8_t *ohot = reinterpret_cast<int8_t *>(terms + groups * 32 * TP);  // [16][16]: entry c is the one-hot of c
+    if (tid < 16) {
+        const uint32_t one = 1u << (8 * (tid & 3)), d = tid >> 2;
+        *reinterpret_cast<uint4 *>(ohot + tid * 16) =
+            make_uint4(d == 0 ? one : 0u, d == 1 ? one : 0u, d == 2 ? one : 0u, d == 3 ? one : 0u);
+    }
+    const size_t bk = static_cast<size_t>(J.blk0 + blk);
+    const uint8_t *IDX = J.idx;
+    const uint32_t hs = 4u * static_cast<uint32_t>(half);  // a lane half takes the odd nibbles
+    bool first = true;
+    // the epilogue's operands for the wavefront's fold activations (t0 + k,
+    // clamped to the activations), loaded now so that they are in registers
+    // by the fold: positions and residuals here, the RoPE rows after the
+    // products
+    constexpr int FA = 32 / kTabWaves;
+    const Epilogue E(J);
+    const int t0 = at * 32 + w * FA, nt = min(FA, J.rows - t0);
+    const int rview = min(max((E.blk0 + blk) * 64 + lane - E.row0, 0), E.out - 1);  // the lane's view row, clamped
+    int pk[FA];
+    float rv[FA], cv[FA], sv[FA];
+#pragma unroll
+    for (int k = 0; k < FA; ++k) {
+        const long long tk = min(t0 + k, J.rows - 1);
+        pk[k] = E.app_q ? E.app_pos[tk] : -1;
+        rv[k] = E.resid ? E.resid[tk * E.resid_stride + rview] : 0.0f;
+    }
+
+    for (int g = w; g < groups; g += kTabWaves) {
+        const int8_t *A = a.tab + (static_cast<size_t>(at) * groups + g) * NP * 2048 + lane * 16;
+        i32x4 Al[D], Ah[D];
+#pragma unroll
+        for (int p = 0; p < D; ++p) {
+            Al[p] = *reinterpret_cast<const i32x4 *>(A + p * 2048);
+            Ah[p] = *reinterpret_cast<const i32x4 *>(A + p * 2048 + 1024);
+        }
+        uint32_t idx[M::UPG][2][4];
+#pragma unroll
+        for (int u = 0; u < M::UPG; ++u)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(
+                    IDX + ((bk * units + g * M::UPG + u) * 64 + rt * 32 + l32) * 16);
+                idx[u][rt][0] = v.x; idx[u][rt][1] = v.y; idx[u][rt][2] = v.z; idx[u][rt][3] = v.w;
+            }
+        unsigned short nrm16[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) nrm16[rt] = J.norm[(bk * groups + g) * 64 + rt * 32 + l32];
+        // the steps of the lane's 16 accumulator activations (used at the
+        // group's end)
+        float st[16];
+        const float *SP = a.tstp + (static_cast<size_t>(at) * groups + g) * 32 + half * 4;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st[i] = SP[(i >> 2) * 8 + (i & 3)];
+        __builtin_amdgcn_sched_barrier(0);
+        if (first) {
+            lds_barrier();  // the one-hot table is whole
+            first = false;
+        }
+        // this half's nibble of pair k in the high nibble of byte k: a
+        // one-hot's offset in the table is one SDWA and
+#pragma unroll
+        for (int u = 0; u < M::UPG; ++u)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) idx[u][rt][e] = (idx[u][rt][e] >> hs) << 4;
+        auto onehot = [&](int rt, int pp) -> i32x4 {
+            const uint32_t w4 = idx[pp >> 4][rt][(pp >> 2) & 3];
+            uint32_t off;
+            switch (pp & 3) {
+                case 0: off = and_byte<0>(0xf0u, w4); break;
+                case 1: off = and_byte<1>(0xf0u, w4); break;
+                case 2: off = and_byte<2>(0xf0u, w4); break;
+                default: off = and_byte<3>(0xf0u, w4); break;
+            }
+            return *reinterpret_cast<const i32x4 *>(ohot + off);
+        };
+        i32x4 B[2][2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) B[0][rt] = onehot(rt, 0);
+        i32x16 accl[2] = {i32x16{}, i32x16{}}, acch[2] = {i32x16{}, i32x16{}};
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) {
+            const int s = pp % D, sb = pp & 1;
+            if (pp + 1 < NP) {
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) B[sb ^ 1][rt] = onehot(rt, pp + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // the next pair's one-hot reads go out before these MFMAs
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+                accl[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al[s], B[sb][rt], accl[rt], 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+                acch[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah[s], B[sb][rt], acch[rt], 0, 0, 0);
+            // the slot's next pair goes out here, kTabDepth pairs before its
+            // use (the compiler would otherwise move the loads next to it)
+            __builtin_amdgcn_sched_barrier(0);
+            if (pp + D < NP) {
+                Al[s] = *reinterpret_cast<const i32x4 *>(A + (pp + D) * 2048);
+                Ah[s] = *reinterpret_cast<const i32x4 *>(A + (pp + D) * 2048 + 1024);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float nrm[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) nrm[rt] = __half2float(__ushort_as_half(nrm16[rt]));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int tt = (i >> 2) * 8 + half * 4 + (i & 3);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int sum = accl[rt][i] + 64 * acch[rt][i];
+                const float coef = nrm[rt] * st[i];
+                terms[(g * 32 + tt) * TP + rt * 32 + l32] = static_cast<float>(sum) * coef;
+            }
+        }
+    }
+    if (first) lds_barrier();  // a wavefront without groups still meets the table barrier
+#pragma unroll
+    for (int k = 0; k < FA; ++k) {
+        cv[k] = sv[k] = 0.0f;
+        if (E.app_cos) {
+            const int pc = pk[k] >= 0 && pk[k] < E.app_cap ? pk[k] : 0;
+            cv[k] = E.app_cos[pc * 32 + (lane & 31)];
+            sv[k] = E.app_sin[pc * 32 + (lane & 31)];
+        }
+    }
+    __syncthreads();
+
+    // The fold: wavefront w's 8 activations together, lane = row.
+    float y[FA];
+#pragma unroll
+    for (int k = 0; k < FA; ++k) y[k] = 0.0f;
+    for (int g = 0; g < groups; ++g) {
+        const float *tp = terms + (g * 32 + w * FA) * TP + lane;
+        float v[FA];
+#pragma unroll
+        for (int k = 0; k < FA; ++k) v[k] = tp[k * TP];
+#pragma unroll
+        for (int k = 0; k < FA; ++k) y[k] = y[k] + v[k];
+    }
+    fold_epilogue<FA>(E, t0, nt, blk, lane, y, pk, cv, sv, rv);
+}
+
+template <int BITS>
+size_t tab_lds_bytes(int groups) {
+    return sizeof(float) * static_cast<size_t>(groups) * 32 * 64 + 16 * 16;
+}
+
+template <int BITS>
+hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStream_t s) {
+    hipLaunchKernelGGL((lut_tables_kernel<BITS>), dim3(t.tiles * 32 / kTabActs, t.groups), dim3(256), 0, s, t);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    static bool attr = false;  // idempotent attribute write; a race is benign
+    if (!attr) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_mfma_tab_kernel<BITS>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(tab_lds_bytes<BITS>(kTabMaxGroups)));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), dim3(blocks * a.tab_at), dim3(64 * kTabWaves),
+                       tab_lds_bytes<BITS>(t.groups), s, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 int mfma_split_rows_per_workgroup() { return 64 * kSplitWaves; }
@@ -1016,6 +1471,23 @@ hipError_t launch_lut_mfma_split(const LutLaunch &a, int bits, int fold_blocks, 
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(mfma_fold_kernel, dim3(fold_blocks, (a.jobs[0].rows + 3) / 4), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+size_t tab_table_bytes(int bits, int groups, int tiles) {
+    const int np = bits == 4 ? MfmaGeo<4>::NJ / 2 : MfmaGeo<2>::NJ / 2;
+    return static_cast<size_t>(tiles) * groups * np * 2048;
+}
+
+size_t tab_step_bytes(int groups, int tiles) { return static_cast<size_t>(tiles) * groups * 32 * sizeof(float); }
+
+int tab_max_groups() { return kTabMaxGroups; }
+
+hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s) {
+    if (blocks <= 0 || a.tab_at <= 0 || a.njobs <= 0) return hipSuccess;
+    if (t.groups > kTabMaxGroups || t.tiles != a.tab_at) return hipErrorInvalidValue;
+    if (bits == 4) return launch_tab_t<4>(t, a, blocks, s);
+    if (bits == 2) return launch_tab_t<2>(t, a, blocks, s);
+    return hipErrorInvalidValue;
 }
 
 bool mfma_geometry_supported(int bits, int group) { return group == 128 && (bits == 2 || bits == 4); }

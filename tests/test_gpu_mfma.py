@@ -117,9 +117,10 @@ def test_mfma_path_choice_and_misuse():
 
     g = synth.rng(9)
     m = cq.New(synth.random_packed(g, 2048, 512, 128, 4))
-    # the lut kernel per activation for few activations, the split MFMA form
-    # where the 512-row form would leave CUs idle, the 512-row form at scale
-    assert m.gemm_path(1) == "lut" and m.gemm_path(256) == "lut"
+    # the lut kernel per activation for few activations, the table form at
+    # some hundred over 2048 rows, the split MFMA form where the 512-row form
+    # would leave CUs idle, the 512-row form at scale
+    assert m.gemm_path(1) == "lut" and m.gemm_path(256) == "lut-mfma-tab"
     assert m.gemm_path(375) == "lut-mfma-split" and m.gemm_path(12000) == "lut-mfma"
     assert m.Exact().gemm_path(12000) == "nibble4"
     z = torch.zeros(64 * 2048, dtype=torch.float32, device="cuda")
