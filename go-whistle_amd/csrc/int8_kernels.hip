@@ -380,9 +380,13 @@ __device__ __forceinline__ unsigned lds_offset(const void *p) {
 // One 16-byte global load per lane straight into LDS: lane l's bytes land
 // at lds + 16 * l (global_load_lds_dwordx4, M0 = lds). Issued as inline
 // assembly so that the compiler does not wait for it before every later LDS
-// read; its completion is the caller's wait_vm before a barrier.
+// read; its completion is the caller's wait_vm before a barrier. The K/V
+// rows are read once per call, so the load is non-temporal (nt): streaming
+// them does not push the products' weights and inputs out of the caches
+// (decode step at batch 256: 1.769 -> 1.686 ms, the cross call ~7% faster
+// alone).
 __device__ __forceinline__ void dma16(const void *src, unsigned lds) {
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+    asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
 // Geometry of the streamed attention kernel: value heads of VD codes,
@@ -1132,9 +1136,9 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
 
 // One 4-byte global load per active lane straight into LDS: lane l's word
 // lands at lds + 4 * l (global_load_lds_dword, M0 = lds); lanes off in EXEC
-// neither load nor write.
+// neither load nor write. Non-temporal, as dma16.
 __device__ __forceinline__ void dma4(const void *src, unsigned lds) {
-    asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+    asm volatile("global_load_lds_dword %0, off nt" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
 constexpr int kRingJc = 32;                     // keys per ring chunk
