@@ -745,6 +745,9 @@ int cq_new(int out, int in, int group, int bits, int width, const float *codeboo
     const size_t nrows = static_cast<size_t>(std::max(st->nblk, 1)) * kBlockRows;
     st->idx_bytes = nrows * st->row_bytes;
     st->norm_bytes = nrows * groups * sizeof(uint16_t);
+    if (st->idx_bytes > static_cast<size_t>(INT32_MAX))  // the lut kernel's buffer loads take 32-bit offsets
+        return fail(CQ_ERR_UNSUPPORTED, "cq: %zu index bytes (this library holds at most 2 GiB per matrix)",
+                    st->idx_bytes);
     std::vector<uint8_t> hidx(st->idx_bytes, 0);
     std::vector<uint16_t> hnorm(nrows * groups, 0);
     const int U = st->unit_bytes;

@@ -71,6 +71,8 @@ __device__ __forceinline__ CQ_GLOBAL T *gptr_w(T *p) {
     return (CQ_GLOBAL T *)p;
 }
 
+constexpr int kCpolNt = 2;  // a buffer load's cache policy: non-temporal (nt)
+
 // An index unit of U bytes. NTL: a non-temporal load, for launches that
 // stream more index bytes than the caches hold; the decode step's
 // matrices, read again every step, are loaded plainly and stay in the
@@ -380,6 +382,12 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     for (int c = 0; c < 16; ++c) cbv[c] = jr.template get<float>(offsetof(JobDesc, cb) + 4 * c);
     const int groups = JOB(jr, int, groups), units = JOB(jr, int, units), blk0 = JOB(jr, int, blk0) + b0;
     const CQ_GLOBAL uint8_t *idx = gptr(JOB(jr, const uint8_t *, idx));
+    // 16-byte units are buffer loads off the matrix's index array: a 32-bit
+    // offset per lane instead of a 64-bit address (cq_new keeps the array
+    // under 2 GiB)
+    const __amdgpu_buffer_rsrc_t irs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(JOB(jr, const uint8_t *, idx)), 0, 0x7fffffff,
+                                          0x00020000);
     const long long j_xstride = JOB(jr, long long, x_stride);
     const CQ_GLOBAL float *x = gptr(JOB(jr, const float *, x)) + static_cast<long long>(act) * j_xstride;
     const float *j_xgate = JOB(jr, const float *, xgate);
@@ -610,11 +618,13 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
         const Pos first = S == 1 ? Pos{w, 0} : Pos{bbs, gs};
         uint32_t buf[DG][UPGV][4];
         uint32_t nv[DG];
-        // Loads past the wavefront's last item read one 16-byte line of the
-        // activation row instead (kept in L2 by the tables' reads of it): the
-        // stream issues the same loads every turn, so each of its waits is a
-        // fixed count, and no index byte is fetched twice.
-        const CQ_GLOBAL uint8_t *spare = (const CQ_GLOBAL uint8_t *)(reinterpret_cast<uintptr_t>(x) & ~uintptr_t(15));
+        // Loads past the wavefront's last item read one 16-byte line again
+        // (the index array's first, or of the activation row for narrower
+        // units; kept in L2): the stream issues the same loads every turn, so
+        // each of its waits is a fixed count, and no index byte is fetched
+        // twice.
+        const CQ_GLOBAL uint8_t *spare =
+            U == 16 ? idx : (const CQ_GLOBAL uint8_t *)(reinterpret_cast<uintptr_t>(x) & ~uintptr_t(15));
         auto load_group = [&](const Pos &p, bool real, uint32_t (&bf)[UPGV][4], uint32_t &nrm) {
             const CQ_GLOBAL uint8_t *ip =
                 real ? idx + (static_cast<size_t>(blk0 + p.bb) * units + static_cast<size_t>(g0 + p.gi) * UPG +
@@ -622,8 +632,18 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
                            static_cast<size_t>(lane) * U
                      : spare;
             const size_t ustride = real ? static_cast<size_t>(64) * U : 0;
+            if constexpr (U == 16) {
+                const unsigned off = static_cast<unsigned>(ip - idx);
 #pragma unroll
-            for (int u = 0; u < UPGV; ++u) load_unit<U, NTL>(ip + u * ustride, bf[u]);
+                for (int u = 0; u < UPGV; ++u) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(irs, off + u * static_cast<unsigned>(ustride),
+                                                                          0, NTL ? kCpolNt : 0);
+                    bf[u][0] = v.x; bf[u][1] = v.y; bf[u][2] = v.z; bf[u][3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < UPGV; ++u) load_unit<U, NTL>(ip + u * ustride, bf[u]);
+            }
             // The row norm as the aligned 32-bit word holding it (this
             // lane's half: lane & 1), the norm table's own first word on a
             // spare turn: a merge of 32-bit loads needs no extension where
