@@ -1136,9 +1136,10 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
 
 // One 4-byte global load per active lane straight into LDS: lane l's word
 // lands at lds + 4 * l (global_load_lds_dword, M0 = lds); lanes off in EXEC
-// neither load nor write. Non-temporal, as dma16.
+// neither load nor write. (Plain: the scales of 32 keys share one line,
+// which non-temporal loads fetched again.)
 __device__ __forceinline__ void dma4(const void *src, unsigned lds) {
-    asm volatile("global_load_lds_dword %0, off nt" ::"v"(src), "{m0}"(lds) : "memory");
+    asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
 constexpr int kRingJc = 32;                     // keys per ring chunk
