@@ -99,8 +99,9 @@ int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *
  * it; cq_gemm_dev picks it by itself when its grid is large enough. Group
  * 128, 2 or 4 bits, not an Exact view; else CQ_ERR_UNSUPPORTED. */
 int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream);
-/* The kernel cq_gemm_dev runs for `rows` activations: "lut", "lut-mfma" or
- * "nibble4". */
+/* The kernel cq_gemm_dev runs for `rows` activations: "lut", "lut-mfma",
+ * "lut-mfma-tab" (the table pre-pass and its MFMA product), "lut-mfma-split"
+ * or "nibble4". */
 const char *cq_gemm_path(const cq_matrix *m, int rows);
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream);
 /* cq_gemms_dev with the decode step's neighbours fused into the product
