@@ -147,7 +147,7 @@ def batched_gemm_leg(gw, torch, reps=5):
     """The encoder's batched CQ GEMMs: X [M x In] ~N(0, 1) times 4/2-bit
     2048x512 and 512x2048 (FFN up/down), M in {375, 1500, 12000}, through
     cq_gemm_dev (which picks the lut kernel or its MFMA form). Flops are the
-    dense equivalent 2*M*Out*In; for the MFMA form, mfma_util is the int8 MFMA
+    dense equivalent 2*M*Out*In; for the MFMA forms, mfma_util is the int8 MFMA
     work it issues (one 32x32x32 product per 64-row block, 64-activation tile,
     position and 32x32 quadrant) over the time, against 5.0 POP/s."""
     g = gw.synth.rng(31)
@@ -169,9 +169,10 @@ def batched_gemm_leg(gw, torch, reps=5):
                 us = e0.elapsed_time(e1) * 1e3 / reps
                 path = m.gemm_path(M)
                 rec = {"path": path, "us": round(us, 2), "dense_TFLOPs": round(2.0 * M * o * i / us / 1e6, 2)}
-                if path in ("lut-mfma", "lut-mfma-split"):
+                if path in ("lut-mfma", "lut-mfma-split", "lut-mfma-tab"):
                     # one 32x32x32 int8 product per 32 weight rows, 32 activations and table position
-                    # (the 512-row form pads activations to its 64-wide tiles, the split form to 32)
+                    # (the 512-row form pads activations to its 64-wide tiles, the split and table
+                    # forms to 32)
                     positions = (i // GROUP) * (2 * GROUP * bits // 8)
                     tile = 64 if path == "lut-mfma" else 32
                     mfmas = -(-o // 64) * 2 * (-(-M // tile) * tile // 32) * positions

@@ -514,25 +514,31 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 
 // ---- the table form ----
 //
-// Between the lut kernel's few activations and the split form's several
-// hundred: a pre-pass builds each activation's tables once and the MFMAs of
-// every 64-row block stream them. A workgroup reads its 32 activations'
-// tables whole (16 KiB per activation and 512 inputs), so the form pays
-// where there are enough row blocks to spread that over the CUs. Measured
-// on MI355X at 256 activations (pre-pass + product against the lut kernel):
-// the four 512x512 CQ4 q/k/v/gate products with the norm 18.6 against 28.2
-// us, 2048x512 CQ2 with the norm and SiLU 16.2 against 18.8 us, the
-// 16384x512 head 64.4 us against the 512-row MFMA form's 69.5 us; it loses
-// at 1024 rows or fewer (a 512x512 CQ4 product 14.9 against 9.6 us,
-// 2x512x512 with the norm 17.9 against 17.0 us) and at 16 groups. The views
-// must share their tables (one pre-pass serves them all). The tables live
-// in the split form's workspace.
-constexpr int kTabMinRows = 64;
+// A pre-pass builds each activation's tables once and the MFMAs of every
+// 64-row block stream them. A workgroup reads its 32 activations' tables
+// whole (16 KiB per activation and 512 inputs), so the form pays where there
+// are enough row blocks, or (block, tile) workgroups, to spread that over the
+// CUs, from about 96 activations (below, the lut kernel's cost, linear in
+// them, is lower) up to a few thousand (past that the tables outgrow the
+// XCDs' L2s). Measured on MI355X (pre-pass + product against the form chosen
+// otherwise): at 256 activations the four 512x512 CQ4 q/k/v/gate products
+// with the norm 18.6 against 28.2 us, 2048x512 CQ2 with the norm and SiLU
+// 16.0 against 19.1 us, the 16384x512 head 60.2 against 64.4 us, but a
+// 512x512 CQ4 product 14.9 against 9.6 us (64 workgroups); 2048x512 CQ4 at
+// 64, 96, 192 activations 14.7, 16.1, 17.5 us against the lut kernel's 10.8,
+// 17.0, 26.8 us; at 375, 1024, 1500 and 3072 activations 25.6, 43.4, 61.4,
+// 117.7 us against 31.4, 57.7, 67.5, 123.9 us (split, split, MFMA, MFMA), CQ2
+// 17.2, 27.8, 36.6, 61.1 against 25.5, 49.2, 43.9, 78.2 us; 1024x512 CQ4 at
+// 1500 and 3000 38.8 and 63.2 us against the split form's 43.2 and 70.2 us.
+// The views must share their tables (one pre-pass serves them all). The
+// tables live in the split form's workspace.
+constexpr int kTabMinRows = 96;
+constexpr int kTabMaxRows = 3072;
 constexpr int kTabMinBlocks = 32;  // 64-row blocks over the views: 2048 rows
 constexpr int kTabMaxGroups = 8;
 
 bool tab_pays(cq_matrix *const *ms, int n, int rows) {
-    if (rows < kTabMinRows || rows >= kSplitMinRows || n > kKernargJobs) return false;
+    if (rows < kTabMinRows || rows > kTabMaxRows || n > kKernargJobs) return false;
     const CqStore &s0 = *ms[0]->st;
     if (!mfma_geometry_supported(s0.width, s0.group) || s0.groups > std::min(kTabMaxGroups, tab_max_groups()))
         return false;
@@ -541,7 +547,7 @@ bool tab_pays(cq_matrix *const *ms, int n, int rows) {
         if (!uses_lut(ms[k]) || !shares_tables(s0, *ms[k]->st)) return false;
         blocks += (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
     }
-    return blocks >= kTabMinBlocks;
+    return blocks >= kTabMinBlocks || blocks * ((rows + 31) / 32) >= device_info().cus;
 }
 
 int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,

@@ -1263,9 +1263,8 @@ __global__ __launch_bounds__(256) void lut_tables_kernel(TabArgs a) {
     }
 }
 
-// The product: a workgroup per (64-row block, 32-activation tile), the
-// tiles of one block on consecutive workgroups so that a tile's workgroups
-// share an XCD's L2 (dispatch goes round the XCDs) when there are 8 tiles.
+// The product: a workgroup per (64-row block, 32-activation tile), a
+// tile's workgroups all on one XCD, which shares their tables in its L2.
 // Wavefront w takes groups w, w + 4, ...: per position pair it reads the
 // pair's two A planes (1 KiB each, kTabDepth pairs ahead), builds the
 // one-hots of its two 32-row tiles and runs 4 MFMAs; at the group's end its
@@ -1281,7 +1280,13 @@ __global__ __launch_bounds__(64 * kTabWaves) void lut_mfma_tab_kernel(LutLaunch 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
     const int nat = a.tab_at;
     const int L = blockIdx.x;
-    const int at = L % nat, rb = L / nat;
+    // workgroup L runs on XCD L % 8 (dispatch goes round the XCDs): tile at
+    // takes the workgroups with L % 8 == at % 8, so that a tile's tables are
+    // read by one XCD and stay in its L2; with a tile count that is no
+    // multiple of 8 a row block's last workgroups have no tile
+    const int nat8 = (nat + 7) / 8;
+    const int at = (L & 7) + 8 * ((L >> 3) % nat8), rb = (L >> 3) / nat8;
+    if (at >= nat) return;  // the whole workgroup
     int jb = 0;
 #pragma unroll
     for (int k = 1; k < kKernargJobs; ++k)
@@ -1453,7 +1458,7 @@ hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStr
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), dim3(blocks * a.tab_at), dim3(64 * kTabWaves),
+    hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), dim3(blocks * 8 * ((a.tab_at + 7) / 8)), dim3(64 * kTabWaves),
                        tab_lds_bytes<BITS>(t.groups), s, a);
     return hipGetLastError();
 }

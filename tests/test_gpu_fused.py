@@ -63,8 +63,8 @@ def test_norm_prologue(rows, shape, bits):
     torch.cuda.synchronize()
     for a, b in zip(got, want):
         assert same(a.cpu().numpy(), b.cpu().numpy())
-    if rows >= 256:  # the table form at 256, the MFMA form's 64-activation tiles at 2048
-        assert ms[0].gemm_path(rows) == ("lut-mfma-tab" if rows < 320 else "lut-mfma")
+    if rows >= 256:  # the table form up to 3072 activations
+        assert ms[0].gemm_path(rows) == "lut-mfma-tab"
 
 
 @pytest.mark.parametrize("rows,bits", [(1, 4), (7, 2), (256, 4)])
@@ -271,8 +271,8 @@ def test_sigmoid_gate_vs_oracle():
 def test_gated_product(rows, shape, bits, resid):
     """cq_gemms_gated_dev (x * sigmoid(gate) inside the product, then the
     residual add) bit for bit the separate gate, product and add; at 300
-    activations of a 16384-row matrix the table form's pre-pass carries the
-    gate, at 2048 the MFMA form."""
+    and 2048 activations of a 16384-row matrix the table form's pre-pass
+    carries the gate."""
     import torch
 
     out, inp = shape
@@ -294,7 +294,7 @@ def test_gated_product(rows, shape, bits, resid):
     assert same(got.cpu().numpy(), want.cpu().numpy())
     assert torch.equal(gate, gate_before)  # the gate is only read
     if rows >= 300:
-        assert m.gemm_path(rows) == ("lut-mfma-tab" if rows < 320 else "lut-mfma")
+        assert m.gemm_path(rows) == "lut-mfma-tab"
 
 
 def test_gated_product_vs_oracle():

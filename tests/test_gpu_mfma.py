@@ -89,7 +89,7 @@ def test_mfma_rows_views(bits):
 
 
 def test_mfma_gemms_shared_input():
-    # q, k, v over one input (ApplyShared) at 1500 frames: one MFMA launch
+    # q, k, v over one input (ApplyShared) at 4000 frames: one MFMA launch
     # for the three matrices, each bit for bit its own GEMM (sampled frames).
     import torch
 
@@ -98,14 +98,14 @@ def test_mfma_gemms_shared_input():
     for p in ps[1:]:
         p.Codebook = ps[0].Codebook.copy()
     ms = [cq.New(p) for p in ps]
-    rows = 1500
-    assert ms[0].gemm_path(rows) == "lut-mfma"  # the three together fill a larger grid still
+    rows = 4000
+    assert ms[0].gemm_path(rows) == "lut-mfma"
     x = g.standard_normal((rows, 512)).astype(np.float32)
     xd = torch.from_numpy(x).cuda()
     ys = [torch.zeros(rows, p.Out, dtype=torch.float32, device="cuda") for p in ps]
     cq.gemms_dev(ms, ys, xd, rows)
     torch.cuda.synchronize()
-    pick = np.array([0, 1, 63, 64, 700, 1437, 1499])
+    pick = np.array([0, 1, 63, 64, 700, 1437, 1499, 2048, 3999])
     for p, y in zip(ps, ys):
         want = orc.OMatrix.new(p).gemm(x[pick].ravel(), len(pick), orc.LUT).reshape(len(pick), p.Out)
         got = y.cpu().numpy()[pick]
@@ -121,7 +121,7 @@ def test_mfma_path_choice_and_misuse():
     # some hundred over 2048 rows, the split MFMA form where the 512-row form
     # would leave CUs idle, the 512-row form at scale
     assert m.gemm_path(1) == "lut" and m.gemm_path(256) == "lut-mfma-tab"
-    assert m.gemm_path(375) == "lut-mfma-split" and m.gemm_path(12000) == "lut-mfma"
+    assert m.gemm_path(375) == "lut-mfma-tab" and m.gemm_path(12000) == "lut-mfma"
     assert m.Exact().gemm_path(12000) == "nibble4"
     z = torch.zeros(64 * 2048, dtype=torch.float32, device="cuda")
     with pytest.raises(gw.CQDeviceError):  # not a lut view

@@ -42,8 +42,10 @@ def test_split_gemm_bit_exact(bits, out, inp, rows):
     path = m.gemm_path(rows)
     want = orc.OMatrix.new(p).gemm(x.reshape(-1), rows, orc.LUT).reshape(rows, out)
     assert same(y.cpu().numpy(), want), path
-    if (out, inp, rows) in ((2048, 512, 375), (512, 2048, 375)) and bits == 4:
+    if (out, inp, rows) == (512, 2048, 375) and bits == 4:
         assert path == "lut-mfma-split"
+    if (out, inp, rows) == (2048, 512, 375):
+        assert path == "lut-mfma-tab"  # enough (block, tile) workgroups for the table form
     if rows == 100:
         assert path == "lut"
 
@@ -82,7 +84,7 @@ def test_split_fused_prologues_and_epilogues(bits):
     pd = synth.random_packed(g, D, F, 128, bits, sigma=0.05)
     mu, md = cq.New(pu), cq.New(pd)
     assert md.gemm_path(rows) == "lut-mfma-split"
-    assert mu.gemm_path(rows) == ("lut-mfma-split" if bits == 4 else "lut")
+    assert mu.gemm_path(rows) == "lut-mfma-tab"
     x = (g.standard_normal((rows, D)) * 3).astype(np.float32)
     gain = (1 + g.standard_normal(D) * 0.1).astype(np.float32)
     u = torch.zeros(rows, F, device="cuda")
@@ -128,9 +130,11 @@ def test_split_workspace_grows_and_is_reused():
 
 @pytest.mark.parametrize("views", [False, True])
 def test_split_append_epilogue(views):
-    # the K/V appends (RoPE on K) in the split form's fold, bit for bit the
-    # product followed by the separate append kernels, at 400 streams each at
-    # its own position (some outside the cache)
+    # the K/V appends (RoPE on K) in the fold, bit for bit the product
+    # followed by the separate append kernels, at 400 streams each at its own
+    # position (some outside the cache): three matrices of their own
+    # codebooks take the split form, three views of one root (one pre-pass
+    # serves them) the table form
     import torch
 
     from go_whistle_amd import decoder as dec

@@ -1,10 +1,11 @@
 """The table form of the MFMA product (lut_tables_kernel, then
-lut_mfma_tab_kernel), through the C ABI: products of 64 to 319 activations
-over 2048 rows or more (the decode step's q/k/v/gate and FFN-up products
-and its head at batch 256), bit for bit the oracle's lut product
-(internal/cq/lut.go), with row views, several matrices on one input,
-activations that do not fill a 32-wide tile, every fused prologue and
-epilogue, and the K/V append."""
+lut_mfma_tab_kernel), through the C ABI: products of 96 to 3072 activations
+over 2048 rows, or whose (64-row block, 32-activation tile) workgroups reach
+the CUs (the decode step's q/k/v/gate and FFN-up products and its head at
+batch 256, the encoder's products at 375 and 1500 frames), bit for bit the
+oracle's lut product (internal/cq/lut.go), with row views, several matrices
+on one input, activations that do not fill a 32-wide tile, every fused
+prologue and epilogue, and the K/V append."""
 
 import numpy as np
 import pytest
@@ -27,8 +28,9 @@ def _t(a):
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-@pytest.mark.parametrize("out,inp,rows", [(2048, 512, 256), (2048, 512, 64), (2048, 512, 100), (2048, 512, 319),
-                                          (2100, 384, 200), (4096, 1024, 256), (2048, 128, 96)])
+@pytest.mark.parametrize("out,inp,rows", [(2048, 512, 256), (2048, 512, 96), (2048, 512, 100), (2048, 512, 319),
+                                          (2100, 384, 200), (4096, 1024, 256), (2048, 128, 96), (2048, 512, 375),
+                                          (1536, 512, 1500), (512, 512, 3000)])
 def test_tab_gemm_bit_exact(bits, out, inp, rows):
     import torch
 
@@ -45,13 +47,16 @@ def test_tab_gemm_bit_exact(bits, out, inp, rows):
 
 
 def test_tab_path_bounds():
-    # the form runs from 64 activations to 319 over 2048 rows or more and
-    # at most 8 groups; fewer rows, more groups or more activations leave it
+    # the form runs from 96 activations to 3072 over 2048 rows or when its
+    # (block, tile) workgroups reach the CUs, at most 8 groups; fewer, more
+    # groups or more activations leave it
     g = synth.rng(3)
     m = cq.New(synth.random_packed(g, 2048, 512, 128, 4, sigma=0.05))
-    assert m.gemm_path(63) == "lut" and m.gemm_path(64) == "lut-mfma-tab"
-    assert m.gemm_path(319) == "lut-mfma-tab" and m.gemm_path(320) == "lut-mfma-split"
-    assert cq.New(synth.random_packed(g, 1024, 512, 128, 4, sigma=0.05)).gemm_path(256) == "lut"
+    assert m.gemm_path(95) == "lut" and m.gemm_path(96) == "lut-mfma-tab"
+    assert m.gemm_path(375) == "lut-mfma-tab" and m.gemm_path(3072) == "lut-mfma-tab"
+    assert m.gemm_path(3073) == "lut-mfma"
+    m1 = cq.New(synth.random_packed(g, 1024, 512, 128, 4, sigma=0.05))
+    assert m1.gemm_path(256) == "lut" and m1.gemm_path(1024) == "lut-mfma-tab"
     assert cq.New(synth.random_packed(g, 2048, 2048, 128, 2, sigma=0.05)).gemm_path(256) == "lut"
 
 
@@ -180,11 +185,12 @@ def test_tab_workspace_shared_with_split():
 
     g = synth.rng(321)
     cases = [(synth.random_packed(g, 2048, 512, 128, 4, sigma=0.05), 256),
-             (synth.random_packed(g, 4096, 512, 128, 4, sigma=0.05), 1024),
+             (synth.random_packed(g, 512, 2048, 128, 4, sigma=0.05), 1024),
              (synth.random_packed(g, 2048, 512, 128, 2, sigma=0.05), 128)]
-    for p, rows in cases:
+    for (p, rows), path in zip(cases, ("lut-mfma-tab", "lut-mfma-split", "lut-mfma-tab")):
         m = cq.New(p)
-        x = g.standard_normal((rows, 512)).astype(np.float32)
+        assert m.gemm_path(rows) == path
+        x = g.standard_normal((rows, p.In)).astype(np.float32)
         y = torch.zeros(rows, p.Out, device="cuda")
         m.gemm_dev(y, _t(x), rows)
         torch.cuda.synchronize()
