@@ -519,26 +519,32 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 // whole (16 KiB per activation and 512 inputs), so the form pays where there
 // are enough row blocks, or (block, tile) workgroups, to spread that over the
 // CUs, from about 96 activations (below, the lut kernel's cost, linear in
-// them, is lower) up to a few thousand (past that the tables outgrow the
-// XCDs' L2s). Measured on MI355X (pre-pass + product against the form chosen
-// otherwise): at 256 activations the four 512x512 CQ4 q/k/v/gate products
-// with the norm 18.6 against 28.2 us, 2048x512 CQ2 with the norm and SiLU
-// 16.0 against 19.1 us, the 16384x512 head 60.2 against 64.4 us, but a
-// 512x512 CQ4 product 14.9 against 9.6 us (64 workgroups); 2048x512 CQ4 at
-// 64, 96, 192 activations 14.7, 16.1, 17.5 us against the lut kernel's 10.8,
-// 17.0, 26.8 us; at 375, 1024, 1500 and 3072 activations 25.6, 43.4, 61.4,
-// 117.7 us against 31.4, 57.7, 67.5, 123.9 us (split, split, MFMA, MFMA), CQ2
-// 17.2, 27.8, 36.6, 61.1 against 25.5, 49.2, 43.9, 78.2 us; 1024x512 CQ4 at
-// 1500 and 3000 38.8 and 63.2 us against the split form's 43.2 and 70.2 us.
-// The views must share their tables (one pre-pass serves them all). The
-// tables live in the split form's workspace.
+// them, is lower); past 3072 activations only over 1024 rows or more (over
+// fewer the tables, read by few blocks, cost more than the 512-row MFMA
+// form's own table builds). Measured on MI355X (pre-pass + product against
+// the form chosen otherwise): at 256 activations the four 512x512 CQ4
+// q/k/v/gate products with the norm 18.6 against 28.2 us, 2048x512 CQ2 with
+// the norm and SiLU 16.0 against 19.1 us, the 16384x512 head 60.2 against
+// 64.4 us, but a 512x512 CQ4 product 14.9 against 9.6 us (64 workgroups);
+// 2048x512 CQ4 at 64, 96, 192 activations 14.7, 16.1, 17.5 us against the
+// lut kernel's 10.8, 17.0, 26.8 us; at 375, 1024, 1500, 3000, 6000 and
+// 12000 activations 25.8, 44.0, 57.5, 107.1, 194.4, 361.1 us against 31.4,
+// 57.7, 67.5, 118.0, 244.0, 363.8 us (split, split, then the 512-row MFMA
+// form), CQ2 at 375, 1500, 6000, 12000 16.9, 36.7, 106.7, 203.4 against
+// 25.5, 43.9, 154.3, 236.1 us; 1024x512 CQ4 at 1500, 6000, 12000 37.5,
+// 101.7, 202.2 us against 43.2, 114.4, 220.3 us; 512x512 CQ4 at 12000 120.3
+// against the MFMA form's 111.4 us. The views must share their tables (one
+// pre-pass serves them all). The tables live in the split form's workspace
+// (at 12288 activations of 1024 inputs, 384 MiB).
 constexpr int kTabMinRows = 96;
-constexpr int kTabMaxRows = 3072;
+constexpr int kTabMaxRows = 3072;       // any row count
+constexpr int kTabMaxRowsWide = 12288;  // over kTabWideBlocks blocks or more
+constexpr int kTabWideBlocks = 16;
 constexpr int kTabMinBlocks = 32;  // 64-row blocks over the views: 2048 rows
 constexpr int kTabMaxGroups = 8;
 
 bool tab_pays(cq_matrix *const *ms, int n, int rows) {
-    if (rows < kTabMinRows || rows > kTabMaxRows || n > kKernargJobs) return false;
+    if (rows < kTabMinRows || rows > kTabMaxRowsWide || n > kKernargJobs) return false;
     const CqStore &s0 = *ms[0]->st;
     if (!mfma_geometry_supported(s0.width, s0.group) || s0.groups > std::min(kTabMaxGroups, tab_max_groups()))
         return false;
@@ -547,6 +553,7 @@ bool tab_pays(cq_matrix *const *ms, int n, int rows) {
         if (!uses_lut(ms[k]) || !shares_tables(s0, *ms[k]->st)) return false;
         blocks += (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
     }
+    if (rows > kTabMaxRows) return blocks >= kTabWideBlocks;
     return blocks >= kTabMinBlocks || blocks * ((rows + 31) / 32) >= device_info().cus;
 }
 

@@ -1282,10 +1282,12 @@ __global__ __launch_bounds__(64 * kTabWaves) void lut_mfma_tab_kernel(LutLaunch 
     const int L = blockIdx.x;
     // workgroup L runs on XCD L % 8 (dispatch goes round the XCDs): tile at
     // takes the workgroups with L % 8 == at % 8, so that a tile's tables are
-    // read by one XCD and stay in its L2; with a tile count that is no
-    // multiple of 8 a row block's last workgroups have no tile
-    const int nat8 = (nat + 7) / 8;
-    const int at = (L & 7) + 8 * ((L >> 3) % nat8), rb = (L >> 3) / nat8;
+    // read by one XCD, and on that XCD the row blocks of one tile come one
+    // after the other, so that its tables stay in the L2 while they run;
+    // with a tile count that is no multiple of 8 the last XCDs' last
+    // workgroups have no tile
+    const int nat8 = (nat + 7) / 8, nb = gridDim.x / (8 * nat8);
+    const int at = (L & 7) + 8 * ((L >> 3) / nb), rb = (L >> 3) % nb;
     if (at >= nat) return;  // the whole workgroup
     int jb = 0;
 #pragma unroll

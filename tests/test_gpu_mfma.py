@@ -89,8 +89,9 @@ def test_mfma_rows_views(bits):
 
 
 def test_mfma_gemms_shared_input():
-    # q, k, v over one input (ApplyShared) at 4000 frames: one MFMA launch
-    # for the three matrices, each bit for bit its own GEMM (sampled frames).
+    # q, k, v over one input (ApplyShared) at 13000 frames (past the table
+    # form): one MFMA launch for the three matrices, each bit for bit its own
+    # GEMM (sampled frames).
     import torch
 
     g = synth.rng(808)
@@ -98,14 +99,14 @@ def test_mfma_gemms_shared_input():
     for p in ps[1:]:
         p.Codebook = ps[0].Codebook.copy()
     ms = [cq.New(p) for p in ps]
-    rows = 4000
+    rows = 13000
     assert ms[0].gemm_path(rows) == "lut-mfma"
     x = g.standard_normal((rows, 512)).astype(np.float32)
     xd = torch.from_numpy(x).cuda()
     ys = [torch.zeros(rows, p.Out, dtype=torch.float32, device="cuda") for p in ps]
     cq.gemms_dev(ms, ys, xd, rows)
     torch.cuda.synchronize()
-    pick = np.array([0, 1, 63, 64, 700, 1437, 1499, 2048, 3999])
+    pick = np.array([0, 1, 63, 64, 700, 1437, 1499, 2048, 3999, 12287, 12999])
     for p, y in zip(ps, ys):
         want = orc.OMatrix.new(p).gemm(x[pick].ravel(), len(pick), orc.LUT).reshape(len(pick), p.Out)
         got = y.cpu().numpy()[pick]
@@ -118,10 +119,10 @@ def test_mfma_path_choice_and_misuse():
     g = synth.rng(9)
     m = cq.New(synth.random_packed(g, 2048, 512, 128, 4))
     # the lut kernel per activation for few activations, the table form at
-    # some hundred over 2048 rows, the split MFMA form where the 512-row form
-    # would leave CUs idle, the 512-row form at scale
+    # some hundred to 12288 over 2048 rows, the 512-row form beyond
     assert m.gemm_path(1) == "lut" and m.gemm_path(256) == "lut-mfma-tab"
-    assert m.gemm_path(375) == "lut-mfma-tab" and m.gemm_path(12000) == "lut-mfma"
+    assert m.gemm_path(375) == "lut-mfma-tab" and m.gemm_path(12000) == "lut-mfma-tab"
+    assert m.gemm_path(12289) == "lut-mfma"
     assert m.Exact().gemm_path(12000) == "nibble4"
     z = torch.zeros(64 * 2048, dtype=torch.float32, device="cuda")
     with pytest.raises(gw.CQDeviceError):  # not a lut view
@@ -134,16 +135,17 @@ def test_mfma_path_choice_and_misuse():
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-def test_mfma_12000_frames_sampled(bits):
+@pytest.mark.parametrize("rows,path", [(12000, "lut-mfma-tab"), (12800, "lut-mfma")])
+def test_mfma_12000_frames_sampled(bits, rows, path):
     # The encoder's 8-utterance batch: 12000 activations through the device
-    # pointer API; 40 sampled activations against the oracle.
+    # pointer API (the table form), and 12800 (the 512-row MFMA form); 40
+    # sampled activations against the oracle.
     import torch
 
-    g = synth.rng(12000 + bits)
+    g = synth.rng(rows + bits)
     p = synth.random_packed(g, 2048, 512, 128, bits, sigma=0.05)
     m, o = cq.New(p), orc.OMatrix.new(p)
-    rows = 12000
-    assert m.gemm_path(rows) == "lut-mfma"
+    assert m.gemm_path(rows) == path
     x = g.standard_normal((rows, 512)).astype(np.float32)
     y = torch.zeros(rows, 2048, dtype=torch.float32, device="cuda")
     m.gemm_dev(y, torch.from_numpy(x).cuda(), rows)

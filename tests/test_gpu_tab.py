@@ -1,8 +1,9 @@
 """The table form of the MFMA product (lut_tables_kernel, then
 lut_mfma_tab_kernel), through the C ABI: products of 96 to 3072 activations
 over 2048 rows, or whose (64-row block, 32-activation tile) workgroups reach
-the CUs (the decode step's q/k/v/gate and FFN-up products and its head at
-batch 256, the encoder's products at 375 and 1500 frames), bit for bit the
+the CUs, and up to 12288 over 1024 rows or more (the decode step's
+q/k/v/gate and FFN-up products and its head at batch 256, the encoder's
+products at 375, 1500 and 12000 frames), bit for bit the
 oracle's lut product (internal/cq/lut.go), with row views, several matrices
 on one input, activations that do not fill a 32-wide tile, every fused
 prologue and epilogue, and the K/V append."""
@@ -48,13 +49,16 @@ def test_tab_gemm_bit_exact(bits, out, inp, rows):
 
 def test_tab_path_bounds():
     # the form runs from 96 activations to 3072 over 2048 rows or when its
-    # (block, tile) workgroups reach the CUs, at most 8 groups; fewer, more
-    # groups or more activations leave it
+    # (block, tile) workgroups reach the CUs, and to 12288 over 1024 rows or
+    # more, at most 8 groups; fewer, more groups or more activations leave it
     g = synth.rng(3)
     m = cq.New(synth.random_packed(g, 2048, 512, 128, 4, sigma=0.05))
     assert m.gemm_path(95) == "lut" and m.gemm_path(96) == "lut-mfma-tab"
     assert m.gemm_path(375) == "lut-mfma-tab" and m.gemm_path(3072) == "lut-mfma-tab"
-    assert m.gemm_path(3073) == "lut-mfma"
+    assert m.gemm_path(3073) == "lut-mfma-tab" and m.gemm_path(12288) == "lut-mfma-tab"
+    assert m.gemm_path(12289) == "lut-mfma"
+    m512 = cq.New(synth.random_packed(g, 512, 512, 128, 4, sigma=0.05))
+    assert m512.gemm_path(3072) == "lut-mfma-tab" and m512.gemm_path(3073) != "lut-mfma-tab"
     m1 = cq.New(synth.random_packed(g, 1024, 512, 128, 4, sigma=0.05))
     assert m1.gemm_path(256) == "lut" and m1.gemm_path(1024) == "lut-mfma-tab"
     assert cq.New(synth.random_packed(g, 2048, 2048, 128, 2, sigma=0.05)).gemm_path(256) == "lut"
@@ -195,3 +199,26 @@ def test_tab_workspace_shared_with_split():
         m.gemm_dev(y, _t(x), rows)
         torch.cuda.synchronize()
         assert same(y.cpu().numpy().reshape(-1), orc.OMatrix.new(p).gemm(x.reshape(-1), rows, orc.LUT)), rows
+
+
+@pytest.mark.parametrize("out,bits,rows", [(1024, 4, 6000), (2048, 2, 12288), (1536, 4, 3100)])
+def test_tab_many_activations_sampled(out, bits, rows):
+    # past 3072 activations over 1024 rows or more: 48 sampled activations
+    # (the first and last tiles, a tile edge mid-way, random ones) against
+    # the oracle, each activation's product being its own
+    import torch
+
+    g = synth.rng(out + bits + rows)
+    p = synth.random_packed(g, out, 512, 128, bits, sigma=0.05)
+    m = cq.New(p)
+    assert m.gemm_path(rows) == "lut-mfma-tab"
+    x = g.standard_normal((rows, 512)).astype(np.float32)
+    y = torch.full((rows, out), float("nan"), device="cuda")
+    m.gemm_dev(y, _t(x), rows)
+    torch.cuda.synchronize()
+    mid = (rows // 64) * 32
+    pick = np.unique(np.concatenate([[0, 1, 31, 32, mid - 1, mid, rows - 33, rows - 32, rows - 1],
+                                     g.choice(rows, size=39, replace=False)]))
+    got = y.cpu().numpy()[pick]
+    want = orc.OMatrix.new(p).gemm(x[pick].reshape(-1), len(pick), orc.LUT).reshape(len(pick), out)
+    assert same(got, want)
