@@ -1055,20 +1055,25 @@ hipError_t launch_split_t(const LutLaunch &a, int grid, hipStream_t s) {
 // 64 rows x 32 activations a workgroup, its four wavefronts taking the
 // groups in turn. The arithmetic is the split form's, so the result is bit
 // for bit the lut kernel's.
-constexpr int kTabActs = 8;       // activations per workgroup of the pre-pass
 constexpr int kTabWaves = 4;      // wavefronts per workgroup of the product
 constexpr int kTabDepth = 4;      // position pairs of A operands in flight per wavefront
 constexpr int kTabMaxGroups = 16;  // groups whose terms the product's LDS holds
+constexpr int kTabPre4Rows = 3072;  // activations up to which the pre-pass takes 4 a workgroup
 
-// The pre-pass: a workgroup per 8 activations and one group g. Wavefront w
-// rotates activations w and w + 4 (two values per lane), then every thread
-// builds items (an activation's 16 entries at one position, both planes):
-// threads 8j .. 8j + 7 take position j (and j + 32, ...) of the 8
-// activations, so each plane write of 8 threads is 128 contiguous bytes.
-template <int BITS>
+// The pre-pass: a workgroup per TT activations (4 or 8) and one group g.
+// Wavefront w rotates activations w, w + 4, ... (two values per lane), then
+// every thread builds items (an activation's 16 entries at one position,
+// both planes): threads TT j .. TT j + TT - 1 take position j (and j + 256 /
+// TT, ...) of the TT activations, so each plane write of TT threads is 16 TT
+// contiguous bytes. Measured on MI355X: 4 activations a workgroup (twice
+// the workgroups) make the batch-256 decode step's table-form products 1-1.5
+// us faster each (the norm's in-order float64 chains run on twice the CUs)
+// and lose at 12,000 activations (2048x512 CQ4 376 -> 392 us).
+template <int BITS, int TT>
 __global__ __launch_bounds__(256) void lut_tables_kernel(TabArgs a) {
     using M = MfmaGeo<BITS>;
-    constexpr int G = M::G, AP = M::AP, NJ = M::NJ, NP = NJ / 2, TT = kTabActs, PW = TT / 4;
+    constexpr int G = M::G, AP = M::AP, NJ = M::NJ, NP = NJ / 2, PW = TT / 4, PS = 256 / TT;
+    static_assert(TT % 4 == 0 && NJ % PS == 0, "positions per pass");
     __shared__ float av[TT * AP];      // scaled rotated groups
     __shared__ double stage[TT * 512];  // the norm's squares, 512 columns at a time
     __shared__ double zpart[4 * TT];
@@ -1231,8 +1236,8 @@ __global__ __launch_bounds__(256) void lut_tables_kernel(TabArgs a) {
     const int tt = tid % TT, jb = tid / TT, t = t0 + tt;
     int8_t *base = a.tab + (static_cast<size_t>(t >> 5) * a.groups + g) * NP * 2048 + (t & 31) * 16;
 #pragma unroll
-    for (int k = 0; k < NJ / 32; ++k) {
-        const int j = jb + 32 * k;
+    for (int k = 0; k < NJ / PS; ++k) {
+        const int j = jb + PS * k;
         float x0, x1 = 0.0f;
         if constexpr (BITS == 4) {
             x0 = av[tt * AP + j];
@@ -1449,7 +1454,10 @@ size_t tab_lds_bytes(int groups) {
 
 template <int BITS>
 hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStream_t s) {
-    hipLaunchKernelGGL((lut_tables_kernel<BITS>), dim3(t.tiles * 32 / kTabActs, t.groups), dim3(256), 0, s, t);
+    if (t.rows <= kTabPre4Rows)
+        hipLaunchKernelGGL((lut_tables_kernel<BITS, 4>), dim3(t.tiles * 32 / 4, t.groups), dim3(256), 0, s, t);
+    else
+        hipLaunchKernelGGL((lut_tables_kernel<BITS, 8>), dim3(t.tiles * 32 / 8, t.groups), dim3(256), 0, s, t);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     static bool attr = false;  // idempotent attribute write; a race is benign

@@ -222,3 +222,25 @@ def test_tab_many_activations_sampled(out, bits, rows):
     got = y.cpu().numpy()[pick]
     want = orc.OMatrix.new(p).gemm(x[pick].reshape(-1), len(pick), orc.LUT).reshape(len(pick), out)
     assert same(got, want)
+
+
+def test_tab_norm_many_activations_sampled():
+    # ZCRMSNorm in front and SiLU behind at 3100 activations (the pre-pass
+    # takes 8 activations a workgroup past 3072): 40 sampled activations
+    # against the oracle's separate steps
+    import torch
+
+    g = synth.rng(3100)
+    rows, D, F = 3100, 512, 2048
+    p = synth.random_packed(g, F, D, 128, 2, sigma=0.05)
+    m = cq.New(p)
+    assert m.gemm_path(rows) == "lut-mfma-tab"
+    x = (g.standard_normal((rows, D)) * 3).astype(np.float32)
+    gain = (1 + g.standard_normal(D) * 0.1).astype(np.float32)
+    u = torch.full((rows, F), float("nan"), device="cuda")
+    cq.gemms_fused_dev([m], [u], _t(x), rows, norm_gain=_t(gain), act=1)
+    torch.cuda.synchronize()
+    pick = np.unique(np.concatenate([[0, 7, 8, 3071, 3072, 3099], g.choice(rows, size=34, replace=False)]))
+    h = orc.zc_rmsnorm(x[pick].reshape(-1), gain, D)
+    want = orc.silu(orc.OMatrix.new(p).gemm(h, len(pick), orc.LUT)).reshape(len(pick), F)
+    assert same(u.cpu().numpy()[pick], want)
