@@ -516,16 +516,18 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 //
 // A pre-pass builds each activation's tables once and the MFMAs of every
 // 64-row block stream them. A workgroup reads its 32 activations' tables
-// whole (16 KiB per activation and 512 inputs), so the form pays where there
-// are enough row blocks, or (block, tile) workgroups, to spread that over the
-// CUs, from about 96 activations (below, the lut kernel's cost, linear in
-// them, is lower); past 3072 activations only over 1024 rows or more (over
-// fewer the tables, read by few blocks, cost more than the 512-row MFMA
-// form's own table builds). Measured on MI355X (pre-pass + product against
-// the form chosen otherwise): at 256 activations the four 512x512 CQ4
-// q/k/v/gate products with the norm 18.6 against 28.2 us, 2048x512 CQ2 with
-// the norm and SiLU 16.0 against 19.1 us, the 16384x512 head 60.2 against
-// 64.4 us, but a 512x512 CQ4 product 14.9 against 9.6 us (64 workgroups);
+// whole (16 KiB per activation and 512 inputs), so the form pays where the
+// lut kernel's work, linear in rows x activations, outgrows the form's
+// ~15 us floor at these sizes (from about 256K row-activations at 4 bits,
+// 384K at 2), or where its (block, tile) workgroups reach the CUs; past
+// 3072 activations only over 1024 rows or more (over fewer the tables, read
+// by few blocks, cost more than the 512-row MFMA form's own table builds).
+// Measured on MI355X (pre-pass + product against the form chosen
+// otherwise): at 256 activations the four 512x512 CQ4 q/k/v/gate products
+// with the norm 18.6 against 28.2 us, 2048x512 CQ2 with the norm and SiLU
+// 16.0 against 19.1 us, the 16384x512 head 60.2 against 64.4 us, 1536x512
+// CQ4 16.2 against 23.5 us, 1024x512 CQ4 15.9 against 16.7 us, but 1024x512
+// CQ2 12.0 against 10.8 us and a 512x512 CQ4 product 14.9 against 9.6 us;
 // 2048x512 CQ4 at 64, 96, 192 activations 14.7, 16.1, 17.5 us against the
 // lut kernel's 10.8, 17.0, 26.8 us; at 375, 1024, 1500, 3000, 6000 and
 // 12000 activations 25.8, 44.0, 57.5, 107.1, 194.4, 361.1 us against 31.4,
@@ -540,7 +542,8 @@ constexpr int kTabMinRows = 96;
 constexpr int kTabMaxRows = 3072;       // any row count
 constexpr int kTabMaxRowsWide = 12288;  // over kTabWideBlocks blocks or more
 constexpr int kTabWideBlocks = 16;
-constexpr int kTabMinBlocks = 32;  // 64-row blocks over the views: 2048 rows
+constexpr long long kTabMinWork4 = 256LL * 1024;  // rows x activations, 4-bit
+constexpr long long kTabMinWork2 = 384LL * 1024;  // rows x activations, 2-bit
 constexpr int kTabMaxGroups = 8;
 
 bool tab_pays(cq_matrix *const *ms, int n, int rows) {
@@ -554,7 +557,8 @@ bool tab_pays(cq_matrix *const *ms, int n, int rows) {
         blocks += (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
     }
     if (rows > kTabMaxRows) return blocks >= kTabWideBlocks;
-    return blocks >= kTabMinBlocks || blocks * ((rows + 31) / 32) >= device_info().cus;
+    const long long work = blocks * 64LL * rows;  // in whole 64-row blocks
+    return work >= (s0.width == 4 ? kTabMinWork4 : kTabMinWork2) || blocks * ((rows + 31) / 32) >= device_info().cus;
 }
 
 int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,

@@ -1,7 +1,8 @@
 """The table form of the MFMA product (lut_tables_kernel, then
 lut_mfma_tab_kernel), through the C ABI: products of 96 to 3072 activations
-over 2048 rows, or whose (64-row block, 32-activation tile) workgroups reach
-the CUs, and up to 12288 over 1024 rows or more (the decode step's
+of 256K row-activations or more (384K at 2 bits), or whose (64-row block,
+32-activation tile) workgroups reach the CUs, and up to 12288 over 1024 rows
+or more (the decode step's
 q/k/v/gate and FFN-up products and its head at batch 256, the encoder's
 products at 375, 1500 and 12000 frames), bit for bit the
 oracle's lut product (internal/cq/lut.go), with row views, several matrices
@@ -29,8 +30,8 @@ def _t(a):
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-@pytest.mark.parametrize("out,inp,rows", [(2048, 512, 256), (2048, 512, 96), (2048, 512, 100), (2048, 512, 319),
-                                          (2100, 384, 200), (4096, 1024, 256), (2048, 128, 96), (2048, 512, 375),
+@pytest.mark.parametrize("out,inp,rows", [(2048, 512, 256), (2048, 512, 193), (2048, 512, 230), (2048, 512, 319),
+                                          (2100, 384, 200), (4096, 1024, 256), (2048, 128, 250), (2048, 512, 375),
                                           (1536, 512, 1500), (512, 512, 3000)])
 def test_tab_gemm_bit_exact(bits, out, inp, rows):
     import torch
@@ -48,19 +49,22 @@ def test_tab_gemm_bit_exact(bits, out, inp, rows):
 
 
 def test_tab_path_bounds():
-    # the form runs from 96 activations to 3072 over 2048 rows or when its
-    # (block, tile) workgroups reach the CUs, and to 12288 over 1024 rows or
-    # more, at most 8 groups; fewer, more groups or more activations leave it
+    # the form runs from 96 activations to 3072 at 256K row-activations (384K
+    # at 2 bits) or when its (block, tile) workgroups reach the CUs, and to
+    # 12288 over 1024 rows or more, at most 8 groups; fewer, more groups or
+    # more activations leave it
     g = synth.rng(3)
     m = cq.New(synth.random_packed(g, 2048, 512, 128, 4, sigma=0.05))
-    assert m.gemm_path(95) == "lut" and m.gemm_path(96) == "lut-mfma-tab"
+    assert m.gemm_path(127) == "lut" and m.gemm_path(128) == "lut-mfma-tab"
+    m2 = cq.New(synth.random_packed(g, 2048, 512, 128, 2, sigma=0.05))
+    assert m2.gemm_path(191) == "lut" and m2.gemm_path(192) == "lut-mfma-tab"
     assert m.gemm_path(375) == "lut-mfma-tab" and m.gemm_path(3072) == "lut-mfma-tab"
     assert m.gemm_path(3073) == "lut-mfma-tab" and m.gemm_path(12288) == "lut-mfma-tab"
     assert m.gemm_path(12289) == "lut-mfma"
     m512 = cq.New(synth.random_packed(g, 512, 512, 128, 4, sigma=0.05))
     assert m512.gemm_path(3072) == "lut-mfma-tab" and m512.gemm_path(3073) != "lut-mfma-tab"
     m1 = cq.New(synth.random_packed(g, 1024, 512, 128, 4, sigma=0.05))
-    assert m1.gemm_path(256) == "lut" and m1.gemm_path(1024) == "lut-mfma-tab"
+    assert m1.gemm_path(255) == "lut" and m1.gemm_path(256) == "lut-mfma-tab"
     assert cq.New(synth.random_packed(g, 2048, 2048, 128, 2, sigma=0.05)).gemm_path(256) == "lut"
 
 
@@ -190,7 +194,7 @@ def test_tab_workspace_shared_with_split():
     g = synth.rng(321)
     cases = [(synth.random_packed(g, 2048, 512, 128, 4, sigma=0.05), 256),
              (synth.random_packed(g, 512, 2048, 128, 4, sigma=0.05), 1024),
-             (synth.random_packed(g, 2048, 512, 128, 2, sigma=0.05), 128)]
+             (synth.random_packed(g, 2048, 512, 128, 2, sigma=0.05), 200)]
     for (p, rows), path in zip(cases, ("lut-mfma-tab", "lut-mfma-split", "lut-mfma-tab")):
         m = cq.New(p)
         assert m.gemm_path(rows) == path
