@@ -519,7 +519,8 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 // whole (16 KiB per activation and 512 inputs), so the form pays where the
 // lut kernel's work, linear in rows x activations, outgrows the form's
 // ~15 us floor at these sizes (from about 256K row-activations at 4 bits,
-// 384K at 2), or where its (block, tile) workgroups reach the CUs; past
+// 384K at 2, and 16 activations), or where its (block, tile) workgroups
+// reach the CUs; past
 // 3072 activations only over 1024 rows or more (over fewer the tables, read
 // by few blocks, cost more than the 512-row MFMA form's own table builds).
 // Measured on MI355X (pre-pass + product against the form chosen
@@ -528,6 +529,9 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 // 16.0 against 19.1 us, the 16384x512 head 60.2 against 64.4 us, 1536x512
 // CQ4 16.2 against 23.5 us, 1024x512 CQ4 15.9 against 16.7 us, but 1024x512
 // CQ2 12.0 against 10.8 us and a 512x512 CQ4 product 14.9 against 9.6 us;
+// the 16384x512 CQ4 head at 16, 32, 64 and 95 activations 15.5, 15.7, 22.6,
+// 30.3 us against 16.8, 28.0, 50.4, 70.1 us (CQ2 at 32 and 64 12.1 and 16.0
+// against 17.7 and 30.4 us);
 // 2048x512 CQ4 at 64, 96, 192 activations 14.7, 16.1, 17.5 us against the
 // lut kernel's 10.8, 17.0, 26.8 us; at 375, 1024, 1500, 3000, 6000 and
 // 12000 activations 25.8, 44.0, 57.5, 107.1, 194.4, 361.1 us against 31.4,
@@ -538,7 +542,7 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 // against the MFMA form's 111.4 us. The views must share their tables (one
 // pre-pass serves them all). The tables live in the split form's workspace
 // (at 12288 activations of 1024 inputs, 384 MiB).
-constexpr int kTabMinRows = 96;
+constexpr int kTabMinRows = 16;
 constexpr int kTabMaxRows = 3072;       // any row count
 constexpr int kTabMaxRowsWide = 12288;  // over kTabWideBlocks blocks or more
 constexpr int kTabWideBlocks = 16;
@@ -599,6 +603,7 @@ int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     a.tab = t.tab;
     a.tstp = t.stp;
     a.tab_at = tiles;
+    a.tab_nb = blocks;
     HIP_TRY(launch_lut_tab(t, a, s0.width, blocks, stream), "lut table-form launch");
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;

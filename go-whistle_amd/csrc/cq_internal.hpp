@@ -126,10 +126,11 @@ struct LutLaunch {
     int fold0[kKernargJobs];  // the job's first 256-row group in the fold's grid
     int split_tiles, split_at;
     // The table form: the activations' table planes and steps as
-    // lut_tables_kernel wrote them, for tab_at tiles of 32 activations.
+    // lut_tables_kernel wrote them, for tab_at tiles of 32 activations over
+    // tab_nb 64-row blocks (all jobs).
     const int8_t *tab;
     const float *tstp;
-    int tab_at;
+    int tab_at, tab_nb;
 };
 
 // The table pre-pass of the table form (mfma_kernels.hip): per activation

@@ -1269,7 +1269,7 @@ __global__ __launch_bounds__(256) void lut_tables_kernel(TabArgs a) {
 }
 
 // The product: a workgroup per (64-row block, 32-activation tile), a
-// tile's workgroups all on one XCD, which shares their tables in its L2.
+// tile's workgroups on one XCD (or two), which shares their tables in its L2.
 // Wavefront w takes groups w, w + 4, ...: per position pair it reads the
 // pair's two A planes (1 KiB each, kTabDepth pairs ahead), builds the
 // one-hots of its two 32-row tiles and runs 4 MFMAs; at the group's end its
@@ -1285,15 +1285,15 @@ __global__ __launch_bounds__(64 * kTabWaves) void lut_mfma_tab_kernel(LutLaunch 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
     const int nat = a.tab_at;
     const int L = blockIdx.x;
-    // workgroup L runs on XCD L % 8 (dispatch goes round the XCDs): tile at
-    // takes the workgroups with L % 8 == at % 8, so that a tile's tables are
-    // read by one XCD, and on that XCD the row blocks of one tile come one
-    // after the other, so that its tables stay in the L2 while they run;
-    // with a tile count that is no multiple of 8 the last XCDs' last
-    // workgroups have no tile
-    const int nat8 = (nat + 7) / 8, nb = gridDim.x / (8 * nat8);
-    const int at = (L & 7) + 8 * ((L >> 3) / nb), rb = (L >> 3) % nb;
-    if (at >= nat) return;  // the whole workgroup
+    // workgroup L runs on XCD L % 8 (dispatch goes round the XCDs), as its
+    // (L / 8)-th there. The (tile, row block) items, tile by tile, are cut
+    // into 8 equal runs, one per XCD: an XCD's workgroups take the row blocks
+    // of one tile one after the other, so that its tables stay in that L2
+    // while they run, and every XCD has the same share of the work
+    const int nb = a.tab_nb, total = nat * nb, per = (total + 7) / 8;
+    const int k8 = L >> 3, item = (L & 7) * per + k8;
+    if (k8 >= per || item >= total) return;  // the whole workgroup
+    const int at = item / nb, rb = item % nb;
     int jb = 0;
 #pragma unroll
     for (int k = 1; k < kKernargJobs; ++k)
@@ -1468,7 +1468,7 @@ hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStr
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), dim3(blocks * 8 * ((a.tab_at + 7) / 8)), dim3(64 * kTabWaves),
+    hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), dim3(8 * ((a.tab_at * blocks + 7) / 8)), dim3(64 * kTabWaves),
                        tab_lds_bytes<BITS>(t.groups), s, a);
     return hipGetLastError();
 }
@@ -1499,7 +1499,7 @@ int tab_max_groups() { return kTabMaxGroups; }
 
 hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s) {
     if (blocks <= 0 || a.tab_at <= 0 || a.njobs <= 0) return hipSuccess;
-    if (t.groups > kTabMaxGroups || t.tiles != a.tab_at) return hipErrorInvalidValue;
+    if (t.groups > kTabMaxGroups || t.tiles != a.tab_at || a.tab_nb != blocks) return hipErrorInvalidValue;
     if (bits == 4) return launch_tab_t<4>(t, a, blocks, s);
     if (bits == 2) return launch_tab_t<2>(t, a, blocks, s);
     return hipErrorInvalidValue;

@@ -1,5 +1,5 @@
 """The table form of the MFMA product (lut_tables_kernel, then
-lut_mfma_tab_kernel), through the C ABI: products of 96 to 3072 activations
+lut_mfma_tab_kernel), through the C ABI: products of 16 to 3072 activations
 of 256K row-activations or more (384K at 2 bits), or whose (64-row block,
 32-activation tile) workgroups reach the CUs, and up to 12288 over 1024 rows
 or more (the decode step's
@@ -49,7 +49,7 @@ def test_tab_gemm_bit_exact(bits, out, inp, rows):
 
 
 def test_tab_path_bounds():
-    # the form runs from 96 activations to 3072 at 256K row-activations (384K
+    # the form runs from 16 activations to 3072 at 256K row-activations (384K
     # at 2 bits) or when its (block, tile) workgroups reach the CUs, and to
     # 12288 over 1024 rows or more, at most 8 groups; fewer, more groups or
     # more activations leave it
@@ -65,6 +65,8 @@ def test_tab_path_bounds():
     assert m512.gemm_path(3072) == "lut-mfma-tab" and m512.gemm_path(3073) != "lut-mfma-tab"
     m1 = cq.New(synth.random_packed(g, 1024, 512, 128, 4, sigma=0.05))
     assert m1.gemm_path(255) == "lut" and m1.gemm_path(256) == "lut-mfma-tab"
+    mh = cq.New(synth.random_packed(g, 16384, 512, 128, 4, sigma=0.05))
+    assert mh.gemm_path(15) == "lut" and mh.gemm_path(16) == "lut-mfma-tab"
     assert cq.New(synth.random_packed(g, 2048, 2048, 128, 2, sigma=0.05)).gemm_path(256) == "lut"
 
 
@@ -248,3 +250,25 @@ def test_tab_norm_many_activations_sampled():
     h = orc.zc_rmsnorm(x[pick].reshape(-1), gain, D)
     want = orc.silu(orc.OMatrix.new(p).gemm(h, len(pick), orc.LUT)).reshape(len(pick), F)
     assert same(u.cpu().numpy()[pick], want)
+
+
+@pytest.mark.parametrize("bits,rows", [(4, 16), (4, 40), (2, 33)])
+def test_tab_tall_few_activations(bits, rows):
+    # a 16384-row matrix (the head of a beam search) at 16 to 40 activations,
+    # one or two partial tiles spread over the XCDs: every activation against
+    # the oracle on the first and last 512 rows
+    import torch
+
+    g = synth.rng(900 + rows + bits)
+    p = synth.random_packed(g, 16384, 512, 128, bits, sigma=0.05)
+    m = cq.New(p)
+    assert m.gemm_path(rows) == "lut-mfma-tab"
+    x = g.standard_normal((rows, 512)).astype(np.float32)
+    y = torch.full((rows, 16384), float("nan"), device="cuda")
+    m.gemm_dev(y, _t(x), rows)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    om = orc.OMatrix.new(p)
+    for lo, hi in ((0, 512), (15872, 16384)):
+        want = om.rows(lo, hi).gemm(x.reshape(-1), rows, orc.LUT).reshape(rows, hi - lo)
+        assert same(got[:, lo:hi], want), (lo, hi)
