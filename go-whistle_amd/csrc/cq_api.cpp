@@ -520,9 +520,9 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 // lut kernel's work, linear in rows x activations, outgrows the form's
 // ~15 us floor at these sizes (from about 256K row-activations at 4 bits,
 // 384K at 2, and 16 activations), or where its (block, tile) workgroups
-// reach the CUs; past
-// 3072 activations only over 1024 rows or more (over fewer the tables, read
-// by few blocks, cost more than the 512-row MFMA form's own table builds).
+// reach the CUs; past 3072 activations over 768 rows or more, at 2 bits,
+// or up to 6144 activations (a 512-row CQ4 matrix's tables, read by few
+// blocks, cost more than the 512-row MFMA form's own table builds at 12000).
 // Measured on MI355X (pre-pass + product against the form chosen
 // otherwise): at 256 activations the four 512x512 CQ4 q/k/v/gate products
 // with the norm 18.6 against 28.2 us, 2048x512 CQ2 with the norm and SiLU
@@ -539,13 +539,18 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 // form), CQ2 at 375, 1500, 6000, 12000 16.9, 36.7, 106.7, 203.4 against
 // 25.5, 43.9, 154.3, 236.1 us; 1024x512 CQ4 at 1500, 6000, 12000 37.5,
 // 101.7, 202.2 us against 43.2, 114.4, 220.3 us; 512x512 CQ4 at 12000 120.3
-// against the MFMA form's 111.4 us. The views must share their tables (one
+// against the MFMA form's 111.4 us, but at 4000 and 6000 activations 50.9
+// and 68.5 us against the split form's 53.8 and 75.3 us (CQ2 at 4000, 6000,
+// 12000: 35.8, 45.6, 73.9 against 52.8, 74.8, 83.8 us); 768x512 CQ4 at 4000,
+// 6000, 12000 62.2, 85.7, 162.6 us against the MFMA form's 70.2, 117.9,
+// 225.6 us. The views must share their tables (one
 // pre-pass serves them all). The tables live in the split form's workspace
 // (at 12288 activations of 1024 inputs, 384 MiB).
 constexpr int kTabMinRows = 16;
 constexpr int kTabMaxRows = 3072;       // any row count
-constexpr int kTabMaxRowsWide = 12288;  // over kTabWideBlocks blocks or more
-constexpr int kTabWideBlocks = 16;
+constexpr int kTabMaxRowsWide = 12288;  // over kTabWideBlocks blocks, at 2 bits, or to kTabMidRows
+constexpr int kTabWideBlocks = 12;
+constexpr int kTabMidRows = 6144;
 constexpr long long kTabMinWork4 = 256LL * 1024;  // rows x activations, 4-bit
 constexpr long long kTabMinWork2 = 384LL * 1024;  // rows x activations, 2-bit
 constexpr int kTabMaxGroups = 8;
@@ -560,7 +565,7 @@ bool tab_pays(cq_matrix *const *ms, int n, int rows) {
         if (!uses_lut(ms[k]) || !shares_tables(s0, *ms[k]->st)) return false;
         blocks += (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
     }
-    if (rows > kTabMaxRows) return blocks >= kTabWideBlocks;
+    if (rows > kTabMaxRows) return blocks >= kTabWideBlocks || s0.width == 2 || rows <= kTabMidRows;
     const long long work = blocks * 64LL * rows;  // in whole 64-row blocks
     return work >= (s0.width == 4 ? kTabMinWork4 : kTabMinWork2) || blocks * ((rows + 31) / 32) >= device_info().cus;
 }

@@ -1,8 +1,8 @@
 """The table form of the MFMA product (lut_tables_kernel, then
 lut_mfma_tab_kernel), through the C ABI: products of 16 to 3072 activations
 of 256K row-activations or more (384K at 2 bits), or whose (64-row block,
-32-activation tile) workgroups reach the CUs, and up to 12288 over 1024 rows
-or more (the decode step's
+32-activation tile) workgroups reach the CUs, and up to 12288 over 768 rows
+or more or at 2 bits (6144 otherwise) (the decode step's
 q/k/v/gate and FFN-up products and its head at batch 256, the encoder's
 products at 375, 1500 and 12000 frames), bit for bit the
 oracle's lut product (internal/cq/lut.go), with row views, several matrices
@@ -51,8 +51,8 @@ def test_tab_gemm_bit_exact(bits, out, inp, rows):
 def test_tab_path_bounds():
     # the form runs from 16 activations to 3072 at 256K row-activations (384K
     # at 2 bits) or when its (block, tile) workgroups reach the CUs, and to
-    # 12288 over 1024 rows or more, at most 8 groups; fewer, more groups or
-    # more activations leave it
+    # 12288 over 768 rows or more or at 2 bits (6144 otherwise), at most 8
+    # groups; fewer, more groups or more activations leave it
     g = synth.rng(3)
     m = cq.New(synth.random_packed(g, 2048, 512, 128, 4, sigma=0.05))
     assert m.gemm_path(127) == "lut" and m.gemm_path(128) == "lut-mfma-tab"
@@ -62,7 +62,9 @@ def test_tab_path_bounds():
     assert m.gemm_path(3073) == "lut-mfma-tab" and m.gemm_path(12288) == "lut-mfma-tab"
     assert m.gemm_path(12289) == "lut-mfma"
     m512 = cq.New(synth.random_packed(g, 512, 512, 128, 4, sigma=0.05))
-    assert m512.gemm_path(3072) == "lut-mfma-tab" and m512.gemm_path(3073) != "lut-mfma-tab"
+    assert m512.gemm_path(6144) == "lut-mfma-tab" and m512.gemm_path(6145) != "lut-mfma-tab"
+    m512b = cq.New(synth.random_packed(g, 512, 512, 128, 2, sigma=0.05))
+    assert m512b.gemm_path(12288) == "lut-mfma-tab"
     m1 = cq.New(synth.random_packed(g, 1024, 512, 128, 4, sigma=0.05))
     assert m1.gemm_path(255) == "lut" and m1.gemm_path(256) == "lut-mfma-tab"
     mh = cq.New(synth.random_packed(g, 16384, 512, 128, 4, sigma=0.05))
@@ -207,9 +209,11 @@ def test_tab_workspace_shared_with_split():
         assert same(y.cpu().numpy().reshape(-1), orc.OMatrix.new(p).gemm(x.reshape(-1), rows, orc.LUT)), rows
 
 
-@pytest.mark.parametrize("out,bits,rows", [(1024, 4, 6000), (2048, 2, 12288), (1536, 4, 3100)])
+@pytest.mark.parametrize("out,bits,rows", [(1024, 4, 6000), (2048, 2, 12288), (1536, 4, 3100), (512, 4, 5000),
+                                           (512, 2, 9000), (768, 4, 7000)])
 def test_tab_many_activations_sampled(out, bits, rows):
-    # past 3072 activations over 1024 rows or more: 48 sampled activations
+    # past 3072 activations (over 768 rows or more, at 2 bits, or to 6144):
+    # 48 sampled activations
     # (the first and last tiles, a tile edge mid-way, random ones) against
     # the oracle, each activation's product being its own
     import torch
