@@ -38,6 +38,8 @@ SIGNATURES = {
     "cq_gemm_mfma_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "cq_gemm_path": (c_char_p, [c_void_p, c_int]),
     "cq_gemms_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p]),
+    "cq_workspace_held": (c_longlong, []),
+    "cq_workspace_trim": (c_longlong, []),
     "cq_row_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "cq_row_gather_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "cq_batch_new": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p), POINTER(c_int),

@@ -405,35 +405,161 @@ int run_mfma(cq_matrix *const *ms, int n, float *const *dsts, const float *x, in
     return CQ_OK;
 }
 
-// ---- the MFMA form split over groups ----
+// ---- workspaces of the table and split forms ----
 //
-// Its workspace holds the groups' float terms between the two launches.
-// Each host thread has its own per device, grown when a product needs more
-// and never freed or moved while the process runs (a captured graph keeps
-// the address it recorded), so products queued from different threads do
-// not share one; products queued from one thread on several streams at once
-// would.
-struct SplitWorkspace {
+// Both forms keep tables or float terms in device memory between their two
+// launches. A product leases a workspace for its launches and returns it
+// with an event recorded behind them, in one pool per process that every
+// thread shares under a mutex:
+// - an idle workspace last used on the same stream is reused at once
+//   (stream order protects it); one last used on another stream only once
+//   its event has completed; otherwise the product gets a new one, of the
+//   size it asks for rounded up to 1 MiB. So products queued at the same
+//   time on two streams never share one, from one thread or many;
+// - before a new one is allocated, idle workspaces of that device whose
+//   work has completed are freed: a device keeps about one workspace per
+//   stream with products in flight, each the size of its largest product;
+// - a product queued while its stream is captured into a graph leases a
+//   workspace of its own, shared only by the products of that capture
+//   sequence on that stream (in the graph's order), and never reused or
+//   freed: the graph replays it at that address, and the library cannot
+//   see when the graph is destroyed. Its allocation is made in relaxed
+//   capture mode, so the first product of a shape may be captured.
+struct Workspace {
     void *buf = nullptr;
     size_t size = 0;
-};
-thread_local SplitWorkspace t_split[64];
-
-int split_workspace(size_t bytes, float **out) {
     int dev = -1;
-    HIP_TRY(hipGetDevice(&dev), "current device");
-    if (dev < 0 || dev >= 64) return fail(CQ_ERR_DEVICE, "cq: device %d has no workspace slot", dev);
-    SplitWorkspace &w = t_split[dev];
-    if (w.size < bytes) {
-        void *p = nullptr;
-        const size_t want = std::max(bytes, 2 * w.size);
-        HIP_TRY(hipMalloc(&p, want), "hipMalloc split workspace");
-        w.buf = p;  // the smaller one stays allocated: a graph may still use it
-        w.size = want;
-    }
-    *out = static_cast<float *>(w.buf);
+    hipStream_t stream = nullptr;
+    hipEvent_t done = nullptr;  // recorded behind the last lease's launches
+    unsigned long long capture = 0;  // capture sequence id of a graph's workspace, 0 otherwise
+};
+
+struct WorkspacePool {
+    std::mutex mu;
+    std::vector<Workspace *> idle;   // eager workspaces not leased
+    std::vector<Workspace *> graph;  // held for captured graphs
+    size_t held = 0;                 // bytes of all workspaces
+};
+
+WorkspacePool &ws_pool() {
+    static WorkspacePool *pool = new WorkspacePool;  // never destroyed: graphs may outlive static teardown
+    return *pool;
+}
+
+constexpr size_t kWsRound = size_t(1) << 20;
+
+struct WsLease {
+    Workspace *w = nullptr;
+    hipStream_t stream = nullptr;
+    bool graph = false;
+};
+
+int ws_alloc(Workspace *w, size_t bytes, bool capturing) {
+    const size_t want = (std::max<size_t>(bytes, 1) + kWsRound - 1) / kWsRound * kWsRound;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (capturing) HIP_TRY(hipThreadExchangeStreamCaptureMode(&mode), "capture mode");
+    const hipError_t e = hipMalloc(&w->buf, want);
+    if (capturing) (void)hipThreadExchangeStreamCaptureMode(&mode);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc workspace");
+    w->size = want;
     return CQ_OK;
 }
+
+int ws_acquire(size_t bytes, hipStream_t stream, WsLease &l) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev), "current device");
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (stream) HIP_TRY(hipStreamGetCaptureInfo(stream, &cs, &cid), "capture info");
+    WorkspacePool &p = ws_pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    l.stream = stream;
+    if (cs == hipStreamCaptureStatusActive) {
+        l.graph = true;
+        Workspace *best = nullptr;
+        for (Workspace *w : p.graph)
+            if (w->dev == dev && w->capture == cid && w->stream == stream && w->size >= bytes &&
+                (!best || w->size < best->size))
+                best = w;
+        if (!best) {
+            std::unique_ptr<Workspace> w(new Workspace);
+            if (int e = ws_alloc(w.get(), bytes, true)) return e;
+            w->dev = dev;
+            w->stream = stream;
+            w->capture = cid;
+            p.held += w->size;
+            best = w.release();
+            p.graph.push_back(best);
+        }
+        l.w = best;
+        return CQ_OK;
+    }
+    // An idle workspace of this device: one last used on this stream first,
+    // else one whose work has completed.
+    int pick = -1;
+    for (size_t i = 0; i < p.idle.size(); ++i) {
+        Workspace *w = p.idle[i];
+        if (w->dev != dev || w->size < bytes) continue;
+        if (w->stream == stream) {
+            pick = static_cast<int>(i);
+            break;
+        }
+        if (pick < 0 && hipEventQuery(w->done) == hipSuccess) pick = static_cast<int>(i);
+    }
+    if (pick >= 0) {
+        l.w = p.idle[pick];
+        p.idle.erase(p.idle.begin() + pick);
+        return CQ_OK;
+    }
+    // None fits: free this device's completed idle workspaces (all smaller
+    // than the request, or busy on other streams), then allocate.
+    for (size_t i = 0; i < p.idle.size();) {
+        Workspace *w = p.idle[i];
+        if (w->dev == dev && hipEventQuery(w->done) == hipSuccess) {
+            (void)hipEventDestroy(w->done);
+            (void)hipFree(w->buf);
+            p.held -= w->size;
+            delete w;
+            p.idle.erase(p.idle.begin() + i);
+        } else {
+            ++i;
+        }
+    }
+    std::unique_ptr<Workspace> w(new Workspace);
+    if (int e = ws_alloc(w.get(), bytes, false)) return e;
+    const hipError_t e = hipEventCreateWithFlags(&w->done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipFree(w->buf);
+        return hip_fail(e, "workspace event");
+    }
+    w->dev = dev;
+    p.held += w->size;
+    l.w = w.release();
+    return CQ_OK;
+}
+
+// Returns a lease after its launches were queued (or failed to queue).
+int ws_release(WsLease &l) {
+    if (!l.w || l.graph) return CQ_OK;
+    Workspace *w = l.w;
+    l.w = nullptr;
+    const hipError_t e = hipEventRecord(w->done, l.stream);
+    WorkspacePool &p = ws_pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    if (e != hipSuccess) {  // nothing marks its last use: keep it out of reuse
+        p.graph.push_back(w);
+        return hip_fail(e, "workspace event record");
+    }
+    w->stream = l.stream;
+    p.idle.push_back(w);
+    return CQ_OK;
+}
+
+// Holds a lease for the scope of one product.
+struct WsScope {
+    WsLease l;
+    ~WsScope() { (void)ws_release(l); }
+};
 
 constexpr int kSplitMinRows = 320;  // activations from which the split form pays
 
@@ -499,14 +625,16 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
         if (a.njobs == 0 || nr == 0) return CQ_OK;
         a.split_at = (nr + ta - 1) / ta;
         a.split_tiles = wg * a.split_at;
-        float *ws = nullptr;
-        if (int e = split_workspace(terms * sizeof(float), &ws)) return e;
+        WsScope ws;
+        if (int e = ws_acquire(terms * sizeof(float), stream, ws.l)) return e;
+        float *const base = static_cast<float *>(ws.l.w->buf);
         size_t off = 0;
         for (int k = 0; k < a.njobs; ++k) {
-            a.term[k] = ws + off;
+            a.term[k] = base + off;
             off += static_cast<size_t>(a.jobs[k].groups) * nr * a.jobs[k].nblk * kBlockRows;
         }
         HIP_TRY(launch_lut_mfma_split(a, s0.width, fold, stream), "lut mfma split launch");
+        if (int e = ws_release(ws.l)) return e;
     }
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;
@@ -543,9 +671,13 @@ int run_split(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 // and 68.5 us against the split form's 53.8 and 75.3 us (CQ2 at 4000, 6000,
 // 12000: 35.8, 45.6, 73.9 against 52.8, 74.8, 83.8 us); 768x512 CQ4 at 4000,
 // 6000, 12000 62.2, 85.7, 162.6 us against the MFMA form's 70.2, 117.9,
-// 225.6 us. The views must share their tables (one
-// pre-pass serves them all). The tables live in the split form's workspace
-// (at 12288 activations of 1024 inputs, 384 MiB).
+// 225.6 us; small matrices past 3072 activations keep the form at 2 bits
+// (64x512 CQ2 at 3500 / 12000: 23.5 / 40.8 against the MFMA form's 40.5 /
+// 77.3 us, 384x512 CQ2 at 12000 70.1 against 79.0 us) and at 4 bits to
+// 6144 (64x512 CQ4 at 6000: 40.2 against 62.4 us; at 12000 the two are
+// within 1%). The views must share their tables (one
+// pre-pass serves them all). The tables live in a leased workspace (at 12288
+// activations of 1024 inputs, 384 MiB).
 constexpr int kTabMinRows = 16;
 constexpr int kTabMaxRows = 3072;       // any row count
 constexpr int kTabMaxRowsWide = 12288;  // over kTabWideBlocks blocks, at 2 bits, or to kTabMidRows
@@ -601,15 +733,17 @@ int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     t.cb_max = s0.cb_max;
     t.lut_step = s0.lut_step;
     const size_t tb = tab_table_bytes(s0.width, s0.groups, tiles), sb = tab_step_bytes(s0.groups, tiles);
-    float *ws = nullptr;
-    if (int e = split_workspace(tb + sb, &ws)) return e;
-    t.tab = reinterpret_cast<int8_t *>(ws);
-    t.stp = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + tb);
+    WsScope ws;
+    if (int e = ws_acquire(tb + sb, stream, ws.l)) return e;
+    char *const base = static_cast<char *>(ws.l.w->buf);
+    t.tab = reinterpret_cast<int8_t *>(base);
+    t.stp = reinterpret_cast<float *>(base + tb);
     a.tab = t.tab;
     a.tstp = t.stp;
     a.tab_at = tiles;
     a.tab_nb = blocks;
     HIP_TRY(launch_lut_tab(t, a, s0.width, blocks, stream), "lut table-form launch");
+    if (int e = ws_release(ws.l)) return e;
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;
 }
@@ -881,6 +1015,30 @@ static int nil_operands(int n, float *const *dsts, const float *x, int rows) {
     for (int k = 0; k < n; ++k)
         if (!dsts[k]) return fail(CQ_ERR_MISUSE, "cq: GEMMs with a nil output %d", k);
     return CQ_OK;
+}
+
+long long cq_workspace_held(void) {
+    WorkspacePool &p = ws_pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    return static_cast<long long>(p.held);
+}
+
+long long cq_workspace_trim(void) {
+    WorkspacePool &p = ws_pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    for (size_t i = 0; i < p.idle.size();) {
+        Workspace *w = p.idle[i];
+        if (hipEventQuery(w->done) == hipSuccess) {
+            (void)hipEventDestroy(w->done);
+            (void)hipFree(w->buf);
+            p.held -= w->size;
+            delete w;
+            p.idle.erase(p.idle.begin() + i);
+        } else {
+            ++i;
+        }
+    }
+    return static_cast<long long>(p.held);
 }
 
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream) {

@@ -18,6 +18,19 @@
  * Threads: matrices are immutable after construction and safe for
  * concurrent use from any thread (internal/cq/matrix.go:22-24). Host-slice
  * calls run on a per-thread stream with per-thread staging buffers.
+ *
+ * Workspaces: the table and split forms of a batched product keep tables
+ * or float terms in device memory between their two launches. They lease
+ * it from one pool per process for the length of the call and return it
+ * with an event behind their launches; a workspace is reused at once on the
+ * stream that last used it, on another stream only once that work has
+ * completed. Products queued at the same time on several streams, from one
+ * thread or many, therefore never share one. A product queued while its
+ * stream is captured into a graph gets a workspace that only its capture
+ * sequence uses and that is held until the process ends (the graph replays
+ * it at that address); such a first product of a shape may itself be
+ * captured. cq_workspace_held and cq_workspace_trim report and release the
+ * pool's memory.
  */
 #ifndef CQHIP_H
 #define CQHIP_H
@@ -104,6 +117,13 @@ int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, v
  * or "nibble4". */
 const char *cq_gemm_path(const cq_matrix *m, int rows);
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream);
+/* Bytes of device memory the workspace pool holds on every device (leased,
+ * idle and held for graphs). No reference counterpart (the Go code's
+ * scratch comes from a sync.Pool, internal/cq/kernel.go:59-74). */
+long long cq_workspace_held(void);
+/* Frees the idle workspaces whose work has completed, on every device;
+ * returns the bytes still held. No reference counterpart. */
+long long cq_workspace_trim(void);
 /* cq_gemms_dev with the decode step's neighbours fused into the product
  * (no reference counterpart: one launch instead of three, results bit for
  * bit those of the separate steps). norm_gain non-null: every input row is

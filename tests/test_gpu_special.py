@@ -177,6 +177,48 @@ def test_gemv_and_mfma_nan_inf():
         assert same_nan(yl.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("form", ["tab2", "tab4", "split"])
+def test_batched_forms_nan_inf_prologues(form):
+    # NaN and +-Inf activations through the table form (2 and 4 bits) and
+    # the split form, plain, behind the fused ZCRMSNorm prologue and behind
+    # the gated input: each activation holding one gives NaN rows (Go's max
+    # keeps the NaN bound, lut.go:239-282; the norm's and the gate's NaN
+    # reach the bound the same way), the others the oracle's bits
+    import torch
+
+    if form == "split":
+        out, inp, bits, rows = 512, 2048, 4, 1024
+        path = "lut-mfma-split"
+    else:
+        out, inp, bits, rows = 2048, 512, int(form[-1]), 400
+        path = "lut-mfma-tab"
+    g = synth.rng(60 + len(form) + bits)
+    p = synth.random_packed(g, out, inp, 128, bits, sigma=0.05)
+    m, om = cq.New(p), orc.OMatrix.new(p)
+    assert m.gemm_path(rows) == path
+    x = _special_rows(g, rows, inp, every=7)
+    gain = (1 + g.standard_normal(inp) * 0.1).astype(np.float32)
+    gate = (g.standard_normal((rows, inp)) * 2).astype(np.float32)
+    gate[3, 11], gate[10, 0] = NAN, -INF  # rows 3 and 10 hold no special x
+    xd, gd = _t(x), _t(gate)
+    y = torch.zeros(rows, out, device="cuda")
+    m.gemm_dev(y, xd, rows)
+    torch.cuda.synchronize()
+    want = om.gemm(x.reshape(-1), rows).reshape(rows, out)
+    assert np.isnan(want[0]).all() and np.isfinite(want[1]).all()
+    assert same_nan(y.cpu().numpy(), want)
+    cq.gemms_fused_dev([m], [y], xd, rows, norm_gain=_t(gain))
+    torch.cuda.synchronize()
+    want = om.gemm(orc.zc_rmsnorm(x.reshape(-1), gain, inp), rows).reshape(rows, out)
+    assert same_nan(y.cpu().numpy(), want)
+    cq.gemms_gated_dev([m], [y], xd, gd, rows)
+    torch.cuda.synchronize()
+    xs, _ = orc.sigmoid_gate(x.reshape(-1), gate.reshape(-1))
+    want = om.gemm(xs, rows).reshape(rows, out)
+    assert np.isnan(want[3]).all()
+    assert same_nan(y.cpu().numpy(), want)
+
+
 def _attend(q, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, spans, nk, quant_q, batch, kv_stride, s_stride):
     import torch
 

@@ -70,6 +70,16 @@ def test_tab_path_bounds():
     mh = cq.New(synth.random_packed(g, 16384, 512, 128, 4, sigma=0.05))
     assert mh.gemm_path(15) == "lut" and mh.gemm_path(16) == "lut-mfma-tab"
     assert cq.New(synth.random_packed(g, 2048, 2048, 128, 2, sigma=0.05)).gemm_path(256) == "lut"
+    # small matrices past 3072 activations: the table form at 2 bits (64x512
+    # CQ2 at 3500 / 12000 activations measured 23.5 / 40.8 us against the
+    # 512-row MFMA form's 40.5 / 77.3 us) and at 4 bits up to 6144
+    # (64x512 CQ4 at 6000: 40.2 against 62.4 us); at 4 bits beyond, the
+    # MFMA form (the two measured within 1%)
+    for o in (64, 128, 256, 384):
+        s2 = cq.New(synth.random_packed(g, o, 512, 128, 2, sigma=0.05))
+        s4 = cq.New(synth.random_packed(g, o, 512, 128, 4, sigma=0.05))
+        assert s2.gemm_path(3500) == s2.gemm_path(12000) == "lut-mfma-tab"
+        assert s4.gemm_path(6000) == "lut-mfma-tab" and s4.gemm_path(12000) == "lut-mfma"
 
 
 @pytest.mark.parametrize("bits", [2, 4])
