@@ -428,10 +428,39 @@ def attention_leg(gw, torch, with_cpu, cpu_seconds):
     return res
 
 
+def _decode_rate(gw, torch, model, batch, tokens):
+    """tokens/s and ms per step of one captured step graph replayed per
+    token, from position 0."""
+    from go_whistle_amd import decoder as dec
+
+    d = dec.Decoder(model, batch)
+    d.set_memory(7, "numpy" if batch == 1 else "device")
+    first = list(range(1, batch + 1))
+    d.reset(first)
+    g = d.capture()
+    for _ in range(3):
+        g.replay()
+    d.reset(first)
+    d._reserve(tokens)  # the caches and RoPE tables hold max_pos positions
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(tokens):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    return d, g, {"tokens_per_s": round(batch * tokens / ms * 1e3, 1), "ms_per_step": round(ms / tokens, 4)}
+
+
 def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
     """Greedy decode of the synthetic 8-layer decoder (d 512, 8 heads, FFN
     2048, vocab 16384, 1500-frame int8 cross memory per stream), 200 tokens
-    at batch 1 and 256: one captured step graph replayed per token."""
+    at batch 1 and 256: one captured step graph replayed per token. Then
+    the same decoder with the reference step's features on (3 taps, q/k
+    norms, post norms and residual factors, 4 mHC lanes; the paged step),
+    and the cost of its fork at two positions (independent of the
+    position: full pages are shared)."""
     from go_whistle_amd import decoder as dec
 
     cfg = dec.DecoderConfig()
@@ -441,27 +470,34 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
                     "self/cross KV; cross memory: 1500 random encoder states through CQ4 K/V projections",
            "tokens": tokens}
     for batch in (1, 256):
-        d = dec.Decoder(model, batch)
-        d.set_memory(7, "numpy" if batch == 1 else "device")
-        first = list(range(1, batch + 1))
-        d.reset(first)
-        g = d.capture()
-        for _ in range(3):
-            g.replay()
-        d.reset(first)
-        d._reserve(tokens)  # the caches and RoPE tables hold max_pos positions
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(tokens):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1)
-        res[f"batch{batch}"] = {"tokens_per_s": round(batch * tokens / ms * 1e3, 1),
-                                "ms_per_step": round(ms / tokens, 4)}
+        d, g, res[f"batch{batch}"] = _decode_rate(gw, torch, model, batch, tokens)
         del d, g
         torch.cuda.empty_cache()
+    wcfg = dec.DecoderConfig.whistle()
+    wmodel = dec.make_model(7, wcfg)
+    wres = {"model": "the same decoder with the reference step's features: causal taps (3) on q/k/v, per-head "
+                     "q/k ZCRMSNorm before RoPE, the attention's post norm and residual factor, the cross q/k "
+                     "norms, post norm and residual factor, 4 mHC lanes (RMSUnit, CQ4 phi products on int8 "
+                     "input, Sinkhorn heads, lane mix) around every layer; paged self caches"}
+    for batch in (1, 256):
+        d, g, wres[f"batch{batch}"] = _decode_rate(gw, torch, wmodel, batch, tokens)
+        if batch == 256:  # fork cost at two positions (random parents, as a beam step reorders)
+            rng = __import__("numpy").random.default_rng(3)
+            fk = {}
+            for at in (40, 200):
+                d.reset(list(range(1, batch + 1)))
+                for _ in range(at):
+                    g.replay()
+                d.steps = at
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                d.fork(list(rng.integers(0, batch, size=batch)))
+                torch.cuda.synchronize()
+                fk[f"pos{at}"] = {"ms": round((time.perf_counter() - t0) * 1e3, 3), "page_copies": d.fork_copies}
+            wres["fork_batch256"] = fk
+        del d, g
+        torch.cuda.empty_cache()
+    res["whistle_step"] = wres
     if with_cpu:
         if ROOT not in sys.path:
             sys.path.insert(0, ROOT)
@@ -470,6 +506,9 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
         base = cpu_legs.decode_baseline(tokens, cpu_threads(), cpu_threads())
         res["cpu_baseline"] = dict(base["batch1"], host=cpu_host())
         res["cpu_baseline_batch256"] = dict(base["batch256"], host=cpu_host())
+        wb = cpu_legs.decode_baseline(tokens, cpu_threads(), cpu_threads(), cfg=wcfg)
+        wres["cpu_baseline"] = dict(wb["batch1"], host=cpu_host())
+        wres["cpu_baseline_batch256"] = dict(wb["batch256"], host=cpu_host())
     return res
 
 

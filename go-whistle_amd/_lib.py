@@ -39,6 +39,18 @@ SIGNATURES = {
     "cq_gemm_path": (c_char_p, [c_void_p, c_int]),
     "cq_gemms_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_int, c_void_p]),
     "cq_workspace_held": (c_longlong, []),
+    "kv_attend_int8_paged_dev": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p,
+                                         c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_float,
+                                         c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                         c_void_p]),
+    "nd_qkv_prep_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p,
+                                c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "nd_norm_scaled_add_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_int, c_int, c_void_p]),
+    "nd_expand_lanes_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "nd_collapse_lanes_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "kv_page_copy_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "nd_gather_rows_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_longlong, c_void_p]),
     "cq_workspace_trim": (c_longlong, []),
     "cq_row_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "cq_row_gather_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p]),

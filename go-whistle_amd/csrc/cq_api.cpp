@@ -1490,7 +1490,8 @@ static int attend_impl(float *out, long long out_stride, const float *q, long lo
                        const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
                        int v_cols, int vd, long long kv_stride, long long s_stride, const int32_t *spans, int nk_max,
                        float scale, int quant_q, int batch, const float *rope_cos, const float *rope_sin,
-                       const int32_t *qpos, const int32_t *kv_index, int kv_streams, void *stream) {
+                       const int32_t *qpos, const int32_t *kv_index, int kv_streams, void *stream,
+                       const int32_t *pages = nullptr, int page_stride = 0, int page_rows = 0, int pool_pages = 0) {
     if (rope_cos && (!rope_sin || !qpos || qk % 2 != 0))
         return fail(CQ_ERR_MISUSE, "needle: RoPE of query heads of %d", qk);
     if (kv_index && kv_streams < 0) return fail(CQ_ERR_MISUSE, "needle: %d shared caches", kv_streams);
@@ -1514,9 +1515,19 @@ static int attend_impl(float *out, long long out_stride, const float *q, long lo
     const int fit = static_cast<int>(96 * 1024 / vd);
     const int vchunk = (wgs <= 2LL * device_info().cus && nk_max <= fit) ? std::max(1, nk_max) : std::min(256, fit / 2);
     const int resident = wgs <= 2LL * device_info().cus ? 1 : 0;
+    int page_shift = 0;
+    if (pages) {
+        if (kv_index) return fail(CQ_ERR_MISUSE, "needle: paged caches with a shared-cache index");
+        if (page_rows <= 0 || (page_rows & (page_rows - 1)) != 0 ||
+            static_cast<long long>(page_stride) * page_rows < nk_max || pool_pages <= 0)
+            return fail(CQ_ERR_MISUSE, "needle: %d pages of %d rows for %d keys (pool %d)", page_stride, page_rows,
+                        nk_max, pool_pages);
+        while ((1 << page_shift) < page_rows) ++page_shift;
+        kv_stride = s_stride = 0;  // the page table gives every row
+    }
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,
                  kv_stride, s_stride, spans, nk_max, vchunk, resident, scale, quant_q, batch,
-                 rope_cos, rope_sin, qpos, kv_index, kv_streams};
+                 rope_cos, rope_sin, qpos, kv_index, kv_streams, pages, page_stride, page_shift, pool_pages};
     HIP_TRY(launch_attend_int8(a, static_cast<hipStream_t>(stream)), "attend launch");
     return CQ_OK;
 }
@@ -1549,6 +1560,78 @@ int kv_attend_int8_rope_dev(float *out, long long out_stride, const float *q, lo
     if (!cos_t) return fail(CQ_ERR_MISUSE, "needle: RoPE tables missing");
     return attend_impl(out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, kv_stride,
                        s_stride, spans, nk_max, scale, quant_q, batch, cos_t, sin_t, qpos, nullptr, 0, stream);
+}
+
+int kv_attend_int8_paged_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                             const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                             int v_cols, int vd, const int32_t *spans, int nk_max, float scale, int quant_q, int batch,
+                             const float *cos_t, const float *sin_t, const int32_t *qpos, const int32_t *pages,
+                             int page_stride, int page_rows, int pool_pages, void *stream) {
+    if (!pages && static_cast<long long>(t) * heads * batch > 0)
+        return fail(CQ_ERR_MISUSE, "needle: paged caches without a page table");
+    if (cos_t && (!sin_t || !qpos)) return fail(CQ_ERR_MISUSE, "needle: RoPE tables missing");
+    return attend_impl(out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd, 0, 0, spans,
+                       nk_max, scale, quant_q, batch, cos_t, sin_t, qpos, nullptr, 0, stream, pages, page_stride,
+                       page_rows, pool_pages);
+}
+
+int nd_qkv_prep_dev(float *q, const float *k, const float *v, int batch, int dim, float *hist, const float *taps_w,
+                    int taps, const float *q_gain, const float *k_gain, const float *cos_t, const float *sin_t,
+                    int positions, const int32_t *pos, int cap, int8_t *kq, float *ks, int8_t *vq, float *vs,
+                    const int32_t *pages, int page_stride, int page_rows, int pool_pages, void *stream) {
+    if (batch < 0 || dim <= 0 || dim % 64 != 0 || dim > 1024 || taps < 0 || cap < 0)
+        return fail(CQ_ERR_MISUSE, "needle: q/k/v of %d rows of %d with %d taps", batch, dim, taps);
+    if (batch == 0) return CQ_OK;
+    if (!q || !k || !v || !pos || !kq || !ks || !vq || !vs || !pages || (taps > 0 && !taps_w) ||
+        (taps > 1 && !hist) || (cos_t && !sin_t))
+        return fail(CQ_ERR_MISUSE, "needle: q/k/v preparation with a nil operand");
+    if (page_rows <= 0 || (page_rows & (page_rows - 1)) != 0 || static_cast<long long>(page_stride) * page_rows < cap ||
+        pool_pages <= 0)
+        return fail(CQ_ERR_MISUSE, "needle: %d pages of %d rows for %d positions (pool %d)", page_stride, page_rows,
+                    cap, pool_pages);
+    int shift = 0;
+    while ((1 << shift) < page_rows) ++shift;
+    PrepArgs a{q, k, v, hist, taps_w, taps, q_gain, k_gain, cos_t, sin_t, positions, pos, cap, kq, vq, ks, vs,
+               pages, page_stride, shift, pool_pages, dim};
+    HIP_TRY(launch_qkv_prep(a, batch, static_cast<hipStream_t>(stream)), "q/k/v preparation launch");
+    return CQ_OK;
+}
+
+int nd_norm_scaled_add_dev(float *h, const float *y, const float *gain, float scale, int rows, int dim, void *stream) {
+    if (rows < 0 || dim <= 0 || dim > 8192) return fail(CQ_ERR_MISUSE, "needle: %d rows of %d", rows, dim);
+    if (rows > 0 && (!h || !y || !gain)) return fail(CQ_ERR_MISUSE, "needle: post norm with a nil operand");
+    HIP_TRY(launch_norm_scaled_add(h, y, gain, scale, rows, dim, static_cast<hipStream_t>(stream)), "post norm launch");
+    return CQ_OK;
+}
+
+int nd_expand_lanes_dev(float *stream_rows, const float *x, int rows, int lanes, int dim, void *stream) {
+    if (rows < 0 || lanes <= 0 || dim <= 0) return fail(CQ_ERR_MISUSE, "needle: %d rows of %d lanes x %d", rows, lanes, dim);
+    HIP_TRY(launch_expand_lanes(stream_rows, x, rows, lanes, dim, static_cast<hipStream_t>(stream)), "lanes launch");
+    return CQ_OK;
+}
+
+int nd_collapse_lanes_dev(float *x, const float *stream_rows, int rows, int lanes, int dim, void *stream) {
+    if (rows < 0 || lanes <= 0 || dim <= 0) return fail(CQ_ERR_MISUSE, "needle: %d rows of %d lanes x %d", rows, lanes, dim);
+    HIP_TRY(launch_collapse_lanes(x, stream_rows, rows, lanes, dim, static_cast<hipStream_t>(stream)), "lanes launch");
+    return CQ_OK;
+}
+
+int kv_page_copy_dev(int8_t *q, float *s, const int32_t *src, const int32_t *dst, int n, int page_rows, int cols,
+                     int width, int pool_pages, void *stream) {
+    if (n < 0 || page_rows <= 0 || cols <= 0 || width <= 0 || cols % width != 0)
+        return fail(CQ_ERR_MISUSE, "needle: %d pages of %d rows of %d in heads of %d", n, page_rows, cols, width);
+    if (n > 0 && (!q || !s || !src || !dst)) return fail(CQ_ERR_MISUSE, "needle: page copy with a nil operand");
+    HIP_TRY(launch_page_copy(q, s, src, dst, n, page_rows, cols, cols / width, pool_pages,
+                             static_cast<hipStream_t>(stream)),
+            "page copy launch");
+    return CQ_OK;
+}
+
+int nd_gather_rows_dev(float *dst, const float *src, const int32_t *idx, int rows, long long width, void *stream) {
+    if (rows < 0 || width < 0) return fail(CQ_ERR_MISUSE, "needle: gather of %d rows of %lld", rows, width);
+    if (rows > 0 && width > 0 && (!dst || !src)) return fail(CQ_ERR_MISUSE, "needle: gather with a nil operand");
+    HIP_TRY(launch_gather_float_rows(dst, src, idx, rows, width, static_cast<hipStream_t>(stream)), "gather launch");
+    return CQ_OK;
 }
 
 // ---- decode-step float blocks -------------------------------------------------

@@ -229,6 +229,14 @@ struct AttendArgs {
     // untouched.
     const int32_t *kv_index;
     int kv_streams;
+    // Paged caches (null: none; kv_stride and s_stride are then 0): key j of
+    // stream b is row pages[b * page_stride + (j >> page_shift)] *
+    // 2^page_shift + (j & (2^page_shift - 1)) of the arrays, which are one
+    // pool of pool_pages pages shared by every stream (a forked stream reads
+    // its parent's full pages through its own table). An entry outside the
+    // pool reads page 0.
+    const int32_t *pages;
+    int page_stride, page_shift, pool_pages;
 };
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream);
 
@@ -238,6 +246,15 @@ __device__ __forceinline__ long long attend_cache_of(const AttendArgs &a, int b)
     if (!a.kv_index) return b;
     const int c = a.kv_index[b];
     return (c >= 0 && c < a.kv_streams) ? c : -1;
+}
+
+// The array row that holds key `key` of stream b: through the page table,
+// or row `key` of the stream's own cache.
+__device__ __forceinline__ long long attend_row(const AttendArgs &a, int b, int key) {
+    if (!a.pages) return key;
+    long long pg = a.pages[static_cast<long long>(b) * a.page_stride + (key >> a.page_shift)];
+    if (pg < 0 || pg >= a.pool_pages) pg = 0;
+    return (pg << a.page_shift) + (key & ((1 << a.page_shift) - 1));
 }
 
 // HadamardMLP, Whistle's Monarch FFN (hadamard_kernels.hip): rows of dim
@@ -280,5 +297,42 @@ hipError_t launch_sigmoid_gate(float *out, float *gate, long long n, hipStream_t
 hipError_t launch_append(int8_t *q, float *sc, const float *x, int batch, int cols, int width, long long q_stride,
                          long long s_stride, const int32_t *pos, int cap, const float *cos_t, const float *sin_t,
                          hipStream_t s);
+
+// The decode step's features around the products (layer_kernels.hip).
+// qkv_prep: for each stream b, the q, k, v rows of one token (dim values,
+// heads of 64) at position pos[b]: the causal taps (taps_w [3][taps][dim]
+// over hist [batch][taps][3][dim], the raw rows by position mod taps),
+// the per-head ZCRMSNorm of q and k (gains qg, kg of 64; null: none), RoPE
+// of k at pos[b] (tables of 32 per row, `positions` rows; null: none), and
+// the int8 appends of k and v at row pos[b] (< cap) of each stream's pages
+// (pages[b * page_stride + pos >> page_shift], pages of 2^page_shift rows of
+// dim codes and dim/64 scales; an entry outside [0, pool_pages) skips the
+// append). q is written back in place.
+struct PrepArgs {
+    float *q;
+    const float *k, *v;
+    float *hist;
+    const float *taps_w;
+    int taps;
+    const float *qg, *kg;
+    const float *cos_t, *sin_t;
+    int positions;
+    const int32_t *pos;
+    int cap;
+    int8_t *kq, *vq;
+    float *ks, *vs;
+    const int32_t *pages;
+    int page_stride, page_shift, pool_pages;
+    int dim;
+};
+hipError_t launch_qkv_prep(const PrepArgs &a, int batch, hipStream_t s);
+hipError_t launch_norm_scaled_add(float *h, const float *y, const float *gain, float sc, int rows, int dim,
+                                  hipStream_t s);
+hipError_t launch_expand_lanes(float *stream, const float *x, int rows, int lanes, int dim, hipStream_t s);
+hipError_t launch_collapse_lanes(float *x, const float *stream, int rows, int lanes, int dim, hipStream_t s);
+hipError_t launch_page_copy(int8_t *q, float *sc, const int32_t *src, const int32_t *dst, int n, int page_rows,
+                            int cols, int heads, int pool_pages, hipStream_t s);
+hipError_t launch_gather_float_rows(float *dst, const float *src, const int32_t *idx, int rows, long long width,
+                                    hipStream_t s);
 
 }  // namespace cqhip

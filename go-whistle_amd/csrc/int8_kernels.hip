@@ -192,7 +192,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
                 for (int u = 0; u < 8; ++u) {
                     const int e = min(e0 + u * nt, total - 1);
                     const int jj = e / per, part = e - (e / per) * per;
-                    w[u] = *reinterpret_cast<const int4 *>(vq + static_cast<long long>(key_of(j0 + jj)) * a.v_cols +
+                    w[u] = *reinterpret_cast<const int4 *>(vq + attend_row(a, b, key_of(j0 + jj)) * a.v_cols +
                                                            kv * a.vd + part * 16);
                 }
 #pragma unroll
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         } else {
             for (int e = t0; e < cnt * a.vd; e += nt) {
                 const int jj = e / a.vd, d = e - (e / a.vd) * a.vd;
-                buf[jj * a.vd + d] = vq[static_cast<long long>(key_of(j0 + jj)) * a.v_cols + kv * a.vd + d];
+                buf[jj * a.vd + d] = vq[attend_row(a, b, key_of(j0 + jj)) * a.v_cols + kv * a.vd + d];
             }
         }
     };
@@ -217,8 +217,8 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     // a time so that their loads are in flight together.
     auto logit = [&](int j) -> float {
         const int key = key_of(j);
-        const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
-        const float sk = ks[static_cast<long long>(key) * kv_heads + kv];
+        const int8_t *krow = kq + attend_row(a, b, key) * a.k_cols + kv * a.qk;
+        const float sk = ks[attend_row(a, b, key) * kv_heads + kv];
         if (a.quant_q) {
             int dot = 0;  // exact in any order
             if (wide) {
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const float sum = sum_sh;
     for (int j = tid; j < n; j += kAttThreads) {
         const float p = s[j] / sum;
-        s[j] = p * vs[static_cast<long long>(key_of(j)) * kv_heads + kv];
+        s[j] = p * vs[attend_row(a, b, key_of(j)) * kv_heads + kv];
     }
 
     // 3. axpysI8 per output, keys in order: the first ceil(vd/64)
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
             const int p = u * 64 + lane;
             const int seg = p / G::kJC, jj = p - seg * G::kJC;
             const int key = key_of(j0 + (jj < cnt ? jj : 0));
-            dma16(vq + static_cast<long long>(key) * a.v_cols + kv * VD + seg * 16, lds_offset(slot + u * 64 * 16));
+            dma16(vq + attend_row(a, b, key) * a.v_cols + kv * VD + seg * 16, lds_offset(slot + u * 64 * 16));
         }
     };
 
@@ -507,12 +507,12 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
     float skr[KPT], vsr[KPT];
     auto kload = [&](int g, int j) {
         const int key = key_of(j);
-        const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
+        const int8_t *krow = kq + attend_row(a, b, key) * a.k_cols + kv * a.qk;
 #pragma unroll
         for (int p = 0; p < kStreamQk / 16; ++p)
             if (p < kpieces) kw[g][p] = *reinterpret_cast<const int4 *>(krow + 16 * p);
-        skr[g] = ks[static_cast<long long>(key) * kv_heads + kv];
-        vsr[g] = vs[static_cast<long long>(key) * kv_heads + kv];
+        skr[g] = ks[attend_row(a, b, key) * kv_heads + kv];
+        vsr[g] = vs[attend_row(a, b, key) * kv_heads + kv];
     };
     auto logit = [&](int g) -> float {
         if (a.quant_q) {
@@ -835,7 +835,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
         const int p = u * 64 + lane;
         const int jj = p >> 2, seg = p & 3;
         const int key = key_of(j0 + (jj < cnt ? jj : 0));
-        dma16(vq + static_cast<long long>(key) * a.v_cols + kv * kChainVd + seg * 16, lds_offset(slot + u * 64 * 16));
+        dma16(vq + attend_row(a, b, key) * a.v_cols + kv * kChainVd + seg * 16, lds_offset(slot + u * 64 * 16));
     };
 
     // 1. The query, then each thread's first KPT keys, in flight together.
@@ -846,12 +846,12 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     float skr[KPT], svr[KPT];  // key scales; value scales (kept when one round covers every key)
     auto kload = [&](int g, int j) {
         const int key = key_of(j);
-        const int8_t *krow = kq + static_cast<long long>(key) * a.k_cols + kv * a.qk;
+        const int8_t *krow = kq + attend_row(a, b, key) * a.k_cols + kv * a.qk;
 #pragma unroll
         for (int p = 0; p < kStreamQk / 16; ++p)
             if (p < kpieces) kw[g][p] = *reinterpret_cast<const int4 *>(krow + 16 * p);
-        skr[g] = ks[static_cast<long long>(key) * kv_heads + kv];
-        svr[g] = vs[static_cast<long long>(key) * kv_heads + kv];
+        skr[g] = ks[attend_row(a, b, key) * kv_heads + kv];
+        svr[g] = vs[attend_row(a, b, key) * kv_heads + kv];
     };
     auto logit = [&](int g) -> float {
         if (a.quant_q) {
@@ -990,7 +990,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     } else {
         for (int j = tid; j < n; j += NT) {
             const float p = s[j] / sum;
-            s[j] = p * vs[static_cast<long long>(key_of(j)) * kv_heads + kv];
+            s[j] = p * vs[attend_row(a, b, key_of(j)) * kv_heads + kv];
         }
     }
     if constexpr (RES) {
@@ -1224,11 +1224,11 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
             const int p = u * 64 + lane;
             const int jj = p >> 2, seg = p & 3;
             const int key = key_of(j0 + (jj < cnt ? jj : 0));
-            dma16(base + static_cast<long long>(key) * cols + seg * 16, lds_offset(slot + u * 64 * 16));
+            dma16(base + attend_row(a, b, key) * cols + seg * 16, lds_offset(slot + u * 64 * 16));
         }
         const float *sc = keys ? ks : vs;
         const int key = key_of(j0 + (lane < cnt ? lane : 0));
-        if (lane < JC) dma4(sc + static_cast<long long>(key) * kv_heads + kv, lds_offset(slot + JC * ROW));
+        if (lane < JC) dma4(sc + attend_row(a, b, key) * kv_heads + kv, lds_offset(slot + JC * ROW));
     };
     // Chunk g has landed: at most the chunks issued after it are in flight.
     auto wait_chunk = [&](int g) {

@@ -59,9 +59,26 @@ class DecoderConfig:
     ffn_bits: int = 2
     group: int = 128
     theta: float = 1e5
+    # The reference decode step's features (each off by default):
+    taps: int = 0             # causal taps on the raw q/k/v (Whistle: 3; cache.go:143-154)
+    qk_norm: bool = False     # per-head q/k ZCRMSNorm before RoPE (attention.go:298-330)
+    post_norm: bool = False   # the attention's post norm, h += float32(gate * a) (block.go:183-188)
+    cross_norm: bool = False  # cross q/k norms, post norm, residual factor (cross.go:181-264)
+    lanes: int = 0            # mHC lanes around each layer (Whistle: 4; mhc.go:182-299)
+
+    @staticmethod
+    def whistle(**kw):
+        """Every feature of Whistle's decode step on: 3 taps, the q/k norms,
+        both post norms and residual factors, 4 mHC lanes."""
+        return DecoderConfig(taps=3, qk_norm=True, post_norm=True, cross_norm=True, lanes=4, **kw)
+
+    @property
+    def features(self):
+        return bool(self.taps or self.qk_norm or self.post_norm or self.cross_norm or self.lanes)
 
 
 LAYER_MATS = ("wq", "wk", "wv", "wg", "wo", "wcq", "wcg", "wco", "wck", "wcv", "w1", "w2")
+PHI_MATS = ("phi_pre", "phi_post", "phi_res")
 
 
 @dataclass
@@ -73,6 +90,13 @@ class Model:
     rope_cos: np.ndarray
     rope_sin: np.ndarray
     scale: np.float32 = field(default=np.float32(0))
+    # the decode step's features (present whatever the configuration enables)
+    qk_gains: np.ndarray = None    # [layers, 4, head_dim]: self q, self k, cross q, cross k (ZCRMSNorm gains)
+    post_gains: np.ndarray = None  # [layers, 2, dim]: the self and cross post norms
+    res_scale: np.ndarray = None   # [layers, 2]: sigmoid(attn_gate), sigmoid(cross_gate) as loaded
+    taps_w: np.ndarray = None      # [layers, 3, taps, dim]: q, k, v taps
+    mhc_affine: np.ndarray = None  # [layers, 3 + 4 lanes + lanes^2]: a_pre, a_post, a_res, b_pre, pre_off,
+    #                                b_post, post_off, b_res
 
 
 def _share(p, cb):
@@ -132,13 +156,93 @@ def make_model(seed, cfg=DecoderConfig()):
     cos, sin = rope_tables(cfg.head_dim, cfg.max_pos, cfg.theta)
     # The unscaled input (Whistle's InputScale off, decoder.go:322-326): with
     # sqrt(d), a random tied embedding makes every token its own argmax.
-    return Model(cfg=cfg, emb=emb, layers=layers, gains=gains, rope_cos=cos, rope_sin=sin, scale=np.float32(1))
+    model = Model(cfg=cfg, emb=emb, layers=layers, gains=gains, rope_cos=cos, rope_sin=sin, scale=np.float32(1))
+    _feature_weights(model, seed, cb4)
+    return model
+
+
+def lane_offsets(n, layer):
+    """laneOffsets (internal/needle/mhc.go:122-135): the layer's own lane
+    gets pre +4 and post 0, the others -4 and -4."""
+    pre, post = np.full(n, -4, np.float32), np.full(n, -4, np.float32)
+    pre[layer % n], post[layer % n] = 4, 0
+    return pre, post
+
+
+def _feature_weights(model, seed, cb4):
+    """The weights of the decode step's features, from their own seeded
+    stream (the base model's draws stay as they are): ZCRMSNorm gains 1 +
+    N(0, 0.1), residual factors in (0.2, 0.8), taps 1 + N(0, 0.1) at the
+    current position and N(0, 0.3) before it, and per layer the three mHC
+    phi products (CQ4 of lanes x lanes*dim, lanes x lanes*dim, lanes^2 x
+    lanes*dim on the attention codebook) with affine maps a = 0.5 + U(0, 0.5),
+    b ~ N(0, 0.5) and the lane offsets."""
+    cfg = model.cfg
+    g = synth.rng(seed * 7919 + 17)
+    L, D, hd = cfg.layers, cfg.dim, cfg.head_dim
+    nt, n = max(cfg.taps, 1), max(cfg.lanes, 1)
+    model.qk_gains = (1 + g.standard_normal((L, 4, hd)) * 0.1).astype(np.float32)
+    model.post_gains = (1 + g.standard_normal((L, 2, D)) * 0.1).astype(np.float32)
+    model.res_scale = g.uniform(0.2, 0.8, (L, 2)).astype(np.float32)
+    tw = (g.standard_normal((L, 3, nt, D)) * 0.3).astype(np.float32)
+    tw[:, :, 0] = (1 + g.standard_normal((L, 3, D)) * 0.1).astype(np.float32)
+    model.taps_w = tw
+    aff = np.zeros((L, 3 + 4 * n + n * n), np.float32)
+    for l in range(L):
+        pre, post = lane_offsets(n, l)
+        aff[l, :3] = 0.5 + g.uniform(0, 0.5, 3)
+        aff[l, 3:3 + n] = g.standard_normal(n) * 0.5
+        aff[l, 3 + n:3 + 2 * n] = pre
+        aff[l, 3 + 2 * n:3 + 3 * n] = g.standard_normal(n) * 0.5
+        aff[l, 3 + 3 * n:3 + 4 * n] = post
+        aff[l, 3 + 4 * n:] = g.standard_normal(n * n) * 0.5
+    model.mhc_affine = aff
+    if cfg.lanes:
+        for l in range(L):
+            for name, out in zip(PHI_MATS, (n, n, n * n)):
+                p = synth.random_packed(g, out, n * D, cfg.group, 4, sigma=0.05)
+                groups = (n * D + cfg.group - 1) // cfg.group
+                exp = g.integers(12, 16, size=out * groups).astype(np.uint16)
+                man = g.integers(0, 1024, size=out * groups).astype(np.uint16)
+                p.Norms = ((exp << 10) | man).astype("<u2").view(np.uint8)
+                model.layers[l][name] = _share(p, cb4)
 
 
 def encoder_states(seed, cfg, stream):
     """One stream's encoder output, N(0, 1), [frames, dim]."""
     g = synth.rng(seed * 1000003 + stream)
     return g.standard_normal(cfg.frames * cfg.dim).astype(np.float32)
+
+
+def fork_page_tables(pt, parents, pos, page_rows, pool_pages):
+    """The page tables after stream b takes stream parents[b]'s state at
+    position pos[b] (KVCache.Fork, internal/needle/cache.go:62-67: the rows
+    so far are shared until one side appends). pt is [streams, pages per
+    stream] of pool pages. Every stream starts from its parent's table; the
+    pages from the one its next append writes on (pos // page_rows) onward
+    must be its own, so each of them that another entry still references is
+    replaced by a free pool page, and the partly filled one (pos not on a
+    page boundary) is copied first. Returns (tables, [(from, to)] page
+    copies). With one page row per stream's position there are at most
+    len(parents) copies, whatever the positions; the pool needs no more
+    pages than streams x pages per stream."""
+    pt = np.asarray(pt, np.int32)[np.asarray(parents, np.int64)].copy()
+    streams, per = pt.shape
+    counts = np.bincount(pt.ravel(), minlength=pool_pages)
+    free = list(np.flatnonzero(counts == 0)[::-1])
+    copies = []
+    for b in range(streams):
+        lp0 = min(int(pos[b]) // page_rows, per)
+        for lp in range(lp0, per):
+            ph = int(pt[b, lp])
+            if counts[ph] > 1:
+                nf = int(free.pop())
+                counts[ph] -= 1
+                counts[nf] += 1
+                pt[b, lp] = nf
+                if lp == lp0 and pos[b] % page_rows:
+                    copies.append((ph, nf))
+    return pt, copies
 
 
 def _ptr(t):
@@ -153,13 +257,21 @@ class Decoder:
     appends ride in the products and the attention (8 launches per layer
     instead of 21, the same bits)."""
 
-    def __init__(self, model, batch, device="cuda", fused=True):
+    PAGE_ROWS = 16  # rows per page of the paged self caches
+
+    def __init__(self, model, batch, device="cuda", fused=True, paged=None):
         import torch
 
         self.model, self.cfg, self.batch, self.fused = model, model.cfg, batch, fused
         c, B = model.cfg, batch
+        # The paged step: the decode-step features and self caches read
+        # through per-stream page tables, so that a fork shares the rows so
+        # far (the default whenever a feature is on).
+        self.paged = c.features if paged is None else bool(paged)
+        if self.paged and (c.head_dim != 64 or c.max_pos % self.PAGE_ROWS != 0):
+            raise ValueError("the paged step runs heads of 64 and max_pos a multiple of 16")
         self.emb = cq.New(model.emb)
-        self.mats = [{n: cq.New(p[n]) for n in LAYER_MATS} for p in model.layers]
+        self.mats = [{n: cq.New(p[n]) for n in p} for p in model.layers]
         f32, i8, i32 = torch.float32, torch.int8, torch.int32
         z = lambda *shape, dt=f32: torch.zeros(*shape, dtype=dt, device=device)
         self.gains = torch.from_numpy(model.gains).to(device)
@@ -200,6 +312,35 @@ class Decoder:
         self.cross_ks = [z(B, hk, c.frames) for _ in range(c.layers)]
         self.cross_v = [z(B, hk, c.frames, c.head_dim, dt=i8) for _ in range(c.layers)]
         self.cross_vs = [z(B, hk, c.frames) for _ in range(c.layers)]
+        if self.paged:
+            self._init_paged(torch, z)
+
+    def _init_paged(self, torch, z):
+        """The paged step's state: the page tables (identity: stream b's
+        logical page j is pool page b * pages_per_stream + j, the same layout
+        as the unpaged caches), the tap histories, the feature weights and
+        the mHC buffers."""
+        c, B, m = self.cfg, self.batch, self.model
+        f32 = torch.float32
+        dev = self.x.device
+        self.page_stride = c.max_pos // self.PAGE_ROWS
+        self.pool_pages = B * self.page_stride
+        self.pt = np.arange(self.pool_pages, dtype=np.int32).reshape(B, self.page_stride)
+        self.pages = torch.from_numpy(self.pt.copy()).to(dev)
+        # the tap history: a ring of taps slots per stream, [batch][taps][3][dim]
+        self.hist = [z(B, c.taps, 3, c.dim) for _ in range(c.layers)] if c.taps > 1 else None
+        dv = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+        self.qk_gains, self.post_gains = dv(m.qk_gains), dv(m.post_gains)
+        self.taps_w, self.mhc_affine = dv(m.taps_w), dv(m.mhc_affine)
+        self.res_scale = np.asarray(m.res_scale, np.float32)
+        self.o = z(B, c.dim)
+        if c.lanes:
+            n = c.lanes
+            self.lane_s = [z(B, n * c.dim), z(B, n * c.dim)]
+            self.nx, self.nxq = z(B, n * c.dim), z(B, n * c.dim)
+            self.pl, self.ql, self.rl = z(B, n), z(B, n), z(B, n * n)
+            self.hp, self.hq, self.hr = z(B, n), z(B, n), z(B, n * n)
+            self.u_mhc, self.blk = z(B, c.dim), z(B, c.dim)
 
     def set_memory(self, seed, generator="numpy"):
         """Builds each stream's int8 cross memory from its encoder states
@@ -224,6 +365,9 @@ class Decoder:
                 m = self.mats[layer]
                 cq.gemms_dev([m["wck"], m["wcv"]], [tmp_k, tmp_v], enc, c.frames)
                 hk = c.dim // c.head_dim
+                if c.cross_norm:  # the memory keys' per-head norm (cross.go:186-188)
+                    check(lib().nd_zcrmsnorm_dev(_ptr(tmp_k), _ptr(tmp_k), _ptr(self.qk_gains[layer, 3]),
+                                                 c.frames * hk, c.head_dim, cq._stream()))
                 for tmp, dq, ds in ((tmp_k, self.cross_k[layer][b], self.cross_ks[layer][b]),
                                     (tmp_v, self.cross_v[layer][b], self.cross_vs[layer][b])):
                     # head-major rows of one head each: QuantizeRow per 64-wide chunk, as on the key-major rows
@@ -251,6 +395,9 @@ class Decoder:
         self.done.zero_()
         self._sync_spans()
         self.steps = 0
+        if self.paged:
+            self.pt = np.arange(self.pool_pages, dtype=np.int32).reshape(self.batch, self.page_stride)
+            self.pages.copy_(torch.from_numpy(self.pt.copy()))
 
     def _sync_spans(self):
         """The self-attention key bound of the next step, pos + 1 (the step
@@ -295,7 +442,9 @@ class Decoder:
         """One greedy token for every stream: reads tok and pos, writes the
         next token to tok and advances pos (and the key bound pos + 1)."""
         self._reserve(1)
-        if self.fused:
+        if self.paged:
+            self._step_paged()
+        elif self.fused:
             self._step_fused()
         else:
             self._step_plain()
@@ -378,6 +527,106 @@ class Decoder:
         self.emb.gemm_dev(self.logits, self.h, B)
         self._advance(s)
 
+    def _step_paged(self):
+        """One token with the reference step's features (each per the
+        configuration): the layer of decoder.go:446-505 (Block.run with the
+        cross branch after the attention, block.go:147-215) inside the mHC
+        lanes (mhc.go:182-299), the self caches read and written through the
+        page tables."""
+        c, B, L = self.cfg, self.batch, lib()
+        s = cq._stream()
+        D, H, hd = c.dim, c.heads, c.head_dim
+        n = c.lanes
+        P = _ptr
+        rope = (self.cos, self.sin)
+        self.emb.row_gather_dev(self.x, self.tok, float(self.model.scale))
+        cur = None
+        if n:
+            check(L.nd_expand_lanes_dev(P(self.lane_s[0]), P(self.x), B, n, D, s))
+            cur, nxt = self.lane_s
+        for l in range(c.layers):
+            m = self.mats[l]
+            if n:  # the mHC heads and the block input u (mhc.go:196-219)
+                check(L.nd_rms_unit_dev(P(self.nx), P(cur), B, n * D, s))
+                check(L.nd_fake_quant_dev(P(self.nxq), P(self.nx), B, n * D, n * D, s))
+                cq.gemms_dev([m["phi_pre"], m["phi_post"], m["phi_res"]], [self.pl, self.ql, self.rl], self.nxq, B)
+                check(L.nd_mhc_heads_dev(P(self.hp), P(self.hq), P(self.hr), P(self.u_mhc), P(self.pl), P(self.ql),
+                                         P(self.rl), P(cur), B, n, D, P(self.mhc_affine[l]), s))
+                check(L.nd_gather_rows_dev(P(self.x), P(self.u_mhc), None, B, D, s))
+            cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.x, B,
+                               norm_gain=self.gains[3 * l])
+            qg = P(self.qk_gains[l, 0]) if c.qk_norm else None
+            kg = P(self.qk_gains[l, 1]) if c.qk_norm else None
+            hist = P(self.hist[l]) if self.hist is not None else None
+            check(L.nd_qkv_prep_dev(P(self.q), P(self.k), P(self.v), B, D, hist, P(self.taps_w[l]), c.taps, qg, kg,
+                                    P(self.cos), P(self.sin), c.max_pos, P(self.pos), c.max_pos, P(self.self_k[l]),
+                                    P(self.self_ks[l]), P(self.self_v[l]), P(self.self_vs[l]), P(self.pages),
+                                    self.page_stride, self.PAGE_ROWS, self.pool_pages, s))
+            check(L.kv_attend_int8_paged_dev(P(self.att), 0, P(self.q), 0, 1, H, P(self.self_k[l]), P(self.self_ks[l]),
+                                             D, hd, P(self.self_v[l]), P(self.self_vs[l]), D, hd, P(self.spans_self),
+                                             c.max_pos, float(np.float32(math.sqrt(hd))), 1, B, P(self.cos),
+                                             P(self.sin), P(self.pos), P(self.pages), self.page_stride,
+                                             self.PAGE_ROWS, self.pool_pages, s))
+            if c.post_norm:  # block.go:183-188
+                cq.gemms_gated_dev([m["wo"]], [self.o], self.att, self.g, B)
+                check(L.nd_norm_scaled_add_dev(P(self.x), P(self.o), P(self.post_gains[l, 0]),
+                                               float(self.res_scale[l, 0]), B, D, s))
+            else:
+                cq.gemms_gated_dev([m["wo"]], [self.x], self.att, self.g, B, resid=self.x)
+            cq.gemms_fused_dev([m["wcq"], m["wcg"]], [self.q, self.g], self.x, B, norm_gain=self.gains[3 * l + 1])
+            if c.cross_norm:  # cross.go:217-219
+                check(L.nd_zcrmsnorm_dev(P(self.q), P(self.q), P(self.qk_gains[l, 2]), B * H, hd, s))
+            self._attend(l, True, s)
+            if c.cross_norm:  # cross.go:255-263 and the hook's add
+                cq.gemms_gated_dev([m["wco"]], [self.o], self.att, self.g, B)
+                check(L.nd_norm_scaled_add_dev(P(self.x), P(self.o), P(self.post_gains[l, 1]),
+                                               float(self.res_scale[l, 1]), B, D, s))
+            else:
+                cq.gemms_gated_dev([m["wco"]], [self.x], self.att, self.g, B, resid=self.x)
+            cq.gemms_fused_dev([m["w1"]], [self.u], self.x, B, norm_gain=self.gains[3 * l + 2], act=1)
+            if n:  # the block's output, then y = out - u and the lane mix (mhc.go:221-234)
+                cq.gemms_fused_dev([m["w2"]], [self.blk], self.u, B, resid=self.x)
+                check(L.nd_mhc_mix_dev(P(nxt), P(cur), P(self.hr), P(self.hq), P(self.blk), P(self.u_mhc), B, n, D,
+                                       s))
+                cur, nxt = nxt, cur
+            else:
+                cq.gemms_fused_dev([m["w2"]], [self.x], self.u, B, resid=self.x)
+        if n:
+            check(L.nd_collapse_lanes_dev(P(self.x), P(cur), B, n, D, s))
+        cq.gemms_fused_dev([self.emb], [self.logits], self.x, B, norm_gain=self.gains[3 * c.layers])
+        self._advance(s)
+
+    def _fork_paged(self, parents, pos):
+        """The paged fork: stream b takes its parent's page table, so the
+        full pages so far are shared, never copied; every page from the one
+        the next append writes on must be the stream's own, so a shared one
+        is replaced by a free page (the partly filled one copied first, at
+        most a page of rows per stream and layer, whatever the position).
+        Then the tap histories follow the parents."""
+        import torch
+
+        c, B, R = self.cfg, self.batch, self.PAGE_ROWS
+        pt, copies = fork_page_tables(self.pt, parents, pos, R, self.pool_pages)
+        self.pt = pt
+        dev = self.x.device
+        self.pages.copy_(torch.from_numpy(pt))
+        s = cq._stream()
+        if copies:
+            cp = torch.as_tensor(np.array(copies, np.int32).T.copy(), device=dev)
+            for l in range(c.layers):
+                for q, sc in ((self.self_k[l], self.self_ks[l]), (self.self_v[l], self.self_vs[l])):
+                    check(lib().kv_page_copy_dev(_ptr(q), _ptr(sc), _ptr(cp[0]), _ptr(cp[1]), len(copies), R, c.dim,
+                                                 c.head_dim, self.pool_pages, s))
+        if self.hist is not None:
+            par = torch.as_tensor(np.asarray(parents, np.int32), device=dev)
+            width = self.hist[0][0].numel()
+            if getattr(self, "_hist_tmp", None) is None:
+                self._hist_tmp = torch.empty_like(self.hist[0])
+            for h in self.hist:
+                check(lib().nd_gather_rows_dev(_ptr(self._hist_tmp), _ptr(h), _ptr(par), B, width, s))
+                check(lib().nd_gather_rows_dev(_ptr(h), _ptr(self._hist_tmp), None, B, width, s))
+        self.fork_copies = len(copies)
+
     def fork(self, parents):
         """KVCache.Fork / State.Fork for every stream at once (cache.go:
         62-67, decoder.go:223-240), as a beam search reorders its
@@ -400,15 +649,18 @@ class Decoder:
         par = torch.as_tensor(parents.astype(np.int32), device=dev)
         self_len = self.pos.index_select(0, par.long()).to(torch.int32)
         hk = c.dim // c.head_dim
-        if getattr(self, "_fork_tmp", None) is None:
-            self._fork_tmp = (torch.empty(B * c.max_pos * c.dim, dtype=torch.int8, device=dev),
-                              torch.empty(B * c.max_pos * hk, dtype=torch.float32, device=dev))
-        tq, ts = self._fork_tmp
-        s = cq._stream()
-        for l in range(c.layers):
-            for q, sc in ((self.self_k[l], self.self_ks[l]), (self.self_v[l], self.self_vs[l])):
-                check(lib().kv_reorder_dev(_ptr(q), _ptr(sc), _ptr(tq), _ptr(ts), _ptr(par), _ptr(self_len), B,
-                                           c.max_pos, c.dim, c.head_dim, s))
+        if self.paged:
+            self._fork_paged(parents, self_len.cpu().numpy())
+        else:
+            if getattr(self, "_fork_tmp", None) is None:
+                self._fork_tmp = (torch.empty(B * c.max_pos * c.dim, dtype=torch.int8, device=dev),
+                                  torch.empty(B * c.max_pos * hk, dtype=torch.float32, device=dev))
+            tq, ts = self._fork_tmp
+            s = cq._stream()
+            for l in range(c.layers):
+                for q, sc in ((self.self_k[l], self.self_ks[l]), (self.self_v[l], self.self_vs[l])):
+                    check(lib().kv_reorder_dev(_ptr(q), _ptr(sc), _ptr(tq), _ptr(ts), _ptr(par), _ptr(self_len), B,
+                                               c.max_pos, c.dim, c.head_dim, s))
         self.mem_of = self.mem_of[parents]
         blocks = (self.mem_of[:, None] * hk + np.arange(hk)[None, :]).astype(np.int32).reshape(-1)
         self.mem_index = torch.as_tensor(blocks, device=dev)

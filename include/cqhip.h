@@ -344,6 +344,59 @@ int nd_mhc_heads_dev(float *h_pre, float *h_post, float *h_res, float *u, const 
  * + h_post[i, a] y. out must not be the stream. */
 int nd_mhc_mix_dev(float *out, const float *stream_rows, const float *h_res, const float *h_post,
                    const float *block_out, const float *u, int rows, int lanes, int dim, void *stream);
+/* AttendInt8Spans over paged int8 caches: the arrays kq/ks/vq/vs are one
+ * pool of pool_pages pages of page_rows rows (a power of two; codes k_cols /
+ * v_cols per row, scales per head), and key j of stream b is row
+ * pages[b*page_stride + j/page_rows]*page_rows + j%page_rows. Otherwise
+ * kv_attend_int8_rope_dev (cos_t null: no RoPE of the query). Forked
+ * streams share their full pages without a copy, as KVCache.Fork shares the
+ * rows so far until one side appends (internal/needle/cache.go:62-67). An
+ * entry outside [0, pool_pages) reads page 0. */
+int kv_attend_int8_paged_dev(float *out, long long out_stride, const float *q, long long q_stride, int t, int heads,
+                             const int8_t *kq, const float *ks, int k_cols, int qk, const int8_t *vq, const float *vs,
+                             int v_cols, int vd, const int32_t *spans, int nk_max, float scale, int quant_q, int batch,
+                             const float *cos_t, const float *sin_t, const int32_t *qpos, const int32_t *pages,
+                             int page_stride, int page_rows, int pool_pages, void *stream);
+/* Attention.Extend's steps between the projections and the attention for
+ * one token per stream (internal/needle/cache.go:88-125): q, k, v are batch
+ * rows of dim (heads of 64) at positions pos[b]. In order: the causal taps
+ * (taps > 0; applyTaps on extendTaps' rows, attention.go:597-613,
+ * cache.go:143-154): out = sum_j taps_w[z][j] * row(pos - j) over j <= pos,
+ * from 0 in j order, products rounded; hist [batch][taps][3][dim] holds the
+ * raw rows of the last positions at slot position mod taps and is updated
+ * (slot pos[b] mod taps, which the step does not read: running a position
+ * again gives the same result); the per-head ZCRMSNorm of q and k (q_gain / k_gain of 64; null:
+ * none; normRotate, attention.go:298-330); RoPE of k at pos[b] (cos_t null:
+ * none; tables of 32 per row, `positions` rows); then k and v quantized per
+ * head and appended at row pos[b] (< cap) through the page table (as
+ * kv_attend_int8_paged_dev reads them; an entry outside the pool skips the
+ * append). q is written back, normed and not rotated (the attention rotates
+ * it). dim a multiple of 64 up to 1024. No reference counterpart as one call. */
+int nd_qkv_prep_dev(float *q, const float *k, const float *v, int batch, int dim, float *hist, const float *taps_w,
+                    int taps, const float *q_gain, const float *k_gain, const float *cos_t, const float *sin_t,
+                    int positions, const int32_t *pos, int cap, int8_t *kq, float *ks, int8_t *vq, float *vs,
+                    const int32_t *pages, int page_stride, int page_rows, int pool_pages, void *stream);
+/* h += float32(scale * ZCRMSNorm(y)) per row of dim: the attention's post
+ * norm and residual factor, h += float32(gate * postNorm(a))
+ * (internal/needle/block.go:183-188), and the cross branch's
+ * (internal/decoder/cross.go:255-263 with the hook's add, decoder.go:461-465).
+ * y is only read. */
+int nd_norm_scaled_add_dev(float *h, const float *y, const float *gain, float scale, int rows, int dim, void *stream);
+/* ExpandLanes / CollapseLanes (internal/needle/mhc.go:137-170): each row of
+ * x to `lanes` equal lanes of the stream (rows x lanes x dim), and back as
+ * the lane mean (lanes summed in order from 0, then divided by lanes). */
+int nd_expand_lanes_dev(float *stream_rows, const float *x, int rows, int lanes, int dim, void *stream);
+int nd_collapse_lanes_dev(float *x, const float *stream_rows, int rows, int lanes, int dim, void *stream);
+/* Page dst[j] of a paged int8 cache (page_rows rows of cols codes, cols/width
+ * scales) becomes a copy of page src[j], j < n: the copy-on-write of a
+ * forked stream's partly filled page. Pairs outside [0, pool_pages) are
+ * skipped. No reference counterpart (its Fork copies on the next append). */
+int kv_page_copy_dev(int8_t *q, float *s, const int32_t *src, const int32_t *dst, int n, int page_rows, int cols,
+                     int width, int pool_pages, void *stream);
+/* dst row r = src row idx[r] (idx null: r), rows of width floats: a fork's
+ * tap history (State.Fork shares it, decoder.go:218-240). dst must not
+ * overlap src. */
+int nd_gather_rows_dev(float *dst, const float *src, const int32_t *idx, int rows, long long width, void *stream);
 /* The attention's output gate (internal/needle/attention.go:245-249):
  * gate[i] = sigmoid(gate[i]), out[i] *= gate[i], sigmoid being jax.nn.sigmoid
  * in float32 as the reference writes it, float32(1 / (1 + exp(-float64(x))))

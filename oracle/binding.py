@@ -22,6 +22,23 @@ class _Packed(Structure):
                 ("index_len", c_size_t), ("norms_len", c_size_t), ("codebook_len", c_size_t)]
 
 
+class DecModel(Structure):
+    """orc_dec_model (oracle.h)."""
+    _fields_ = [("vocab", c_int), ("dim", c_int), ("heads", c_int), ("head_dim", c_int), ("ffn", c_int),
+                ("layers", c_int), ("frames", c_int), ("max_pos", c_int), ("taps", c_int), ("qk_norm", c_int),
+                ("post_norm", c_int), ("cross_norm", c_int), ("lanes", c_int), ("scale", c_float),
+                ("emb", c_void_p), ("mats", POINTER(c_void_p)), ("gains", POINTER(c_float)),
+                ("rope_cos", POINTER(c_float)), ("rope_sin", POINTER(c_float)), ("qk_gains", POINTER(c_float)),
+                ("post_gains", POINTER(c_float)), ("res_scale", POINTER(c_float)), ("taps_w", POINTER(c_float)),
+                ("mhc_affine", POINTER(c_float))]
+
+
+class DecMemory(Structure):
+    """orc_dec_memory (oracle.h)."""
+    _fields_ = [("kq", POINTER(c_void_p)), ("ks", POINTER(c_void_p)), ("vq", POINTER(c_void_p)),
+                ("vs", POINTER(c_void_p))]
+
+
 _lib = None
 
 
@@ -85,6 +102,18 @@ def lib():
                                               POINTER(c_float), c_int, c_int, POINTER(c_int8), POINTER(c_float), c_int,
                                               c_int, c_int, POINTER(c_int32), c_float, c_int, c_int, POINTER(c_float)]),
         }
+        dm, dmem = POINTER(DecModel), POINTER(DecMemory)
+        sig.update({
+            "orc_dec_new": (c_void_p, [dm, dmem]),
+            "orc_dec_fork": (c_void_p, [c_void_p]),
+            "orc_dec_free": (None, [c_void_p]),
+            "orc_dec_len": (c_int, [c_void_p]),
+            "orc_dec_step": (c_int, [c_void_p, c_int, POINTER(c_float)]),
+            "orc_dec_greedy": (c_int, [c_void_p, c_int, c_int, c_int, POINTER(c_int32), POINTER(c_float),
+                                       POINTER(c_int)]),
+            "orc_dec_streams": (c_int, [dm, dmem, c_int, POINTER(c_int32), c_int, c_int, POINTER(c_int32),
+                                        POINTER(c_int32)]),
+        })
         for name, (res, args) in sig.items():
             f = getattr(lb, name)
             f.restype = res

@@ -163,6 +163,60 @@ void orc_mhc_heads(float *h_pre, float *h_post, float *h_res, float *u, const fl
 void orc_mhc_mix(float *out, const float *stream, const float *h_res, const float *h_post, const float *block_out,
                  const float *u, int rows, int n, int dim);                          /* mhc.go:229-299 */
 
+/* ---- the synthetic decoder's greedy decode (decode_oracle.c) ------------ */
+
+/* The matrices of a layer, in order: wq wk wv wg wo wcq wcg wco wck wcv w1
+ * w2, then (with lanes) phi_pre phi_post phi_res. */
+enum { ORC_DEC_NMATS = 15 };
+
+typedef struct {
+    int vocab, dim, heads, head_dim, ffn, layers, frames, max_pos;
+    int taps;       /* causal taps on q/k/v (0: none) */
+    int qk_norm;    /* per-head q/k ZCRMSNorm before RoPE */
+    int post_norm;  /* the attention's post norm and residual factor */
+    int cross_norm; /* the cross q norm, post norm and residual factor */
+    int lanes;      /* mHC lanes around every layer (0: none) */
+    float scale;    /* the embedding row's factor */
+    orc_matrix *emb;                 /* vocab x dim, tied head */
+    orc_matrix *const *mats;         /* layers x ORC_DEC_NMATS (unused slots NULL) */
+    const float *gains;              /* (3 layers + 1) x dim: attention, cross, FFN norms; final */
+    const float *rope_cos, *rope_sin; /* max_pos x head_dim/2 */
+    const float *qk_gains;           /* layers x 4 x head_dim: self q, self k, cross q, cross k */
+    const float *post_gains;         /* layers x 2 x dim: self, cross */
+    const float *res_scale;          /* layers x 2: self, cross */
+    const float *taps_w;             /* layers x 3 (q, k, v) x taps x dim */
+    const float *mhc_affine;         /* layers x (3 + 4 lanes + lanes^2), orc_mhc_heads' affine */
+} orc_dec_model;
+
+/* One stream's int8 cross memory: per layer, frames key-major rows of dim
+ * codes and heads scales (cross.project with Int8.KV, cross.go:181-204). */
+typedef struct {
+    const int8_t *const *kq;
+    const float *const *ks;
+    const int8_t *const *vq;
+    const float *const *vs;
+} orc_dec_memory;
+
+typedef struct orc_dec_state orc_dec_state;
+orc_dec_state *orc_dec_new(const orc_dec_model *m, const orc_dec_memory *mem); /* NewState (decoder.go:212-215) */
+orc_dec_state *orc_dec_fork(const orc_dec_state *s);                           /* State.Fork (decoder.go:218-240) */
+void orc_dec_free(orc_dec_state *s);
+int orc_dec_len(const orc_dec_state *s);
+/* Decoder.Extend of one token (decoder.go:248-302, 446-523): the next
+ * token's logits (vocab floats, NULL: not kept); returns their argmax, or
+ * -1 past max_pos or for a token out of range. */
+int orc_dec_step(orc_dec_state *s, int token, float *logits);
+/* GreedyMemory's loop (greedy.go:30-69) from `first`: up to n tokens, each
+ * step's logits to logits[i] (NULL: not kept), stopping at eos (>= 0; not
+ * written, *stopped = 1). Returns the count, -1 on a failed step. */
+int orc_dec_greedy(orc_dec_state *s, int first, int n, int eos, int32_t *tokens, float *logits, int *stopped);
+/* streams greedy decodes from fresh states, n tokens each (no stop), on
+ * `threads` threads, a stream per thread at a time: tokens [streams][n],
+ * counts [streams]. The lut products must run on one thread
+ * (orc_set_cpu(.., 1)). */
+int orc_dec_streams(const orc_dec_model *m, const orc_dec_memory *mems, int streams, const int32_t *first, int n,
+                    int threads, int32_t *tokens, int32_t *counts);
+
 #ifdef __cplusplus
 }
 #endif
