@@ -263,6 +263,7 @@ def ref_shapes_leg(gw, torch, with_cpu, cpu_seconds):
                                                        "weight_GBps": round(weight_bytes(o, i, bits) / us / 1e3, 1)}
         del graph, m, x, y
     res = {"shapes": out}
+    res.update(ref_benchmarks(gw, torch, with_cpu))
     if with_cpu:
         from oracle import cpu_legs
 
@@ -272,6 +273,142 @@ def ref_shapes_leg(gw, torch, with_cpu, cpu_seconds):
         res["cpu_baseline"] = {"unit": "us per call", "cores": 1, "kind": "port", "host": cpu_host(),
                                "sample": f"oracle lut GEMM on one thread (AVX2 where the host has it), each "
                                          f"shape repeated for about {cpu_seconds:.2f} s"}
+    return res
+
+
+def _graph_us(torch, fn, calls=20, reps=5):
+    """Microseconds per call of fn, from a captured graph of `calls` calls
+    replayed `reps` times (inputs cache-resident, as repeated b.Loop calls)."""
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (calls * reps)
+
+
+def _cpu_us(fn, seconds):
+    fn()
+    done, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return el / done * 1e6
+
+
+# BenchmarkGEMMs (internal/cq/bench_test.go:92-150): matrices reading one
+# input, shared tables (GEMMs) against a GEMM per matrix, with the
+# published M5 Pro -cpu 1 times (docs/FINDINGS.md:3244-3251), us.
+REF_GEMMS = [("qkvg", 512, 2, (384, 96, 96, 384), {1: (6.47, 8.20), 375: (2430.0, 3040.0)}),
+             ("phi", 2048, 4, (4, 4, 16), {1: (7.43, 13.2), 375: (2800.0, 4960.0)})]
+
+
+def ref_benchmarks(gw, torch, with_cpu, cpu_seconds=0.3):
+    """The reference's other benchmarks of this path on the device, each
+    next to its published M5 Pro time and the oracle on one host thread:
+    BenchmarkGEMMs (shared tables vs a GEMM per matrix, at 1 and 375 rows),
+    BenchmarkCrossAttendStep (one decode step's int8 cross-attention, 8 heads
+    of qk 48 / vd 64 over 375 frames; internal/needle/int8_bench_test.go:
+    35-56; published 23.9 us NEON int8, 55.0 us float32) and
+    BenchmarkQuantizeRow (one row of 48, 64 and 2048 values, int8_bench_test.go:
+    18-33; published 0.83 ns per value), the latter also over 65536 rows in
+    one launch."""
+    import numpy as np
+
+    from go_whistle_amd import needle
+
+    orc = None
+    if with_cpu:
+        if ROOT not in sys.path:
+            sys.path.insert(0, ROOT)
+        from oracle import binding as orc
+
+        orc.set_cpu(orc.have_avx2(), 1)
+    res = {}
+    try:
+        gem = {}
+        for name, inp, bits, outs, pub in REF_GEMMS:
+            g = gw.synth.rng(38 + inp)
+            packs = [gw.synth.random_packed(g, o, inp, GROUP, bits, sigma=0.05) for o in outs]
+            for p in packs[1:]:
+                p.Codebook = packs[0].Codebook  # one codebook per width, as in .cact
+            ms = [gw.cq.New(p) for p in packs]
+            for rows in (1, 375):
+                x = torch.from_numpy(gw.synth.activations(g, rows, inp)).cuda()
+                ys = [torch.empty(rows, o, device="cuda") for o in outs]
+                shared = _graph_us(torch, lambda: gw.cq.gemms_dev(ms, ys, x, rows))
+
+                def separate():
+                    for m, y in zip(ms, ys):
+                        m.gemm_dev(y, x, rows)
+
+                sep = _graph_us(torch, separate)
+                e = {"shared_us": round(shared, 2), "separate_us": round(sep, 2),
+                     "m5pro_1core_shared_us": pub[rows][0], "m5pro_1core_separate_us": pub[rows][1]}
+                if orc is not None:
+                    oms = [orc.OMatrix.new(p) for p in packs]
+                    xh = gw.synth.activations(g, rows, inp)
+                    e["cpu_1t_shared_us"] = round(_cpu_us(lambda: orc.gemms(oms, xh, rows), cpu_seconds), 2)
+                gem[f"{name}_rows{rows}"] = e
+        res["gemms"] = gem
+
+        H, qk, vd, frames = 8, 48, 64, 375
+        g = gw.synth.rng(34)
+        kf = g.standard_normal((frames, H * qk)).astype(np.float32)
+        vf = g.standard_normal((frames, H * vd)).astype(np.float32)
+        q = g.standard_normal(H * qk).astype(np.float32)
+        kq, ks = torch.empty(frames * H * qk, dtype=torch.int8, device="cuda"), torch.empty(frames * H, device="cuda")
+        vq, vs = torch.empty(frames * H * vd, dtype=torch.int8, device="cuda"), torch.empty(frames * H, device="cuda")
+        kd, vdev, qd = torch.from_numpy(kf).cuda(), torch.from_numpy(vf).cuda(), torch.from_numpy(q).cuda()
+        needle.quantize_rows_dev(kq, ks, kd, frames, H * qk, qk)
+        needle.quantize_rows_dev(vq, vs, vdev, frames, H * vd, vd)
+        spans = torch.tensor([[0, 0, 0, frames]], dtype=torch.int32, device="cuda")
+        o = torch.empty(H * vd, device="cuda")
+        us = _graph_us(torch, lambda: needle.attend_int8_dev(o, qd, 1, H, kq, ks, H * qk, qk, vq, vs, H * vd, vd,
+                                                              spans, frames, np.float32(6.928203), True))
+        ca = {"us": round(us, 2), "m5pro_1core_int8_neon_us": 23.9, "m5pro_1core_float32_us": 55.0}
+        if orc is not None:
+            kq8, ks8 = orc.quantize_rows(kf.reshape(-1), H * qk, qk)
+            vq8, vs8 = orc.quantize_rows(vf.reshape(-1), H * vd, vd)
+            sp = np.array([[0, 0, 0, frames]], np.int32)
+            ca["cpu_1t_us"] = round(_cpu_us(lambda: orc.attend_int8_spans(q, 1, H, kq8, ks8, H * qk, qk, vq8, vs8,
+                                                                            H * vd, vd, frames, sp,
+                                                                            np.float32(6.928203), True, 1),
+                                            cpu_seconds), 2)
+        res["cross_attend_step_8x48_375"] = ca
+
+        qr = {}
+        for n in (48, 64, 2048):
+            x = torch.from_numpy(g.standard_normal(n).astype(np.float32)).cuda()
+            q8, sc = torch.empty(n, dtype=torch.int8, device="cuda"), torch.empty(1, device="cuda")
+            one = _graph_us(torch, lambda: needle.quantize_rows_dev(q8, sc, x, 1, n, n))
+            rows = 65536
+            xb = torch.from_numpy(g.standard_normal(rows * n).astype(np.float32) if n < 2048 else
+                                  g.standard_normal(rows * n // 16).astype(np.float32)).cuda()
+            rb = xb.numel() // n
+            qb, sb = torch.empty(xb.numel(), dtype=torch.int8, device="cuda"), torch.empty(rb, device="cuda")
+            many = _graph_us(torch, lambda: needle.quantize_rows_dev(qb, sb, xb, rb, n, n), calls=10)
+            e = {"one_row_us": round(one, 3), "rows_per_launch": rb,
+                 "ns_per_value": round(many * 1e3 / (rb * n), 5), "m5pro_1core_ns_per_value": 0.83}
+            if orc is not None:
+                xh = g.standard_normal(n).astype(np.float32)
+                e["cpu_1t_ns_per_value"] = round(_cpu_us(lambda: orc.quantize_row(xh), cpu_seconds) * 1e3 / n, 3)
+            qr[str(n)] = e
+        res["quantize_row"] = qr
+    finally:
+        if orc is not None:
+            orc.set_cpu(False, 1)
     return res
 
 
@@ -453,7 +590,7 @@ def _decode_rate(gw, torch, model, batch, tokens):
     return d, g, {"tokens_per_s": round(batch * tokens / ms * 1e3, 1), "ms_per_step": round(ms / tokens, 4)}
 
 
-def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
+def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu, models=("synthetic", "whistle")):
     """Greedy decode of the synthetic 8-layer decoder (d 512, 8 heads, FFN
     2048, vocab 16384, 1500-frame int8 cross memory per stream), 200 tokens
     at batch 1 and 256: one captured step graph replayed per token. Then
@@ -469,11 +606,21 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
                     "CQ4 (self q/k/v/gate/o, cross q/gate/o: sigmoid output gates), tied CQ4 head 16384x512, int8 "
                     "self/cross KV; cross memory: 1500 random encoder states through CQ4 K/V projections",
            "tokens": tokens}
-    for batch in (1, 256):
+    for batch in (1, 256) if "synthetic" in models else ():
         d, g, res[f"batch{batch}"] = _decode_rate(gw, torch, model, batch, tokens)
         del d, g
         torch.cuda.empty_cache()
     wcfg = dec.DecoderConfig.whistle()
+    if "whistle" not in models:
+        if with_cpu:
+            if ROOT not in sys.path:
+                sys.path.insert(0, ROOT)
+            from oracle import cpu_legs
+
+            base = cpu_legs.decode_baseline(tokens, cpu_threads(), cpu_threads())
+            res["cpu_baseline"] = dict(base["batch1"], host=cpu_host())
+            res["cpu_baseline_batch256"] = dict(base["batch256"], host=cpu_host())
+        return res
     wmodel = dec.make_model(7, wcfg)
     wres = {"model": "the same decoder with the reference step's features: causal taps (3) on q/k/v, per-head "
                      "q/k ZCRMSNorm before RoPE, the attention's post norm and residual factor, the cross q/k "
@@ -484,6 +631,7 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
         if batch == 256:  # fork cost at two positions (random parents, as a beam step reorders)
             rng = __import__("numpy").random.default_rng(3)
             fk = {}
+            d.fork(list(rng.integers(0, batch, size=batch)))  # untimed: its first call allocates its buffers
             for at in (40, 200):
                 d.reset(list(range(1, batch + 1)))
                 for _ in range(at):
@@ -503,9 +651,10 @@ def decode_leg(gw, torch, tokens, cpu_seconds, with_cpu):
             sys.path.insert(0, ROOT)
         from oracle import cpu_legs
 
-        base = cpu_legs.decode_baseline(tokens, cpu_threads(), cpu_threads())
-        res["cpu_baseline"] = dict(base["batch1"], host=cpu_host())
-        res["cpu_baseline_batch256"] = dict(base["batch256"], host=cpu_host())
+        if "synthetic" in models:
+            base = cpu_legs.decode_baseline(tokens, cpu_threads(), cpu_threads())
+            res["cpu_baseline"] = dict(base["batch1"], host=cpu_host())
+            res["cpu_baseline_batch256"] = dict(base["batch256"], host=cpu_host())
         wb = cpu_legs.decode_baseline(tokens, cpu_threads(), cpu_threads(), cfg=wcfg)
         wres["cpu_baseline"] = dict(wb["batch1"], host=cpu_host())
         wres["cpu_baseline_batch256"] = dict(wb["batch256"], host=cpu_host())
@@ -525,6 +674,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-model", choices=("both", "synthetic", "whistle"), default="both",
+                    help="the decode leg's decoders: the synthetic one, the one with the reference step's features")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM leg")
     ap.add_argument("--gemm-only", action="store_true", help="run only the batched GEMM leg (prints its JSON)")
     ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (prints its JSON)")
@@ -564,7 +715,9 @@ def main():
         print(json.dumps({"attention": attention_leg(gw, torch, not args.no_cpu, 1.0)}))
         return
     if args.decode_only:
-        print(json.dumps({"decode": decode_leg(gw, torch, args.decode_tokens, args.cpu_seconds, not args.no_cpu)}))
+        models = ("synthetic", "whistle") if args.decode_model == "both" else (args.decode_model,)
+        print(json.dumps({"decode": decode_leg(gw, torch, args.decode_tokens, args.cpu_seconds, not args.no_cpu,
+                                               models)}))
         return
 
     g = gw.synth.rng(20261201)

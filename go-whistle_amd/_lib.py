@@ -46,7 +46,8 @@ SIGNATURES = {
     "nd_qkv_prep_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p,
                                 c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
-    "nd_norm_scaled_add_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_int, c_int, c_void_p]),
+    "nd_norm_scaled_add_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_int, c_void_p]),
+    "nd_rms_unit_quant_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "nd_expand_lanes_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "nd_collapse_lanes_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "kv_page_copy_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),

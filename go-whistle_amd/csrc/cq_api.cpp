@@ -1597,10 +1597,21 @@ int nd_qkv_prep_dev(float *q, const float *k, const float *v, int batch, int dim
     return CQ_OK;
 }
 
-int nd_norm_scaled_add_dev(float *h, const float *y, const float *gain, float scale, int rows, int dim, void *stream) {
-    if (rows < 0 || dim <= 0 || dim > 8192) return fail(CQ_ERR_MISUSE, "needle: %d rows of %d", rows, dim);
+int nd_norm_scaled_add_dev(float *h, const float *resid, const float *y, const float *gain, float scale, int rows,
+                           int dim, void *stream) {
+    if (rows < 0 || !row_kernel_dim(dim))
+        return fail(CQ_ERR_MISUSE, "needle: post norm of %d rows of %d (a multiple of 256 up to 4096)", rows, dim);
     if (rows > 0 && (!h || !y || !gain)) return fail(CQ_ERR_MISUSE, "needle: post norm with a nil operand");
-    HIP_TRY(launch_norm_scaled_add(h, y, gain, scale, rows, dim, static_cast<hipStream_t>(stream)), "post norm launch");
+    HIP_TRY(launch_norm_scaled_add(h, resid ? resid : h, y, gain, scale, rows, dim, static_cast<hipStream_t>(stream)),
+            "post norm launch");
+    return CQ_OK;
+}
+
+int nd_rms_unit_quant_dev(float *dst, const float *x, int rows, int dim, void *stream) {
+    if (rows < 0 || !row_kernel_dim(dim))
+        return fail(CQ_ERR_MISUSE, "needle: RMSUnit of %d rows of %d (a multiple of 256 up to 4096)", rows, dim);
+    if (rows > 0 && (!dst || !x)) return fail(CQ_ERR_MISUSE, "needle: RMSUnit with a nil operand");
+    HIP_TRY(launch_rms_unit_row(dst, x, rows, dim, 1, static_cast<hipStream_t>(stream)), "RMSUnit launch");
     return CQ_OK;
 }
 
@@ -1735,7 +1746,10 @@ int nd_hadamard_mlp_dev(float *out, const float *x, int rows, int dim, int na, i
 
 int nd_rms_unit_dev(float *dst, const float *x, int rows, int dim, void *stream) {
     if (rows < 0 || dim <= 0) return fail(CQ_ERR_MISUSE, "needle: RMSUnit of %d rows of %d", rows, dim);
-    HIP_TRY(launch_rms_unit(dst, x, rows, dim, static_cast<hipStream_t>(stream)), "RMSUnit launch");
+    if (row_kernel_dim(dim))  // 256 threads a row, the squares' chains read ahead from LDS
+        HIP_TRY(launch_rms_unit_row(dst, x, rows, dim, 0, static_cast<hipStream_t>(stream)), "RMSUnit launch");
+    else
+        HIP_TRY(launch_rms_unit(dst, x, rows, dim, static_cast<hipStream_t>(stream)), "RMSUnit launch");
     return CQ_OK;
 }
 

@@ -173,6 +173,39 @@ __device__ __forceinline__ double zc_partial(const float *row, int dim, int k) {
     return s;
 }
 
+// The same partial sum k for a row held in LDS transposed, t[k * stride +
+// j] = row[4j + k] for j < q = dim / 4 (dim a multiple of 64): the lane
+// reads its q values as float4s, 16 ahead of the adds, so the chain of q
+// dependent float64 adds does not wait on each read. Equal to
+// zc_partial(row, dim, k) bit for bit (the same squares in the same order).
+__device__ __forceinline__ double zc_partial_t(const float *t, int stride, int q, int k) {
+    const float4 *r = reinterpret_cast<const float4 *>(t + k * stride);
+    const int n4 = q / 4;
+    double s = 0.0;
+    float4 a0 = r[0], a1 = r[1], a2 = r[2], a3 = r[3];
+    for (int j = 0; j < n4; j += 4) {
+        float4 b0 = a0, b1 = a1, b2 = a2, b3 = a3;
+        if (j + 4 < n4) {
+            b0 = r[j + 4];
+            b1 = r[j + 5];
+            b2 = r[j + 6];
+            b3 = r[j + 7];
+        }
+        const float v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                             a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const double d = v[e];
+            s = s + d * d;
+        }
+        a0 = b0;
+        a1 = b1;
+        a2 = b2;
+        a3 = b3;
+    }
+    return s;
+}
+
 // ZCRMSNorm's divisor from the four partial sums (norm.go:53-66):
 // float32(sqrt(float64(float32(s / dim) + 1e-6))).
 __device__ __forceinline__ float zc_rms(double p0, double p1, double p2, double p3, int dim) {

@@ -326,8 +326,13 @@ struct PrepArgs {
     int dim;
 };
 hipError_t launch_qkv_prep(const PrepArgs &a, int batch, hipStream_t s);
-hipError_t launch_norm_scaled_add(float *h, const float *y, const float *gain, float sc, int rows, int dim,
-                                  hipStream_t s);
+// Row kernels of 256 threads (dim a multiple of 256, at most 4096): h =
+// resid + float32(sc * ZCRMSNorm(y)); RMSUnit, with quant then fakeQuant of
+// the whole row.
+bool row_kernel_dim(int dim);
+hipError_t launch_norm_scaled_add(float *h, const float *resid, const float *y, const float *gain, float sc, int rows,
+                                  int dim, hipStream_t s);
+hipError_t launch_rms_unit_row(float *dst, const float *x, int rows, int dim, int quant, hipStream_t s);
 hipError_t launch_expand_lanes(float *stream, const float *x, int rows, int lanes, int dim, hipStream_t s);
 hipError_t launch_collapse_lanes(float *x, const float *stream, int rows, int lanes, int dim, hipStream_t s);
 hipError_t launch_page_copy(int8_t *q, float *sc, const int32_t *src, const int32_t *dst, int n, int page_rows,

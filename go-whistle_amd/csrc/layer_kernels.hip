@@ -93,28 +93,96 @@ __global__ __launch_bounds__(1024) void qkv_prep_kernel(PrepArgs a) {
     if (lane == 0) s8[row * hk + hh] = sc;
 }
 
-__global__ __launch_bounds__(64) void norm_scaled_add_kernel(float *h, const float *y, const float *gain, float s,
-                                                             int dim) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    float *row = reinterpret_cast<float *>(smem);
-    const int r = blockIdx.x, lane = threadIdx.x;
-    const float *yr = y + static_cast<long long>(r) * dim;
-    float *hr = h + static_cast<long long>(r) * dim;
-    for (int i = lane; i < dim; i += 64) row[i] = yr[i];
+// A row of dim values (a multiple of 256, at most 4096) by 256 threads:
+// thread t holds values t, t + 256, ... in registers and stores them in LDS
+// transposed for the mean square's four in-order partial sums
+// (zc_partial_t), which lanes 0-3 of wavefront 0 add. Returns the
+// partials' sum of squares in float64 to every thread through LDS
+// (norm.go:91-109).
+constexpr int kRowMax = 4096;
+
+__device__ __forceinline__ double row_square_sum(const float *row, int dim, float (&v)[kRowMax / 256], float *t,
+                                                 double *sum_sh) {
+    const int tid = threadIdx.x;
+    const int V = dim >> 8, q = dim >> 2, stride = q + 4;
+#pragma unroll
+    for (int e = 0; e < kRowMax / 256; ++e)
+        if (e < V) {
+            const int i = tid + 256 * e;
+            v[e] = row[i];
+            t[(i & 3) * stride + (i >> 2)] = v[e];
+        }
     __syncthreads();
     double part = 0.0;
-    if (lane < 4) part = zc_partial(row, dim, lane);
+    if (tid < 4) part = zc_partial_t(t, stride, q, tid);
     const double p1 = __shfl(part, 1), p2 = __shfl(part, 2), p3 = __shfl(part, 3);
-    __shared__ float rms_sh;
-    if (lane == 0) rms_sh = zc_rms(part, p1, p2, p3, dim);
+    if (tid == 0) *sum_sh = ((part + p1) + p2) + p3;
     __syncthreads();
-    const float rms = rms_sh;
-    for (int c = lane; c < dim; c += 64) {
-        const float gx = gain[c] * row[c];
-        const float nv = gx / rms;
-        const float sv = s * nv;
-        hr[c] = hr[c] + sv;
+    return *sum_sh;
+}
+
+// h = resid + float32(s * ZCRMSNorm(y)) per row (resid may be h).
+__global__ __launch_bounds__(256) void norm_scaled_add_kernel(float *h, const float *resid, const float *y,
+                                                              const float *gain, float s, int dim) {
+    __shared__ __align__(16) float t[4 * (kRowMax / 4 + 4)];
+    __shared__ double sum_sh;
+    const int r = blockIdx.x, tid = threadIdx.x;
+    float v[kRowMax / 256];
+    const double sum = row_square_sum(y + static_cast<long long>(r) * dim, dim, v, t, &sum_sh);
+    // zc_rms: float32(sqrt(float64(float32(s / dim) + 1e-6)))
+    const float ms = static_cast<float>(sum / static_cast<double>(dim));
+    const float e = ms + 1e-6f;
+    const float rms = static_cast<float>(sqrt(static_cast<double>(e)));
+    const float *rr = resid + static_cast<long long>(r) * dim;
+    float *hr = h + static_cast<long long>(r) * dim;
+#pragma unroll
+    for (int k = 0; k < kRowMax / 256; ++k)
+        if (k < (dim >> 8)) {
+            const int c = tid + 256 * k;
+            const float gx = gain[c] * v[k];
+            const float nv = gx / rms;
+            const float sv = s * nv;
+            hr[c] = rr[c] + sv;
+        }
+}
+
+// RMSUnit (norm.go:68-81) of each row, x * float32(1 / sqrt(float64(ms +
+// 1e-6))); with quant, then the fakeQuant of the whole row (int8.go:57-75,
+// one chunk of dim): the mHC phi products' int8 input (mhc.go:99-106,
+// linear.go:80-87).
+__global__ __launch_bounds__(256) void rms_unit_row_kernel(float *dst, const float *x, int dim, int quant) {
+    __shared__ __align__(16) float t[4 * (kRowMax / 4 + 4)];
+    __shared__ double sum_sh;
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int V = dim >> 8;
+    float v[kRowMax / 256];
+    const double sum = row_square_sum(x + static_cast<long long>(r) * dim, dim, v, t, &sum_sh);
+    const float ms = static_cast<float>(sum / static_cast<double>(dim));
+    const float e = ms + 1e-6f;
+    const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(e)));
+#pragma unroll
+    for (int k = 0; k < kRowMax / 256; ++k)
+        if (k < V) v[k] = v[k] * inv;
+    if (quant) {  // QuantizeRow's bound with Go's NaN-keeping max, then code * scale
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kRowMax / 256; ++k)
+            if (k < V) m = go_max(m, fabsf(v[k]));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = go_max(m, __shfl_xor(m, off));
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        m = go_max(go_max(red[0], red[1]), go_max(red[2], red[3]));
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+#pragma unroll
+        for (int k = 0; k < kRowMax / 256; ++k)
+            if (k < V) v[k] = static_cast<float>(go_int8_code(rintf(v[k] / sc))) * sc;
     }
+    float *out = dst + static_cast<long long>(r) * dim;
+#pragma unroll
+    for (int k = 0; k < kRowMax / 256; ++k)
+        if (k < V) out[tid + 256 * k] = v[k];
 }
 
 __global__ __launch_bounds__(256) void expand_lanes_kernel(float *stream, const float *x, int lanes, int dim,
@@ -176,10 +244,18 @@ hipError_t launch_qkv_prep(const PrepArgs &a, int batch, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_norm_scaled_add(float *h, const float *y, const float *gain, float sc, int rows, int dim,
-                                  hipStream_t s) {
+bool row_kernel_dim(int dim) { return dim > 0 && dim % 256 == 0 && dim <= kRowMax; }
+
+hipError_t launch_norm_scaled_add(float *h, const float *resid, const float *y, const float *gain, float sc, int rows,
+                                  int dim, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(norm_scaled_add_kernel, dim3(rows), dim3(64), sizeof(float) * dim, s, h, y, gain, sc, dim);
+    hipLaunchKernelGGL(norm_scaled_add_kernel, dim3(rows), dim3(256), 0, s, h, resid, y, gain, sc, dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_unit_row(float *dst, const float *x, int rows, int dim, int quant, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rms_unit_row_kernel, dim3(rows), dim3(256), 0, s, dst, x, dim, quant);
     return hipGetLastError();
 }
 

@@ -711,6 +711,22 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
         float acc = 0.0f;
         Pos cp = first;
         for (int q0 = 0; q0 < Q; q0 += DG) {
+            // Longest remaining work first. A CU's SIMDs issue their oldest
+            // wavefront first, so the workgroups of a CU finished in age
+            // order and the end of a launch ran on ever fewer wavefronts;
+            // priorities by the items a wavefront has left (s_setprio)
+            // keep the long units ahead and the CU full to the end. On
+            // MI355X: the GEMV sweep's 4-bit launch 70.4 -> 69.8 us,
+            // 64 x 16384x512 CQ4 54.7 -> 52.3 us, the 2-bit launch 38.8 ->
+            // 35.7 us (bit for bit the same results).
+            if constexpr (V == 1 && !PRE) {
+                const int nch = (groups + gc - 1) / gc;
+                const int left = (nch - g0 / gc) * Q - q0;
+                if (left > 12) __builtin_amdgcn_s_setprio(3);
+                else if (left > 8) __builtin_amdgcn_s_setprio(2);
+                else if (left > 4) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+            }
 #pragma unroll
             for (int d = 0; d < DG; ++d) {
                 if (q0 + d < Q) {

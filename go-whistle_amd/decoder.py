@@ -337,7 +337,7 @@ class Decoder:
         if c.lanes:
             n = c.lanes
             self.lane_s = [z(B, n * c.dim), z(B, n * c.dim)]
-            self.nx, self.nxq = z(B, n * c.dim), z(B, n * c.dim)
+            self.nxq = z(B, n * c.dim)
             self.pl, self.ql, self.rl = z(B, n), z(B, n), z(B, n * n)
             self.hp, self.hq, self.hr = z(B, n), z(B, n), z(B, n * n)
             self.u_mhc, self.blk = z(B, c.dim), z(B, c.dim)
@@ -546,14 +546,14 @@ class Decoder:
             cur, nxt = self.lane_s
         for l in range(c.layers):
             m = self.mats[l]
+            h_in = self.x  # the block's input h; with lanes u, which stays unchanged for the mix
             if n:  # the mHC heads and the block input u (mhc.go:196-219)
-                check(L.nd_rms_unit_dev(P(self.nx), P(cur), B, n * D, s))
-                check(L.nd_fake_quant_dev(P(self.nxq), P(self.nx), B, n * D, n * D, s))
+                check(L.nd_rms_unit_quant_dev(P(self.nxq), P(cur), B, n * D, s))
                 cq.gemms_dev([m["phi_pre"], m["phi_post"], m["phi_res"]], [self.pl, self.ql, self.rl], self.nxq, B)
                 check(L.nd_mhc_heads_dev(P(self.hp), P(self.hq), P(self.hr), P(self.u_mhc), P(self.pl), P(self.ql),
                                          P(self.rl), P(cur), B, n, D, P(self.mhc_affine[l]), s))
-                check(L.nd_gather_rows_dev(P(self.x), P(self.u_mhc), None, B, D, s))
-            cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.x, B,
+                h_in = self.u_mhc
+            cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], h_in, B,
                                norm_gain=self.gains[3 * l])
             qg = P(self.qk_gains[l, 0]) if c.qk_norm else None
             kg = P(self.qk_gains[l, 1]) if c.qk_norm else None
@@ -567,19 +567,19 @@ class Decoder:
                                              c.max_pos, float(np.float32(math.sqrt(hd))), 1, B, P(self.cos),
                                              P(self.sin), P(self.pos), P(self.pages), self.page_stride,
                                              self.PAGE_ROWS, self.pool_pages, s))
-            if c.post_norm:  # block.go:183-188
+            if c.post_norm:  # block.go:183-188: x = h + float32(gate * postNorm(o))
                 cq.gemms_gated_dev([m["wo"]], [self.o], self.att, self.g, B)
-                check(L.nd_norm_scaled_add_dev(P(self.x), P(self.o), P(self.post_gains[l, 0]),
+                check(L.nd_norm_scaled_add_dev(P(self.x), P(h_in), P(self.o), P(self.post_gains[l, 0]),
                                                float(self.res_scale[l, 0]), B, D, s))
             else:
-                cq.gemms_gated_dev([m["wo"]], [self.x], self.att, self.g, B, resid=self.x)
+                cq.gemms_gated_dev([m["wo"]], [self.x], self.att, self.g, B, resid=h_in)
             cq.gemms_fused_dev([m["wcq"], m["wcg"]], [self.q, self.g], self.x, B, norm_gain=self.gains[3 * l + 1])
             if c.cross_norm:  # cross.go:217-219
                 check(L.nd_zcrmsnorm_dev(P(self.q), P(self.q), P(self.qk_gains[l, 2]), B * H, hd, s))
             self._attend(l, True, s)
             if c.cross_norm:  # cross.go:255-263 and the hook's add
                 cq.gemms_gated_dev([m["wco"]], [self.o], self.att, self.g, B)
-                check(L.nd_norm_scaled_add_dev(P(self.x), P(self.o), P(self.post_gains[l, 1]),
+                check(L.nd_norm_scaled_add_dev(P(self.x), None, P(self.o), P(self.post_gains[l, 1]),
                                                float(self.res_scale[l, 1]), B, D, s))
             else:
                 cq.gemms_gated_dev([m["wco"]], [self.x], self.att, self.g, B, resid=self.x)

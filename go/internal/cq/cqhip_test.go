@@ -17,26 +17,36 @@ import (
 	"github.com/cwbudde/go-whistle/internal/cact"
 )
 
-// packedFor draws a packed CQ tensor: sorted N(0, 1/group) levels, uniform
-// index bytes, FP16 norms 2^-4..2^4.
-func packedFor(rng *rand.Rand, out, in, group, bits int) cact.Packed {
+// synthPacked returns an out x in CQ tensor of `bits` for these tests:
+// every index value drawn on its own, uniform over the 2^bits codes, and
+// packed LSB first into its row's bytes (the layout cact.Packed documents,
+// internal/cact/packed.go:18-40); 2^bits levels mirrored about zero with
+// magnitudes |N(0, 1/group)|, sorted; FP16 norms of 2^-4 .. 2^4.
+func synthPacked(rng *rand.Rand, out, in, group, bits int) cact.Packed {
 	p := cact.Packed{Out: out, In: in, Group: group, Bits: bits, Width: bits}
-	p.Codebook = make([]float32, 1<<bits)
+	sigma := 1 / math.Sqrt(float64(group))
+	levels := make([]float32, 0, 1<<bits)
+	for range 1 << (bits - 1) {
+		m := float32(math.Abs(rng.NormFloat64()) * sigma)
+		levels = append(levels, m, -m)
+	}
+	slices.Sort(levels)
+	p.Codebook = levels
 
-	for i := range p.Codebook {
-		p.Codebook[i] = float32(rng.NormFloat64() / math.Sqrt(float64(group)))
+	rowBytes, perByte := p.RowBytes(), 8/bits
+	p.Index = make([]byte, out*rowBytes)
+	for r := range out {
+		row := p.Index[r*rowBytes : (r+1)*rowBytes]
+		for k := range rowBytes * perByte {
+			code := byte(rng.IntN(1 << bits))
+			row[k/perByte] |= code << (uint(k%perByte) * uint(bits))
+		}
 	}
 
-	slices.Sort(p.Codebook)
-
-	p.Index = make([]byte, out*p.RowBytes())
-	for i := range p.Index {
-		p.Index[i] = byte(rng.Uint32())
-	}
-
-	for range out * p.Groups() {
-		e := uint16(11 + rng.IntN(9))
-		p.Norms = binary.LittleEndian.AppendUint16(p.Norms, e<<10|uint16(rng.IntN(1024)))
+	p.Norms = make([]byte, 2*out*p.Groups())
+	for i := 0; i < len(p.Norms); i += 2 {
+		exp := uint16(11 + rng.IntN(9)) // biased exponent: 2^-4 .. 2^4
+		binary.LittleEndian.PutUint16(p.Norms[i:], exp<<10|uint16(rng.IntN(1<<10)))
 	}
 
 	return p
@@ -69,7 +79,7 @@ func TestCQHIPProducts(t *testing.T) {
 	for _, s := range []struct{ out, in, bits int }{{96, 512, 2}, {384, 512, 2}, {128, 2048, 4}, {8199, 512, 4}} {
 		rng := rand.New(rand.NewPCG(uint64(s.out), uint64(s.in)))
 
-		m, err := New(packedFor(rng, s.out, s.in, 128, s.bits))
+		m, err := New(synthPacked(rng, s.out, s.in, 128, s.bits))
 		if err != nil {
 			t.Fatal(err)
 		}
@@ -97,7 +107,7 @@ func TestCQHIPProducts(t *testing.T) {
 
 func TestCQHIPBatchesAndViews(t *testing.T) {
 	rng := rand.New(rand.NewPCG(3, 4))
-	p := packedFor(rng, 4*512, 512, 128, 4)
+	p := synthPacked(rng, 4*512, 512, 128, 4)
 
 	m, err := New(p)
 	if err != nil {
@@ -146,7 +156,7 @@ func TestCQHIPBatchesAndViews(t *testing.T) {
 }
 
 func TestCQHIPNewErrors(t *testing.T) {
-	good := packedFor(rand.New(rand.NewPCG(7, 8)), 2, 128, 128, 2)
+	good := synthPacked(rand.New(rand.NewPCG(7, 8)), 2, 128, 128, 2)
 
 	for _, tc := range []struct {
 		name string
@@ -170,7 +180,7 @@ func TestCQHIPNewErrors(t *testing.T) {
 }
 
 func TestCQHIPPanics(t *testing.T) {
-	m, err := New(packedFor(rand.New(rand.NewPCG(9, 10)), 4, 128, 128, 4))
+	m, err := New(synthPacked(rand.New(rand.NewPCG(9, 10)), 4, 128, 128, 4))
 	if err != nil {
 		t.Fatal(err)
 	}

@@ -376,12 +376,19 @@ int nd_qkv_prep_dev(float *q, const float *k, const float *v, int batch, int dim
                     int taps, const float *q_gain, const float *k_gain, const float *cos_t, const float *sin_t,
                     int positions, const int32_t *pos, int cap, int8_t *kq, float *ks, int8_t *vq, float *vs,
                     const int32_t *pages, int page_stride, int page_rows, int pool_pages, void *stream);
-/* h += float32(scale * ZCRMSNorm(y)) per row of dim: the attention's post
- * norm and residual factor, h += float32(gate * postNorm(a))
- * (internal/needle/block.go:183-188), and the cross branch's
- * (internal/decoder/cross.go:255-263 with the hook's add, decoder.go:461-465).
- * y is only read. */
-int nd_norm_scaled_add_dev(float *h, const float *y, const float *gain, float scale, int rows, int dim, void *stream);
+/* h = resid + float32(scale * ZCRMSNorm(y)) per row of dim (resid null or
+ * h: h += ...): the attention's post norm and residual factor, h +=
+ * float32(gate * postNorm(a)) (internal/needle/block.go:183-188), and the
+ * cross branch's (internal/decoder/cross.go:255-263 with the hook's add,
+ * decoder.go:461-465). y is only read. dim a multiple of 256 up to 4096. */
+int nd_norm_scaled_add_dev(float *h, const float *resid, const float *y, const float *gain, float scale, int rows,
+                           int dim, void *stream);
+/* RMSUnit (internal/needle/norm.go:68-81) of each row of dim, then its
+ * fakeQuant as one chunk (int8.go:57-75): the mHC phi products' int8 input
+ * (mhc.go:99-106 with Linear.WithInt8Input, linear.go:80-87), one launch,
+ * bit for bit nd_rms_unit_dev then nd_fake_quant_dev. dim a multiple of 256
+ * up to 4096; dst may be x. */
+int nd_rms_unit_quant_dev(float *dst, const float *x, int rows, int dim, void *stream);
 /* ExpandLanes / CollapseLanes (internal/needle/mhc.go:137-170): each row of
  * x to `lanes` equal lanes of the stream (rows x lanes x dim), and back as
  * the lane mean (lanes summed in order from 0, then divided by lanes). */

@@ -255,11 +255,31 @@ def test_norm_scaled_add_and_lanes():
     h, y = g.standard_normal((rows, D)).astype(np.float32), (g.standard_normal((rows, D)) * 5).astype(np.float32)
     gain = (1 + g.standard_normal(D) * 0.1).astype(np.float32)
     hd, yd, gd, h2 = _t(h), _t(y), _t(gain), _t(h)
-    check(lib().nd_norm_scaled_add_dev(_p(hd), _p(yd), _p(gd), 0.37, rows, D, _s()))
+    check(lib().nd_norm_scaled_add_dev(_p(hd), None, _p(yd), _p(gd), 0.37, rows, D, _s()))
+    r = g.standard_normal((rows, D)).astype(np.float32)
+    rd, od = _t(r), torch.zeros(rows, D, device="cuda")
+    check(lib().nd_norm_scaled_add_dev(_p(od), _p(rd), _p(yd), _p(gd), 0.37, rows, D, _s()))
     torch.cuda.synchronize()
     ny = orc.zc_rmsnorm(y.ravel(), gain, D).reshape(rows, D)
     want = (h + (np.float32(0.37) * ny).astype(np.float32)).astype(np.float32)
     assert same(hd.cpu().numpy(), want)
+    assert same(od.cpu().numpy(), (r + (np.float32(0.37) * ny).astype(np.float32)).astype(np.float32))
+    # RMSUnit and its fused fakeQuant over rows of 2048 (and 512), with a zero
+    # row and rows holding NaN / Inf, against the oracle
+    for dim in (2048, 512):
+        xs = (g.standard_normal((6, dim)) * 3).astype(np.float32)
+        xs[1] = 0
+        xs[2, 7], xs[3, 100], xs[4, 5] = np.nan, np.inf, -np.inf
+        xsd, u1, u2 = _t(xs), torch.zeros(6, dim, device="cuda"), torch.zeros(6, dim, device="cuda")
+        check(lib().nd_rms_unit_dev(_p(u1), _p(xsd), 6, dim, _s()))
+        check(lib().nd_rms_unit_quant_dev(_p(u2), _p(xsd), 6, dim, _s()))
+        torch.cuda.synchronize()
+        wu = orc.rms_unit(xs.ravel(), 6, dim)
+        wq = orc.fake_quant(wu, dim, dim)
+        for got, want in ((u1, wu), (u2, wq)):
+            a, b = got.cpu().numpy().ravel(), want.ravel()
+            nb = np.isnan(b)
+            assert np.array_equal(np.isnan(a), nb) and np.array_equal(a[~nb].view(np.uint32), b[~nb].view(np.uint32))
     st = torch.zeros(rows, n * D, device="cuda")
     check(lib().nd_expand_lanes_dev(_p(st), _p(h2), rows, n, D, _s()))
     s2 = g.standard_normal((rows, n * D)).astype(np.float32)
