@@ -302,10 +302,11 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     a.tb = kLutTile;
     a.gc = lut_chunk(groups_max);
     // A launch that fills at most a quarter of the CUs is latency-bound: wide
-    // rows then take their tables in fewer chunks (up to 32 KiB of tables),
+    // rows then take their tables in fewer chunks (up to 64 KiB of tables,
+    // all 16 groups of a 4-bit row of 2048 in one chunk of 16 wavefronts),
     // each chunk costing a table build and a barrier.
     if (units * rows * 4 <= device_info().cus)
-        while (a.gc * 2 <= groups_max && 2 * a.gc * 2 * s0.group_bytes * 16 * static_cast<int>(sizeof(short)) <= 32 * 1024)
+        while (a.gc * 2 <= groups_max && 2 * a.gc * 2 * s0.group_bytes * 16 * static_cast<int>(sizeof(short)) <= 64 * 1024)
             a.gc *= 2;
     a.bpw_max = a.bpw;
     // Latency-bound launches of one-block units (batch-1 decode) take the
@@ -1523,6 +1524,8 @@ static int attend_impl(float *out, long long out_stride, const float *q, long lo
             return fail(CQ_ERR_MISUSE, "needle: %d pages of %d rows for %d keys (pool %d)", page_stride, page_rows,
                         nk_max, pool_pages);
         while ((1 << page_shift) < page_rows) ++page_shift;
+        if ((nk_max + page_rows - 1) / page_rows > kAttendMaxPages)
+            return fail(CQ_ERR_UNSUPPORTED, "needle: %d keys in pages of %d rows", nk_max, page_rows);
         kv_stride = s_stride = 0;  // the page table gives every row
     }
     AttendArgs a{out, out_stride, q, q_stride, t, heads, kq, ks, k_cols, qk, vq, vs, v_cols, vd,

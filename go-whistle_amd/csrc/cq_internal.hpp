@@ -237,8 +237,10 @@ struct AttendArgs {
     // pool reads page 0.
     const int32_t *pages;
     int page_stride, page_shift, pool_pages;
+    int page_lds;  // set by the launcher: the byte offset of the LDS copy of the page table
 };
 hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream);
+constexpr int kAttendMaxPages = 1024;  // a paged launch's pages per stream
 
 // The cache stream a workgroup of stream b reads (kv_index, or b itself),
 // or -1 when the index is outside the caches.
@@ -248,13 +250,27 @@ __device__ __forceinline__ long long attend_cache_of(const AttendArgs &a, int b)
     return (c >= 0 && c < a.kv_streams) ? c : -1;
 }
 
-// The array row that holds key `key` of stream b: through the page table,
-// or row `key` of the stream's own cache.
-__device__ __forceinline__ long long attend_row(const AttendArgs &a, int b, int key) {
+// A paged launch copies stream b's page table into LDS at page_lds (its
+// entries outside the pool read page 0) before any key is read: key rows are
+// then addressed without a global load each, which would also hold up the
+// kernels' counted waits on their streamed rows. Every thread of the
+// workgroup calls it.
+__device__ __forceinline__ void attend_stage_pages(const AttendArgs &a, int b, unsigned char *smem) {
+    if (!a.pages) return;
+    int32_t *pw = reinterpret_cast<int32_t *>(smem + a.page_lds);
+    const int np = (a.nk_max + (1 << a.page_shift) - 1) >> a.page_shift;
+    for (int i = threadIdx.x; i < np; i += blockDim.x) {
+        const int pg = a.pages[static_cast<long long>(b) * a.page_stride + i];
+        pw[i] = (pg >= 0 && pg < a.pool_pages) ? pg : 0;
+    }
+    __syncthreads();
+}
+
+// The array row that holds key `key` of the workgroup's stream: through its
+// page table in LDS, or row `key` of the stream's own cache.
+__device__ __forceinline__ long long attend_row(const AttendArgs &a, const int32_t *pgs, int key) {
     if (!a.pages) return key;
-    long long pg = a.pages[static_cast<long long>(b) * a.page_stride + (key >> a.page_shift)];
-    if (pg < 0 || pg >= a.pool_pages) pg = 0;
-    return (pg << a.page_shift) + (key & ((1 << a.page_shift) - 1));
+    return (static_cast<long long>(pgs[key >> a.page_shift]) << a.page_shift) + (key & ((1 << a.page_shift) - 1));
 }
 
 // HadamardMLP, Whistle's Monarch FFN (hadamard_kernels.hip): rows of dim

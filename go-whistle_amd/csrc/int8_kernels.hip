@@ -139,6 +139,8 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const long long kb = attend_cache_of(a, b);  // the cache this stream reads
     if (kb < 0 || lo0 < 0 || len0 < 0 || sp[1] > a.nk_max || lo1 < 0 || len1 < 0 || sp[3] > a.nk_max)
         return;  // spans off the cache, or no cache
+    attend_stage_pages(a, b, smem);  // paged: the stream's page table into LDS
+    const int32_t *pgs = reinterpret_cast<const int32_t *>(smem + a.page_lds);
 
     float *s = reinterpret_cast<float *>(smem);  // n logits, then weights
     int8_t *vbuf = reinterpret_cast<int8_t *>(s + ((a.nk_max + 3) & ~3));  // value codes: one or two chunks
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
                 for (int u = 0; u < 8; ++u) {
                     const int e = min(e0 + u * nt, total - 1);
                     const int jj = e / per, part = e - (e / per) * per;
-                    w[u] = *reinterpret_cast<const int4 *>(vq + attend_row(a, b, key_of(j0 + jj)) * a.v_cols +
+                    w[u] = *reinterpret_cast<const int4 *>(vq + attend_row(a, pgs, key_of(j0 + jj)) * a.v_cols +
                                                            kv * a.vd + part * 16);
                 }
 #pragma unroll
@@ -207,7 +209,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         } else {
             for (int e = t0; e < cnt * a.vd; e += nt) {
                 const int jj = e / a.vd, d = e - (e / a.vd) * a.vd;
-                buf[jj * a.vd + d] = vq[attend_row(a, b, key_of(j0 + jj)) * a.v_cols + kv * a.vd + d];
+                buf[jj * a.vd + d] = vq[attend_row(a, pgs, key_of(j0 + jj)) * a.v_cols + kv * a.vd + d];
             }
         }
     };
@@ -217,8 +219,8 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     // a time so that their loads are in flight together.
     auto logit = [&](int j) -> float {
         const int key = key_of(j);
-        const int8_t *krow = kq + attend_row(a, b, key) * a.k_cols + kv * a.qk;
-        const float sk = ks[attend_row(a, b, key) * kv_heads + kv];
+        const int8_t *krow = kq + attend_row(a, pgs, key) * a.k_cols + kv * a.qk;
+        const float sk = ks[attend_row(a, pgs, key) * kv_heads + kv];
         if (a.quant_q) {
             int dot = 0;  // exact in any order
             if (wide) {
@@ -310,7 +312,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const float sum = sum_sh;
     for (int j = tid; j < n; j += kAttThreads) {
         const float p = s[j] / sum;
-        s[j] = p * vs[attend_row(a, b, key_of(j)) * kv_heads + kv];
+        s[j] = p * vs[attend_row(a, pgs, key_of(j)) * kv_heads + kv];
     }
 
     // 3. axpysI8 per output, keys in order: the first ceil(vd/64)
@@ -462,6 +464,8 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
         if (tid < VD) outp[tid] = 0.0f;
         return;
     }
+    attend_stage_pages(a, b, smem);  // paged: the stream's page table into LDS
+    const int32_t *pgs = reinterpret_cast<const int32_t *>(smem + a.page_lds);
 
     const int nk_pad = (a.nk_max + 3) & ~3;
     float *s = reinterpret_cast<float *>(smem);  // logits, exponentials, then weights
@@ -494,7 +498,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
             const int p = u * 64 + lane;
             const int seg = p / G::kJC, jj = p - seg * G::kJC;
             const int key = key_of(j0 + (jj < cnt ? jj : 0));
-            dma16(vq + attend_row(a, b, key) * a.v_cols + kv * VD + seg * 16, lds_offset(slot + u * 64 * 16));
+            dma16(vq + attend_row(a, pgs, key) * a.v_cols + kv * VD + seg * 16, lds_offset(slot + u * 64 * 16));
         }
     };
 
@@ -507,12 +511,12 @@ __global__ __launch_bounds__(kAttThreads) void attend_stream_kernel(AttendArgs a
     float skr[KPT], vsr[KPT];
     auto kload = [&](int g, int j) {
         const int key = key_of(j);
-        const int8_t *krow = kq + attend_row(a, b, key) * a.k_cols + kv * a.qk;
+        const int8_t *krow = kq + attend_row(a, pgs, key) * a.k_cols + kv * a.qk;
 #pragma unroll
         for (int p = 0; p < kStreamQk / 16; ++p)
             if (p < kpieces) kw[g][p] = *reinterpret_cast<const int4 *>(krow + 16 * p);
-        skr[g] = ks[attend_row(a, b, key) * kv_heads + kv];
-        vsr[g] = vs[attend_row(a, b, key) * kv_heads + kv];
+        skr[g] = ks[attend_row(a, pgs, key) * kv_heads + kv];
+        vsr[g] = vs[attend_row(a, pgs, key) * kv_heads + kv];
     };
     auto logit = [&](int g) -> float {
         if (a.quant_q) {
@@ -809,6 +813,8 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
         if (tid < kChainVd) outp[tid] = 0.0f;
         return;
     }
+    attend_stage_pages(a, b, smem);  // paged: the stream's page table into LDS
+    const int32_t *pgs = reinterpret_cast<const int32_t *>(smem + a.page_lds);
 
     const int nk_pad = (a.nk_max + 3) & ~3;
     float *s = reinterpret_cast<float *>(smem);   // logits, exponentials, then weights
@@ -835,7 +841,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
         const int p = u * 64 + lane;
         const int jj = p >> 2, seg = p & 3;
         const int key = key_of(j0 + (jj < cnt ? jj : 0));
-        dma16(vq + attend_row(a, b, key) * a.v_cols + kv * kChainVd + seg * 16, lds_offset(slot + u * 64 * 16));
+        dma16(vq + attend_row(a, pgs, key) * a.v_cols + kv * kChainVd + seg * 16, lds_offset(slot + u * 64 * 16));
     };
 
     // 1. The query, then each thread's first KPT keys, in flight together.
@@ -846,12 +852,12 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     float skr[KPT], svr[KPT];  // key scales; value scales (kept when one round covers every key)
     auto kload = [&](int g, int j) {
         const int key = key_of(j);
-        const int8_t *krow = kq + attend_row(a, b, key) * a.k_cols + kv * a.qk;
+        const int8_t *krow = kq + attend_row(a, pgs, key) * a.k_cols + kv * a.qk;
 #pragma unroll
         for (int p = 0; p < kStreamQk / 16; ++p)
             if (p < kpieces) kw[g][p] = *reinterpret_cast<const int4 *>(krow + 16 * p);
-        skr[g] = ks[attend_row(a, b, key) * kv_heads + kv];
-        svr[g] = vs[attend_row(a, b, key) * kv_heads + kv];
+        skr[g] = ks[attend_row(a, pgs, key) * kv_heads + kv];
+        svr[g] = vs[attend_row(a, pgs, key) * kv_heads + kv];
     };
     auto logit = [&](int g) -> float {
         if (a.quant_q) {
@@ -990,7 +996,7 @@ __global__ __launch_bounds__(64 * NW) void attend_chain_kernel(AttendArgs a, int
     } else {
         for (int j = tid; j < n; j += NT) {
             const float p = s[j] / sum;
-            s[j] = p * vs[attend_row(a, b, key_of(j)) * kv_heads + kv];
+            s[j] = p * vs[attend_row(a, pgs, key_of(j)) * kv_heads + kv];
         }
     }
     if constexpr (RES) {
@@ -1196,6 +1202,8 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
         outp[lane] = 0.0f;
         return;
     }
+    attend_stage_pages(a, b, smem);  // paged: the stream's page table into LDS
+    const int32_t *pgs = reinterpret_cast<const int32_t *>(smem + a.page_lds);
     const int nk_pad = (a.nk_max + 3) & ~3;
     float *s = reinterpret_cast<float *>(smem);  // logits, exponentials, then weights
     int8_t *ring = reinterpret_cast<int8_t *>(s + nk_pad);
@@ -1224,11 +1232,11 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
             const int p = u * 64 + lane;
             const int jj = p >> 2, seg = p & 3;
             const int key = key_of(j0 + (jj < cnt ? jj : 0));
-            dma16(base + attend_row(a, b, key) * cols + seg * 16, lds_offset(slot + u * 64 * 16));
+            dma16(base + attend_row(a, pgs, key) * cols + seg * 16, lds_offset(slot + u * 64 * 16));
         }
         const float *sc = keys ? ks : vs;
         const int key = key_of(j0 + (lane < cnt ? lane : 0));
-        if (lane < JC) dma4(sc + attend_row(a, b, key) * kv_heads + kv, lds_offset(slot + JC * ROW));
+        if (lane < JC) dma4(sc + attend_row(a, pgs, key) * kv_heads + kv, lds_offset(slot + JC * ROW));
     };
     // Chunk g has landed: at most the chunks issued after it are in flight.
     auto wait_chunk = [&](int g) {
@@ -1521,8 +1529,18 @@ size_t chain_lds(const AttendArgs &a, int jc, int rs) {
 // The resident form also holds the two product buffers behind the rows.
 size_t chain_res_lds(const AttendArgs &a, int rs) { return chain_lds(a, 64, rs) + 2 * sizeof(float) * kProdFloats; }
 
-hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
+hipError_t launch_attend_int8(const AttendArgs &args, hipStream_t stream) {
+    AttendArgs a = args;
     if (a.t <= 0 || a.heads <= 0 || a.batch <= 0) return hipSuccess;
+    // A paged launch keeps the stream's page table behind the kernel's own
+    // dynamic LDS (with_pages gives the total and sets its offset).
+    const size_t pb = a.pages ? ((static_cast<size_t>((a.nk_max + (1 << a.page_shift) - 1) >> a.page_shift) * 4 + 15) &
+                                 ~size_t(15))
+                              : 0;
+    auto with_pages = [&](size_t lds) {
+        a.page_lds = static_cast<int>((lds + 15) & ~size_t(15));
+        return static_cast<size_t>(a.page_lds) + pb;
+    };
     const bool aligned = (a.kv_stride & 15) == 0 && (reinterpret_cast<uintptr_t>(a.kq) & 15) == 0 &&
                          (reinterpret_cast<uintptr_t>(a.vq) & 15) == 0;
     const bool stream_ok = aligned && (a.qk & 15) == 0 && a.qk <= kStreamQk && (a.k_cols & 15) == 0 &&
@@ -1530,18 +1548,19 @@ hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
     if (stream_ok && a.vd == kChainVd) {
         if (a.resident) {
             const int rs = std::max(1, (a.nk_max + 63) / 64);
-            const size_t lds = chain_res_lds(a, rs);
+            const size_t lds = with_pages(chain_res_lds(a, rs));
             if (lds <= 150 * 1024) return launch_attend_chain<4, 64, true>(a, rs, lds, stream);
         }
         if (a.qk == kChainVd) {
             // many streams: key and value chunks through a ring of 6 slots
             // (eight workgroups per CU at 1500 keys)
             constexpr int rs = 6;
-            const size_t lds = 4 * ((static_cast<size_t>(a.nk_max) + 3) & ~size_t(3)) + static_cast<size_t>(rs) * kRingSlot;
+            const size_t lds = with_pages(4 * ((static_cast<size_t>(a.nk_max) + 3) & ~size_t(3)) +
+                                          static_cast<size_t>(rs) * kRingSlot);
             if (lds <= 150 * 1024) return launch_attend_ring<rs>(a, lds, stream);
         }
         const int rs = 4;
-        const size_t lds = chain_lds(a, 32, rs);
+        const size_t lds = with_pages(chain_lds(a, 32, rs));
         if (lds <= 150 * 1024) return launch_attend_chain<1, 32, false>(a, rs, lds, stream);
     }
     // (64-code value heads the chain kernel does not fit need more LDS than
@@ -1549,23 +1568,23 @@ hipError_t launch_attend_int8(const AttendArgs &a, hipStream_t stream) {
     int rs = 0;
     size_t slds = 0;
     if (stream_ok && a.vd == 128) {
-        if (a.resident && stream_plan<128, 64>(a, true, rs, slds))
-            return launch_attend_stream<128, 64>(a, rs, slds, stream);
-        if (stream_plan<128, 32>(a, false, rs, slds)) return launch_attend_stream<128, 32>(a, rs, slds, stream);
+        if (a.resident && stream_plan<128, 64>(a, true, rs, slds) && with_pages(slds) <= 150 * 1024)
+            return launch_attend_stream<128, 64>(a, rs, with_pages(slds), stream);
+        if (stream_plan<128, 32>(a, false, rs, slds) && with_pages(slds) <= 150 * 1024)
+            return launch_attend_stream<128, 32>(a, rs, with_pages(slds), stream);
     }
-    const AttendArgs &b = a;
     const bool one_chunk = a.vchunk >= a.nk_max;
     const size_t vbytes = (one_chunk ? 1 : 2) * static_cast<size_t>(a.vchunk) * a.vd;
-    const size_t lds = sizeof(float) * static_cast<size_t>((a.nk_max + 3) & ~3) + vbytes;
+    const size_t lds = with_pages(sizeof(float) * static_cast<size_t>((a.nk_max + 3) & ~3) + vbytes);
     static bool attr = false;
     if (!attr) {
         // dynamic LDS beside the kernel's static arrays: 96 KiB of values + up to 8192 logits
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 132 * 1024);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL(attend_kernel, dim3(a.heads, a.t, a.batch), dim3(kAttThreads), lds, stream, b);
+    hipLaunchKernelGGL(attend_kernel, dim3(a.heads, a.t, a.batch), dim3(kAttThreads), lds, stream, a);
     return hipGetLastError();
 }
 
