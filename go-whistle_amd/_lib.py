@@ -29,6 +29,7 @@ SIGNATURES = {
     "cq_device_bytes": (c_longlong, [c_void_p]),
     "cq_rows": (c_int, [c_void_p, c_int, c_int, POINTER(c_void_p)]),
     "cq_exact": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "cq_dense": (c_int, [c_void_p, POINTER(c_void_p)]),
     "cq_kernel_name": (c_char_p, [c_void_p]),
     "cq_row": (c_int, [c_void_p, POINTER(c_float), c_size_t, c_int]),
     "cq_gemm": (c_int, [c_void_p, POINTER(c_float), c_size_t, POINTER(c_float), c_size_t, c_int]),

@@ -110,6 +110,15 @@ class Matrix:
         check(lib().cq_exact(self._h, ctypes.byref(v)))
         return Matrix(v.value)
 
+    def Dense(self):
+        """A view whose products of 16 or more activations run the dense fp32
+        MFMA form of Exact's semantics (within float32 rounding of Exact,
+        not bit for bit); fewer run Exact's nibble kernels. No counterpart
+        in the reference."""
+        v = c_void_p()
+        check(lib().cq_dense(self._h, ctypes.byref(v)))
+        return Matrix(v.value)
+
     def Kernel(self):
         return lib().cq_kernel_name(self._h).decode()
 

@@ -124,6 +124,7 @@ struct cq_matrix {
     std::shared_ptr<CqStore> st;
     int row0, out;
     bool exact;
+    bool dense = false;  // a Dense view: Exact's semantics, batched products on the fp32 MFMA form
 };
 
 namespace {
@@ -750,6 +751,96 @@ int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
 }
 
 // Launches the product of up to kMaxMatrices views sharing their tables.
+// ---- the dense form of Dense views ----
+
+// Activations from which a Dense view's product runs the fp32 MFMA form;
+// fewer run Exact's nibble kernels, whose result (bit for bit Exact's) is
+// within the same bound.
+constexpr int kDenseMinRows = 16;
+
+bool dense_pays(cq_matrix *const *ms, int n, int rows) {
+    if (rows < kDenseMinRows) return false;
+    const CqStore &s0 = *ms[0]->st;
+    if (!dense_geometry_supported(s0.width, s0.group)) return false;
+    for (int k = 0; k < n; ++k)
+        if (!ms[k]->dense || ms[k]->st->group != s0.group || ms[k]->st->groups != s0.groups ||
+            ms[k]->st->width != s0.width)
+            return false;
+    return true;
+}
+
+// K runs of a view's dense product: one where its 128 x 128 tiles fill two
+// workgroups a CU, else enough runs (of two chunks of 64 coordinates or
+// more) to, whose partial sums the fold adds.
+void dense_split(int tiles, int nch, int &ksplit, int &kchunks) {
+    const int slots = 2 * device_info().cus;
+    ksplit = tiles >= slots ? 1 : std::min((slots + tiles - 1) / tiles, std::max(1, nch / 2));
+    kchunks = (nch + ksplit - 1) / ksplit;
+    ksplit = (nch + kchunks - 1) / kchunks;
+}
+
+// One rotation of the activations into a workspace, then one product launch
+// (and its fold) per view.
+int run_dense(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream) {
+    const CqStore &s0 = *ms[0]->st;
+    const int tn = dense_tile_activations(), tmr = dense_tile_rows() / kBlockRows;
+    const int kin = s0.groups * s0.group, kpad = (kin + 63) / 64 * 64, nch = kpad / 64;
+    const int tiles_n = (rows + tn - 1) / tn;
+    size_t part = 0;
+    for (int k = 0; k < n; ++k) {
+        const int nblk = (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
+        int ks, kc;
+        dense_split(((nblk + tmr - 1) / tmr) * tiles_n, nch, ks, kc);
+        if (ks > 1) part = std::max(part, static_cast<size_t>(ks) * rows * ms[k]->out * sizeof(float));
+    }
+    DenseRotArgs r;
+    std::memset(&r, 0, sizeof r);
+    r.x = x;
+    r.x_stride = s0.in;
+    r.rows = rows;
+    r.rows_pad = tiles_n * tn;
+    r.in = s0.in;
+    r.G = s0.group;
+    r.groups = s0.groups;
+    r.kpad = kpad;
+    r.inv_sqrt = s0.inv_sqrt;
+    const size_t xh_bytes = align256(static_cast<size_t>(r.rows_pad) * kpad * sizeof(float));
+    WsScope ws;
+    if (int e = ws_acquire(xh_bytes + part, stream, ws.l)) return e;
+    r.xh = static_cast<float *>(ws.l.w->buf);
+    HIP_TRY(launch_dense_rotate(r, stream), "dense rotation launch");
+    for (int k = 0; k < n; ++k) {
+        const cq_matrix *m = ms[k];
+        if (m->out == 0) continue;
+        const CqStore &s = *m->st;
+        DenseArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.idx = s.d_idx;
+        a.norm = s.d_norm;
+        a.xh = r.xh;
+        a.y = dsts[k];
+        a.part = reinterpret_cast<float *>(static_cast<char *>(ws.l.w->buf) + xh_bytes);
+        a.y_stride = m->out;
+        a.row0 = m->row0;
+        a.out = m->out;
+        a.blk0 = m->row0 / kBlockRows;
+        a.nblk = (m->row0 + m->out + kBlockRows - 1) / kBlockRows - a.blk0;
+        a.rows = rows;
+        a.kpad = kpad;
+        a.kin = kin;
+        a.groups = s.groups;
+        a.G = s.group;
+        a.U = s.unit_bytes;
+        a.units = s.units;
+        a.tiles_m = (a.nblk + tmr - 1) / tmr;
+        a.tiles_n = tiles_n;
+        dense_split(a.tiles_m * a.tiles_n, nch, a.ksplit, a.kchunks);
+        for (int c = 0; c < 16; ++c) a.cb[c] = c < s.ncb ? s.cb[c] : 0.0f;
+        HIP_TRY(launch_dense(a, s.width, stream), "dense product launch");
+    }
+    return ws_release(ws.l);
+}
+
 int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
                 const Fuse *fz = nullptr) {
     const CqStore &s0 = *ms[0]->st;
@@ -763,6 +854,7 @@ int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x,
     if (fz && fz->any())
         return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel (this is %s, group bytes %d)",
                     mode == kModeLut ? "lut" : "exact", s0.group_bytes);
+    if (ms[0]->dense && dense_pays(ms, n, rows)) return run_dense(ms, n, dsts, x, rows, stream);
     int rc = check_geometry(s0, mode);
     if (rc) return rc;
     ProdArgs a;
@@ -813,7 +905,7 @@ int gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, i
     int k = 0;
     while (k < n) {
         int e = k + 1;
-        while (e < n && e - k < kMaxMatrices && uses_lut(ms[e]) == uses_lut(ms[k]) &&
+        while (e < n && e - k < kMaxMatrices && uses_lut(ms[e]) == uses_lut(ms[k]) && ms[e]->dense == ms[k]->dense &&
                shares_tables(*ms[k]->st, *ms[e]->st))
             ++e;
         int rc = run_product(ms + k, e - k, dsts + k, x, rows, stream, fz);
@@ -966,7 +1058,7 @@ long long cq_device_bytes(const cq_matrix *m) {
 int cq_rows(const cq_matrix *m, int lo, int hi, cq_matrix **view) {
     if (!m || !view) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
     if (lo < 0 || hi < lo || hi > m->out) return fail(CQ_ERR_MISUSE, "cq: Rows(%d, %d) of %d rows", lo, hi, m->out);
-    *view = new cq_matrix{m->st, m->row0 + lo, hi - lo, m->exact};
+    *view = new cq_matrix{m->st, m->row0 + lo, hi - lo, m->exact, m->dense};
     return CQ_OK;
 }
 
@@ -976,7 +1068,16 @@ int cq_exact(const cq_matrix *m, cq_matrix **view) {
     return CQ_OK;
 }
 
-const char *cq_kernel_name(const cq_matrix *m) { return m && uses_lut(m) ? "lut" : "nibble4"; }
+int cq_dense(const cq_matrix *m, cq_matrix **view) {
+    if (!m || !view) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    *view = new cq_matrix{m->st, m->row0, m->out, true, true};
+    return CQ_OK;
+}
+
+const char *cq_kernel_name(const cq_matrix *m) {
+    if (m && m->dense) return "dense-f32";
+    return m && uses_lut(m) ? "lut" : "nibble4";
+}
 
 int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream) {
     if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
@@ -991,8 +1092,9 @@ int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, v
 }
 
 const char *cq_gemm_path(const cq_matrix *m, int rows) {
-    if (!m || !uses_lut(m)) return "nibble4";
     cq_matrix *mm = const_cast<cq_matrix *>(m);
+    if (m && m->dense && dense_pays(&mm, 1, rows)) return "dense-f32";
+    if (!m || !uses_lut(m)) return "nibble4";
     if (tab_pays(&mm, 1, rows)) return "lut-mfma-tab";
     if (mfma_geometry_supported(m->st->width, m->st->group) && mfma_pays(&mm, 1, rows)) return "lut-mfma";
     if (split_pays(&mm, 1, rows)) return "lut-mfma-split";

@@ -182,6 +182,38 @@ int mfma_split_rows_per_workgroup();
 int mfma_split_activations();
 hipError_t launch_lut_mfma_split(const LutLaunch &a, int bits, int fold_blocks, hipStream_t s);
 
+// Dense fp32 MFMA form of Exact's product (dense_kernels.hip), groups of 32
+// to 1024. The rotation writes xh [rows_pad][kpad], each activation rotated
+// as Exact rotates it (zero rows past rows, zero columns past groups * G).
+struct DenseRotArgs {
+    const float *x;
+    long long x_stride;
+    float *xh;
+    int rows, rows_pad, in, G, groups, kpad;
+    float inv_sqrt;
+};
+// The product of one view: tiles of dense_tile_rows() weight rows (from
+// block blk0, nblk blocks) by dense_tile_activations() activations, K in
+// ksplit runs of kchunks chunks of 64 coordinates (more than one: partial
+// sums in part [ksplit][rows][out], then the fold into y).
+struct DenseArgs {
+    const uint8_t *idx;
+    const uint16_t *norm;
+    const float *xh;
+    float *y;
+    float *part;
+    long long y_stride;
+    int row0, out, blk0, nblk;
+    int rows, kpad, kin, groups, G, units, U;
+    int tiles_m, tiles_n, ksplit, kchunks;
+    float cb[16];
+};
+bool dense_geometry_supported(int bits, int group);
+int dense_tile_rows();
+int dense_tile_activations();
+hipError_t launch_dense_rotate(const DenseRotArgs &r, hipStream_t s);
+hipError_t launch_dense(const DenseArgs &a, int bits, hipStream_t s);
+
 struct RowArgs {
     const uint8_t *idx;
     const uint16_t *norm;

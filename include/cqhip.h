@@ -87,8 +87,20 @@ int cq_rows(const cq_matrix *m, int lo, int hi, cq_matrix **view);
 /* Matrix.Exact (matrix.go:152-157): a view whose products use the float
  * nibble tables (kernel.go:239-374) instead of the lut kernel. */
 int cq_exact(const cq_matrix *m, cq_matrix **view);
-/* Name of the kernel the matrix's products run: "lut" or "nibble4"
- * (kernel.go:30-43, 92-98). */
+/* A view sharing m's storage whose products of 16 or more activations run
+ * Exact's semantics as a dense fp32 MFMA contraction: the activations
+ * rotated as Exact rotates them (kernel.go:203-217), times W[r][k] =
+ * norm[r][k/G] * codebook[index(r, k)] dequantized tile by tile into LDS, on
+ * v_mfma_f32_32x32x2_f32. The sums run in the MFMA's order, so results are
+ * within float32 rounding of Exact's (tests hold them within 1e-5 of the
+ * largest |y| of each activation), not bit for bit; fewer activations,
+ * and groups outside 32..1024, run Exact's nibble kernels. No counterpart in the
+ * reference: for batched encoder-frame products that take Exact's
+ * arithmetic at matrix-core rates. Rows views keep the setting; cq_exact
+ * of it is a plain Exact view. */
+int cq_dense(const cq_matrix *m, cq_matrix **view);
+/* Name of the kernel the matrix's products run: "lut", "nibble4" or, for a
+ * Dense view, "dense-f32" (kernel.go:30-43, 92-98). */
 const char *cq_kernel_name(const cq_matrix *m);
 
 /* Matrix.Row (matrix.go:161-181): row r dequantised as cact.CQ does, bit
@@ -113,8 +125,8 @@ int cq_gemm_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *
  * 128, 2 or 4 bits, not an Exact view; else CQ_ERR_UNSUPPORTED. */
 int cq_gemm_mfma_dev(const cq_matrix *m, float *dst, const float *x, int rows, void *stream);
 /* The kernel cq_gemm_dev runs for `rows` activations: "lut", "lut-mfma",
- * "lut-mfma-tab" (the table pre-pass and its MFMA product), "lut-mfma-split"
- * or "nibble4". */
+ * "lut-mfma-tab" (the table pre-pass and its MFMA product), "lut-mfma-split",
+ * "dense-f32" (a Dense view's fp32 MFMA form) or "nibble4". */
 const char *cq_gemm_path(const cq_matrix *m, int rows);
 int cq_gemms_dev(int n, cq_matrix *const *ms, float *const *dsts, const float *x, int rows, void *stream);
 /* Bytes of device memory the workspace pool holds on every device (leased,
