@@ -769,14 +769,26 @@ bool dense_pays(cq_matrix *const *ms, int n, int rows) {
     return true;
 }
 
-// K runs of a view's dense product: one where its 128 x 128 tiles fill two
-// workgroups a CU, else enough runs (of two chunks of 64 coordinates or
-// more) to, whose partial sums the fold adds.
-void dense_split(int tiles, int nch, int &ksplit, int &kchunks) {
-    const int slots = 2 * device_info().cus;
-    ksplit = tiles >= slots ? 1 : std::min((slots + tiles - 1) / tiles, std::max(1, nch / 2));
+// K runs of a view's dense product, chosen by a cost model: its items
+// (128 x 128 tiles x runs) go round the CUs, two resident on a CU at a
+// time, and a CU works through its ceil(items / CUs) items at about 4 us a
+// chunk of 64 coordinates (measured on MI355X: a CU holding two items takes
+// about twice as long as one holding one); more than one run adds the
+// partial sums' traffic (each run writes rows x out floats, the fold reads
+// them all and writes y once, at about 4 TB/s) and a launch.
+void dense_split(int tiles, int nch, int rows, int out, int &ksplit, int &kchunks) {
+    const long long slots = device_info().cus;
+    double best = 0;
+    ksplit = 1;
+    for (int ks = 1; ks <= nch; ++ks) {
+        const int kc = (nch + ks - 1) / ks;
+        if ((nch + kc - 1) / kc != ks) continue;  // the same runs as a smaller count
+        const long long items = static_cast<long long>(tiles) * ks;
+        double us = static_cast<double>((items + slots - 1) / slots) * kc * 4.0;
+        if (ks > 1) us += (2.0 * ks + 1) * rows * static_cast<double>(out) * 4 / 4e6 + 3.0;
+        if (ks == 1 || us < best) best = us, ksplit = ks;
+    }
     kchunks = (nch + ksplit - 1) / ksplit;
-    ksplit = (nch + kchunks - 1) / kchunks;
 }
 
 // One rotation of the activations into a workspace, then one product launch
@@ -790,7 +802,7 @@ int run_dense(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
     for (int k = 0; k < n; ++k) {
         const int nblk = (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
         int ks, kc;
-        dense_split(((nblk + tmr - 1) / tmr) * tiles_n, nch, ks, kc);
+        dense_split(((nblk + tmr - 1) / tmr) * tiles_n, nch, rows, ms[k]->out, ks, kc);
         if (ks > 1) part = std::max(part, static_cast<size_t>(ks) * rows * ms[k]->out * sizeof(float));
     }
     DenseRotArgs r;
@@ -834,7 +846,7 @@ int run_dense(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
         a.units = s.units;
         a.tiles_m = (a.nblk + tmr - 1) / tmr;
         a.tiles_n = tiles_n;
-        dense_split(a.tiles_m * a.tiles_n, nch, a.ksplit, a.kchunks);
+        dense_split(a.tiles_m * a.tiles_n, nch, rows, a.out, a.ksplit, a.kchunks);
         for (int c = 0; c < 16; ++c) a.cb[c] = c < s.ncb ? s.cb[c] : 0.0f;
         HIP_TRY(launch_dense(a, s.width, stream), "dense product launch");
     }
