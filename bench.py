@@ -167,15 +167,21 @@ def cpu_baseline(gw, packs, seconds):
 
 
 INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA, ops/s
+FP32_PEAK_FLOPS = 157.3e12  # MI355X dense fp32 MFMA, flop/s
 
 
 def batched_gemm_leg(gw, torch, reps=5):
     """The encoder's batched CQ GEMMs: X [M x In] ~N(0, 1) times 4/2-bit
     2048x512 and 512x2048 (FFN up/down), M in {375, 1500, 12000}, through
-    cq_gemm_dev (which picks the lut kernel or its MFMA form). Flops are the
+    cq_gemm_dev (which picks the lut kernel or its MFMA form), each timed
+    over `reps` calls after 20 ms of the same calls. Flops are the
     dense equivalent 2*M*Out*In; for the MFMA forms, mfma_util is the int8 MFMA
     work it issues (one 32x32x32 product per 64-row block, 64-activation tile,
-    position and 32x32 quadrant) over the time, against 5.0 POP/s."""
+    position and 32x32 quadrant) over the time, against 5.0 POP/s. dense_f32
+    times the same matrix's Dense view (Exact's semantics on fp32 MFMA, the
+    whole call: rotation, product and any fold); its mfma_util_fp32 is the
+    fp32 MFMA work the padded 128 x 128 tiles issue over that time, against
+    157.3 TFLOP/s."""
     g = gw.synth.rng(31)
     out = {}
     for bits in (4, 2):
@@ -186,6 +192,7 @@ def batched_gemm_leg(gw, torch, reps=5):
                 y = torch.empty(M, o, device="cuda")
                 m.gemm_dev(y, x, M)
                 torch.cuda.synchronize()
+                prewarm(torch, lambda: m.gemm_dev(y, x, M), 20)
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
                 for _ in range(reps):
@@ -205,6 +212,23 @@ def batched_gemm_leg(gw, torch, reps=5):
                     ops = mfmas * 2 * 32 * 32 * 32
                     rec["mfma_TOPs"] = round(ops / us / 1e6, 1)
                     rec["mfma_util"] = round(ops / (us * 1e-6) / INT8_PEAK_OPS, 4)
+                # The Dense view of the same matrix: Exact's semantics on fp32
+                # MFMA (v_mfma_f32_32x32x2_f32 over 128 x 128 tiles, the
+                # activations rotated first), within float32 rounding of Exact.
+                d = m.Dense()
+                d.gemm_dev(y, x, M)
+                torch.cuda.synchronize()
+                prewarm(torch, lambda: d.gemm_dev(y, x, M), 20)
+                e0.record()
+                for _ in range(reps):
+                    d.gemm_dev(y, x, M)
+                e1.record()
+                torch.cuda.synchronize()
+                dus = e0.elapsed_time(e1) * 1e3 / reps
+                issued = 2.0 * (-(-M // 128) * 128) * (-(-o // 128) * 128) * (-(-i // 64) * 64)
+                rec["dense_f32"] = {"path": d.gemm_path(M), "us": round(dus, 2),
+                                    "dense_TFLOPs": round(2.0 * M * o * i / dus / 1e6, 2),
+                                    "mfma_util_fp32": round(issued / (dus * 1e-6) / FP32_PEAK_FLOPS, 4)}
                 out[f"cq{bits}_{o}x{i}_M{M}"] = rec
                 del x, y
     return out
