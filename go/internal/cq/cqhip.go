@@ -157,6 +157,20 @@ func (m *Matrix) Exact() *Matrix {
 	return wrap(v)
 }
 
+// Dense returns a view whose products of 16 or more activations run
+// Exact's arithmetic as an fp32 MFMA contraction (within float32 rounding
+// of Exact, not bit for bit); fewer run the nibble kernels. It has no
+// counterpart in the reference: for batched encoder frames that take
+// Exact's semantics.
+func (m *Matrix) Dense() *Matrix {
+	var v *C.cq_matrix
+
+	must(func() C.int { return C.cq_dense(m.h, &v) })
+	runtime.KeepAlive(m)
+
+	return wrap(v)
+}
+
 func fptr(s []float32) *C.float {
 	if len(s) == 0 {
 		return nil
