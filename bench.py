@@ -532,7 +532,9 @@ def attention_leg(gw, torch, with_cpu, cpu_seconds):
     cross over 1500 frames, K/V ~N(0,1) quantised per row on the device
     (QuantizeRows), Q ~N(0,1), int8 query. Microseconds per call (a captured
     graph of 20 calls), stream-steps/s and the K/V bytes read (codes and
-    scales) per second against 8 TB/s."""
+    scales) per second against 8 TB/s. The cross cases are timed in the
+    key-major layout ([stream][frame][8 heads x 64]) and, as _head_major,
+    in the decoder's ([stream][head][frame][64])."""
     from go_whistle_amd import needle
 
     H, D = 8, 64
@@ -559,26 +561,41 @@ def attention_leg(gw, torch, with_cpu, cpu_seconds):
                 needle.attend_int8_dev(o, q, 1, H, kq, ks, C, D, vq, vs, C, D, spans, n, math.sqrt(D), True,
                                        batch=batch, kv_stride=n * C, s_stride=n * H)
 
-            call()
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                for _ in range(20):
-                    call()
-            graph.replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(5):
-                graph.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / 100
             kv = batch * n * (2 * C + 2 * 4 * H)
-            out[f"b{batch}_{kind}{n}"] = {"us": round(us, 2), "stream_steps_per_s": round(batch / us * 1e6, 1),
-                                          "kv_GBps": round(kv / us / 1e3, 1),
-                                          "hbm_frac": round(kv / us / 1e3 / HBM_PEAK_GBS, 4)}
-            del graph, kq, vq, ks, vs, q, o, spans
+
+            def timed(fn, name):
+                fn()
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for _ in range(20):
+                        fn()
+                graph.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(5):
+                    graph.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / 100
+                out[name] = {"us": round(us, 2), "stream_steps_per_s": round(batch / us * 1e6, 1),
+                             "kv_GBps": round(kv / us / 1e3, 1), "hbm_frac": round(kv / us / 1e3 / HBM_PEAK_GBS, 4)}
+                del graph
+
+            timed(call, f"b{batch}_{kind}{n}")
+            if kind == "cross":
+                # The decoder's layout of the cross memory: head-major, [stream][head][frame][64], one
+                # AttendInt8Spans stream per (stream, head) (the same bytes, read as batch * 8 streams).
+                spans_hm = torch.tensor([span] * (batch * H), dtype=torch.int32, device="cuda")
+
+                def call_hm():
+                    needle.attend_int8_dev(o, q, 1, 1, kq, ks, D, D, vq, vs, D, D, spans_hm, n, math.sqrt(D), True,
+                                           batch=batch * H, kv_stride=n * D, s_stride=n)
+
+                timed(call_hm, f"b{batch}_{kind}{n}_head_major")
+                del spans_hm
+            del kq, vq, ks, vs, q, o, spans
         torch.cuda.empty_cache()
     res = {"cases": out}
     if with_cpu:

@@ -1519,7 +1519,9 @@ int kv_reorder_dev(int8_t *q, float *s, int8_t *tmp_q, float *tmp_s, const int32
 // without ordering) race; the reorder needs nothing in it cleared.
 }  // extern "C"
 
-constexpr size_t kScratchBytes = size_t(64) << 20;
+// 16 MiB: a 256-stream reorder of 64 rows of 512 codes (8.5 MiB with its
+// scales) fits; the paged self caches' forks share pages and need none.
+constexpr size_t kScratchBytes = size_t(16) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {

@@ -216,13 +216,13 @@ int kv_quantize_rows_dev(int8_t *q, float *s, const float *x, int rows, int cols
 int kv_reorder_dev(int8_t *q, float *s, int8_t *tmp_q, float *tmp_s, const int32_t *parent, const int32_t *len,
                    int streams, int cap, int cols, int width, void *stream);
 /* kv_reorder_dev without the temporaries and without any allocation: the
- * temporaries live in a device array of 64 MiB that the library holds on
+ * temporaries live in a device array of 16 MiB that the library holds on
  * each GPU it runs on until the process ends. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, a serving loop's beam reorder, harnesses that
  * forbid hipMalloc). A reorder whose temporaries (streams * cap * cols
  * codes, 256-byte aligned, plus streams * cap * cols/width float scales)
- * exceed 64 MiB returns CQ_ERR_MISUSE. Every call on one GPU uses that
+ * exceed 16 MiB returns CQ_ERR_MISUSE. Every call on one GPU uses that
  * GPU's one array: calls that overlap on one GPU race. */
 int kv_reorder_noalloc_dev(int8_t *q, float *s, const int32_t *parent, const int32_t *len, int streams, int cap,
                            int cols, int width, void *stream);

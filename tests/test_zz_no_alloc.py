@@ -65,7 +65,7 @@ def test_noalloc_reorder_refuses_more_than_its_array():
     import torch
 
     z = torch.zeros(16, dtype=torch.int32, device="cuda")
-    # 256 streams x 512 rows x 512 codes = 64 MiB of codes alone, plus scales
+    # 256 streams x 128 rows x 512 codes = 16 MiB of codes alone, plus scales
     with pytest.raises(CQPanic) as e:
-        check(lib().kv_reorder_noalloc_dev(_p(z), _p(z), _p(z), _p(z), 256, 512, 512, 64, cq._stream()))
-    assert "64" in str(e.value) or "67108864" in str(e.value)
+        check(lib().kv_reorder_noalloc_dev(_p(z), _p(z), _p(z), _p(z), 256, 128, 512, 64, cq._stream()))
+    assert "16777216" in str(e.value)
