@@ -228,20 +228,30 @@ def fork_page_tables(pt, parents, pos, page_rows, pool_pages):
     pages than streams x pages per stream."""
     pt = np.asarray(pt, np.int32)[np.asarray(parents, np.int64)].copy()
     streams, per = pt.shape
-    counts = np.bincount(pt.ravel(), minlength=pool_pages)
-    free = list(np.flatnonzero(counts == 0)[::-1])
-    copies = []
-    for b in range(streams):
-        lp0 = min(int(pos[b]) // page_rows, per)
-        for lp in range(lp0, per):
-            ph = int(pt[b, lp])
-            if counts[ph] > 1:
-                nf = int(free.pop())
-                counts[ph] -= 1
-                counts[nf] += 1
-                pt[b, lp] = nf
-                if lp == lp0 and pos[b] % page_rows:
-                    copies.append((ph, nf))
+    pos = np.asarray(pos, np.int64)
+    lp0 = np.minimum(pos // page_rows, per)
+    # References a stream must own from now on, in stream-then-page order.
+    # Taken one at a time in that order, a page's reference is replaced
+    # while another entry still references it: all of a page's must-own
+    # references but the last, and that one too unless every reference to
+    # the page is one of them. Free pages go out smallest first.
+    must = np.arange(per)[None, :] >= lp0[:, None]
+    total = np.bincount(pt.ravel(), minlength=pool_pages)
+    b_idx, lp_idx = np.nonzero(must)
+    mp = pt[b_idx, lp_idx].astype(np.int64)
+    mcount = np.bincount(mp, minlength=pool_pages)
+    order = np.argsort(mp, kind="stable")
+    ranks = np.empty(mp.size, np.int64)
+    ranks[order] = np.arange(mp.size) - np.searchsorted(mp[order], mp[order], side="left")
+    repl = ~((total[mp] == mcount[mp]) & (ranks == mcount[mp] - 1))
+    free = np.flatnonzero(total == 0)
+    if repl.sum() > free.size:
+        raise ValueError(f"decoder: a fork needs {int(repl.sum())} free pages, the pool has {free.size}")
+    newp = mp.copy()
+    newp[repl] = free[:int(repl.sum())]
+    pt[b_idx, lp_idx] = newp
+    partial = repl & (lp_idx == lp0[b_idx]) & (pos[b_idx] % page_rows != 0)
+    copies = list(zip(mp[partial].tolist(), newp[partial].tolist()))
     return pt, copies
 
 
@@ -296,18 +306,27 @@ class Decoder:
         # After a fork, stream b reads the cross memory built for stream
         # mem_of[b] (State.Fork shares it, decoder.go:223-240): the
         # attention takes the (stream, head) -> memory-block index.
+        # After a fork the attention reads the index from one buffer, updated
+        # in place, so a step graph captured after a fork stays valid across
+        # later forks.
         self.mem_of = np.arange(B)
         self.mem_index = None
+        self._mem_index_buf = z(B * hk, dt=i32)
         self.x, self.h = z(B, c.dim), z(B, c.dim)
         self.q, self.k, self.v, self.g = z(B, c.dim), z(B, c.dim), z(B, c.dim), z(B, c.dim)
         self.att, self.o = z(B, c.dim), z(B, c.dim)
         self.u = z(B, c.ffn)
         self.logits = z(B, c.vocab)
         hk = c.dim // c.head_dim
-        self.self_k = [z(B, c.max_pos, c.dim, dt=i8) for _ in range(c.layers)]
-        self.self_ks = [z(B, c.max_pos, hk) for _ in range(c.layers)]
-        self.self_v = [z(B, c.max_pos, c.dim, dt=i8) for _ in range(c.layers)]
-        self.self_vs = [z(B, c.max_pos, hk) for _ in range(c.layers)]
+        # Every layer's self K and V caches are slices of one array (codes and
+        # scales), [2 * layers][stream][position][...], K of layer l at 2l and
+        # V at 2l + 1: the paged fork copies all their pages in one launch.
+        self._self_q = z(2 * c.layers, B, c.max_pos, c.dim, dt=i8)
+        self._self_s = z(2 * c.layers, B, c.max_pos, hk)
+        self.self_k = [self._self_q[2 * l] for l in range(c.layers)]
+        self.self_ks = [self._self_s[2 * l] for l in range(c.layers)]
+        self.self_v = [self._self_q[2 * l + 1] for l in range(c.layers)]
+        self.self_vs = [self._self_s[2 * l + 1] for l in range(c.layers)]
         self.cross_k = [z(B, hk, c.frames, c.head_dim, dt=i8) for _ in range(c.layers)]
         self.cross_ks = [z(B, hk, c.frames) for _ in range(c.layers)]
         self.cross_v = [z(B, hk, c.frames, c.head_dim, dt=i8) for _ in range(c.layers)]
@@ -328,7 +347,9 @@ class Decoder:
         self.pt = np.arange(self.pool_pages, dtype=np.int32).reshape(B, self.page_stride)
         self.pages = torch.from_numpy(self.pt.copy()).to(dev)
         # the tap history: a ring of taps slots per stream, [batch][taps][3][dim]
-        self.hist = [z(B, c.taps, 3, c.dim) for _ in range(c.layers)] if c.taps > 1 else None
+        # (all layers' in one array: a fork gathers them in one launch)
+        self._hist_all = z(c.layers, B, c.taps, 3, c.dim) if c.taps > 1 else None
+        self.hist = [self._hist_all[l] for l in range(c.layers)] if c.taps > 1 else None
         dv = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
         self.qk_gains, self.post_gains = dv(m.qk_gains), dv(m.post_gains)
         self.taps_w, self.mhc_affine = dv(m.taps_w), dv(m.mhc_affine)
@@ -375,6 +396,7 @@ class Decoder:
                     needle.quantize_rows_dev(dq, ds, hm, hk * c.frames, c.head_dim, c.head_dim)
         self.mem_of = np.arange(self.batch)
         self.mem_index = None
+        self._mem_index_buf.copy_(torch.arange(self._mem_index_buf.numel(), dtype=torch.int32))  # graphs that read it
         torch.cuda.synchronize()
 
     def encoder_states_device(self, seed, stream):
@@ -612,19 +634,25 @@ class Decoder:
         self.pages.copy_(torch.from_numpy(pt))
         s = cq._stream()
         if copies:
-            cp = torch.as_tensor(np.array(copies, np.int32).T.copy(), device=dev)
-            for l in range(c.layers):
-                for q, sc in ((self.self_k[l], self.self_ks[l]), (self.self_v[l], self.self_vs[l])):
-                    check(lib().kv_page_copy_dev(_ptr(q), _ptr(sc), _ptr(cp[0]), _ptr(cp[1]), len(copies), R, c.dim,
-                                                 c.head_dim, self.pool_pages, s))
+            # every layer's K and V pool at once: pool k of the 2 * layers
+            # is pages [k * pool_pages, (k + 1) * pool_pages) of one array
+            npool = 2 * c.layers
+            base = np.arange(npool, dtype=np.int64)[:, None] * self.pool_pages
+            cp = np.array(copies, np.int64).T
+            src, dst = (cp[0][None, :] + base).ravel(), (cp[1][None, :] + base).ravel()
+            cpd = torch.as_tensor(np.stack([src, dst]).astype(np.int32), device=dev)
+            check(lib().kv_page_copy_dev(_ptr(self._self_q), _ptr(self._self_s), _ptr(cpd[0]), _ptr(cpd[1]), src.size,
+                                         R, c.dim, c.head_dim, npool * self.pool_pages, s))
         if self.hist is not None:
-            par = torch.as_tensor(np.asarray(parents, np.int32), device=dev)
+            # row l * B + b of every layer's history takes row l * B + parents[b]
+            L = c.layers
+            idx = (np.arange(L, dtype=np.int64)[:, None] * B + np.asarray(parents, np.int64)[None, :]).ravel()
+            par = torch.as_tensor(idx.astype(np.int32), device=dev)
             width = self.hist[0][0].numel()
             if getattr(self, "_hist_tmp", None) is None:
-                self._hist_tmp = torch.empty_like(self.hist[0])
-            for h in self.hist:
-                check(lib().nd_gather_rows_dev(_ptr(self._hist_tmp), _ptr(h), _ptr(par), B, width, s))
-                check(lib().nd_gather_rows_dev(_ptr(h), _ptr(self._hist_tmp), None, B, width, s))
+                self._hist_tmp = torch.empty_like(self._hist_all)
+            check(lib().nd_gather_rows_dev(_ptr(self._hist_tmp), _ptr(self._hist_all), _ptr(par), L * B, width, s))
+            check(lib().nd_gather_rows_dev(_ptr(self._hist_all), _ptr(self._hist_tmp), None, L * B, width, s))
         self.fork_copies = len(copies)
 
     def fork(self, parents):
@@ -663,7 +691,8 @@ class Decoder:
                                                c.max_pos, c.dim, c.head_dim, s))
         self.mem_of = self.mem_of[parents]
         blocks = (self.mem_of[:, None] * hk + np.arange(hk)[None, :]).astype(np.int32).reshape(-1)
-        self.mem_index = torch.as_tensor(blocks, device=dev)
+        self._mem_index_buf.copy_(torch.from_numpy(blocks))
+        self.mem_index = self._mem_index_buf
         self.tok.copy_(self.tok.index_select(0, par.long()))
         self.pos.copy_(self.pos.index_select(0, par.long()))
         self.done.copy_(self.done.index_select(0, par.long()))

@@ -93,14 +93,14 @@ def test_quantize_rows_misuse_through_the_abi():
 
 
 def test_noalloc_reorder_refuses_oversize_before_the_device():
-    # kv_reorder_noalloc_dev checks its temporaries against its 64 MiB array
+    # kv_reorder_noalloc_dev checks its temporaries against its 16 MiB array
     # before any device call: 256 streams x 512 rows x 512 codes exceed it
     from ctypes import c_void_p
 
     p = c_void_p(256)  # never dereferenced: the size check comes first
     with pytest.raises(gw.CQPanic) as e:
         _lib.check(_lib.lib().kv_reorder_noalloc_dev(p, p, p, p, 256, 512, 512, 64, None))
-    assert "67108864" in str(e.value)
+    assert "16777216" in str(e.value)
 
 
 @pytest.mark.parametrize("eos,done", [(-1, True), (16384, True), (5, False)])

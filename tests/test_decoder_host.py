@@ -91,6 +91,51 @@ def test_fork_page_tables_match_deep_copies():
         _simulate_forks(seed, streams=6, per=8, rows=4, rounds=40)
 
 
+def _fork_page_tables_in_turn(pt, parents, pos, page_rows, pool_pages):
+    """fork_page_tables one reference at a time, in stream-then-page order:
+    each page a stream must own from pos // page_rows on is replaced by the
+    smallest free page while another entry still references it."""
+    import numpy as np
+
+    pt = np.asarray(pt, np.int32)[np.asarray(parents, np.int64)].copy()
+    streams, per = pt.shape
+    counts = np.bincount(pt.ravel(), minlength=pool_pages)
+    free = list(np.flatnonzero(counts == 0)[::-1])
+    copies = []
+    for b in range(streams):
+        lp0 = min(int(pos[b]) // page_rows, per)
+        for lp in range(lp0, per):
+            ph = int(pt[b, lp])
+            if counts[ph] > 1:
+                nf = int(free.pop())
+                counts[ph] -= 1
+                counts[nf] += 1
+                pt[b, lp] = nf
+                if lp == lp0 and pos[b] % page_rows:
+                    copies.append((ph, nf))
+    return pt, copies
+
+
+def test_fork_page_tables_equal_the_reference_at_a_time_form():
+    # the vectorised bookkeeping gives the same tables and copies as taking
+    # the references one at a time, over random beam rounds (256 streams of
+    # 16 pages of 16 rows, as the decoder's batch-256 paged step)
+    import numpy as np
+
+    g = np.random.default_rng(7)
+    streams, per, rows = 256, 16, 16
+    pool = streams * per
+    pt = np.arange(pool, dtype=np.int32).reshape(streams, per)
+    pos = np.zeros(streams, np.int64)
+    for _ in range(30):
+        pos = np.minimum(pos + g.integers(0, 24, size=streams), per * rows)
+        parents = g.integers(0, streams, size=streams)
+        want, wc = _fork_page_tables_in_turn(pt, parents, pos[parents], rows, pool)
+        got, gc = dec.fork_page_tables(pt, parents, pos[parents], rows, pool)
+        assert np.array_equal(got, want) and gc == wc
+        pt, pos = got, pos[parents]
+
+
 def test_fork_page_tables_no_copy_on_boundaries():
     import numpy as np
 
