@@ -171,6 +171,42 @@ def test_capture_at_a_later_position_keeps_the_taps():
         assert list(a[s]) + list(b[s]) == want, s
 
 
+def test_graph_captured_after_a_fork_replays_after_another():
+    # a step graph captured after one fork and replayed after a second: the
+    # graph reads the page tables, the cross-memory index and the tap
+    # histories in place, so every stream still continues as its oracle fork
+    cfg = dec.DecoderConfig(**SMALL, **FEATURES["all"])
+    model = dec.make_model(23, cfg)
+    batch = 4
+    d = dec.Decoder(model, batch)
+    d.set_memory(23)
+    ref = decoder_ref.RefDecoder(model)
+    states = [ref.state(ref.build_memory(dec.encoder_states(23, cfg, b))) for b in range(batch)]
+    first = [3, 4, 5, 6]
+    d.reset(first)
+    got = d.resume(7).cpu().numpy()
+    last = []
+    for b in range(batch):
+        want, _, _ = states[b].greedy(first[b], 7)
+        assert list(got[b]) == want, b
+        last.append(want[-1])
+    for k, parents in enumerate(([1, 1, 3, 0], [2, 0, 0, 3])):
+        d.fork(parents)
+        states = [states[p].fork() for p in parents]
+        last = [last[p] for p in parents]
+        if k == 0:
+            g = d.capture()
+    toks = []
+    for _ in range(6):
+        g.replay()
+        d.steps += 1
+        toks.append(d.tok.cpu().numpy().copy())
+    got = np.stack(toks, 1)
+    for b in range(batch):
+        want, _, _ = states[b].greedy(last[b], 6)
+        assert list(got[b]) == want, (b, list(got[b]), want)
+
+
 def test_fork_plain_config_paged():
     # the synthetic decoder (no features) on the paged step forks by pages too
     cfg = dec.DecoderConfig(**SMALL)
