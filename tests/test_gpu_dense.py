@@ -18,9 +18,10 @@ Two checks per case:
 Covers the encoder's batched shapes (2048x512 and 512x2048 at 2 and 4 bits,
 375 / 1500 / 12000 activations, the last sampled: each activation's product
 is independent of the others), ragged activation counts, Rows views that
-start and end mid-block, groups of 32 to 256 with padded inputs, GEMMs over
+start and end mid-block, groups of 32 to 1024 with padded inputs, GEMMs over
 shared inputs (one rotation), mixed GEMMs of Dense and lut views, and the
-nibble fallback under 16 activations (bit for bit Exact)."""
+nibble fallback under 16 activations and outside groups 32..1024 (bit for
+bit Exact)."""
 
 import numpy as np
 import pytest
