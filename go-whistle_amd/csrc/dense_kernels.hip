@@ -8,7 +8,7 @@
 // zero-padded to groups * G, the plain FWHT in stage order h = 1, 2, ...,
 // G/2, times 1/sqrt(G) rounded once). Written densely it is Y = Xh * W^T
 // with W[r][k] = norm[r][k / G] * codebook[idx(r, k)], which this form
-// computes in two launches:
+// computes in two launches (three where K is split):
 //   1. dense_rotate_kernel writes Xh [activation][kpad] fp32 into a
 //      workspace, bit for bit rotate's values (the FWHT in registers, a
 //      wavefront per group); columns past groups * G (up to a multiple of
