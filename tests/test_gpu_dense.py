@@ -21,7 +21,8 @@ is independent of the others), ragged activation counts, Rows views that
 start and end mid-block, groups of 32 to 1024 with padded inputs, GEMMs over
 shared inputs (one rotation), mixed GEMMs of Dense and lut views, and the
 nibble fallback under 16 activations and outside groups 32..1024 (bit for
-bit Exact)."""
+bit Exact), and NaN and Inf activations (non-finite outputs for those, the
+bars for the activations that share their tiles)."""
 
 import numpy as np
 import pytest
@@ -220,3 +221,25 @@ def test_dense_small_groups_and_misuse():
         m.gemm_dev(z, z, -1)
     with pytest.raises(gw.CQDeviceError):  # fused products run the lut kernel
         cq.gemms_fused_dev([cq.New(synth.random_packed(g, 128, 256, 128, 4)).Dense()], [z], z, 32, norm_gain=z)
+
+
+def test_dense_non_finite_activations():
+    # NaN and +-Inf activations (in both 128-activation tiles): the rotation
+    # spreads them over their group, so every output of that activation is
+    # non-finite, as in Exact (whose NaN and Inf may fall differently: the
+    # sums run in another order); the activations beside them in the same
+    # tiles keep the bar
+    g = synth.rng(91)
+    p = synth.random_packed(g, 512, 512, 128, 4, sigma=0.05)
+    m, o = cq.New(p).Dense(), orc.OMatrix.new(p)
+    rows = 200
+    x = g.standard_normal((rows, 512)).astype(np.float32)
+    bad = {3: (10, np.nan), 70: (300, np.inf), 150: (0, -np.inf), 199: (511, np.nan)}
+    for t, (k, v) in bad.items():
+        x[t, k] = v
+    got = dense_gemm(m, x, rows)
+    want = o.gemm(x.ravel(), rows, orc.NIBBLE4).reshape(rows, -1)
+    for t in bad:
+        assert not np.isfinite(got[t]).any() and not np.isfinite(want[t]).any(), t
+    good = np.array([t for t in range(rows) if t not in bad])
+    check(got[good], x, p, o, good)
