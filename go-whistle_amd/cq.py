@@ -262,6 +262,6 @@ class Batch:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value:
+        if h is not None and h.value and lib is not None:  # module globals are gone at interpreter exit
             lib().cq_batch_free(h)
             self._h = None
