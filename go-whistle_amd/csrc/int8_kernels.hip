@@ -1386,12 +1386,20 @@ __global__ __launch_bounds__(64) void attend_ring_kernel(AttendArgs a, int swz) 
         const int8_t *slot = sl + lane;
         const float *wj = s + j0;
         if (cnt == JC) {
-            float cd[JC];
+            // Every code and weight read of the chunk goes out before the
+            // first product: left to itself the compiler reused 8 registers
+            // for the codes and waited on each 8 reads in turn (batch-256
+            // cross call 89.5 -> 86.8 us, bit for bit the same).
+            int ci[JC];
             float4 wv[JC / 4];
 #pragma unroll
-            for (int k = 0; k < JC; ++k) cd[k] = static_cast<float>(slot[k * ROW]);
+            for (int k = 0; k < JC; ++k) ci[k] = slot[k * ROW];
 #pragma unroll
             for (int q = 0; q < JC / 4; ++q) wv[q] = *reinterpret_cast<const float4 *>(wj + 4 * q);
+            __builtin_amdgcn_sched_barrier(0);
+            float cd[JC];
+#pragma unroll
+            for (int k = 0; k < JC; ++k) cd[k] = static_cast<float>(ci[k]);
 #pragma unroll
             for (int q = 0; q < JC / 4; ++q) {
                 const float p0 = wv[q].x * cd[4 * q], p1 = wv[q].y * cd[4 * q + 1];
