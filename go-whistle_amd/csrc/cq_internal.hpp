@@ -15,7 +15,24 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace cqhip {
+
+// A kernel's dynamic-LDS limit, set once per device (the attribute belongs to
+// the function on the current device; `done` holds one bit per device
+// ordinal below 64, higher ordinals set it on every launch). Concurrent
+// first launches both set it: the write is idempotent.
+inline hipError_t lds_limit_once(const void *fn, int bytes, std::atomic<unsigned long long> &done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const unsigned long long bit = dev >= 0 && dev < 64 ? 1ULL << dev : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+    return e;
+}
 
 constexpr int kBlockRows = 64;   // rows per block: one per lane of a wavefront
 constexpr int kThreads = 256;    // threads per workgroup: four wavefronts

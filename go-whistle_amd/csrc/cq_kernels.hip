@@ -337,13 +337,9 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProdArgs a) {
 
 template <int BITS, int GB, int MODE>
 hipError_t launch_one(const ProdArgs &a, size_t lds, hipStream_t stream) {
-    static bool attr_set = false;  // benign race: the attribute write is idempotent
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&product_kernel<BITS, GB, MODE>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<unsigned long long> attr{0};
+    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&product_kernel<BITS, GB, MODE>), 160 * 1024, attr))
+        return e;
     for (int r0 = 0; r0 < a.rows; r0 += 65535) {
         ProdArgs b = a;
         b.rows = min(65535, a.rows - r0);

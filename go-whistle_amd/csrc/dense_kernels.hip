@@ -332,7 +332,8 @@ hipError_t launch_dense_rotate(const DenseRotArgs &r, hipStream_t s) {
 hipError_t launch_dense(const DenseArgs &a, int bits, hipStream_t s) {
     const void *fn = bits == 4 ? reinterpret_cast<const void *>(&dense_mfma_kernel<4>)
                                : reinterpret_cast<const void *>(&dense_mfma_kernel<2>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kDenseLds));
+    static std::atomic<unsigned long long> attr[2] = {{0}, {0}};
+    hipError_t e = lds_limit_once(fn, static_cast<int>(kDenseLds), attr[bits == 4]);
     if (e != hipSuccess) return e;
     const dim3 grid(a.tiles_m * a.tiles_n * a.ksplit);
     if (bits == 4)

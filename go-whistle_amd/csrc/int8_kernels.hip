@@ -1467,13 +1467,8 @@ hipError_t launch_quantize_rows(int8_t *q, float *s, const float *x, long long c
 
 template <int VD, int JC>
 hipError_t launch_attend_stream(const AttendArgs &a, int rs, size_t lds, hipStream_t stream) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_stream_kernel<VD, JC>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<unsigned long long> attr{0};
+    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&attend_stream_kernel<VD, JC>), 152 * 1024, attr)) return e;
     const long long wgs = static_cast<long long>(a.heads) * a.t * a.batch;
     hipLaunchKernelGGL((attend_stream_kernel<VD, JC>), dim3(static_cast<unsigned>(wgs)), dim3(kAttThreads), lds,
                        stream, a, rs, a.batch >= 8 ? 1 : 0);
@@ -1503,13 +1498,8 @@ bool stream_plan(const AttendArgs &a, bool resident, int &rs, size_t &lds) {
 
 template <int NW, int JC, bool RES>
 hipError_t launch_attend_chain(const AttendArgs &a, int rs, size_t lds, hipStream_t stream) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_chain_kernel<NW, JC, RES>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<unsigned long long> attr{0};
+    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&attend_chain_kernel<NW, JC, RES>), 152 * 1024, attr)) return e;
     const long long wgs = static_cast<long long>(a.heads) * a.t * a.batch;
     hipLaunchKernelGGL((attend_chain_kernel<NW, JC, RES>), dim3(static_cast<unsigned>(wgs)), dim3(64 * NW), lds,
                        stream, a, rs, a.batch >= 8 ? 1 : 0);
@@ -1518,13 +1508,8 @@ hipError_t launch_attend_chain(const AttendArgs &a, int rs, size_t lds, hipStrea
 
 template <int RS>
 hipError_t launch_attend_ring(const AttendArgs &a, size_t lds, hipStream_t stream) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_ring_kernel<RS>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<unsigned long long> attr{0};
+    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&attend_ring_kernel<RS>), 152 * 1024, attr)) return e;
     const long long wgs = static_cast<long long>(a.heads) * a.t * a.batch;
     hipLaunchKernelGGL((attend_ring_kernel<RS>), dim3(static_cast<unsigned>(wgs)), dim3(64), lds, stream, a,
                        a.batch >= 8 ? 1 : 0);
@@ -1589,14 +1574,9 @@ hipError_t launch_attend_int8(const AttendArgs &args, hipStream_t stream) {
     const bool one_chunk = a.vchunk >= a.nk_max;
     const size_t vbytes = (one_chunk ? 1 : 2) * static_cast<size_t>(a.vchunk) * a.vd;
     const size_t lds = with_pages(sizeof(float) * static_cast<size_t>((a.nk_max + 3) & ~3) + vbytes);
-    static bool attr = false;
-    if (!attr) {
-        // dynamic LDS beside the kernel's static arrays: 96 KiB of values + up to 8192 logits
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 132 * 1024);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    // dynamic LDS beside the kernel's static arrays: 96 KiB of values + up to 8192 logits
+    static std::atomic<unsigned long long> attr{0};
+    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&attend_kernel), 132 * 1024, attr)) return e;
     hipLaunchKernelGGL(attend_kernel, dim3(a.heads, a.t, a.batch), dim3(kAttThreads), lds, stream, a);
     return hipGetLastError();
 }

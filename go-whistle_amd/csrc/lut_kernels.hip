@@ -840,13 +840,9 @@ __global__ __launch_bounds__(1024) void lut_kernel_wide(LutLaunch a) {
 
 template <int BITS, int GB, int V>
 hipError_t launch_wide(const LutLaunch &a, int gx, int gy, size_t lds, hipStream_t s) {
-    static bool attr = false;  // idempotent attribute write; a race is benign
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_kernel_wide<BITS, GB, V>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<unsigned long long> attr{0};
+    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&lut_kernel_wide<BITS, GB, V>), 160 * 1024, attr))
+        return e;
     hipLaunchKernelGGL((lut_kernel_wide<BITS, GB, V>), dim3(gx, gy, a.njobs), dim3(64 * a.waves), lds, s, a);
     return hipGetLastError();
 }
@@ -863,12 +859,8 @@ hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, h
     const bool dev = a.dunits != nullptr;
     const void *fn = dev ? reinterpret_cast<const void *>(&lut_kernel<BITS, GB, true>)
                          : reinterpret_cast<const void *>(&lut_kernel<BITS, GB, false>);
-    static bool attr[2] = {false, false};  // idempotent attribute write; a race is benign
-    if (!attr[dev]) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        attr[dev] = true;
-    }
+    static std::atomic<unsigned long long> attr[2] = {{0}, {0}};
+    if (hipError_t e = lds_limit_once(fn, 160 * 1024, attr[dev])) return e;
     if (dev)
         hipLaunchKernelGGL((lut_kernel<BITS, GB, true>), dim3(gx), dim3(64 * waves), lds, s, a);
     else

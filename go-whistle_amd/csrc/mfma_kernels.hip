@@ -527,14 +527,11 @@ size_t mfma_lds_bytes2() {
 
 template <int BITS, int TA>
 hipError_t launch_mfma_t(const LutLaunch &a, int wg, int act_tiles, hipStream_t s) {
-    static bool attr = false;  // idempotent attribute write; a race is benign
+    static std::atomic<unsigned long long> attr{0};
     const size_t lds = mfma_lds_bytes2<BITS, TA>();
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_mfma_kernel<BITS, TA>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&lut_mfma_kernel<BITS, TA>), static_cast<int>(lds),
+                                      attr))
+        return e;
     hipLaunchKernelGGL((lut_mfma_kernel<BITS, TA>), dim3(wg, act_tiles), dim3(kMfmaThreads), lds, s, a);
     return hipGetLastError();
 }
@@ -1460,14 +1457,10 @@ hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStr
         hipLaunchKernelGGL((lut_tables_kernel<BITS, 8>), dim3(t.tiles * 32 / 8, t.groups), dim3(256), 0, s, t);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    static bool attr = false;  // idempotent attribute write; a race is benign
-    if (!attr) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_mfma_tab_kernel<BITS>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(tab_lds_bytes<BITS>(kTabMaxGroups)));
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<unsigned long long> attr{0};
+    e = lds_limit_once(reinterpret_cast<const void *>(&lut_mfma_tab_kernel<BITS>),
+                       static_cast<int>(tab_lds_bytes<BITS>(kTabMaxGroups)), attr);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), dim3(8 * ((a.tab_at * blocks + 7) / 8)), dim3(64 * kTabWaves),
                        tab_lds_bytes<BITS>(t.groups), s, a);
     return hipGetLastError();
