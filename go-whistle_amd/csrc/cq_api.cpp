@@ -253,6 +253,10 @@ void apply_fuse(JobDesc &j, const Fuse *f, int k) {
 constexpr int kLutTile = 4;     // blocks per tile of the lut kernel
 constexpr int kLutChunk = 4;    // groups per LDS chunk
 constexpr int kLutMaxBpw = 16;  // most blocks per workgroup
+// LDS a chunk may take when a launch widens its chunks (six workgroups of the
+// 2-bit kernel per CU; wider chunks lost: 16 groups of 512x2048 CQ2 at 256
+// activations 25.5 us, 8 groups of 512x2048 CQ4 36.5 us against 29.7 with 4)
+constexpr size_t kLutChunkLds = 26 * 1024;
 
 int lut_chunk(int groups_max) { return std::min(kLutChunk, std::max(1, groups_max)); }
 
@@ -302,6 +306,13 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     for (int k = 0; k < a.njobs; ++k) units += (a.jobs[k].nblk + a.bpw - 1) / a.bpw;
     a.tb = kLutTile;
     a.gc = lut_chunk(groups_max);
+    // Wider rows take their tables in fewer chunks where the LDS still holds
+    // the kernel's workgroups: each chunk costs a table build, two barriers
+    // and a pass of the fold (the batch-256 decode step's FFN-down, 512x2048
+    // CQ2 at 256 activations, 21.5 -> 20.1 us with 8 groups a chunk).
+    while (a.gc * 2 <= groups_max &&
+           lut_lds_bytes(s0.width, s0.group_bytes, a.gc * 2, kLutTile, a.bpw) <= kLutChunkLds)
+        a.gc *= 2;
     // A launch that fills at most a quarter of the CUs is latency-bound: wide
     // rows then take their tables in fewer chunks (up to 64 KiB of tables,
     // all 16 groups of a 4-bit row of 2048 in one chunk of 16 wavefronts),
