@@ -99,6 +99,7 @@ SIGNATURES = {
     "nd_sigmoid_gate_dev": (c_int, [c_void_p, c_void_p, c_longlong, c_void_p]),
     "nd_rms_unit_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "nd_mhc_heads_dev": (c_int, [c_void_p] * 8 + [c_int, c_int, c_int, c_void_p, c_void_p]),
+    "nd_mhc_heads_stacked_dev": (c_int, [c_void_p] * 6 + [c_int, c_int, c_int, c_void_p, c_void_p]),
     "nd_mhc_mix_dev": (c_int, [c_void_p] * 6 + [c_int, c_int, c_int, c_void_p]),
     "nd_hadamard_mlp_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, POINTER(c_void_p),
                                     POINTER(c_void_p), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

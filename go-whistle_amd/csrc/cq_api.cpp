@@ -1906,6 +1906,29 @@ int nd_mhc_heads_dev(float *h_pre, float *h_post, float *h_res, float *u, const 
     return CQ_OK;
 }
 
+int nd_mhc_heads_stacked_dev(float *h_pre, float *h_post, float *h_res, float *u, const float *logits,
+                             const float *stream_rows, int rows, int lanes, int dim, const float *affine, void *stream) {
+    if (rows < 0 || !mhc_shape_ok(lanes, dim))
+        return fail(CQ_ERR_MISUSE, "needle: mHC heads of %d rows, %d lanes of %d", rows, lanes, dim);
+    if (rows == 0) return CQ_OK;
+    MhcArgs m;
+    std::memset(&m, 0, sizeof m);
+    m.h_pre = h_pre;
+    m.h_post = h_post;
+    m.h_res = h_res;
+    m.u = u;
+    m.pre_logits = logits;
+    m.post_logits = logits + lanes;
+    m.res_logits = logits + 2 * lanes;
+    m.logit_stride = 2 * lanes + lanes * lanes;
+    m.stream = stream_rows;
+    m.affine = affine;
+    m.lanes = lanes;
+    m.dim = dim;
+    HIP_TRY(launch_mhc_heads(m, rows, static_cast<hipStream_t>(stream)), "mHC heads launch");
+    return CQ_OK;
+}
+
 int nd_mhc_mix_dev(float *out, const float *stream_rows, const float *h_res, const float *h_post,
                    const float *block_out, const float *u, int rows, int lanes, int dim, void *stream) {
     if (rows < 0 || !mhc_shape_ok(lanes, dim))

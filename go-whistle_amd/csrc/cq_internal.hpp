@@ -344,6 +344,7 @@ struct MhcArgs {
     float *h_pre, *h_post, *h_res, *u, *out;
     const float *pre_logits, *post_logits, *res_logits, *stream, *block_out, *affine;
     int lanes, dim;
+    int logit_stride;  // floats from one row's logits to the next: 0 for the three separate arrays (lanes, lanes, lanes^2)
 };
 bool mhc_shape_ok(int lanes, int dim);
 hipError_t launch_rms_unit(float *dst, const float *x, int rows, int dim, hipStream_t s);

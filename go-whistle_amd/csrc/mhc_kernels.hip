@@ -80,8 +80,9 @@ __global__ __launch_bounds__(256) void mhc_heads_kernel(MhcArgs m) {
     __shared__ float hp[kMhcMaxLanes], kr[kMhcMaxLanes * kMhcMaxLanes];
     const int i = blockIdx.x, tid = threadIdx.x, n = m.lanes, dim = m.dim;
     const float *A = m.affine;  // {a_pre, a_post, a_res, b_pre[n], pre_off[n], b_post[n], post_off[n], b_res[n*n]}
+    const long long ps = m.logit_stride ? m.logit_stride : n, rs = m.logit_stride ? m.logit_stride : n * n;
     if (tid < n) {
-        float p = m.pre_logits[i * n + tid], q = m.post_logits[i * n + tid];
+        float p = m.pre_logits[i * ps + tid], q = m.post_logits[i * ps + tid];
         if (A) {
             const float ap = A[0] * p;
             p = ap + A[3 + tid] + A[3 + n + tid];
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void mhc_heads_kernel(MhcArgs m) {
         m.h_post[i * n + tid] = 2.0f * gate_sigmoid(q);
     }
     if (tid < n * n) {
-        float v = m.res_logits[static_cast<long long>(i) * n * n + tid];
+        float v = m.res_logits[i * rs + tid];
         if (A) {
             const float av = A[2] * v;
             v = av + A[3 + 4 * n + tid];

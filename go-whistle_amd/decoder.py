@@ -104,6 +104,20 @@ def _share(p, cb):
     return p
 
 
+def stack_rows(ps):
+    """The matrices ps (one input width, group and codebook) stacked row-wise
+    into one: its product is theirs, row for row and bit for bit, with one
+    table build per activation instead of one per matrix."""
+    p0 = ps[0]
+    for p in ps[1:]:
+        if (p.In, p.Group, p.Bits, p.Width) != (p0.In, p0.Group, p0.Bits, p0.Width) or \
+                not np.array_equal(np.asarray(p.Codebook), np.asarray(p0.Codebook)):
+            raise ValueError("stacked matrices share their input width, group, width and codebook")
+    return cq.Packed(Out=sum(p.Out for p in ps), In=p0.In, Group=p0.Group, Bits=p0.Bits, Width=p0.Width,
+                     Codebook=p0.Codebook, Index=np.concatenate([np.asarray(p.Index, np.uint8) for p in ps]),
+                     Norms=np.concatenate([np.asarray(p.Norms, np.uint8) for p in ps]))
+
+
 def rope_tables(head_dim, n, theta):
     """NewRope (internal/needle/rope.go:17-44): float32 frequencies, float64
     cos/sin of float32 angles, rounded to float32."""
@@ -282,6 +296,9 @@ class Decoder:
             raise ValueError("the paged step runs heads of 64 and max_pos a multiple of 16")
         self.emb = cq.New(model.emb)
         self.mats = [{n: cq.New(p[n]) for n in p} for p in model.layers]
+        if c.lanes:  # the three phi products as one: their logits side by side per activation
+            for mm, p in zip(self.mats, model.layers):
+                mm["phi"] = cq.New(stack_rows([p[n] for n in PHI_MATS]))
         f32, i8, i32 = torch.float32, torch.int8, torch.int32
         z = lambda *shape, dt=f32: torch.zeros(*shape, dtype=dt, device=device)
         self.gains = torch.from_numpy(model.gains).to(device)
@@ -359,7 +376,7 @@ class Decoder:
             n = c.lanes
             self.lane_s = [z(B, n * c.dim), z(B, n * c.dim)]
             self.nxq = z(B, n * c.dim)
-            self.pl, self.ql, self.rl = z(B, n), z(B, n), z(B, n * n)
+            self.phil = z(B, 2 * n + n * n)  # pre, post, res logits of each activation
             self.hp, self.hq, self.hr = z(B, n), z(B, n), z(B, n * n)
             self.u_mhc, self.blk = z(B, c.dim), z(B, c.dim)
 
@@ -571,9 +588,9 @@ class Decoder:
             h_in = self.x  # the block's input h; with lanes u, which stays unchanged for the mix
             if n:  # the mHC heads and the block input u (mhc.go:196-219)
                 check(L.nd_rms_unit_quant_dev(P(self.nxq), P(cur), B, n * D, s))
-                cq.gemms_dev([m["phi_pre"], m["phi_post"], m["phi_res"]], [self.pl, self.ql, self.rl], self.nxq, B)
-                check(L.nd_mhc_heads_dev(P(self.hp), P(self.hq), P(self.hr), P(self.u_mhc), P(self.pl), P(self.ql),
-                                         P(self.rl), P(cur), B, n, D, P(self.mhc_affine[l]), s))
+                m["phi"].gemm_dev(self.phil, self.nxq, B)
+                check(L.nd_mhc_heads_stacked_dev(P(self.hp), P(self.hq), P(self.hr), P(self.u_mhc), P(self.phil),
+                                                 P(cur), B, n, D, P(self.mhc_affine[l]), s))
                 h_in = self.u_mhc
             cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], h_in, B,
                                norm_gain=self.gains[3 * l])

@@ -103,6 +103,14 @@ def mhc_heads_dev(h_pre, h_post, h_res, u, pre_logits, post_logits, res_logits, 
                                  p(stream), rows, lanes, dim, p(affine), _stream()))
 
 
+def mhc_heads_stacked_dev(h_pre, h_post, h_res, u, logits, stream, rows, lanes, dim, affine=None):
+    """mhc_heads_dev with the logits of each row side by side, rows x (2 lanes
+    + lanes^2): pre, post, res (one product of the stacked φ matrices)."""
+    p = lambda t: c_void_p(t.data_ptr()) if t is not None else None
+    check(lib().nd_mhc_heads_stacked_dev(p(h_pre), p(h_post), p(h_res), p(u), p(logits), p(stream), rows, lanes, dim,
+                                         p(affine), _stream()))
+
+
 def mhc_mix_dev(out, stream, h_res, h_post, block_out, u, rows, lanes, dim):
     """MHC.forward's output stream (mhc.go:229-299)."""
     p = lambda t: c_void_p(t.data_ptr())

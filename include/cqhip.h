@@ -351,6 +351,13 @@ int nd_rms_unit_dev(float *dst, const float *x, int rows, int dim, void *stream)
 int nd_mhc_heads_dev(float *h_pre, float *h_post, float *h_res, float *u, const float *pre_logits,
                      const float *post_logits, const float *res_logits, const float *stream_rows, int rows, int lanes,
                      int dim, const float *affine, void *stream);
+/* nd_mhc_heads_dev with the three φ products' logits in one array, rows x
+ * (2 lanes + lanes^2): pre, post, then res of each row, as one product of
+ * the three φ matrices stacked row-wise gives them (the same outputs bit
+ * for bit; one table build per activation instead of three). */
+int nd_mhc_heads_stacked_dev(float *h_pre, float *h_post, float *h_res, float *u, const float *logits,
+                             const float *stream_rows, int rows, int lanes, int dim, const float *affine,
+                             void *stream);
 /* MHC.forward's output (internal/needle/mhc.go:229-234, 266-299): y =
  * block_out - u, out[i, a] = sum_b h_res[i, a, b] stream[i, b] (b in order)
  * + h_post[i, a] y. out must not be the stream. */

@@ -1,5 +1,5 @@
-"""The mHC pieces on the device (nd_rms_unit_dev, nd_mhc_heads_dev,
-nd_mhc_mix_dev) bit for bit the oracle (float64 exp-domain Sinkhorn with the
+"""The mHC pieces on the device (nd_rms_unit_dev, nd_mhc_heads_dev and its
+stacked-logits form, nd_mhc_mix_dev) bit for bit the oracle (float64 exp-domain Sinkhorn with the
 same exp; the log domain of huge logits within 1e-6), and within 1e-5 of
 upstream's golden fixture (tests/golden/mhc_fixture.npz)."""
 
@@ -77,6 +77,27 @@ def test_random_rows_with_affine(rows, n, dim, scale):
         assert np.max(np.abs(got[2].reshape(rows, n, n).sum(1) - 1)) <= 4e-7
 
 
+@pytest.mark.parametrize("rows,n,dim,affine", [(7, 4, 512, True), (3, 8, 96, False), (1, 2, 64, True)])
+def test_stacked_logits_equal_separate(rows, n, dim, affine):
+    # nd_mhc_heads_stacked_dev reads row r's logits at r * (2n + n^2): pre,
+    # post, res; the outputs are the separate arrays' bit for bit
+    import torch
+
+    g = np.random.default_rng(rows * 10 + n)
+    pre, post = g.standard_normal((rows, n)).astype(np.float32), g.standard_normal((rows, n)).astype(np.float32)
+    res = g.standard_normal((rows, n * n)).astype(np.float32)
+    stream = g.standard_normal((rows, n, dim)).astype(np.float32)
+    aff = np.concatenate([[0.7, 1.3, 0.9], g.standard_normal(4 * n + n * n) * 0.5]).astype(np.float32) if affine else None
+    want = run_device(pre, post, res, stream, np.zeros((rows, dim), np.float32), rows, n, dim, aff)
+    hp, hq = torch.zeros(rows * n, device="cuda"), torch.zeros(rows * n, device="cuda")
+    hr, u = torch.zeros(rows * n * n, device="cuda"), torch.zeros(rows * dim, device="cuda")
+    stacked = np.concatenate([pre, post, res], axis=1)
+    needle.mhc_heads_stacked_dev(hp, hq, hr, u, _t(stacked), _t(stream), rows, n, dim, None if aff is None else _t(aff))
+    torch.cuda.synchronize()
+    for got, w in zip((hp, hq, hr, u), want[:4]):
+        assert same(got.cpu().numpy(), w)
+
+
 def test_mhc_misuse():
     import torch
 
@@ -85,5 +106,7 @@ def test_mhc_misuse():
     z = torch.zeros(64, device="cuda")
     with pytest.raises(CQPanic):
         needle.mhc_heads_dev(z, z, z, z, z, z, z, z, 1, 9, 4)  # more than 8 lanes
+    with pytest.raises(CQPanic):
+        needle.mhc_heads_stacked_dev(z, z, z, z, z, z, 1, 9, 4)
     with pytest.raises(CQPanic):
         needle.mhc_mix_dev(z, z, z, z, z, z, 1, 4, 4)  # in place
