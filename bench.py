@@ -170,11 +170,45 @@ INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA, ops/s
 FP32_PEAK_FLOPS = 157.3e12  # MI355X dense fp32 MFMA, flop/s
 
 
+def _gemm_times(torch, call, reps):
+    """(graph-replayed us per call, eager us per call) of `call`, each after
+    20 ms of the same work."""
+    call()
+    torch.cuda.synchronize()
+    prewarm(torch, call, 20)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    eager = e0.elapsed_time(e1) * 1e3 / reps
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            call()
+    graph.replay()
+    torch.cuda.synchronize()
+    prewarm(torch, graph.replay, 20)
+    e0.record()
+    for _ in range(4):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (4 * reps)
+    del graph
+    return us, eager
+
+
 def batched_gemm_leg(gw, torch, reps=5):
     """The encoder's batched CQ GEMMs: X [M x In] ~N(0, 1) times 4/2-bit
     2048x512 and 512x2048 (FFN up/down), M in {375, 1500, 12000}, through
-    cq_gemm_dev (which picks the lut kernel or its MFMA form), each timed
-    over `reps` calls after 20 ms of the same calls. Flops are the
+    cq_gemm_dev (which picks the lut kernel or its MFMA form). `us` is the
+    GPU time of one call: a graph of `reps` calls replayed after 20 ms of
+    replays; `us_eager` times `reps` calls queued from Python one after the
+    other (at a few hundred activations the host's per-call work, the ctypes
+    call and the library's launches and workspace lease, is then part of it).
+    Flops are the
     dense equivalent 2*M*Out*In; for the MFMA forms, mfma_util is the int8 MFMA
     work it issues (one 32x32x32 product per 64-row block, 64-activation tile,
     position and 32x32 quadrant) over the time, against 5.0 POP/s. dense_f32
@@ -190,18 +224,10 @@ def batched_gemm_leg(gw, torch, reps=5):
             for M in (375, 1500, 12000):
                 x = torch.randn(M, i, device="cuda")
                 y = torch.empty(M, o, device="cuda")
-                m.gemm_dev(y, x, M)
-                torch.cuda.synchronize()
-                prewarm(torch, lambda: m.gemm_dev(y, x, M), 20)
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                for _ in range(reps):
-                    m.gemm_dev(y, x, M)
-                e1.record()
-                torch.cuda.synchronize()
-                us = e0.elapsed_time(e1) * 1e3 / reps
+                us, us_eager = _gemm_times(torch, lambda: m.gemm_dev(y, x, M), reps)
                 path = m.gemm_path(M)
-                rec = {"path": path, "us": round(us, 2), "dense_TFLOPs": round(2.0 * M * o * i / us / 1e6, 2)}
+                rec = {"path": path, "us": round(us, 2), "us_eager": round(us_eager, 2),
+                       "dense_TFLOPs": round(2.0 * M * o * i / us / 1e6, 2)}
                 if path in ("lut-mfma", "lut-mfma-split", "lut-mfma-tab"):
                     # one 32x32x32 int8 product per 32 weight rows, 32 activations and table position
                     # (the 512-row form pads activations to its 64-wide tiles, the split and table
@@ -216,17 +242,9 @@ def batched_gemm_leg(gw, torch, reps=5):
                 # MFMA (v_mfma_f32_32x32x2_f32 over 128 x 128 tiles, the
                 # activations rotated first), within float32 rounding of Exact.
                 d = m.Dense()
-                d.gemm_dev(y, x, M)
-                torch.cuda.synchronize()
-                prewarm(torch, lambda: d.gemm_dev(y, x, M), 20)
-                e0.record()
-                for _ in range(reps):
-                    d.gemm_dev(y, x, M)
-                e1.record()
-                torch.cuda.synchronize()
-                dus = e0.elapsed_time(e1) * 1e3 / reps
+                dus, dus_eager = _gemm_times(torch, lambda: d.gemm_dev(y, x, M), reps)
                 issued = 2.0 * (-(-M // 128) * 128) * (-(-o // 128) * 128) * (-(-i // 64) * 64)
-                rec["dense_f32"] = {"path": d.gemm_path(M), "us": round(dus, 2),
+                rec["dense_f32"] = {"path": d.gemm_path(M), "us": round(dus, 2), "us_eager": round(dus_eager, 2),
                                     "dense_TFLOPs": round(2.0 * M * o * i / dus / 1e6, 2),
                                     "mfma_util_fp32": round(issued / (dus * 1e-6) / FP32_PEAK_FLOPS, 4)}
                 out[f"cq{bits}_{o}x{i}_M{M}"] = rec
