@@ -540,7 +540,11 @@ int ws_acquire(size_t bytes, hipStream_t stream, WsLease &l) {
     }
     std::unique_ptr<Workspace> w(new Workspace);
     if (int e = ws_alloc(w.get(), bytes, false)) return e;
-    const hipError_t e = hipEventCreateWithFlags(&w->done, hipEventDisableTiming);
+    // Device scope is enough for this event: it only tells when the lease's
+    // kernels are done with the buffer, for reuse on another stream of the
+    // same device or hipFree; a system-scope fence behind every eager
+    // product would write back the L2s between two launches.
+    const hipError_t e = hipEventCreateWithFlags(&w->done, hipEventDisableTiming | hipEventDisableSystemFence);
     if (e != hipSuccess) {
         (void)hipFree(w->buf);
         return hip_fail(e, "workspace event");
