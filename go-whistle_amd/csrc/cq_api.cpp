@@ -327,12 +327,44 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     // spread over more SIMDs.
     a.waves = kLutWaves;
     a.vsplit = 1;
+    int gx = wg;
     if (units * rows * 4 <= device_info().cus && a.bpw == 1 && (s0.group_bytes == 32 || s0.group_bytes == 64)) {
         if (a.gc >= 8) {
             a.waves = std::min(16, a.gc);
         } else if (a.gc >= 2) {
             a.waves = 2 * a.gc;
             a.vsplit = 2;
+        }
+    } else if (s0.group_bytes == 32 || s0.group_bytes == 64) {
+        // Launches of up to one workgroup per CU at the widest form also take
+        // it: units of bp blocks (the fewest that keep the grid to one
+        // round), all the groups in one chunk, a wavefront per (block, group
+        // share), up to 16. Each activation's tables are then built once per
+        // unit of up to 8 blocks instead of once per unit of the 4-wavefront
+        // kernel's 1-2 (measured on MI355X at 256 activations: 512x2048 CQ2
+        // with the residual 20.5 -> 17.2 us, 512x512 CQ4 gated with the
+        // residual 11.5 -> 10.4 us, 24x2048 CQ4 15.0 -> 9.0 us; at 32-64
+        // activations 512x2048 CQ4 15.0 -> 9.1 us, 2048x512 CQ4 8.2 -> 7.5
+        // us; bit for bit the same). A grid of more than one round of such
+        // workgroups lost (2048x512 CQ4 at 96 activations 16.1 -> 18.2 us).
+        int bp = 1;
+        const auto grid = [&](int b) {
+            long long u = 0;
+            for (int k = 0; k < a.njobs; ++k) u += (a.jobs[k].nblk + b - 1) / b;
+            return u * rows;
+        };
+        while (bp < 8 && grid(bp) > device_info().cus) bp *= 2;
+        bp = balanced_blocks(nmax, bp);
+        int g = groups_max;
+        while (g > 1 && lut_lds_bytes(s0.width, s0.group_bytes, g, std::max(kLutTile, bp), bp) > 128 * 1024)
+            g = (g + 1) / 2;
+        const int waves = std::min(16, bp * g);
+        if (grid(bp) <= device_info().cus && waves > kLutWaves) {
+            a.waves = waves;
+            a.bpw = a.bpw_max = bp;
+            a.gc = g;
+            a.tb = std::max(kLutTile, bp);
+            gx = (nmax + bp - 1) / bp;
         }
     }
     const size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, a.gc, a.tb, a.bpw);
@@ -350,7 +382,7 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
                 b.jobs[k].app_pos += r0;
             }
         }
-        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, a.waves, wg, nr, lds, stream), "lut launch");
+        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, a.waves, gx, nr, lds, stream), "lut launch");
     }
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;

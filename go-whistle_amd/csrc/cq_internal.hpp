@@ -130,7 +130,8 @@ struct LutLaunch {
     int wg0[kKernargJobs];       // kernel-argument path: first workgroup of each job
     const JobDesc *djobs;        // device path: job table
     const WorkUnit *dunits;      //              one unit per workgroup
-    int tb;                      // blocks of the lut kernel's term buffer (>= W / 2)
+    int tb;                      // blocks of the lut kernel's term buffer: at least a workgroup's blocks
+                                 // when its wavefronts share blocks
     int gc;                      // groups per LDS chunk
     int bpw_max;                 // LDS sizing: most blocks of any workgroup
     int waves;                   // kernel-argument path: wavefronts per workgroup (> kLutWaves: the wide form)

@@ -823,10 +823,13 @@ __global__ __launch_bounds__(256, (lut_waves_per_simd<BITS, GB>())) void lut_ker
     }
 }
 
-// Latency-bound launches of one-block units (the decode step at batch 1):
-// a.waves wavefronts per workgroup, one per group (V = 1), or two per group
-// each on half its index units (V = 2), so that each wavefront's chain of
-// table lookups is shorter.
+// Latency-bound launches (the decode step at batch 1, and grids of at most
+// one workgroup per CU): a.waves wavefronts per workgroup. V = 1: with one
+// block, a wavefront per group; with a.bpw blocks, wavefronts w take block
+// w / S and groups w % S, w % S + S, ... (S the largest power of two with
+// S * blocks <= waves). V = 2 (one
+// block): two per group, each on half its index units, so that each
+// wavefront's chain of table lookups is shorter.
 template <int BITS, int GB, int V>
 __global__ __launch_bounds__(1024) void lut_kernel_wide(LutLaunch a) {
     const int lane = threadIdx.x & 63;
@@ -851,7 +854,9 @@ template <int BITS, int GB>
 hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, hipStream_t s) {
     if constexpr (GB == 32 || GB == 64) {
         if (a.dunits == nullptr && a.waves > kLutWaves) {
-            if (a.waves != waves || a.waves > 16 || a.bpw != 1) return hipErrorInvalidValue;
+            // a.tb blocks' terms fit in LDS: the wavefronts sharing a block park them there
+            if (a.waves != waves || a.waves > 16 || a.bpw > a.tb || (a.vsplit == 2 && a.bpw != 1))
+                return hipErrorInvalidValue;
             return a.vsplit == 2 ? launch_wide<BITS, GB, 2>(a, gx, gy, lds, s) : launch_wide<BITS, GB, 1>(a, gx, gy, lds, s);
         }
     }

@@ -74,6 +74,29 @@ def test_batch1_wide_units(out, inp, bits):
         assert same_bits(got, o.rows(5, 69).gemm(x, rows, orc.LUT)), rows
 
 
+@pytest.mark.parametrize("out,inp,bits,rows", [(512, 2048, 2, 256), (512, 512, 4, 128), (512, 512, 4, 48),
+                                               (24, 2048, 4, 200), (2048, 512, 4, 48), (1536, 512, 2, 64),
+                                               (600, 1024, 4, 40), (384, 512, 4, 100)])
+def test_one_round_wide_units(out, inp, bits, rows):
+    """Grids of at most one workgroup per CU take the wide form with units
+    of 1-8 blocks: 16 wavefronts on 8 blocks two to a block (512x2048 at
+    256), four or eight to a block, one per group of one block (24x2048),
+    12 wavefronts on units of 3 blocks (384 rows at 100). Bit for bit the
+    oracle, also for a view that cuts blocks."""
+    print(f"one-round wide units {out}x{inp} CQ{bits} rows {rows}", flush=True)
+    g = synth.rng(2500 + out + inp + bits + rows)
+    p = synth.random_packed(g, out, inp, 128, bits, sigma=0.05)
+    m, o = cq.New(p), orc.OMatrix.new(p)
+    assert m.gemm_path(rows) == "lut"
+    x = synth.activations(g, rows, inp)
+    got, want = gemm(m, x, rows), o.gemm(x, rows, orc.LUT)
+    assert same_bits(got, want), first_diff(got, want)
+    lo, hi = 5, min(out, 5 + 300)
+    got = gemm(m.Rows(lo, hi), x, rows)
+    want = o.rows(lo, hi).gemm(x, rows, orc.LUT)
+    assert same_bits(got, want), first_diff(got, want)
+
+
 @pytest.mark.parametrize("shape", TEST_SHAPES)
 @pytest.mark.parametrize("bits", [2, 4])
 def test_small_shapes_all_kernels_bit_exact(shape, bits):

@@ -47,7 +47,7 @@ def _norm(x, gain, rows, dim):
 
 
 @pytest.mark.parametrize("rows,shape,bits", [(1, (512, 512), 4), (5, (2048, 512), 2), (256, (16384, 512), 4),
-                                             (3, (300, 640), 4), (2048, (16384, 512), 2)])
+                                             (3, (300, 640), 4), (2048, (16384, 512), 2), (64, (512, 2048), 4)])
 def test_norm_prologue(rows, shape, bits):
     import torch
 
@@ -67,7 +67,7 @@ def test_norm_prologue(rows, shape, bits):
         assert ms[0].gemm_path(rows) == "lut-mfma-tab"
 
 
-@pytest.mark.parametrize("rows,bits", [(1, 4), (7, 2), (256, 4)])
+@pytest.mark.parametrize("rows,bits", [(1, 4), (7, 2), (48, 4), (40, 2), (256, 4)])
 def test_residual_and_silu_epilogues(rows, bits):
     import torch
 
@@ -132,12 +132,13 @@ def test_append_with_rope():
 
 
 @pytest.mark.parametrize("batch,bits,views", [(1, 4, False), (3, 2, False), (100, 4, False), (256, 4, False),
-                                              (5, 4, True), (300, 2, True)])
+                                              (5, 4, True), (300, 2, True), (64, 4, False), (80, 2, True)])
 def test_append_epilogue(batch, bits, views):
     # The K/V appends riding on the qkv product, bit for bit the product
     # followed by the separate append kernels; batch 1, 100 and 256 cover
     # the kernel's shared-block (4 and 2 wavefronts a block) and one-wavefront
-    # write paths; views: q, k, v as row views of one fused root.
+    # write paths, 64 and 80 its wide form on 8-block units (two wavefronts a
+    # block); views: q, k, v as row views of one fused root.
     import torch
 
     heads, hd, cap = 8, 64, 16
@@ -267,7 +268,8 @@ def test_sigmoid_gate_vs_oracle():
 
 @pytest.mark.parametrize("rows,shape,bits,resid", [(1, (512, 512), 4, True), (6, (512, 2048), 2, True),
                                                    (4, (1024, 512), 4, False), (300, (16384, 512), 4, False),
-                                                   (2048, (16384, 512), 4, True)])
+                                                   (2048, (16384, 512), 4, True), (256, (512, 512), 4, True),
+                                                   (128, (512, 2048), 2, True)])
 def test_gated_product(rows, shape, bits, resid):
     """cq_gemms_gated_dev (x * sigmoid(gate) inside the product, then the
     residual add) bit for bit the separate gate, product and add; at 300
