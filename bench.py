@@ -170,19 +170,21 @@ INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA, ops/s
 FP32_PEAK_FLOPS = 157.3e12  # MI355X dense fp32 MFMA, flop/s
 
 
-def _gemm_times(torch, call, reps):
+def _gemm_times(torch, call, reps, eager_reps=40):
     """(graph-replayed us per call, eager us per call) of `call`, each after
-    20 ms of the same work."""
+    20 ms of the same work: a graph of `reps` calls replayed 4 times, and
+    `eager_reps` calls queued one by one (enough that the first call's host
+    latency does not dominate)."""
     call()
     torch.cuda.synchronize()
     prewarm(torch, call, 20)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
+    for _ in range(eager_reps):
         call()
     e1.record()
     torch.cuda.synchronize()
-    eager = e0.elapsed_time(e1) * 1e3 / reps
+    eager = e0.elapsed_time(e1) * 1e3 / eager_reps
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for _ in range(reps):
@@ -205,9 +207,9 @@ def batched_gemm_leg(gw, torch, reps=5):
     2048x512 and 512x2048 (FFN up/down), M in {375, 1500, 12000}, through
     cq_gemm_dev (which picks the lut kernel or its MFMA form). `us` is the
     GPU time of one call: a graph of `reps` calls replayed after 20 ms of
-    replays; `us_eager` times `reps` calls queued from Python one after the
-    other (at a few hundred activations the host's per-call work, the ctypes
-    call and the library's launches and workspace lease, is then part of it).
+    replays; `us_eager` times 40 calls queued from Python one after the
+    other (the launches' own gaps, and the workspace lease's event between
+    calls, are then part of it).
     Flops are the
     dense equivalent 2*M*Out*In; for the MFMA forms, mfma_util is the int8 MFMA
     work it issues (one 32x32x32 product per 64-row block, 64-activation tile,
