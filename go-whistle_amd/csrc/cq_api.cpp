@@ -751,22 +751,42 @@ bool tab_pays(cq_matrix *const *ms, int n, int rows) {
     return work >= (s0.width == 4 ? kTabMinWork4 : kTabMinWork2) || blocks * ((rows + 31) / 32) >= device_info().cus;
 }
 
+// Row blocks per workgroup of the table form's product: slabs of 4 blocks
+// whose wavefronts share the tile's A operands through LDS (a quarter of the
+// L2 reads) once such workgroups number two per CU or more; below that the
+// workgroup per block spreads wider. Measured on MI355X (one block, against
+// four): 2048x512 CQ4 at 6000 and 12000 activations 188.4 / 359.7 -> 179.5 /
+// 332.2 us, 2048x1024 CQ4 at 12000 809 -> 615 us, the 16384x512 head at 256,
+// 1500 and 12000 66.8 / 315.7 / 2433 -> 64.5 / 297.3 / 2137 us; 2048x512
+// CQ4 at 1500 (376 slab workgroups) 60.0 -> 66.9 us and at 256 (64) 16.4
+// -> 38.3 us.
+int tab_row_blocks(cq_matrix *const *ms, int n, int rows) {
+    long long slabs = 0;
+    for (int k = 0; k < n; ++k) {
+        const int nblk = (ms[k]->row0 + ms[k]->out + kBlockRows - 1) / kBlockRows - ms[k]->row0 / kBlockRows;
+        if (ms[k]->out > 0) slabs += (nblk + 3) / 4;
+    }
+    return slabs * ((rows + 31) / 32) >= 2LL * device_info().cus ? 4 : 1;
+}
+
 int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
             const Fuse *fz = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     LutLaunch a;
     std::memset(&a, 0, sizeof a);
-    int blocks = 0;
+    const int rb = tab_row_blocks(ms, n, rows);
+    int blocks = 0;  // slabs of rb row blocks
     for (int k = 0; k < n; ++k) {
         if (ms[k]->out == 0) continue;
         JobDesc &j = a.jobs[a.njobs];
         fill_job(j, ms[k], x, dsts[k], rows);
         apply_fuse(j, fz, k);
         a.wg0[a.njobs] = blocks;
-        blocks += j.nblk;
+        blocks += (j.nblk + rb - 1) / rb;
         ++a.njobs;
     }
     if (a.njobs == 0 || rows == 0) return CQ_OK;
+    a.tab_rb = rb;
     const int tiles = (rows + 31) / 32;
     TabArgs t;
     std::memset(&t, 0, sizeof t);

@@ -149,6 +149,7 @@ struct LutLaunch {
     const int8_t *tab;
     const float *tstp;
     int tab_at, tab_nb;
+    int tab_rb;  // row blocks per workgroup of the product: 1, or 4 sharing the A operands (tab_nb, wg0 count slabs)
 };
 
 // The table pre-pass of the table form (mfma_kernels.hip): per activation

@@ -1444,6 +1444,250 @@ __global__ __launch_bounds__(64 * kTabWaves) void lut_mfma_tab_kernel(LutLaunch 
     fold_epilogue<FA>(E, t0, nt, blk, lane, y, pk, cv, sv, rv);
 }
 
+// The table form at large grids: a workgroup per (slab of kSaBlocks row
+// blocks, 32-activation tile), wavefront w on block w of the slab, every
+// group in turn. The tile's A operands (its tables, contiguous [group][pair]
+// [plane][1 KiB]) stream once per workgroup through an LDS ring of kSaSlots
+// slots of kSaPairs pairs (global_load_lds, two slots ahead) and all four
+// wavefronts read them there: a quarter of lut_mfma_tab_kernel's L2 -> CU
+// traffic, where every wavefront streams its own. The block's index units,
+// norms and the group's steps also come by DMA, a group ahead, so that no
+// load the compiler tracks is in flight in the loop (it would wait for the
+// DMAs behind it). Each wavefront folds its rows' terms in registers in
+// group order from 0 (lut.go:297-310), then runs the lut kernel's epilogue
+// on its block.
+constexpr int kSaPairs = 8;   // position pairs per ring slot (16 KiB)
+constexpr int kSaSlots = 3;   // ring slots: kSaSlots - 1 in flight while one is read
+constexpr int kSaAhead = kSaSlots - 1;
+constexpr int kSaBlocks = 4;  // row blocks per workgroup, one per wavefront
+constexpr int kSaSlot = kSaPairs * 2048;
+constexpr int kSaDma = kSaSlot / 4096;  // a wavefront's 16-byte DMA loads per slot
+
+// LDS byte offset of a shared-memory pointer (M0 and the DS instructions take it).
+__device__ __forceinline__ unsigned sa_lds(const void *p) {
+    return static_cast<unsigned>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char *)(p)));
+}
+// One 16-byte (or 4-byte) global load per active lane straight into LDS:
+// lane l's bytes land at m0 + 16 l (4 l). Plain loads: the tables are read
+// again by the tile's other slabs.
+__device__ __forceinline__ void sa_dma16(const void *src, unsigned m0) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void sa_dma4(const void *src, unsigned m0) {
+    asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+// s_waitcnt vmcnt(n), n <= 15 (gfx9 encoding; lgkm and exp counts untouched).
+__device__ __forceinline__ void sa_wait_vm(int n) {
+    switch (n) {
+#define CQ_SA_WAIT(K) \
+    case K: __builtin_amdgcn_s_waitcnt((K) | (7 << 4) | (15 << 8)); break;
+        CQ_SA_WAIT(0) CQ_SA_WAIT(1) CQ_SA_WAIT(2) CQ_SA_WAIT(3) CQ_SA_WAIT(4) CQ_SA_WAIT(5) CQ_SA_WAIT(6)
+        CQ_SA_WAIT(7) CQ_SA_WAIT(8) CQ_SA_WAIT(9) CQ_SA_WAIT(10) CQ_SA_WAIT(11) CQ_SA_WAIT(12) CQ_SA_WAIT(13)
+        CQ_SA_WAIT(14) CQ_SA_WAIT(15)
+#undef CQ_SA_WAIT
+        default: __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8)); break;
+    }
+}
+
+template <int BITS>
+constexpr size_t sa_lds_bytes() {
+    return static_cast<size_t>(kSaSlots) * kSaSlot + kSaBlocks * MfmaGeo<BITS>::UPG * 1024 + kSaBlocks * 128 +
+           kSaBlocks * 128 + 256;
+}
+
+template <int BITS>
+__global__ __launch_bounds__(64 * kSaBlocks, 2) void lut_mfma_tabs_kernel(LutLaunch a) {
+    using M = MfmaGeo<BITS>;
+    constexpr int NP = M::NJ / 2, SPG = NP / kSaPairs, UPG = M::UPG, AUX = UPG + 2;
+    // a group's aux loads go out at its second step and must be older than
+    // the next group's first slot
+    static_assert(NP % kSaPairs == 0 && SPG >= kSaAhead + 2, "a group's steps");
+    static_assert(kSaDma * (kSaAhead - 1) + AUX <= 15, "the wait counts fit sa_wait_vm");
+    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char *ring = smem;                                            // [slot][pair][plane][64][16]
+    unsigned char *idxl = ring + kSaSlots * kSaSlot;                       // [wave][unit][64 rows][16]
+    unsigned char *nrml = idxl + kSaBlocks * UPG * 1024;                   // [wave][64 fp16 norms]
+    unsigned char *stpl = nrml + kSaBlocks * 128;                          // [wave][32 steps]
+    int8_t *ohot = reinterpret_cast<int8_t *>(stpl + kSaBlocks * 128);     // [16][16]: entry c is the one-hot of c
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
+    const int nat = a.tab_at, L = blockIdx.x;
+    // workgroup L on XCD L % 8 as its (L / 8)-th; the (tile, slab) items,
+    // tile by tile, in 8 equal runs, one per XCD (as lut_mfma_tab_kernel)
+    const int nb = a.tab_nb, total = nat * nb, per = (total + 7) / 8;
+    const int k8 = L >> 3, item = (L & 7) * per + k8;
+    if (k8 >= per || item >= total) return;  // the whole workgroup
+    const int at = item / nb, rb = item % nb;
+    int jb = 0;
+#pragma unroll
+    for (int k = 1; k < kKernargJobs; ++k)
+        if (k < a.njobs && rb >= a.wg0[k]) jb = k;
+    const JobDesc &J = a.jobs[jb];
+    const int blkS = (rb - a.wg0[jb]) * kSaBlocks;  // the slab's first block (job-relative)
+    if (blkS >= J.nblk) return;                     // the whole workgroup
+    const int nbh = min(kSaBlocks, J.nblk - blkS);
+    const bool mine = w < nbh;                       // a wavefront past the job's blocks reads block nbh - 1, unused
+    const int blk = blkS + (mine ? w : nbh - 1);
+    const size_t bk = static_cast<size_t>(J.blk0 + blk);
+    const int groups = J.groups, units = J.units, nsteps = groups * SPG;
+    if (tid < 16) {
+        const uint32_t one = 1u << (8 * (tid & 3)), d = tid >> 2;
+        *reinterpret_cast<uint4 *>(ohot + tid * 16) =
+            make_uint4(d == 0 ? one : 0u, d == 1 ? one : 0u, d == 2 ? one : 0u, d == 3 ? one : 0u);
+    }
+    const int8_t *T = a.tab + static_cast<size_t>(at) * groups * NP * 2048;  // the tile's A operands
+    const uint8_t *IDX = J.idx;
+    // the ring's step k: kSaSlot bytes of T into slot k % kSaSlots, 1 KiB a wavefront load
+    auto dma_step = [&](int k) {
+        const int8_t *src = T + static_cast<size_t>(k) * kSaSlot + w * 1024 + lane * 16;
+        const unsigned m0 = sa_lds(ring + (k % kSaSlots) * kSaSlot + w * 1024);
+#pragma unroll
+        for (int r = 0; r < kSaDma; ++r) sa_dma16(src + r * 4096, m0 + r * 4096);
+    };
+    // group g's index units, norms and steps for this wavefront's block (AUX loads)
+    auto dma_aux = [&](int g) {
+#pragma unroll
+        for (int u = 0; u < UPG; ++u)
+            sa_dma16(IDX + ((bk * units + static_cast<size_t>(g) * UPG + u) * 64 + lane) * 16,
+                     sa_lds(idxl + (w * UPG + u) * 1024));
+        if (lane < 32) {
+            sa_dma4(reinterpret_cast<const char *>(J.norm + (bk * groups + g) * 64) + lane * 4, sa_lds(nrml + w * 128));
+            sa_dma4(a.tstp + (static_cast<size_t>(at) * groups + g) * 32 + lane, sa_lds(stpl + w * 128));
+        }
+    };
+    dma_aux(0);
+    for (int k = 0; k < kSaAhead && k < nsteps; ++k) dma_step(k);
+
+    const uint32_t hs = 4u * static_cast<uint32_t>(half);  // a lane half takes the odd nibbles
+    float y[2][16];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) y[rt][i] = 0.0f;
+    for (int g = 0; g < groups; ++g) {
+        uint32_t idx[UPG][2][4];
+        unsigned short nrm16[2];
+        float st[16];
+        i32x16 accl[2] = {i32x16{}, i32x16{}}, acch[2] = {i32x16{}, i32x16{}};
+        const bool aux_next = g + 1 < groups;
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
+            const int k = g * SPG + s;
+            // step k's slot (and, at s = 0, the group's aux loads, older) has
+            // landed once only the loads issued after it are in flight: steps
+            // k + 1 .. k + kSaAhead - 1, and the next group's aux loads (issued
+            // at s = 1, behind step 1 + kSaAhead's) until step 1 + kSaAhead
+            sa_wait_vm(kSaDma * min(kSaAhead - 1, nsteps - 1 - k) +
+                       (s >= 2 && s <= kSaAhead + 1 && aux_next ? AUX : 0));
+            lds_barrier();  // every wavefront's share has landed; slot (k - 1) % kSaSlots is read out
+            if (k + kSaAhead < nsteps) dma_step(k + kSaAhead);
+            if (s == 0) {
+#pragma unroll
+                for (int u = 0; u < UPG; ++u)
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) {
+                        const uint4 v = *reinterpret_cast<const uint4 *>(idxl + (w * UPG + u) * 1024 + (rt * 32 + l32) * 16);
+                        idx[u][rt][0] = (v.x >> hs) << 4;
+                        idx[u][rt][1] = (v.y >> hs) << 4;
+                        idx[u][rt][2] = (v.z >> hs) << 4;
+                        idx[u][rt][3] = (v.w >> hs) << 4;
+                    }
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    nrm16[rt] = reinterpret_cast<const unsigned short *>(nrml + w * 128)[rt * 32 + l32];
+                const float *sp = reinterpret_cast<const float *>(stpl + w * 128) + half * 4;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) st[i] = sp[(i >> 2) * 8 + (i & 3)];
+            }
+            if (s == 1 && aux_next) dma_aux(g + 1);  // the buffers were read out at s = 0 (barrier between)
+            // this half's nibble of pair pp in the high nibble of byte pp: a
+            // one-hot's offset in the table is one SDWA and
+            auto onehot = [&](int rt, int pp) -> i32x4 {
+                const uint32_t w4 = idx[pp >> 4][rt][(pp >> 2) & 3];
+                uint32_t off;
+                switch (pp & 3) {
+                    case 0: off = and_byte<0>(0xf0u, w4); break;
+                    case 1: off = and_byte<1>(0xf0u, w4); break;
+                    case 2: off = and_byte<2>(0xf0u, w4); break;
+                    default: off = and_byte<3>(0xf0u, w4); break;
+                }
+                return *reinterpret_cast<const i32x4 *>(ohot + off);
+            };
+            const unsigned char *sl = ring + (k % kSaSlots) * kSaSlot + lane * 16;
+            i32x4 Al[2], Ah[2], B[2][2];
+            Al[0] = *reinterpret_cast<const i32x4 *>(sl);
+            Ah[0] = *reinterpret_cast<const i32x4 *>(sl + 1024);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) B[0][rt] = onehot(rt, s * kSaPairs);
+#pragma unroll
+            for (int p = 0; p < kSaPairs; ++p) {
+                const int c = p & 1;
+                if (p + 1 < kSaPairs) {
+                    Al[c ^ 1] = *reinterpret_cast<const i32x4 *>(sl + (p + 1) * 2048);
+                    Ah[c ^ 1] = *reinterpret_cast<const i32x4 *>(sl + (p + 1) * 2048 + 1024);
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) B[c ^ 1][rt] = onehot(rt, s * kSaPairs + p + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // the next pair's reads go out before these MFMAs
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    accl[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al[c], B[c][rt], accl[rt], 0, 0, 0);
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    acch[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah[c], B[c][rt], acch[rt], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // the group's terms float32(S) * (norm * step), folded in group order
+        float nrm[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) nrm[rt] = __half2float(__ushort_as_half(nrm16[rt]));
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int sum = accl[rt][i] + 64 * acch[rt][i];
+                const float coef = nrm[rt] * st[i];
+                const float t = static_cast<float>(sum) * coef;
+                y[rt][i] = y[rt][i] + t;
+            }
+    }
+    // y to lane = row through LDS (the ring, read out by every wavefront)
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    float *tr = reinterpret_cast<float *>(ring) + w * 32 * 64;  // [activation][row]
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int tt = (i >> 2) * 8 + half * 4 + (i & 3);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) tr[tt * 64 + rt * 32 + l32] = y[rt][i];
+    }
+    if (!mine) return;  // after the last barrier
+    const Epilogue E(J);
+    const int rview = min(max((E.blk0 + blk) * 64 + lane - E.row0, 0), E.out - 1);  // the lane's view row, clamped
+#pragma unroll 1
+    for (int j = 0; j < 4; ++j) {
+        constexpr int FA = 8;
+        const int t0 = at * 32 + j * FA, nt = min(FA, J.rows - t0);
+        if (nt <= 0) break;
+        float yy[FA], rv[FA], cv[FA], sv[FA];
+        int pk[FA];
+#pragma unroll
+        for (int q = 0; q < FA; ++q) {
+            yy[q] = tr[(j * FA + q) * 64 + lane];
+            const long long tk = min(t0 + q, J.rows - 1);
+            pk[q] = E.app_q ? E.app_pos[tk] : -1;
+            rv[q] = E.resid ? E.resid[tk * E.resid_stride + rview] : 0.0f;
+            cv[q] = sv[q] = 0.0f;
+            if (E.app_cos) {
+                const int pc = pk[q] >= 0 && pk[q] < E.app_cap ? pk[q] : 0;
+                cv[q] = E.app_cos[pc * 32 + (lane & 31)];
+                sv[q] = E.app_sin[pc * 32 + (lane & 31)];
+            }
+        }
+        fold_epilogue<FA>(E, t0, nt, blk, lane, yy, pk, cv, sv, rv);
+    }
+}
+
 template <int BITS>
 size_t tab_lds_bytes(int groups) {
     return sizeof(float) * static_cast<size_t>(groups) * 32 * 64 + 16 * 16;
@@ -1457,12 +1701,20 @@ hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStr
         hipLaunchKernelGGL((lut_tables_kernel<BITS, 8>), dim3(t.tiles * 32 / 8, t.groups), dim3(256), 0, s, t);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    static std::atomic<unsigned long long> attr{0};
-    e = lds_limit_once(reinterpret_cast<const void *>(&lut_mfma_tab_kernel<BITS>),
-                       static_cast<int>(tab_lds_bytes<BITS>(kTabMaxGroups)), attr);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), dim3(8 * ((a.tab_at * blocks + 7) / 8)), dim3(64 * kTabWaves),
-                       tab_lds_bytes<BITS>(t.groups), s, a);
+    const dim3 grid(8 * ((a.tab_at * blocks + 7) / 8));  // blocks: slabs of a.tab_rb row blocks
+    static std::atomic<unsigned long long> attr[2] = {{0}, {0}};
+    if (a.tab_rb == kSaBlocks) {
+        e = lds_limit_once(reinterpret_cast<const void *>(&lut_mfma_tabs_kernel<BITS>),
+                           static_cast<int>(sa_lds_bytes<BITS>()), attr[1]);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((lut_mfma_tabs_kernel<BITS>), grid, dim3(64 * kSaBlocks), sa_lds_bytes<BITS>(), s, a);
+    } else {
+        e = lds_limit_once(reinterpret_cast<const void *>(&lut_mfma_tab_kernel<BITS>),
+                           static_cast<int>(tab_lds_bytes<BITS>(kTabMaxGroups)), attr[0]);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((lut_mfma_tab_kernel<BITS>), grid, dim3(64 * kTabWaves), tab_lds_bytes<BITS>(t.groups), s,
+                           a);
+    }
     return hipGetLastError();
 }
 
@@ -1493,6 +1745,7 @@ int tab_max_groups() { return kTabMaxGroups; }
 hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s) {
     if (blocks <= 0 || a.tab_at <= 0 || a.njobs <= 0) return hipSuccess;
     if (t.groups > kTabMaxGroups || t.tiles != a.tab_at || a.tab_nb != blocks) return hipErrorInvalidValue;
+    if (a.tab_rb != 1 && a.tab_rb != kSaBlocks) return hipErrorInvalidValue;
     if (bits == 4) return launch_tab_t<4>(t, a, blocks, s);
     if (bits == 2) return launch_tab_t<2>(t, a, blocks, s);
     return hipErrorInvalidValue;

@@ -82,15 +82,16 @@ def test_tab_path_bounds():
         assert s4.gemm_path(6000) == "lut-mfma-tab" and s4.gemm_path(12000) == "lut-mfma"
 
 
-@pytest.mark.parametrize("bits", [2, 4])
-def test_tab_views_and_shared_input(bits):
-    # four row views of one root (two not block-aligned) on one input at 256
-    # activations: one pre-pass and one product launch, each output bit for
-    # bit its own oracle product
+@pytest.mark.parametrize("bits,rows", [(2, 256), (4, 256), (4, 2000)])
+def test_tab_views_and_shared_input(bits, rows):
+    # four row views of one root (two not block-aligned) on one input: one
+    # pre-pass and one product launch, each output bit for bit its own oracle
+    # product; at 2000 activations the product runs slabs of four blocks (the
+    # last view's third slab partial, its block starting mid-view)
     import torch
 
-    g = synth.rng(170 + bits)
-    D, rows = 512, 256
+    g = synth.rng(170 + bits + rows)
+    D = 512
     proot = synth.random_packed(g, 4 * D, D, 128, bits, sigma=0.05)
     root, oroot = cq.New(proot), orc.OMatrix.new(proot)
     spans = [(0, D), (D, 2 * D), (2 * D, 3 * D - 40), (3 * D - 40, 4 * D)]
@@ -104,15 +105,15 @@ def test_tab_views_and_shared_input(bits):
         assert same(y.cpu().numpy(), want), (lo, hi)
 
 
-@pytest.mark.parametrize("bits", [2, 4])
-def test_tab_fused_prologues_and_epilogues(bits):
+@pytest.mark.parametrize("bits,rows", [(2, 256), (4, 256), (2, 2048)])
+def test_tab_fused_prologues_and_epilogues(bits, rows):
     # ZCRMSNorm in front and SiLU behind (FFN-up), the gated input and the
-    # residual add, each against the oracle's separate steps, at 256
-    # activations over 2048 rows
+    # residual add, each against the oracle's separate steps, over 2048 rows
+    # (at 2048 activations the product runs slabs of four blocks)
     import torch
 
-    g = synth.rng(190 + bits)
-    rows, D, F = 256, 512, 2048
+    g = synth.rng(190 + bits + rows)
+    D, F = 512, 2048
     pu = synth.random_packed(g, F, D, 128, bits, sigma=0.05)
     mu = cq.New(pu)
     assert mu.gemm_path(rows) == "lut-mfma-tab"
@@ -135,17 +136,19 @@ def test_tab_fused_prologues_and_epilogues(bits):
     assert same(yo.cpu().numpy().reshape(-1), want)
 
 
-def test_tab_append_epilogue():
+@pytest.mark.parametrize("batch", [256, 3000])
+def test_tab_append_epilogue(batch):
     # the q/k/v/gate launch of the decode step at 256 streams: the norm in
     # front, the K/V int8 appends (RoPE on K) in the fold, each stream at its
     # own position (some outside the cache); y bit for bit the oracle's
-    # products and the caches those of the separate append kernels
+    # products and the caches those of the separate append kernels; at 3000
+    # streams the product runs slabs of four blocks
     import torch
 
     from go_whistle_amd import decoder as dec
     from go_whistle_amd import needle
 
-    heads, hd, cap, batch = 8, 64, 16, 256
+    heads, hd, cap = 8, 64, 16
     D = heads * hd
     g = synth.rng(600)
     cos, sin = (_t(a) for a in dec.rope_tables(hd, cap, 1e4))
