@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void rope_kernel(float *x, int heads, int head
 // greedy.go's argmax keeps best = 0 and moves to i when v[i] > v[best]: the
 // answer is 0 when v[0] is NaN, else the first index of the largest value
 // that is not NaN (NaN never compares greater; +0 and -0 tie). Each thread
-// takes its values in index order (16-byte loads, eight in flight), NaN
+// takes its values in index order (16-byte loads, sixteen in flight), NaN
 // never a candidate; candidates combine larger value first, then smaller
 // index, across the wavefront (lane exchanges) and the workgroup (LDS).
 struct ArgmaxCand {
@@ -116,9 +116,13 @@ __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *
                                                      int32_t *span_hi, int span_stride, int32_t *done, int eos) {
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // A stream that has stopped keeps its token (the stop token) and its
-    // position: the steps it still runs in the batch change nothing it reports.
-    if (done && done[r]) return;
+    // position: the steps it still runs in the batch change nothing it
+    // reports (the flag is read with the row, and checked before any store).
+    const int stopped = tid == 0 && done ? done[r] : 0;
     const float *row = v + static_cast<long long>(r) * n;
+    // the scalar operands of the end, loaded with the row rather than after it
+    const float v0 = tid == 0 && n > 0 ? row[0] : 0.0f;
+    const int p0 = tid == 0 && pos ? pos[r] : 0;
     ArgmaxCand c{0.0f, INT_MAX};
     auto take = [&](float x, int i) {
         if (x == x && (c.i == INT_MAX || x > c.v)) c = ArgmaxCand{x, i};
@@ -126,15 +130,15 @@ __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *
     if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
         const int n4 = n >> 2;
         const float4 *row4 = reinterpret_cast<const float4 *>(row);
-        for (int base = 0; base < n4; base += 8 * 256) {
-            float4 f[8];
+        for (int base = 0; base < n4; base += 16 * 256) {  // a 16384-entry row in one round of loads
+            float4 f[16];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
+            for (int k = 0; k < 16; ++k) {
                 const int i4 = base + k * 256 + tid;
                 if (i4 < n4) f[k] = row4[i4];
             }
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
+            for (int k = 0; k < 16; ++k) {
                 const int i4 = base + k * 256 + tid;
                 if (i4 < n4) {
                     take(f[k].x, 4 * i4);
@@ -161,13 +165,13 @@ __global__ __launch_bounds__(256) void argmax_kernel(int32_t *out, const float *
         si[wave] = c.i;
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0 && !stopped) {
         for (int w = 1; w < 4; ++w) c = argmax_pick(c, ArgmaxCand{sv[w], si[w]});
-        const bool nan0 = n > 0 && row[0] != row[0];
+        const bool nan0 = n > 0 && v0 != v0;
         const int tok = (n == 0 || nan0 || c.i == INT_MAX) ? 0 : c.i;
         out[r] = tok;
         if (pos) {
-            const int p = pos[r] + 1;
+            const int p = p0 + 1;
             pos[r] = p;
             span_hi[static_cast<long long>(r) * span_stride] = p + 1;
         }
