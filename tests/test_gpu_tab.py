@@ -32,8 +32,10 @@ def _t(a):
 @pytest.mark.parametrize("bits", [2, 4])
 @pytest.mark.parametrize("out,inp,rows", [(2048, 512, 256), (2048, 512, 193), (2048, 512, 230), (2048, 512, 319),
                                           (2100, 384, 200), (4096, 1024, 256), (2048, 128, 250), (2048, 512, 375),
-                                          (1536, 512, 1500), (512, 512, 3000)])
+                                          (1536, 512, 1500), (512, 512, 3000), (2048, 128, 2048), (2100, 384, 2040)])
 def test_tab_gemm_bit_exact(bits, out, inp, rows):
+    # the last two run slabs of four blocks: one group, and three groups over
+    # 33 blocks (the last slab one block) with a partial activation tile
     import torch
 
     g = synth.rng(out + inp + rows + bits + 7)
