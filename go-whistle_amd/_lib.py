@@ -105,6 +105,12 @@ SIGNATURES = {
                                     POINTER(c_void_p), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "cq_gemms_gated_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_void_p, c_int, c_void_p,
                                    c_void_p]),
+    "cq_tables_bytes": (c_size_t, [c_int, POINTER(c_void_p), c_int]),
+    "cq_gemm_tables_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, POINTER(c_void_p),
+                                   c_void_p, c_void_p, c_size_t, POINTER(c_int), c_void_p]),
+    "cq_gemms_tables_dev": (c_int, [c_int, POINTER(c_void_p), POINTER(c_void_p), c_int, c_void_p, c_int,
+                                    POINTER(c_void_p), POINTER(c_void_p), c_longlong, c_longlong, c_void_p, c_int,
+                                    POINTER(c_void_p), POINTER(c_void_p), c_void_p, c_size_t, c_void_p]),
 }
 
 _lib = None

@@ -235,6 +235,55 @@ def gemms_append_dev(ms, ys, x, rows, caches, q_stride, s_stride, pos, cap, norm
                                     s_stride, ptr(pos), cap, cs, sn, _stream()))
 
 
+def tables_bytes(ms, rows):
+    """Bytes of the tables of the product over ms at `rows` activations that
+    gemm_tables_dev can build in the previous product's launch, 0 when that
+    product takes no table buffer (cq_tables_bytes)."""
+    n = len(ms)
+    hs = (c_void_p * max(n, 1))(*[m.handle for m in ms])
+    return int(lib().cq_tables_bytes(n, hs, rows))
+
+
+def gemm_tables_dev(m, y, x, rows, next_ms, tables, gate=None, resid=None, next_gain=None):
+    """y = [resid +] m . (x [* sigmoid(gate)]), as gemms_gated_dev, and where
+    its launch runs a workgroup per activation over all of m's rows, the
+    tables of the next product over next_ms of ZCRMSNorm(y; next_gain) into
+    the uint8 device tensor `tables` (tables_bytes(next_ms, rows) bytes; None:
+    none asked). Returns True when the tables were built, else the next
+    product runs unchained (cq_gemm_tables_dev)."""
+    n = len(next_ms)
+    hs = (c_void_p * max(n, 1))(*[q.handle for q in next_ms])
+    ptr = lambda t: c_void_p(t.data_ptr()) if t is not None else None
+    nbytes = tables.numel() * tables.element_size() if tables is not None else 0
+    built = ctypes.c_int(0)
+    check(lib().cq_gemm_tables_dev(m.handle, ptr(y), ptr(x), ptr(gate), rows, ptr(resid), n, hs, ptr(next_gain),
+                                   ptr(tables), nbytes, ctypes.byref(built), _stream()))
+    return bool(built.value)
+
+
+def gemms_tables_dev(ms, ys, rows, tables, resid=None, act=0, caches=None, q_stride=0, s_stride=0, pos=None, cap=0):
+    """The product over ms of the activations whose tables gemm_tables_dev
+    built into `tables`, with gemms_fused_dev's residual add or SiLU and
+    gemms_append_dev's appends (caches as there; None: none)
+    (cq_gemms_tables_dev)."""
+    n = len(ms)
+    caches = caches if caches is not None else [None] * n
+    if not (n == len(ys) == len(caches)):
+        raise CQPanic(f"cq: GEMMs of {n} matrices into {len(ys)} outputs and {len(caches)} caches")
+    ptr = lambda t: c_void_p(t.data_ptr()) if t is not None else None
+    arr = lambda vals: (c_void_p * max(n, 1))(*vals)
+    hs = arr([m.handle for m in ms])
+    ds = arr([ptr(y) for y in ys])
+    kq = arr([ptr(c[0]) if c is not None else None for c in caches])
+    ks = arr([ptr(c[1]) if c is not None else None for c in caches])
+    rope = [c[2] if c is not None and c[2] is not None else None for c in caches]
+    cs = arr([ptr(r[0]) if r is not None else None for r in rope])
+    sn = arr([ptr(r[1]) if r is not None else None for r in rope])
+    nbytes = tables.numel() * tables.element_size()
+    check(lib().cq_gemms_tables_dev(n, hs, ds, rows, ptr(resid), act, kq, ks, q_stride, s_stride, ptr(pos), cap, cs,
+                                    sn, ptr(tables), nbytes, _stream()))
+
+
 class Batch:
     """A plan of independent products on device tensors (cq_batch_*): job k
     is ms[k].GEMM of rows[k] activations xs[k] into ys[k]. run() queues one

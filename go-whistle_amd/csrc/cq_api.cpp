@@ -283,7 +283,7 @@ int blocks_per_workgroup(long long blocks) {
 // One launch of the lut kernel for up to kKernargJobs views of one geometry
 // and the same activations.
 int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
-            const Fuse *fz = nullptr) {
+            const Fuse *fz = nullptr, const TabOut *to = nullptr, int *built = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     LutLaunch a;
     std::memset(&a, 0, sizeof a);
@@ -367,7 +367,16 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
             gx = (nmax + bp - 1) / bp;
         }
     }
-    const size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, a.gc, a.tb, a.bpw);
+    size_t lds = lut_lds_bytes(s0.width, s0.group_bytes, a.gc, a.tb, a.bpw);
+    // The next product's tables ride on a launch of one workgroup per
+    // activation over all of one view's rows (the wide form), whose
+    // workgroups each hold a whole output row.
+    if (to && built && a.njobs == 1 && gx == 1 && rows <= 256 && a.waves > kLutWaves && a.vsplit == 1 &&
+        s0.group_bytes == s0.width * 16 && a.jobs[0].out == to->in) {
+        a.tout = *to;
+        lds += lut_tout_lds_bytes(to->in);
+        *built = 1;
+    }
     for (int r0 = 0; r0 < rows; r0 += 65535) {
         LutLaunch b = a;
         const int nr = std::min(65535, rows - r0);
@@ -382,7 +391,8 @@ int run_lut(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
                 b.jobs[k].app_pos += r0;
             }
         }
-        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, a.waves, gx, nr, lds, stream), "lut launch");
+        // with the next tables: 256 workgroups, activations spread for the XCDs (the kernel's TB form)
+        HIP_TRY(launch_lut(b, s0.width, s0.group_bytes, a.waves, gx, b.tout.tab ? 256 : nr, lds, stream), "lut launch");
     }
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;
@@ -770,7 +780,7 @@ int tab_row_blocks(cq_matrix *const *ms, int n, int rows) {
 }
 
 int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
-            const Fuse *fz = nullptr) {
+            const Fuse *fz = nullptr, const void *tables = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     LutLaunch a;
     std::memset(&a, 0, sizeof a);
@@ -803,15 +813,18 @@ int run_tab(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int
     t.lut_step = s0.lut_step;
     const size_t tb = tab_table_bytes(s0.width, s0.groups, tiles), sb = tab_step_bytes(s0.groups, tiles);
     WsScope ws;
-    if (int e = ws_acquire(tb + sb, stream, ws.l)) return e;
-    char *const base = static_cast<char *>(ws.l.w->buf);
+    char *base = static_cast<char *>(const_cast<void *>(tables));
+    if (!base) {
+        if (int e = ws_acquire(tb + sb, stream, ws.l)) return e;
+        base = static_cast<char *>(ws.l.w->buf);
+    }
     t.tab = reinterpret_cast<int8_t *>(base);
     t.stp = reinterpret_cast<float *>(base + tb);
     a.tab = t.tab;
     a.tstp = t.stp;
     a.tab_at = tiles;
     a.tab_nb = blocks;
-    HIP_TRY(launch_lut_tab(t, a, s0.width, blocks, stream), "lut table-form launch");
+    HIP_TRY(launch_lut_tab(t, a, s0.width, blocks, stream, tables == nullptr), "lut table-form launch");
     if (int e = ws_release(ws.l)) return e;
     for (int k = 0; k < n; ++k) ms[k]->st->prepared.store(true);
     return CQ_OK;
@@ -921,7 +934,7 @@ int run_dense(cq_matrix *const *ms, int n, float *const *dsts, const float *x, i
 }
 
 int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x, int rows, hipStream_t stream,
-                const Fuse *fz = nullptr) {
+                const Fuse *fz = nullptr, const TabOut *to = nullptr, int *built = nullptr) {
     const CqStore &s0 = *ms[0]->st;
     const int mode = uses_lut(ms[0]) ? kModeLut : kModeExact;
     if (mode == kModeLut && tab_pays(ms, n, rows)) return run_tab(ms, n, dsts, x, rows, stream, fz);
@@ -929,7 +942,8 @@ int run_product(cq_matrix *const *ms, int n, float *const *dsts, const float *x,
         mfma_pays(ms, n, rows))
         return run_mfma(ms, n, dsts, x, rows, stream, fz);
     if (mode == kModeLut && split_pays(ms, n, rows)) return run_split(ms, n, dsts, x, rows, stream, fz);
-    if (mode == kModeLut && lut_fits(s0) && n <= kKernargJobs) return run_lut(ms, n, dsts, x, rows, stream, fz);
+    if (mode == kModeLut && lut_fits(s0) && n <= kKernargJobs)
+        return run_lut(ms, n, dsts, x, rows, stream, fz, to, built);
     if (fz && fz->any())
         return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel (this is %s, group bytes %d)",
                     mode == kModeLut ? "lut" : "exact", s0.group_bytes);
@@ -1320,6 +1334,107 @@ int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const f
     if (tab_pays(ms, n, rows)) return run_tab(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
     if (split_pays(ms, n, rows)) return run_split(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
     return run_lut(ms, n, dsts, x, rows, static_cast<hipStream_t>(stream), &f);
+}
+
+size_t cq_tables_bytes(int n, cq_matrix *const *ms, int rows) {
+    if (n <= 0 || n > kKernargJobs || !ms || rows <= 0) return 0;
+    for (int k = 0; k < n; ++k)
+        if (!ms[k] || ms[k]->st->in != ms[0]->st->in || ms[k]->dense) return 0;
+    if (!tab_pays(ms, n, rows)) return 0;
+    const CqStore &s0 = *ms[0]->st;
+    const int tiles = (rows + 31) / 32;
+    return tab_table_bytes(s0.width, s0.groups, tiles) + tab_step_bytes(s0.groups, tiles);
+}
+
+int cq_gemm_tables_dev(const cq_matrix *m, float *dst, const float *x, const float *gate, int rows, const float *resid,
+                       int n_next, cq_matrix *const *next, const float *next_gain, void *tables, size_t tables_bytes,
+                       int *built, void *stream) {
+    if (!built) return fail(CQ_ERR_MISUSE, "cq: a table-building GEMM without its flag");
+    *built = 0;
+    if (!m) return fail(CQ_ERR_MISUSE, "cq: nil matrix");
+    if (rows < 0) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d rows", rows);
+    if (!uses_lut(m))
+        return fail(CQ_ERR_UNSUPPORTED, "cq: fused products run the lut kernel, not %s", cq_kernel_name(m));
+    if (n_next < 1 || n_next > kKernargJobs || !next)
+        return fail(CQ_ERR_MISUSE, "cq: tables for a product of %d matrices (1 to %d)", n_next, kKernargJobs);
+    for (int k = 0; k < n_next; ++k)
+        if (!next[k] || next[k]->st->in != m->out)
+            return fail(CQ_ERR_MISUSE, "cq: the next product's matrices must take the %d outputs as inputs", m->out);
+    if (int e = nil_operands(1, &dst, x, rows)) return e;
+    if (rows == 0 || m->out == 0) return CQ_OK;
+    const size_t need = cq_tables_bytes(n_next, next, rows);
+    if (tables_bytes != need || (need && !tables))
+        return fail(CQ_ERR_MISUSE, "cq: a table buffer of %zu bytes where the next product's tables take %zu",
+                    tables_bytes, need);
+    Fuse f;
+    f.xgate = gate;
+    f.resid = resid;
+    f.resid_stride = resid ? m->out : 0;
+    cq_matrix *mm = const_cast<cq_matrix *>(m);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (need == 0) return run_product(&mm, 1, &dst, x, rows, st, &f);
+    const CqStore &n0 = *next[0]->st;
+    const int tiles = (rows + 31) / 32;
+    TabOut to;
+    std::memset(&to, 0, sizeof to);
+    to.tab = static_cast<int8_t *>(tables);
+    to.stp = reinterpret_cast<float *>(static_cast<char *>(tables) + tab_table_bytes(n0.width, n0.groups, tiles));
+    to.ngain = next_gain;
+    to.in = n0.in;
+    to.groups = n0.groups;
+    to.bits = n0.width;
+    to.tiles = tiles;
+    for (int c = 0; c < 16; ++c) to.cb[c] = c < n0.ncb ? n0.cb[c] : 0.0f;
+    to.cb_max = n0.cb_max;
+    to.lut_step = n0.lut_step;
+    return run_product(&mm, 1, &dst, x, rows, st, &f, &to, built);
+}
+
+int cq_gemms_tables_dev(int n, cq_matrix *const *ms, float *const *dsts, int rows, const float *resid, int act,
+                        int8_t *const *kv_q, float *const *kv_s, long long q_stride, long long s_stride,
+                        const int32_t *pos, int cap, const float *const *cos_t, const float *const *sin_t,
+                        const void *tables, size_t tables_bytes, void *stream) {
+    if (n < 1 || n > kKernargJobs || !ms || !dsts)
+        return fail(CQ_ERR_MISUSE, "cq: GEMMs over tables of %d matrices (1 to %d)", n, kKernargJobs);
+    if (rows < 0 || cap < 0) return fail(CQ_ERR_MISUSE, "cq: GEMMs of %d rows into %d positions", rows, cap);
+    if (act != 0 && act != 1) return fail(CQ_ERR_MISUSE, "cq: activation %d", act);
+    if (resid && (n != 1 || act != 0))
+        return fail(CQ_ERR_MISUSE, "cq: a residual add takes one matrix and no activation");
+    bool any = false;
+    for (int k = 0; k < n; ++k) {
+        if (!ms[k] || ms[k]->st->in != ms[0]->st->in)
+            return fail(CQ_ERR_MISUSE, "cq: GEMMs over matrices of different input widths");
+        if (!dsts[k] && rows > 0) return fail(CQ_ERR_MISUSE, "cq: GEMMs with a nil output %d", k);
+        if (!kv_q || !kv_q[k]) continue;
+        any = true;
+        if (!kv_s || !kv_s[k] || ms[k]->row0 % kBlockRows || ms[k]->out % kBlockRows)
+            return fail(CQ_ERR_MISUSE, "cq: append of rows [%d, %d) needs scales and heads of %d rows", ms[k]->row0,
+                        ms[k]->row0 + ms[k]->out, kBlockRows);
+        if (cos_t && cos_t[k] && !(sin_t && sin_t[k])) return fail(CQ_ERR_MISUSE, "cq: RoPE cosines without sines");
+    }
+    if (any && !pos) return fail(CQ_ERR_MISUSE, "cq: append without positions");
+    if (rows == 0) return CQ_OK;
+    const size_t need = cq_tables_bytes(n, ms, rows);
+    if (need == 0)
+        return fail(CQ_ERR_MISUSE, "cq: this product of %d rows does not take the table form (no tables)", rows);
+    if (!tables || tables_bytes != need)
+        return fail(CQ_ERR_MISUSE, "cq: a table buffer of %zu bytes where the product's tables take %zu", tables_bytes,
+                    need);
+    Fuse f;
+    f.resid = resid;
+    f.resid_stride = resid ? ms[0]->out : 0;
+    f.act = act;
+    if (any) {
+        f.app_q = kv_q;
+        f.app_s = kv_s;
+        f.app_cos = cos_t;
+        f.app_sin = sin_t;
+        f.app_q_stride = q_stride;
+        f.app_s_stride = s_stride;
+        f.app_pos = pos;
+        f.app_cap = cap;
+    }
+    return run_tab(ms, n, dsts, nullptr, rows, static_cast<hipStream_t>(stream), &f, tables);
 }
 
 int cq_gemm(const cq_matrix *m, float *dst, size_t dst_len, const float *x, size_t x_len, int rows) {

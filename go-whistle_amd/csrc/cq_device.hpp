@@ -223,4 +223,27 @@ __device__ __forceinline__ void rope_pair(float a, float b, float c, float s, fl
     o2 = bc + as;
 }
 
+// A table entry's bits (the table form): RNE(f) for |f| <= 8191.5 as the
+// low bits of f + 1.5 * 2^23 (round to nearest even, exact for |f| < 2^22),
+// bits 0-5 the l plane's value and bits 6-13 the h plane's.
+constexpr float kRneMagic = 12582912.0f;  // 1.5 * 2^23
+
+__device__ __forceinline__ uint32_t rne_bits(float f) { return __float_as_uint(f + kRneMagic); }
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Four entries' bit patterns -> the l plane's 4 bytes (v & 63) and the h
+// plane's 4 bytes ((v >> 6) & 255): the entries' low halfwords are paired,
+// shifted right by 6 two at a time (bits 6-13 land in each halfword's low
+// byte), and the wanted bytes gathered.
+__device__ __forceinline__ void planes4(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, uint32_t &lo,
+                                        uint32_t &hi) {
+    const uint32_t q01 = __builtin_amdgcn_perm(e1, e0, 0x05040100u);  // e0.lo16 | e1.lo16 << 16
+    const uint32_t q23 = __builtin_amdgcn_perm(e3, e2, 0x05040100u);  // e2.lo16 | e3.lo16 << 16
+    lo = __builtin_amdgcn_perm(q23, q01, 0x06040200u) & 0x3f3f3f3fu;  // byte 0 of each halfword
+    const u16x2 r01 = __builtin_bit_cast(u16x2, q01) >> static_cast<unsigned short>(6);
+    const u16x2 r23 = __builtin_bit_cast(u16x2, q23) >> static_cast<unsigned short>(6);
+    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, r23), __builtin_bit_cast(uint32_t, r01), 0x06040200u);
+}
+
 }  // namespace cqhip

@@ -123,6 +123,21 @@ struct WorkUnit {
 constexpr int kKernargJobs = 8;
 constexpr int kLutWaves = 4;  // wavefronts per workgroup of the lut kernel
 
+// The next product's tables, built in a producer's epilogue (the table
+// form's pre-pass, fused): when a workgroup holds all of its activation's
+// output row y, it writes the tables and steps of ZCRMSNorm(y; ngain)
+// (ngain null: y itself) for a product over `in` = the producer's out
+// inputs, as TabArgs describes them (tab, stp for `tiles` tiles of 32
+// activations; slots past the activations are not written).
+struct TabOut {
+    int8_t *tab;  // null: none
+    float *stp;
+    const float *ngain;
+    int in, groups, bits, tiles;
+    float cb[16];
+    float cb_max, lut_step;
+};
+
 struct LutLaunch {
     JobDesc jobs[kKernargJobs];  // kernel-argument jobs (when dunits is null)
     int njobs;
@@ -150,6 +165,9 @@ struct LutLaunch {
     const float *tstp;
     int tab_at, tab_nb;
     int tab_rb;  // row blocks per workgroup of the product: 1, or 4 sharing the A operands (tab_nb, wg0 count slabs)
+    // The lut kernel's wide form, one workgroup per activation over all of
+    // one job's rows: the next product's tables (tout.tab null: none).
+    TabOut tout;
 };
 
 // The table pre-pass of the table form (mfma_kernels.hip): per activation
@@ -176,9 +194,13 @@ size_t tab_step_bytes(int groups, int tiles);
 int tab_max_groups();
 // The pre-pass, then the product: grid over the jobs' 64-row blocks (wg0)
 // times a.tab_at activation tiles. On stream s.
-hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s);
+// pre false: the tables are already there (a producer built them), only the
+// product runs.
+hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s, bool pre = true);
 
 size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw);
+// LDS bytes the wide form adds for a TabOut over `in` inputs.
+size_t lut_tout_lds_bytes(int in);
 // grid_y = activations on the kernel-argument path, 1 on the device path.
 hipError_t launch_lut(const LutLaunch &a, int bits, int group_bytes, int waves, int grid_x, int grid_y, size_t lds,
                       hipStream_t stream);

@@ -357,7 +357,138 @@ struct JobPtr {
 // V = 2 (wide launches of one-block units): two wavefronts share each group
 // of the block, one half of its index units each; their exact int32 sums
 // meet in LDS before the float term.
-template <int BITS, int GB, class JS, int V = 1, bool PRE = false, bool NTL = false>
+// The next product's tables from a finished output row (TabOut): the
+// table form's pre-pass (lut_tables_kernel) for one activation t, fused
+// into the producer's epilogue, op for op the same. yo holds the row (in
+// floats), wsp the LDS work area of lut_tout_lds_bytes(in). The whole
+// workgroup (W wavefronts) comes here and leaves together.
+//   1. ZCRMSNorm's divisor (norm.go:53-109): the squares d * d (exact in
+//      float64) go to LDS as [i mod 4][i / 4], lanes 0-3 add each partial in
+//      order;
+//   2. wavefront w takes groups w, w + W, ...: the gain and divisor, the
+//      plain FWHT in the reference's stage order (kernel.go:384-393), the
+//      bound M and the step M * lutStep, the values scaled by 8191 / M
+//      (lut.go:158-178, 219-225);
+//   3. every thread builds items (one position's 16 entries, both planes,
+//      lut.go:239-282) and writes them in the A-operand order
+//      [tile][group][pair][plane][half][32][16].
+template <int TB>
+__device__ __forceinline__ void next_tables(const TabOut &o, const float *yo, unsigned char *wsp, int t, int tid,
+                                            int lane, int w, int W) {
+    constexpr int G = 128, NJ = G * TB / 4, NP = NJ / 2, AP = G + 1;
+    const int in = o.in, groups = o.groups, qn = in >> 2, qs = qn + 2;
+    double *sq = reinterpret_cast<double *>(wsp + static_cast<size_t>(in) * 4);
+    float *av = reinterpret_cast<float *>(wsp + static_cast<size_t>(in) * 12 + 64);
+    float *zm = av + ((groups * AP + 3) & ~3);
+    const CQ_GLOBAL float *ng = gptr(o.ngain);
+    float rms = 1.0f;
+    if (ng) {
+        for (int i = tid; i < in; i += 64 * W) {
+            const double d = yo[i];
+            sq[(i & 3) * qs + (i >> 2)] = d * d;
+        }
+        __syncthreads();
+        double part = 0.0;
+        if (tid < 4) {
+            const double *row = sq + tid * qs;
+            int m = 0;
+            for (; m + 16 <= qn; m += 16) {
+                double v[16];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) v[k] = row[m + k];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) part = part + v[k];
+            }
+            for (; m < qn; ++m) part = part + row[m];
+        }
+        if (w == 0) {
+            const double p0 = __shfl(part, 0), p1 = __shfl(part, 1), p2 = __shfl(part, 2), p3 = __shfl(part, 3);
+            if (lane == 0) zm[0] = zc_rms(p0, p1, p2, p3, in);
+        }
+        __syncthreads();
+        rms = zm[0];
+    }
+    CQ_GLOBAL float *stp = gptr_w(o.stp);
+    for (int g = w; g < groups; g += W) {
+        float v[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int col = g * G + e * 64 + lane;
+            v[e] = yo[col];
+            if (ng) {
+                const float gx = ng[col] * v[e];
+                v[e] = gx / rms;
+            }
+        }
+#pragma unroll
+        for (int h = 1; h < 64; h <<= 1)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float p = xor_lane(v[e], h);
+                v[e] = (lane & h) ? p - v[e] : v[e] + p;
+            }
+        {
+            const float p = v[0], q = v[1];
+            v[0] = p + q;
+            v[1] = p - q;
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            if constexpr (TB == 4) {
+                mx = go_max(mx, fabsf(v[e]));
+            } else {
+                const float p = xor_lane<1>(v[e]);
+                const float s2 = fabsf(v[e]) + fabsf(p);  // |x̂_2q| + |x̂_2q+1| (lut.go:241-243)
+                mx = go_max(mx, s2);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = go_max(mx, xor_lane(mx, off));
+        const float m = o.cb_max * mx;
+        const float inv = m > 0.0f ? static_cast<float>(kLutQ) / m : 0.0f;  // lutInv (lut.go:219-225)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) av[g * AP + e * 64 + lane] = v[e] * inv;
+        if (lane == 0) stp[(static_cast<size_t>(t >> 5) * groups + g) * 32 + (t & 31)] = m * o.lut_step;
+    }
+    __syncthreads();
+    float cbv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cbv[q] = o.cb[q];
+    CQ_GLOBAL int8_t *tab = gptr_w(o.tab) + (static_cast<size_t>(t >> 5) * groups) * NP * 2048 + (t & 31) * 16;
+    for (int it = tid; it < groups * NJ; it += 64 * W) {
+        const int g = it / NJ, j = it - g * NJ;
+        float x0, x1 = 0.0f;
+        if constexpr (TB == 4) {
+            x0 = av[g * AP + j];
+        } else {
+            x0 = av[g * AP + 2 * j];
+            x1 = av[g * AP + 2 * j + 1];
+        }
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            uint32_t b[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int code = 4 * qd + q;
+                if constexpr (TB == 4) {
+                    b[q] = rne_bits(cbv[code] * x0);
+                } else {  // code = hi << 2 | lo
+                    const float l = cbv[code & 3] * x0, h = cbv[code >> 2] * x1;
+                    const float sm = l + h;
+                    b[q] = rne_bits(sm);
+                }
+            }
+            planes4(b[0], b[1], b[2], b[3], lo[qd], hi[qd]);
+        }
+        CQ_GLOBAL int8_t *dst = tab + static_cast<size_t>(g) * NP * 2048 + (j >> 1) * 2048 + (j & 1) * 512;
+        *reinterpret_cast<CQ_GLOBAL uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<CQ_GLOBAL uint4 *>(dst + 1024) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    }
+}
+
+template <int BITS, int GB, class JS, int V = 1, bool PRE = false, bool NTL = false, int TB = 0>
 __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b0, int bc, int act, int W) {
     using Gm = LutGeo<BITS, GB>;
     constexpr int U = Gm::U, UPG = Gm::UPG, NT = Gm::NT;
@@ -402,6 +533,14 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
     float *yacc = steps + gc;
     float *term = yacc + static_cast<size_t>(a.bpw_max) * 64;
     float *misc = term + static_cast<size_t>(gc) * tc * 64;
+    // With TB: the output row (the next tables' input) and their work area
+    // past misc's 16 bytes, 16-byte aligned.
+    unsigned char *tob = nullptr;
+    float *tyo = nullptr;
+    if constexpr (TB != 0) {
+        tob = smem + ((reinterpret_cast<unsigned char *>(misc + 4) - smem + 15) & ~static_cast<ptrdiff_t>(15));
+        tyo = reinterpret_cast<float *>(tob);
+    }
 
     // Fused ZCRMSNorm of the activation row (norm.go:53-109): the row goes
     // through LDS in pieces (one coalesced read each), lanes 0-3 of
@@ -569,6 +708,7 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
             else if (j_act == 1)
                 out = silu_value(out);
             j_y[static_cast<long long>(act) * j_ystride + (r - j_row0)] = out;
+            if constexpr (TB != 0) tyo[r - j_row0] = out;
         }
     };
 
@@ -799,6 +939,10 @@ __device__ __forceinline__ void lut_unit(const LutLaunch &a, const JS &jr, int b
         chunk(0);
     else
         for (int g0 = 0; g0 < groups; g0 += gc) chunk(g0);
+    if constexpr (TB != 0) {  // the workgroup wrote all of the row (host: one workgroup per activation)
+        __syncthreads();
+        next_tables<TB>(a.tout, tyo, tob, act, tid, lane, w, W);
+    }
 }
 
 template <int BITS, int GB, bool DEV>
@@ -830,7 +974,11 @@ __global__ __launch_bounds__(256, (lut_waves_per_simd<BITS, GB>())) void lut_ker
 // S * blocks <= waves). V = 2 (one
 // block): two per group, each on half its index units, so that each
 // wavefront's chain of table lookups is shorter.
-template <int BITS, int GB, int V>
+//
+// TB (2 or 4): the launch is one workgroup per activation over all rows of
+// its one job, and each builds the next product's TB-bit tables from its
+// output row (next_tables, a.tout).
+template <int BITS, int GB, int V, int TB>
 __global__ __launch_bounds__(1024) void lut_kernel_wide(LutLaunch a) {
     const int lane = threadIdx.x & 63;
     const JobRegs jr = job_regs(&a.jobs[blockIdx.z], lane);
@@ -838,15 +986,26 @@ __global__ __launch_bounds__(1024) void lut_kernel_wide(LutLaunch a) {
     asm volatile("" ::"v"(jr.d), "s"(bpw), "s"(gc), "s"(tb), "s"(bpw_max), "s"(waves));
     const int b0 = static_cast<int>(blockIdx.x) * bpw, nblk = JOB(jr, int, nblk);
     if (b0 >= nblk) return;
-    lut_unit<BITS, GB, JobRegs, V, true>(a, jr, b0, min(bpw, nblk - b0), blockIdx.y, waves);
+    int act = blockIdx.y;
+    if constexpr (TB != 0) {
+        // 256 workgroups, activation (y mod 8) * 32 + y / 8: workgroup y runs
+        // on XCD y mod 8 (dispatch goes round the XCDs), so the 32
+        // activations of a table tile share one L2, where their 16-byte
+        // pieces of each line meet before the line is written back
+        // (measured on MI355X: the batch-256 decode step 1.591 -> 1.561 ms)
+        act = (blockIdx.y & 7) * 32 + (blockIdx.y >> 3);
+        if (act >= JOB(jr, int, rows)) return;  // the whole workgroup, before any barrier
+    }
+    lut_unit<BITS, GB, JobRegs, V, true, false, TB>(a, jr, b0, min(bpw, nblk - b0), act, waves);
 }
 
-template <int BITS, int GB, int V>
+template <int BITS, int GB, int V, int TB = 0>
 hipError_t launch_wide(const LutLaunch &a, int gx, int gy, size_t lds, hipStream_t s) {
     static std::atomic<unsigned long long> attr{0};
-    if (hipError_t e = lds_limit_once(reinterpret_cast<const void *>(&lut_kernel_wide<BITS, GB, V>), 160 * 1024, attr))
+    if (hipError_t e =
+            lds_limit_once(reinterpret_cast<const void *>(&lut_kernel_wide<BITS, GB, V, TB>), 160 * 1024, attr))
         return e;
-    hipLaunchKernelGGL((lut_kernel_wide<BITS, GB, V>), dim3(gx, gy, a.njobs), dim3(64 * a.waves), lds, s, a);
+    hipLaunchKernelGGL((lut_kernel_wide<BITS, GB, V, TB>), dim3(gx, gy, a.njobs), dim3(64 * a.waves), lds, s, a);
     return hipGetLastError();
 }
 
@@ -857,9 +1016,22 @@ hipError_t launch_t(const LutLaunch &a, int waves, int gx, int gy, size_t lds, h
             // a.tb blocks' terms fit in LDS: the wavefronts sharing a block park them there
             if (a.waves != waves || a.waves > 16 || a.bpw > a.tb || (a.vsplit == 2 && a.bpw != 1))
                 return hipErrorInvalidValue;
+            if (a.tout.tab) {
+                // one workgroup per activation over all of one job's rows, 128-weight groups both sides
+                if (gx != 1 || gy != 256 || a.njobs != 1 || a.vsplit != 1 || a.bpw < a.jobs[0].nblk ||
+                    a.tout.in != a.jobs[0].out || a.tout.groups * 128 != a.tout.in || a.tout.groups > 8 ||
+                    a.jobs[0].rows > 256 || a.jobs[0].rows > a.tout.tiles * 32)
+                    return hipErrorInvalidValue;
+                if constexpr (GB == BITS * 16) {
+                    if (a.tout.bits == 4) return launch_wide<BITS, GB, 1, 4>(a, gx, gy, lds, s);
+                    if (a.tout.bits == 2) return launch_wide<BITS, GB, 1, 2>(a, gx, gy, lds, s);
+                }
+                return hipErrorInvalidValue;
+            }
             return a.vsplit == 2 ? launch_wide<BITS, GB, 2>(a, gx, gy, lds, s) : launch_wide<BITS, GB, 1>(a, gx, gy, lds, s);
         }
     }
+    if (a.tout.tab) return hipErrorInvalidValue;  // only the wide form builds tables
     if (a.dunits == nullptr && waves != kLutWaves) return hipErrorInvalidValue;  // that path assumes kLutWaves
     const bool dev = a.dunits != nullptr;
     const void *fn = dev ? reinterpret_cast<const void *>(&lut_kernel<BITS, GB, true>)
@@ -879,6 +1051,11 @@ size_t lut_lds_bytes(int bits, int group_bytes, int gc, int tb, int bpw) {
     (void)bits;
     return static_cast<size_t>(gc) * (2 * group_bytes * 16 * sizeof(short) + static_cast<size_t>(tb) * 64 * 4 + 4) +
            static_cast<size_t>(bpw) * 64 * 4 + 16;
+}
+
+size_t lut_tout_lds_bytes(int in) {
+    const size_t groups = static_cast<size_t>(in) / 128;
+    return 16 + static_cast<size_t>(in) * 12 + 64 + ((groups * 129 + 3) & ~static_cast<size_t>(3)) * 4 + 16;
 }
 
 bool lut_geometry_supported(int bits, int gb) {

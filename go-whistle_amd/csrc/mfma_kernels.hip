@@ -66,26 +66,6 @@ struct MfmaGeo {
 
 constexpr int kMfmaWaves = 8;
 constexpr int kMfmaThreads = 64 * kMfmaWaves;
-constexpr float kRneMagic = 12582912.0f;  // 1.5 * 2^23
-
-__device__ __forceinline__ uint32_t rne_bits(float f) { return __float_as_uint(f + kRneMagic); }
-
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-
-// Four entries' bit patterns -> the l plane's 4 bytes (v & 63) and the h
-// plane's 4 bytes ((v >> 6) & 255): the entries' low halfwords are paired,
-// shifted right by 6 two at a time (bits 6-13 land in each halfword's low
-// byte), and the wanted bytes gathered.
-__device__ __forceinline__ void planes4(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, uint32_t &lo,
-                                        uint32_t &hi) {
-    const uint32_t q01 = __builtin_amdgcn_perm(e1, e0, 0x05040100u);  // e0.lo16 | e1.lo16 << 16
-    const uint32_t q23 = __builtin_amdgcn_perm(e3, e2, 0x05040100u);  // e2.lo16 | e3.lo16 << 16
-    lo = __builtin_amdgcn_perm(q23, q01, 0x06040200u) & 0x3f3f3f3fu;  // byte 0 of each halfword
-    const u16x2 r01 = __builtin_bit_cast(u16x2, q01) >> static_cast<unsigned short>(6);
-    const u16x2 r23 = __builtin_bit_cast(u16x2, q23) >> static_cast<unsigned short>(6);
-    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, r23), __builtin_bit_cast(uint32_t, r01), 0x06040200u);
-}
-
 // m & byte B of t, in one VALU op (an SDWA byte select).
 template <int B>
 __device__ __forceinline__ uint32_t and_byte(uint32_t m, uint32_t t) {
@@ -1694,13 +1674,16 @@ size_t tab_lds_bytes(int groups) {
 }
 
 template <int BITS>
-hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStream_t s) {
-    if (t.rows <= kTabPre4Rows)
-        hipLaunchKernelGGL((lut_tables_kernel<BITS, 4>), dim3(t.tiles * 32 / 4, t.groups), dim3(256), 0, s, t);
-    else
-        hipLaunchKernelGGL((lut_tables_kernel<BITS, 8>), dim3(t.tiles * 32 / 8, t.groups), dim3(256), 0, s, t);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+hipError_t launch_tab_t(const TabArgs &t, const LutLaunch &a, int blocks, hipStream_t s, bool pre) {
+    hipError_t e;
+    if (pre) {
+        if (t.rows <= kTabPre4Rows)
+            hipLaunchKernelGGL((lut_tables_kernel<BITS, 4>), dim3(t.tiles * 32 / 4, t.groups), dim3(256), 0, s, t);
+        else
+            hipLaunchKernelGGL((lut_tables_kernel<BITS, 8>), dim3(t.tiles * 32 / 8, t.groups), dim3(256), 0, s, t);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     const dim3 grid(8 * ((a.tab_at * blocks + 7) / 8));  // blocks: slabs of a.tab_rb row blocks
     static std::atomic<unsigned long long> attr[2] = {{0}, {0}};
     if (a.tab_rb == kSaBlocks) {
@@ -1742,12 +1725,12 @@ size_t tab_step_bytes(int groups, int tiles) { return static_cast<size_t>(tiles)
 
 int tab_max_groups() { return kTabMaxGroups; }
 
-hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s) {
+hipError_t launch_lut_tab(const TabArgs &t, const LutLaunch &a, int bits, int blocks, hipStream_t s, bool pre) {
     if (blocks <= 0 || a.tab_at <= 0 || a.njobs <= 0) return hipSuccess;
     if (t.groups > kTabMaxGroups || t.tiles != a.tab_at || a.tab_nb != blocks) return hipErrorInvalidValue;
     if (a.tab_rb != 1 && a.tab_rb != kSaBlocks) return hipErrorInvalidValue;
-    if (bits == 4) return launch_tab_t<4>(t, a, blocks, s);
-    if (bits == 2) return launch_tab_t<2>(t, a, blocks, s);
+    if (bits == 4) return launch_tab_t<4>(t, a, blocks, s, pre);
+    if (bits == 2) return launch_tab_t<2>(t, a, blocks, s, pre);
     return hipErrorInvalidValue;
 }
 

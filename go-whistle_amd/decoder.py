@@ -334,6 +334,20 @@ class Decoder:
         self.att, self.o = z(B, c.dim), z(B, c.dim)
         self.u = z(B, c.ffn)
         self.logits = z(B, c.vocab)
+        # Chained products (cq.gemm_tables_dev): the launch of wo, cross-wo
+        # and FFN-down also builds the next product's tables where that
+        # product takes the table form, into one buffer the size of the
+        # largest (each producer rewrites it after its consumer has read it,
+        # in stream order).
+        self.chain = fused and not self.paged
+        nb = 0
+        if self.chain:
+            sets = [[self.emb]] + [[mm["wcq"], mm["wcg"]] for mm in self.mats] + [[mm["w1"]] for mm in self.mats]
+            if c.head_dim == 64:
+                sets += [[mm["wq"], mm["wk"], mm["wv"], mm["wg"]] for mm in self.mats]
+            nb = max(cq.tables_bytes(st, B) for st in sets)
+        self.tables = z(max(nb, 1), dt=torch.uint8)
+        self.n_chained = 0  # products of the last step run on tables their producer built
         hk = c.dim // c.head_dim
         # Every layer's self K and V caches are slices of one array (codes and
         # scales), [2 * layers][stream][position][...], K of layer l at 2l and
@@ -501,35 +515,74 @@ class Decoder:
                                                   _ptr(self.pos), _ptr(self.spans_self[:, 3]), 4, _ptr(self.done),
                                                   int(self.eos), s))
 
+    def _produce(self, m, y, x, nxt, gain, gate=None, resid=None):
+        """y = [resid +] m . (x [* sigmoid(gate)]); returns the tables of the
+        next product over nxt (of ZCRMSNorm(y; gain)) when the launch built
+        them, else None (the next product then runs unchained)."""
+        B = self.batch
+        nb = cq.tables_bytes(nxt, B) if self.chain and nxt else 0
+        if nb:
+            t = self.tables[:nb]
+            return t if cq.gemm_tables_dev(m, y, x, B, nxt, t, gate=gate, resid=resid, next_gain=gain) else None
+        if gate is not None:
+            cq.gemms_gated_dev([m], [y], x, gate, B, resid=resid)
+        else:
+            cq.gemms_fused_dev([m], [y], x, B, resid=resid)
+        return None
+
     def _step_fused(self):
         c, B = self.cfg, self.batch
         s = cq._stream()
         D, hk = c.dim, c.dim // c.head_dim
         self.emb.row_gather_dev(self.x, self.tok, float(self.model.scale))
         rope = (self.cos, self.sin)
+        qkvg = lambda m: [m["wq"], m["wk"], m["wv"], m["wg"]]
+        tab = None  # the next product's tables, built by the previous product's launch
+        self.n_chained = 0
         for l in range(c.layers):
             m = self.mats[l]
             if c.head_dim == 64:  # heads are the lut kernel's 64-row blocks: the appends ride on the product
                 caches = [None, (self.self_k[l], self.self_ks[l], rope), (self.self_v[l], self.self_vs[l], None),
                           None]
-                cq.gemms_append_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.x,
-                                    B, caches, c.max_pos * D, c.max_pos * hk, self.pos, c.max_pos,
-                                    norm_gain=self.gains[3 * l])
+                if tab is not None:
+                    self.n_chained += 1
+                    cq.gemms_tables_dev(qkvg(m), [self.q, self.k, self.v, self.g], B, tab, caches=caches,
+                                        q_stride=c.max_pos * D, s_stride=c.max_pos * hk, pos=self.pos, cap=c.max_pos)
+                else:
+                    cq.gemms_append_dev(qkvg(m), [self.q, self.k, self.v, self.g], self.x, B, caches, c.max_pos * D,
+                                        c.max_pos * hk, self.pos, c.max_pos, norm_gain=self.gains[3 * l])
             else:
-                cq.gemms_fused_dev([m["wq"], m["wk"], m["wv"], m["wg"]], [self.q, self.k, self.v, self.g], self.x, B,
-                                   norm_gain=self.gains[3 * l])
+                cq.gemms_fused_dev(qkvg(m), [self.q, self.k, self.v, self.g], self.x, B, norm_gain=self.gains[3 * l])
                 needle.append_dev(self.self_k[l], self.self_ks[l], self.k, B, D, c.head_dim, c.max_pos * D,
                                   c.max_pos * hk, self.pos, c.max_pos, rope=rope)
                 needle.append_dev(self.self_v[l], self.self_vs[l], self.v, B, D, c.head_dim, c.max_pos * D,
                                   c.max_pos * hk, self.pos, c.max_pos)
             self._attend(l, False, s, rope=(self.cos, self.sin, self.pos))
-            cq.gemms_gated_dev([m["wo"]], [self.x], self.att, self.g, B, resid=self.x)
-            cq.gemms_fused_dev([m["wcq"], m["wcg"]], [self.q, self.g], self.x, B, norm_gain=self.gains[3 * l + 1])
+            cross = [m["wcq"], m["wcg"]]
+            tab = self._produce(m["wo"], self.x, self.att, cross, self.gains[3 * l + 1], gate=self.g, resid=self.x)
+            if tab is not None:
+                self.n_chained += 1
+                cq.gemms_tables_dev(cross, [self.q, self.g], B, tab)
+            else:
+                cq.gemms_fused_dev(cross, [self.q, self.g], self.x, B, norm_gain=self.gains[3 * l + 1])
             self._attend(l, True, s)
-            cq.gemms_gated_dev([m["wco"]], [self.x], self.att, self.g, B, resid=self.x)
-            cq.gemms_fused_dev([m["w1"]], [self.u], self.x, B, norm_gain=self.gains[3 * l + 2], act=1)
-            cq.gemms_fused_dev([m["w2"]], [self.x], self.u, B, resid=self.x)
-        cq.gemms_fused_dev([self.emb], [self.logits], self.x, B, norm_gain=self.gains[3 * c.layers])
+            tab = self._produce(m["wco"], self.x, self.att, [m["w1"]], self.gains[3 * l + 2], gate=self.g,
+                                resid=self.x)
+            if tab is not None:
+                self.n_chained += 1
+                cq.gemms_tables_dev([m["w1"]], [self.u], B, tab, act=1)
+            else:
+                cq.gemms_fused_dev([m["w1"]], [self.u], self.x, B, norm_gain=self.gains[3 * l + 2], act=1)
+            if l + 1 < c.layers:
+                nxt = qkvg(self.mats[l + 1]) if c.head_dim == 64 else None
+            else:
+                nxt = [self.emb]
+            tab = self._produce(m["w2"], self.x, self.u, nxt, self.gains[3 * l + 3], resid=self.x)
+        if tab is not None:
+            self.n_chained += 1
+            cq.gemms_tables_dev([self.emb], [self.logits], B, tab)
+        else:
+            cq.gemms_fused_dev([self.emb], [self.logits], self.x, B, norm_gain=self.gains[3 * c.layers])
         self._advance(s)
 
     def _step_plain(self):

@@ -174,6 +174,40 @@ int cq_gemms_append_dev(int n, cq_matrix *const *ms, float *const *dsts, const f
                         const float *norm_gain, int8_t *const *kv_q, float *const *kv_s, long long q_stride,
                         long long s_stride, const int32_t *pos, int cap, const float *const *cos_t,
                         const float *const *sin_t, void *stream);
+/* A product chained to the next one through its tables (no reference
+ * counterpart: the decoder's layer body, internal/decoder/decoder.go:
+ * 446-505, runs each projection on the previous one's output; here the
+ * previous product's launch also builds the next product's lookup tables,
+ * lut.go:158-282, which that product would otherwise build in a launch of
+ * its own). Results bit for bit those of the unchained calls.
+ *
+ * cq_tables_bytes: bytes of the tables of the product over next[0..n) at
+ * `rows` activations, or 0 when that product takes no tables from a buffer
+ * (it then runs as cq_gemms_fused_dev / cq_gemms_append_dev would). */
+size_t cq_tables_bytes(int n, cq_matrix *const *next, int rows);
+/* dst = [resid +] product of m and (x [* sigmoid(gate)]), as
+ * cq_gemms_gated_dev (gate may be null: no gate); and, where the product
+ * runs one workgroup per activation over all of m's rows, the tables of
+ * the next product over next[0..n_next) of ZCRMSNorm(dst; next_gain)
+ * (next_gain null: dst itself) into `tables`, tables_bytes =
+ * cq_tables_bytes(n_next, next, rows) (0: none asked). *built = 1 when the
+ * tables were built, else 0: then the next product runs unchained. The
+ * next matrices take m's outputs as inputs. Calls that overlap on one
+ * table buffer race. */
+int cq_gemm_tables_dev(const cq_matrix *m, float *dst, const float *x, const float *gate, int rows, const float *resid,
+                       int n_next, cq_matrix *const *next, const float *next_gain, void *tables, size_t tables_bytes,
+                       int *built, void *stream);
+/* The product over ms[0..n) of the activations whose tables
+ * cq_gemm_tables_dev built (with `next` ms, or matrices of the same
+ * codebook and geometry, and the same rows), with the epilogues of
+ * cq_gemms_fused_dev (resid, act) and cq_gemms_append_dev (kv_q null: no
+ * appends). The norm and the input are those the tables were built from.
+ * CQ_ERR_MISUSE where cq_tables_bytes(n, ms, rows) is 0 or differs from
+ * tables_bytes. */
+int cq_gemms_tables_dev(int n, cq_matrix *const *ms, float *const *dsts, int rows, const float *resid, int act,
+                        int8_t *const *kv_q, float *const *kv_s, long long q_stride, long long s_stride,
+                        const int32_t *pos, int cap, const float *const *cos_t, const float *const *sin_t,
+                        const void *tables, size_t tables_bytes, void *stream);
 int cq_row_dev(const cq_matrix *m, float *dst, int r, void *stream);
 /* Rows gathered by index: dst[i] = scale * Row(rows[i]) for i < n, rows a
  * device int32 array: the decoder's scaled token-embedding lookup for
